@@ -1,0 +1,345 @@
+"""Benchmark of the MI355X paged-attention hot path (one JSON line on stdout).
+
+A "step" is one batched decode pass over BASELINE configs[1] (C2): 32
+sequences with context lengths uniform in [256, 4096], 16 query / 8 KV heads,
+head_dim 128, bf16 K/V in 16-token blocks whose tables are a seeded
+permutation of a shared pool (+10% free blocks), one new token per sequence.
+K/V/Q are synthetic N(0,1) bf16 already resident in HBM when timing starts.
+
+`value` is the decode kernel's achieved HBM bandwidth in GB/s: the algorithmic
+bytes of one step (K+V rows attended, q, out, block tables, lengths) divided by
+the mean step time from HIP events on the launch stream over --steps steps.
+`secondary` adds the other BASELINE configs (C1, C3 prefill MFMA utilisation,
+C4 window decode/prefill, C5 int8/fp8 decode) measured the same way.
+`cpu_baseline` times the CPU oracle (a C restatement of the reference's
+single-threaded per-head loop) on the same pool, on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "kir-ai_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "paged decode attn: HBM GB/s (% of peak) + µs/step at B=32; prefill MFMA util"
+D = 128
+BT = 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class DecodeWorkload:
+    """A paged batch resident on the device plus its descriptor."""
+
+    def __init__(self, ctx, lens, Hq, Hkv, fmt, window=0, resident_from=None, seed=0, free_frac=0.10):
+        import torch
+        import llm_hip
+        from llm_hip import workloads
+
+        self.torch = torch
+        self.ctx = ctx
+        self.Hq, self.Hkv, self.fmt, self.window = Hq, Hkv, fmt, window
+        self.batch = workloads.paged_batch(lens, BT, free_frac, seed, resident_from)
+        b = self.batch
+        self.pool = ctx.pool(fmt, BT, Hkv, D, b.n_blocks)
+        # every resident block gets N(0,1) rows, quantised on write for int8/fp8
+        ids = [int(b.tables[i, j]) for i in range(b.seq_lens.size)
+               for j in range(int(b.first_block[i]), (int(b.seq_lens[i]) + BT - 1) // BT)]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        chunk = 4096
+        for s in range(0, len(ids), chunk):
+            idx = torch.tensor(ids[s:s + chunk], dtype=torch.int32, device="cuda")
+            n = idx.numel()
+            k = torch.randn((n, BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+            v = torch.randn((n, BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+            ctx.write_blocks(self.pool, idx, k, v)
+        B = b.seq_lens.size
+        self.q = torch.randn((B, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+        self.d_lens = torch.from_numpy(b.seq_lens).cuda()
+        self.d_tab = torch.from_numpy(b.tables).cuda()
+        self.desc = ctx.decode_desc(self.d_lens, self.d_tab, Hq, int(b.seq_lens.max()), window)
+        self.scale = 1.0 / math.sqrt(D)
+        torch.cuda.synchronize()
+        if ctx.device_errors() != 0:
+            raise RuntimeError("device error flags set while building the workload")
+        self.llm_hip = llm_hip
+
+    def attended_rows(self):
+        import numpy as np
+
+        lens = self.batch.seq_lens.astype(np.int64)
+        lo = np.maximum(0, lens - self.window) if self.window > 0 else np.zeros_like(lens)
+        return lens - lo, lo
+
+    def algorithmic_bytes(self) -> int:
+        import numpy as np
+
+        rows, lo = self.attended_rows()
+        elem = 2 if self.fmt == self.llm_hip.KV_BF16 else 1
+        kv = int(rows.sum()) * self.Hkv * D * elem * 2
+        blocks = ((self.batch.seq_lens.astype(np.int64) + BT - 1) // BT) - lo // BT
+        scales = 0
+        if self.fmt == self.llm_hip.KV_INT8:
+            scales = int(rows.sum()) * self.Hkv * 2 * 2
+        elif self.fmt == self.llm_hip.KV_FP8_E4M3:
+            scales = int(blocks.sum()) * self.Hkv * 4 * 2
+        B = self.batch.seq_lens.size
+        qo = 2 * B * self.Hq * D * 2
+        tables = int(blocks.sum()) * 4 + B * 4
+        return kv + scales + qo + tables
+
+    def step(self, stream):
+        self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Mean ms per step from HIP events recorded on the launch stream."""
+    import torch
+
+    stream = torch.cuda.Stream()  # default priority
+    for _ in range(warmup):
+        fn(stream)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn(stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_baseline_decode(w: DecodeWorkload, budget_s: float):
+    """Times the oracle (single-threaded reference loop) on whole decode steps of the same pool."""
+    import numpy as np
+    import oracle
+
+    b = w.batch
+    opool = oracle.Pool.from_raw(w.fmt, BT, w.Hkv, D, b.n_blocks, w.pool.raw())
+    q = w.q.view(w.torch.int16).cpu().numpy().view(np.uint16).ravel()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        st, _ = opool.decode(w.Hq, b.seq_lens, b.tables, w.window, q, w.scale, threads=1)
+        if st != 0:
+            raise RuntimeError(f"oracle decode failed: {st}")
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 20:
+            break
+    sec_per_step = el / reps
+    return {
+        "value": round(w.algorithmic_bytes() / sec_per_step / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{reps} full C2 decode step(s) (32 seqs x 16 heads) of the oracle's per-head loop, "
+                  f"single thread, {el:.1f} s; {sec_per_step * 1e6:.0f} us/step",
+        "us_per_step": round(sec_per_step * 1e6, 1),
+        "host": host_info(),
+    }
+
+
+def host_info() -> str:
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{model} (nproc={os.cpu_count()})"
+
+
+def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos=None):
+    """Prefill workload: B sequences of prefix + chunk tokens, all K/V resident."""
+    import torch
+    import llm_hip
+    from llm_hip import workloads
+
+    ctxlen = prefix + chunk
+    lens = [ctxlen] * B
+    first = None if resident_from_pos is None else [resident_from_pos // BT] * B
+    batch = workloads.paged_batch(lens, BT, 0.10, seed, first)
+    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks)
+    ids = [int(batch.tables[i, j]) for i in range(B) for j in range(int(batch.first_block[i]), (ctxlen + BT - 1) // BT)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    idx = torch.tensor(ids, dtype=torch.int32, device="cuda")
+    k = torch.randn((len(ids), BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((len(ids), BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    ctx.write_blocks(pool, idx, k, v)
+    del k, v
+    q = torch.randn((B * chunk, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    starts = torch.tensor([i * chunk for i in range(B + 1)], dtype=torch.int32, device="cuda")
+    clens = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    tab = torch.from_numpy(batch.tables).cuda()
+    desc = llm_hip.PrefillDesc(num_seqs=B, num_q_heads=Hq, max_blocks_per_seq=batch.max_blocks, window=window,
+                               total_q_rows=B * chunk, max_chunk_len=chunk, d_chunk_starts=starts.data_ptr(),
+                               d_context_lens=clens.data_ptr(), d_block_tables=tab.data_ptr())
+    keep = (pool, q, out, starts, clens, tab)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(stream):
+        ctx.paged_prefill(pool, desc, q, out, scale, stream=stream)
+
+    # FLOPs of unmasked (query, key) pairs only: 4 * D per pair per head
+    pairs = 0
+    for i in range(chunk):
+        pos = prefix + i
+        lo = max(0, pos - window + 1) if window > 0 else 0
+        pairs += pos - lo + 1
+    flops = 4 * D * pairs * Hq * B
+    return step, flops, keep
+
+
+def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10):
+    w = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free)
+    ms = time_steps(w.step, steps, warmup)
+    if ctx.device_errors() != 0:
+        raise RuntimeError(f"{name}: device error flags set during timing")
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    return w, {
+        "config": name,
+        "us_per_step": round(ms * 1e3, 2),
+        "hbm_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
+        "bytes_per_step": w.algorithmic_bytes(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path has no multi-GPU mode (the batch shards by sequence with "
+              "no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import llm_hip
+    from llm_hip import workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    ctx = llm_hip.Context(0)
+
+    # ---- headline: C2 batched paged decode ----
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    log(f"C2 decode: B=32 sum(L)={int(lens.sum())}")
+    w, c2 = measure_decode(ctx, "C2", lens, 16, 8, llm_hip.KV_BF16, args.steps, args.warmup,
+                           seed=workloads.SEED_BASE + 1)
+    ms = c2["us_per_step"] / 1e3
+    value = c2["hbm_gbs"]
+    log(f"C2: {c2['us_per_step']} us/step, {value} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle, 1 thread) on the C2 pool ...")
+        cpu = cpu_baseline_decode(w, args.cpu_seconds)
+        log(f"CPU: {cpu['us_per_step']} us/step")
+    del w
+    torch.cuda.empty_cache()
+
+    secondary = []
+    if not args.no_secondary:
+        sec_steps = max(10, args.steps // 2)
+        _, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, args.warmup,
+                              seed=workloads.SEED_BASE, free=0.0)
+        secondary.append(r)
+        log(f"C1: {r}")
+        L, W = 32768, 4096
+        _, r = measure_decode(ctx, "C4 decode 4x32768 W=4096", [L] * 4, 16, 8, llm_hip.KV_BF16, sec_steps,
+                              args.warmup, window=W, resident_from=[(L - W) // BT] * 4, seed=workloads.SEED_BASE + 3)
+        secondary.append(r)
+        log(f"C4 decode: {r}")
+        for fmt, nm in ((llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
+            wq, r = measure_decode(ctx, f"C5 decode {nm} B=64 L=8192 Hq32/Hkv8", [8192] * 64, 32, 8, fmt,
+                                   sec_steps, args.warmup, seed=workloads.SEED_BASE + 4, free=0.0)
+            secondary.append(r)
+            log(f"C5 {nm}: {r}")
+            del wq
+            torch.cuda.empty_cache()
+        for name, B, prefix, chunk, Hq, Hkv, window, res in (
+                ("C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None),
+                ("C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096)):
+            step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res)
+            pms = time_steps(step, sec_steps, args.warmup)
+            if ctx.device_errors() != 0:
+                raise RuntimeError(f"{name}: device error flags set")
+            tf = flops / (pms * 1e-3) / 1e12
+            r = {"config": name, "us_per_step": round(pms * 1e3, 2), "tflops": round(tf, 1),
+                 "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
+                 "flops_per_step": flops}
+            secondary.append(r)
+            log(f"{name}: {r}")
+            del keep
+            torch.cuda.empty_cache()
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 K/V/Q resident in HBM; seeded lengths and block permutation",
+        "config": {
+            "workload": "C2 batched paged GQA decode: B=32, L~U[256,4096] (seeded), Hq=16, Hkv=8, D=128, "
+                        "bf16 KV in 16-token blocks, permuted pool +10% free, 1 new token/seq",
+            "global_batch": 32,
+            "sum_context_tokens": int(lens.sum()),
+            "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "us_per_step": c2["us_per_step"],
+            "tokens_per_s": c2["tokens_per_s"],
+            "bytes_per_step": c2["bytes_per_step"],
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": value,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,278 @@
+/*
+ * llm_hip.h -- C ABI of the MI355X (gfx950) attention-over-KV-cache library.
+ *
+ * This is the drop-in boundary for kir-ai's accelerated attention path.  In the
+ * reference, the per-layer attention calls cross the `NativeMatvecBackend`
+ * trait (crates/llm-backend/src/core/native_matvec.rs:222-769) into the Metal
+ * implementation (crates/llm-native-runtime/src/native_matvec.rs:3026-4566).
+ * A Rust shim binds the functions below with `extern "C"` and adds a
+ * `NativeTextMatvecBackend::Hip` arm (see INTEGRATION.md for the binding).
+ *
+ * Conventions
+ *   - Every function returns an int status (llh_status); none aborts.
+ *   - Pointers named `d_*` are device pointers; `h_*` are host pointers.
+ *   - Batched entry points are asynchronous on the given stream (hipStream_t
+ *     passed as void*, NULL = the null stream) and allocate nothing once the
+ *     context's workspace is large enough (llh_ctx_reserve_workspace).
+ *   - Trait-mirror entry points (llh_layer_cache_*, llh_full_attention_*,
+ *     llh_append_kv_cache_*) are synchronous, like the reference's awaited
+ *     command buffers (crates/llm-metal/src/device/primitives.rs:1325-1338).
+ *   - A context is safe to use from several threads on distinct streams.
+ */
+#ifndef LLM_HIP_H
+#define LLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLH_ABI_VERSION 1
+
+/* Status codes.  Mirrors MathError / KvCacheError
+ * (crates/llm-backend/src/core/math.rs:10-15, crates/llm-kv-cache/src/lib.rs). */
+typedef enum llh_status {
+  LLH_OK = 0,
+  /* "not handled": the Ok(false) of full_attention_cache_mix_f32_in_place
+   * (native_matvec.rs:656-668); the caller runs its own per-head path. */
+  LLH_NOT_HANDLED = 1,
+  LLH_ERR_INVALID_SHAPE = -1, /* MathError::InvalidShape / KvCacheError::InvalidShape */
+  LLH_ERR_CAPACITY = -2,      /* KvCacheError::CapacityExceeded */
+  LLH_ERR_NON_FINITE = -3,    /* "softmax scores must be finite" (math.rs:485-489), NonFiniteValue */
+  LLH_ERR_UNSUPPORTED = -4,   /* KvCacheError::UnsupportedFormat */
+  LLH_ERR_DEVICE = -5,        /* HIP runtime failure: caller may record a fallback (native_matvec.rs:2979-2999) */
+  LLH_ERR_STALE = -6,         /* block id / revision mismatch (layer.rs:1001-1009) */
+  LLH_ERR_NULL = -7           /* NULL handle or pointer */
+} llh_status;
+
+/* KV storage formats (crates/llm-kv-cache/src/format.rs:5-21 plus the two
+ * quantised device layouts of this build). */
+typedef enum llh_kv_format {
+  LLH_KV_BF16 = 0,    /* bf16 K and V */
+  LLH_KV_INT8 = 1,    /* int8 codes, fp16 scale per (token, kv head): absmax/127 */
+  LLH_KV_FP8_E4M3 = 2 /* OCP e4m3fn codes, f32 scale per (block, kv head) for K and for V: absmax/448 */
+} llh_kv_format;
+
+typedef struct llh_ctx llh_ctx;
+typedef struct llh_kv_pool llh_kv_pool;
+typedef struct llh_layer_cache llh_layer_cache;
+
+/* ------------------------------------------------------------------ */
+/* context                                                            */
+/* ------------------------------------------------------------------ */
+
+/* Creates a context on HIP device `device`.  Replaces NativeTextMatvecBackend::
+ * system_default (crates/llm-native-runtime/src/native_matvec.rs:2823-2832). */
+int llh_ctx_create(int device, llh_ctx **out);
+int llh_ctx_destroy(llh_ctx *ctx);
+/* Message of the last error on this context (like MathError's String); never NULL. */
+const char *llh_ctx_last_error(const llh_ctx *ctx);
+/* Grows the device workspace used by split-K partials and counters so that
+ * later batched calls of at most this size allocate nothing. */
+int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes);
+/* Workspace bytes a llh_paged_decode call with these bounds needs. */
+size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len);
+/* Fallback/attempt counters, as MetalBackendMetrics' attention counters
+ * (crates/llm-native-runtime/src/native_metrics.rs:73-112). */
+typedef struct llh_metrics {
+  uint64_t decode_calls;
+  uint64_t prefill_calls;
+  uint64_t append_calls;
+  uint64_t not_handled;
+  uint64_t device_errors;
+  uint64_t shape_errors;
+} llh_metrics;
+int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
+/* Waits for the device, then reads (and optionally clears) the sticky error
+ * flags the batched kernels raise instead of faulting: 1 = a block table entry
+ * outside the pool, 2 = a sequence longer than the call's max_seq_len allows,
+ * 4 = a non-finite score. */
+int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset);
+
+/* ------------------------------------------------------------------ */
+/* paged KV pool (device resident)                                    */
+/* ------------------------------------------------------------------ */
+/*
+ * One pool holds one layer's K and V for many sequences in fixed-size blocks
+ * (crates/llm-kv-cache/src/block_pool.rs:159-171 makes block size a pool
+ * parameter).  Device layout, block b, kv head h:
+ *   K  [n_blocks][kv_heads][block_tokens][head_dim]   token rows
+ *   V  [n_blocks][kv_heads][head_dim][block_tokens]   dim rows (transposed)
+ *   int8 scales: fp16 [n_blocks][kv_heads][block_tokens] for K and for V
+ *   fp8 scales : f32  [n_blocks][kv_heads]               for K and for V
+ * Position p of a sequence lives in block_table[(p / block_tokens) % max_blocks]
+ * at offset p % block_tokens.  The modulus lets a ring of blocks serve a
+ * sliding window (crates/llm-kv-cache/src/layer.rs:765-805).
+ */
+typedef struct llh_kv_pool_info {
+  int32_t format;
+  int32_t block_tokens;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int64_t n_blocks;
+  void *d_k;
+  void *d_v;
+  void *d_k_scales; /* NULL for bf16 */
+  void *d_v_scales; /* NULL for bf16 */
+  size_t k_bytes;   /* bytes of d_k (and of d_v) */
+  size_t scale_bytes;
+} llh_kv_pool_info;
+
+int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32_t kv_heads,
+                       int32_t head_dim, int64_t n_blocks, llh_kv_pool **out);
+int llh_kv_pool_destroy(llh_kv_pool *pool);
+int llh_kv_pool_get_info(const llh_kv_pool *pool, llh_kv_pool_info *out);
+
+/* Writes whole blocks, quantising on write.  Replaces the block re-quantisation
+ * of LayerInt8KvStore::update_block (crates/llm-kv-cache/src/format.rs:262-276)
+ * and the Metal f32->f16 block upload (native_matvec.rs:384-465).
+ *   d_blocks [n] pool block indices; d_k, d_v [n][block_tokens][kv_heads][head_dim] bf16.
+ * int8: per (token, head) scale = f16(absmax/127), codes with the rounded scale.
+ * fp8 : per (block, head) scale = absmax/448 over the block's tokens. */
+int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks, const void *d_k,
+                        const void *d_v, int32_t n, void *stream);
+
+/* Appends token rows at absolute slots (block * block_tokens + offset),
+ * quantising on write for int8.  Replaces append_kv_cache_sliding_f32
+ * (native_matvec.rs:643-653) and the Metal direct f16/int8 append
+ * (crates/llm-native-runtime/src/native_matvec.rs:575-943).
+ *   d_slots [n] int64; d_k, d_v [n][kv_heads][head_dim] bf16.
+ * fp8 pools return LLH_ERR_UNSUPPORTED (their scale is per block: use llh_kv_write_blocks). */
+int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k,
+                  const void *d_v, int32_t n, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* batched paged attention (the hot path)                             */
+/* ------------------------------------------------------------------ */
+
+/* Per-step decode descriptor.  The reference calls attention once per sequence
+ * (crates/llm-server/src/engine/scheduler.rs:579-712 admits, it does not batch);
+ * this descriptor batches one step of many sequences. */
+typedef struct llh_decode_desc {
+  int32_t num_seqs;
+  int32_t num_q_heads;        /* Hq; kv heads come from the pool; Hq % Hkv == 0 */
+  int32_t max_blocks_per_seq; /* row stride of d_block_tables */
+  int32_t max_seq_len;        /* host-known bound on d_seq_lens (sizes the grid) */
+  int32_t window;             /* 0 = full attention; else attend [max(0, len - window), len) */
+  int32_t reserved;
+  const int32_t *d_seq_lens;     /* [num_seqs] tokens incl. the new one (appended first, native_attention.rs:307-309) */
+  const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] pool block indices */
+} llh_decode_desc;
+
+/* One decode step: out[b][h] = softmax(scale * q[b][h] . K^T) V over the
+ * sequence's attended positions, GQA kv head = h / (Hq / Hkv)
+ * (native_attention.rs:707-773).  d_q, d_out: [num_seqs][Hq][head_dim] bf16. */
+int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                     void *d_out, float score_scale, void *stream);
+
+/* Chunked prefill over cached prefix blocks.  Sequence b owns query rows
+ * [d_chunk_starts[b], d_chunk_starts[b+1]); its context holds d_context_lens[b]
+ * tokens (prefix + the chunk, whose K/V are already in the pool).  Row i sits
+ * at position context_len - chunk_len + i and attends [lo, pos], lo = window ?
+ * pos - window + 1 : 0 (native_attention.rs:356-464: append then attend). */
+typedef struct llh_prefill_desc {
+  int32_t num_seqs;
+  int32_t num_q_heads;
+  int32_t max_blocks_per_seq;
+  int32_t window;
+  int32_t total_q_rows;   /* d_chunk_starts[num_seqs] */
+  int32_t max_chunk_len;  /* host-known bound (sizes the grid) */
+  const int32_t *d_chunk_starts; /* [num_seqs + 1] */
+  const int32_t *d_context_lens; /* [num_seqs] */
+  const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] */
+} llh_prefill_desc;
+
+/* d_q, d_out: [total_q_rows][Hq][head_dim] bf16.  bf16 pools only. */
+int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
+                      void *d_out, float score_scale, void *stream);
+
+/* Bit-exact gather of positions [lo, hi) of sequence `seq` through its block
+ * table into d_out [hi-lo][kv_heads][head_dim] raw elements (2 bytes bf16,
+ * 1 byte int8/fp8); tensor 0 = K, 1 = V.  The gather half of
+ * select_kv_cache_head_rows_f32_in_place (native_matvec.rs:619-641) and of
+ * select_head_rows_* (crates/llm-metal/src/device/shaders/generic.metal:310-360). */
+int llh_debug_gather(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, int32_t seq,
+                     int32_t lo, int32_t hi, int32_t tensor, void *d_out, void *stream);
+
+/* Decodes `n` raw fp8 e4m3 codes with the kernels' own conversion (f32 out). */
+int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int32_t n, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* trait mirror: LayerKvCache + NativeMatvecBackend attention hooks    */
+/* ------------------------------------------------------------------ */
+
+/* LayerKvCache::new_with_config (crates/llm-kv-cache/src/layer.rs:345-400):
+ * a ring of `max_tokens` token slots whose storage is paged device blocks.
+ * format: LLH_KV_BF16 (the reference's f32 rows are stored as bf16) or
+ * LLH_KV_INT8 (per (token, head) fp16 scales).  Errors as the reference:
+ * zero sizes -> INVALID_SHAPE, fp8 -> UNSUPPORTED. */
+int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, size_t head_dim, int32_t format,
+                           llh_layer_cache **out);
+int llh_layer_cache_destroy(llh_layer_cache *cache);
+/* Clone with a fresh cache id that shares blocks until written (layer.rs:237-259, block.rs:124-130). */
+int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out);
+/* clear() (layer.rs:1068-1086) */
+int llh_layer_cache_clear(llh_layer_cache *cache);
+
+typedef struct llh_layer_cache_state {
+  uint64_t id;            /* LayerKvCache::id() */
+  uint64_t revision;      /* revision() */
+  uint64_t max_tokens;
+  uint64_t kv_heads;
+  uint64_t head_dim;
+  uint64_t token_count;   /* token_count() */
+  uint64_t tokens_seen;   /* next_position() */
+  uint64_t window_start;  /* physical slot of logical token 0 */
+  uint64_t block_count;   /* device blocks backing the ring */
+  int32_t format;
+  int32_t block_tokens;
+} llh_layer_cache_state;
+int llh_layer_cache_get_state(const llh_layer_cache *cache, llh_layer_cache_state *out);
+
+/* LayerKvCacheBlockRun / active_blocks() (layer.rs:158-207,972-1044): runs of
+ * logical tokens that are contiguous in one device block. */
+typedef struct llh_block_run {
+  uint64_t block_id;            /* BlockId (0 = invalid, block_id.rs:11-41) */
+  uint64_t block_index;         /* index in the cache's block table */
+  uint64_t logical_token_start;
+  uint64_t physical_token_start;
+  uint64_t block_token_start;
+  uint64_t token_count;
+} llh_block_run;
+int llh_layer_cache_active_blocks(const llh_layer_cache *cache, llh_block_run *h_out, size_t capacity,
+                                  size_t *count);
+/* block_ids() (layer.rs:954-956) */
+int llh_layer_cache_block_ids(const llh_layer_cache *cache, uint64_t *h_out, size_t capacity, size_t *count);
+
+/* NativeMatvecBackend::append_kv_cache_sliding_f32 (native_matvec.rs:643-653):
+ * ring append; once full, overwrites the oldest slot (layer.rs:765-805).
+ * h_key, h_value: [kv_heads * head_dim] f32 host rows. */
+int llh_append_kv_cache_sliding_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key,
+                                    const float *h_value, size_t len);
+/* LayerKvCache::append (strict; capacity error when full, layer.rs:744-763). */
+int llh_append_kv_cache_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key, const float *h_value,
+                            size_t len);
+
+/* NativeMatvecBackend::full_attention_cache_mix_f32_in_place
+ * (native_matvec.rs:656-668): attends the first `row_count` logical rows.
+ * h_query [num_attention_heads * head_dim], h_output [>= same] f32 host.
+ * Returns LLH_OK when handled, LLH_NOT_HANDLED for shapes the device path
+ * does not take, or an error (shape errors as primitives.rs:1113-1128). */
+int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache, const float *h_query,
+                                              size_t query_len, size_t row_count, size_t num_attention_heads,
+                                              size_t num_key_value_heads, size_t head_dim, float score_scale,
+                                              float *h_output, size_t output_len);
+
+/* NativeMatvecBackend::select_kv_cache_head_rows_f32_in_place
+ * (native_matvec.rs:619-641): rows [0, row_count) of one head slice
+ * [head_start, head_start + head_len) of the row vector, as f32. */
+int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache, int32_t tensor,
+                                               size_t row_count, size_t head_start, size_t head_len,
+                                               float *h_output, size_t output_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLM_HIP_H */

@@ -1,0 +1,932 @@
+// Host side of libllm_hip: the C ABI declared in include/llm_hip.h.
+//
+// Batched entry points validate shapes, size the split-K grid, and launch the
+// kernels asynchronously on the caller's stream.  The trait-mirror entry
+// points re-state kir-ai's LayerKvCache ring (crates/llm-kv-cache/src/layer.rs)
+// over device-resident 16-token blocks and answer the NativeMatvecBackend
+// attention hooks (crates/llm-backend/src/core/native_matvec.rs:619-668)
+// synchronously, as the Metal backend does after awaiting its command buffer.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "llh_internal.h"
+#include "llm_hip.h"
+
+using namespace llh;
+
+namespace {
+
+constexpr size_t kCounterSlots = 65536;  // (sequence, kv head) arrival counters
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(int32_t);
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+std::atomic<uint64_t> g_next_block_id{1};
+std::atomic<uint64_t> g_next_cache_id{1};
+
+int env_int(const char *name, int dflt) {
+  const char *v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  return std::atoi(v);
+}
+
+// Split-K sizing for the tuned decode kernel.  `est_blocks` bounds the blocks
+// any sequence attends.  Splits of 4..32 blocks keep the grid at roughly 4096
+// workgroups so every CU gets several.
+struct SplitPlan {
+  int split_blocks;
+  int max_splits;
+  int est_blocks;
+};
+
+SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window) {
+  int span = max_seq_len;
+  if (window > 0) span = std::min(span, window);
+  const int est_blocks = (span + kFastBlockTokens - 1) / kFastBlockTokens + 1;
+  int split = env_int("LLH_DECODE_SPLIT_BLOCKS", 0);
+  if (split <= 0) {
+    const long long work = (long long)num_seqs * kv_heads * est_blocks;
+    split = 4;
+    while (split < 32 && work / (split * 2) >= 4096) split *= 2;
+  }
+  SplitPlan p;
+  p.split_blocks = split;
+  p.est_blocks = est_blocks;
+  p.max_splits = (est_blocks + split - 1) / split;
+  return p;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+struct llh_ctx {
+  int device = 0;
+  std::mutex mu;
+  std::string last_error;
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+  int32_t *d_err = nullptr;
+  std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
+      shape_errors{0};
+
+  int fail(int status, const std::string &msg) {
+    {
+      std::lock_guard<std::mutex> g(err_mu);
+      last_error = msg;
+    }
+    if (status == LLH_ERR_DEVICE) device_errors++;
+    if (status == LLH_ERR_INVALID_SHAPE) shape_errors++;
+    return status;
+  }
+  int hip_fail(hipError_t e, const char *what) {
+    return fail(LLH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+  }
+  // Ensures the workspace holds `bytes`; the counter region is zeroed on growth.
+  int ensure_ws(size_t bytes) {
+    std::lock_guard<std::mutex> g(mu);
+    if (bytes <= ws_bytes) return LLH_OK;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    if (ws) {
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+      (void)hipFree(ws);
+      ws = nullptr;
+      ws_bytes = 0;
+    }
+    size_t nb = align_up(std::max(bytes, kCounterBytes + kAlign));
+    e = hipMalloc(&ws, nb);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+    e = hipMemset(ws, 0, nb);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace)");
+    ws_bytes = nb;
+    return LLH_OK;
+  }
+  std::mutex err_mu;
+};
+
+struct llh_kv_pool {
+  llh_ctx *ctx = nullptr;
+  PoolView view{};
+  void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr;
+  size_t k_bytes = 0, s_bytes = 0;
+};
+
+static size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 ? 2 : 1; }
+
+static size_t scale_bytes_per_block(int32_t format, int32_t kv_heads, int32_t block_tokens) {
+  if (format == LLH_KV_INT8) return (size_t)kv_heads * block_tokens * 2;
+  if (format == LLH_KV_FP8_E4M3) return (size_t)kv_heads * 4;
+  return 0;
+}
+
+extern "C" {
+
+int llh_ctx_create(int device, llh_ctx **out) {
+  if (!out) return LLH_ERR_NULL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return LLH_ERR_DEVICE;
+  auto *ctx = new llh_ctx();
+  ctx->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipMalloc(&ctx->d_err, sizeof(int32_t)) != hipSuccess ||
+      hipMemset(ctx->d_err, 0, sizeof(int32_t)) != hipSuccess) {
+    delete ctx;
+    return LLH_ERR_DEVICE;
+  }
+  *out = ctx;
+  return LLH_OK;
+}
+
+int llh_ctx_destroy(llh_ctx *ctx) {
+  if (!ctx) return LLH_ERR_NULL;
+  (void)hipSetDevice(ctx->device);
+  (void)hipDeviceSynchronize();
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->d_err) (void)hipFree(ctx->d_err);
+  delete ctx;
+  return LLH_OK;
+}
+
+const char *llh_ctx_last_error(const llh_ctx *ctx) {
+  if (!ctx) return "null context";
+  return ctx->last_error.c_str();
+}
+
+int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes) {
+  if (!ctx) return LLH_ERR_NULL;
+  return ctx->ensure_ws(kCounterBytes + bytes);
+}
+
+size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || max_seq_len < 0) return 0;
+  // the smallest split size gives the largest partial count
+  const int est_blocks = (max_seq_len + kFastBlockTokens - 1) / kFastBlockTokens + 1;
+  const size_t max_splits = (size_t)(est_blocks + 3) / 4;
+  const size_t rows = (size_t)num_seqs * num_q_heads * max_splits;
+  const size_t generic = (size_t)num_seqs * num_q_heads * std::max(1, max_seq_len) * sizeof(float);
+  return std::max(align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic);
+}
+
+int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
+  if (!ctx || !out) return LLH_ERR_NULL;
+  out->decode_calls = ctx->decode_calls.load();
+  out->prefill_calls = ctx->prefill_calls.load();
+  out->append_calls = ctx->append_calls.load();
+  out->not_handled = ctx->not_handled.load();
+  out->device_errors = ctx->device_errors.load();
+  out->shape_errors = ctx->shape_errors.load();
+  return LLH_OK;
+}
+
+int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset) {
+  if (!ctx || !flags) return LLH_ERR_NULL;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(flags, ctx->d_err, sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && reset) e = hipMemset(ctx->d_err, 0, sizeof(int32_t));
+  if (e != hipSuccess) return ctx->hip_fail(e, "device error flags");
+  return LLH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// pool
+// ---------------------------------------------------------------------------
+
+int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32_t kv_heads, int32_t head_dim,
+                       int64_t n_blocks, llh_kv_pool **out) {
+  if (!ctx || !out) return LLH_ERR_NULL;
+  *out = nullptr;
+  if (format < LLH_KV_BF16 || format > LLH_KV_FP8_E4M3)
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "unsupported KV format");
+  if (block_tokens <= 0 || kv_heads <= 0 || head_dim <= 0 || n_blocks <= 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "kv pool sizes must be positive");
+  if (format != LLH_KV_BF16 && (block_tokens % 4 != 0 || head_dim % 4 != 0))
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "quantised pools need block_tokens and head_dim divisible by 4");
+  if (n_blocks > INT32_MAX) return ctx->fail(LLH_ERR_INVALID_SHAPE, "block indices are int32");
+  auto *pool = new llh_kv_pool();
+  pool->ctx = ctx;
+  pool->k_bytes = (size_t)n_blocks * kv_heads * block_tokens * head_dim * elem_bytes(format);
+  pool->s_bytes = (size_t)n_blocks * scale_bytes_per_block(format, kv_heads, block_tokens);
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc(&pool->k, pool->k_bytes);
+  if (e == hipSuccess) e = hipMalloc(&pool->v, pool->k_bytes);
+  if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->ks, pool->s_bytes);
+  if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
+  if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->ks, 0, pool->s_bytes);
+  if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->vs, 0, pool->s_bytes);
+  if (e != hipSuccess) {
+    llh_kv_pool_destroy(pool);
+    return ctx->hip_fail(e, "hipMalloc(kv pool)");
+  }
+  pool->view = PoolView{format, block_tokens, kv_heads, head_dim, n_blocks, pool->k, pool->v, pool->ks, pool->vs};
+  *out = pool;
+  return LLH_OK;
+}
+
+int llh_kv_pool_destroy(llh_kv_pool *pool) {
+  if (!pool) return LLH_ERR_NULL;
+  if (pool->ctx) (void)hipSetDevice(pool->ctx->device);
+  if (pool->k) (void)hipFree(pool->k);
+  if (pool->v) (void)hipFree(pool->v);
+  if (pool->ks) (void)hipFree(pool->ks);
+  if (pool->vs) (void)hipFree(pool->vs);
+  delete pool;
+  return LLH_OK;
+}
+
+int llh_kv_pool_get_info(const llh_kv_pool *pool, llh_kv_pool_info *out) {
+  if (!pool || !out) return LLH_ERR_NULL;
+  out->format = pool->view.format;
+  out->block_tokens = pool->view.block_tokens;
+  out->kv_heads = pool->view.kv_heads;
+  out->head_dim = pool->view.head_dim;
+  out->n_blocks = pool->view.n_blocks;
+  out->d_k = pool->k;
+  out->d_v = pool->v;
+  out->d_k_scales = pool->ks;
+  out->d_v_scales = pool->vs;
+  out->k_bytes = pool->k_bytes;
+  out->scale_bytes = pool->s_bytes;
+  return LLH_OK;
+}
+
+int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks, const void *d_k, const void *d_v,
+                        int32_t n, void *stream) {
+  if (!ctx || !pool) return LLH_ERR_NULL;
+  if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "negative block count");
+  if (n == 0) return LLH_OK;
+  if (!d_blocks || !d_k || !d_v) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  WriteBlocksArgs a{};
+  a.pool = pool->view;
+  a.k_dst = pool->k;
+  a.v_dst = pool->v;
+  a.ks_dst = pool->ks;
+  a.vs_dst = pool->vs;
+  a.blocks = d_blocks;
+  a.k = static_cast<const uint16_t *>(d_k);
+  a.v = static_cast<const uint16_t *>(d_v);
+  a.n = n;
+  a.err = ctx->d_err;
+  hipError_t e = launch_write_blocks(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "write_blocks launch");
+  return LLH_OK;
+}
+
+int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
+                  int32_t n, void *stream) {
+  if (!ctx || !pool) return LLH_ERR_NULL;
+  if (pool->view.format == LLH_KV_FP8_E4M3)
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "fp8 pools carry per-block scales: write whole blocks");
+  if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "negative token count");
+  if (n == 0) return LLH_OK;
+  if (!d_slots || !d_k || !d_v) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  AppendArgs a{};
+  a.pool = pool->view;
+  a.k_dst = pool->k;
+  a.v_dst = pool->v;
+  a.ks_dst = pool->ks;
+  a.vs_dst = pool->vs;
+  a.slots = d_slots;
+  a.k = d_k;
+  a.v = d_v;
+  a.n = n;
+  a.src_f32 = 0;
+  a.err = ctx->d_err;
+  ctx->append_calls++;
+  hipError_t e = launch_append(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "append launch");
+  return LLH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// batched attention
+// ---------------------------------------------------------------------------
+
+static int check_desc_common(llh_ctx *ctx, const llh_kv_pool *pool, int32_t num_seqs, int32_t q_heads,
+                             int32_t max_blocks, int32_t window) {
+  if (num_seqs < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "num_seqs must be >= 0");
+  if (q_heads <= 0 || q_heads % pool->view.kv_heads != 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "num_q_heads must be a positive multiple of kv_heads");
+  if (max_blocks <= 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "max_blocks_per_seq must be positive");
+  if (window < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "window must be >= 0");
+  return LLH_OK;
+}
+
+int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q, void *d_out,
+                     float score_scale, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
+  if (st != LLH_OK) return st;
+  if (desc->num_seqs == 0) return LLH_OK;
+  if (desc->max_seq_len < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "max_seq_len must be >= 0");
+  if (!d_q || !d_out || !desc->d_seq_lens || !desc->d_block_tables)
+    return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
+  if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
+  const PoolView &pv = pool->view;
+  const int group = desc->num_q_heads / pv.kv_heads;
+  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
+                    (group == 1 || group == 2 || group == 4 || group == 8) &&
+                    (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !env_int("LLH_FORCE_GENERIC", 0);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ctx->decode_calls++;
+  if (fast) {
+    const SplitPlan plan = plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window);
+    const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
+    const size_t ml_off = kCounterBytes;
+    const size_t o_off = ml_off + align_up(rows * sizeof(float2));
+    st = ctx->ensure_ws(o_off + rows * kFastHeadDim * sizeof(float));
+    if (st != LLH_OK) return st;
+    char *ws = static_cast<char *>(ctx->ws);
+    DecodeArgs a{};
+    a.pool = pv;
+    a.q = static_cast<const uint16_t *>(d_q);
+    a.out = static_cast<uint16_t *>(d_out);
+    a.seq_lens = desc->d_seq_lens;
+    a.tables = desc->d_block_tables;
+    a.ws_o = reinterpret_cast<float *>(ws + o_off);
+    a.ws_ml = reinterpret_cast<float2 *>(ws + ml_off);
+    a.counters = reinterpret_cast<int32_t *>(ws);
+    a.err = ctx->d_err;
+    a.num_seqs = desc->num_seqs;
+    a.q_heads = desc->num_q_heads;
+    a.max_blocks = desc->max_blocks_per_seq;
+    a.window = desc->window;
+    a.split_blocks = plan.split_blocks;
+    a.max_splits = plan.max_splits;
+    a.scale_log2e = score_scale * 1.4426950408889634f;
+    hipError_t e = launch_decode(a, group, desc->max_seq_len, s);
+    if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");
+    return LLH_OK;
+  }
+  // any other shape: reference-order kernel
+  const int span = desc->window > 0 ? std::min(desc->window, desc->max_seq_len) : desc->max_seq_len;
+  const int stride = std::max(1, span);
+  const size_t off = kCounterBytes;
+  st = ctx->ensure_ws(off + (size_t)desc->num_seqs * desc->num_q_heads * stride * sizeof(float));
+  if (st != LLH_OK) return st;
+  GenericDecodeArgs g{};
+  g.pool = pv;
+  g.q = d_q;
+  g.out = d_out;
+  g.seq_lens = desc->d_seq_lens;
+  g.starts = nullptr;
+  g.tables = desc->d_block_tables;
+  g.scores = reinterpret_cast<float *>(static_cast<char *>(ctx->ws) + off);
+  g.err = ctx->d_err;
+  g.num_seqs = desc->num_seqs;
+  g.q_heads = desc->num_q_heads;
+  g.max_blocks = desc->max_blocks_per_seq;
+  g.window = desc->window;
+  g.ring_tokens = 0;
+  g.score_stride = stride;
+  g.scale = score_scale;
+  hipError_t e = launch_decode_generic(g, 0, 0, s);
+  if (e != hipSuccess) return ctx->hip_fail(e, "generic decode launch");
+  return LLH_OK;
+}
+
+int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
+                      void *d_out, float score_scale, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
+  if (st != LLH_OK) return st;
+  if (desc->num_seqs == 0 || desc->total_q_rows == 0) return LLH_OK;
+  if (desc->total_q_rows < 0 || desc->max_chunk_len < 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "row counts must be >= 0");
+  const PoolView &pv = pool->view;
+  if (pv.format != LLH_KV_BF16 || pv.head_dim != kFastHeadDim || pv.block_tokens != kFastBlockTokens) {
+    ctx->not_handled++;
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill takes bf16 pools with head_dim 128 and 16-token blocks");
+  }
+  if (!d_q || !d_out || !desc->d_chunk_starts || !desc->d_context_lens || !desc->d_block_tables)
+    return ctx->fail(LLH_ERR_NULL, "null device pointer in prefill call");
+  if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
+  PrefillArgs a{};
+  a.pool = pv;
+  a.q = static_cast<const uint16_t *>(d_q);
+  a.out = static_cast<uint16_t *>(d_out);
+  a.chunk_starts = desc->d_chunk_starts;
+  a.context_lens = desc->d_context_lens;
+  a.tables = desc->d_block_tables;
+  a.err = ctx->d_err;
+  a.num_seqs = desc->num_seqs;
+  a.q_heads = desc->num_q_heads;
+  a.max_blocks = desc->max_blocks_per_seq;
+  a.window = desc->window;
+  a.q_tiles = std::max(1, (desc->max_chunk_len + 127) / 128);
+  a.scale_log2e = score_scale * 1.4426950408889634f;
+  ctx->prefill_calls++;
+  hipError_t e = launch_prefill(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "prefill launch");
+  return LLH_OK;
+}
+
+int llh_debug_gather(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, int32_t seq, int32_t lo,
+                     int32_t hi, int32_t tensor, void *d_out, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (seq < 0 || seq >= desc->num_seqs || lo < 0 || hi < lo || (tensor != 0 && tensor != 1) ||
+      desc->max_blocks_per_seq <= 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "gather arguments out of range");
+  if (hi == lo) return LLH_OK;
+  if (!d_out || !desc->d_block_tables) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  GatherArgs a{};
+  a.pool = pool->view;
+  a.table = desc->d_block_tables + (size_t)seq * desc->max_blocks_per_seq;
+  a.max_blocks = desc->max_blocks_per_seq;
+  a.lo = lo;
+  a.hi = hi;
+  a.tensor = tensor;
+  a.ring_tokens = 0;
+  a.out = d_out;
+  a.err = ctx->d_err;
+  hipError_t e = launch_gather(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "gather launch");
+  return LLH_OK;
+}
+
+int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int32_t n, void *stream) {
+  if (!ctx) return LLH_ERR_NULL;
+  if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "negative count");
+  if (n > 0 && (!d_codes || !d_out)) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  hipError_t e = launch_decode_fp8(d_codes, d_out, n, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "fp8 decode launch");
+  return LLH_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// LayerKvCache mirror
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kRingBlockTokens = 16;
+
+// Device blocks shared by a cache and its clones, with reference counts
+// (the Arc<CacheBlockStorage> sharing of crates/llm-kv-cache/src/block.rs:124-160).
+struct BlockStore {
+  llh_ctx *ctx = nullptr;
+  int32_t format = 0;
+  int32_t kv_heads = 0;
+  int32_t head_dim = 0;
+  int64_t capacity = 0;
+  void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr;
+  size_t kblock = 0, sblock = 0;
+  std::vector<int32_t> refs;
+  std::vector<int32_t> free_list;
+  std::mutex mu;
+
+  ~BlockStore() {
+    if (ctx) (void)hipSetDevice(ctx->device);
+    for (void *p : {k, v, ks, vs})
+      if (p) (void)hipFree(p);
+  }
+  PoolView view() const {
+    return PoolView{format, kRingBlockTokens, kv_heads, head_dim, capacity, k, v, ks, vs};
+  }
+  hipError_t allocate(int64_t cap) {
+    kblock = (size_t)kv_heads * kRingBlockTokens * head_dim * elem_bytes(format);
+    sblock = scale_bytes_per_block(format, kv_heads, kRingBlockTokens);
+    void *nk = nullptr, *nv = nullptr, *nks = nullptr, *nvs = nullptr;
+    hipError_t e = hipMalloc(&nk, kblock * cap);
+    if (e == hipSuccess) e = hipMalloc(&nv, kblock * cap);
+    if (e == hipSuccess && sblock) e = hipMalloc(&nks, sblock * cap);
+    if (e == hipSuccess && sblock) e = hipMalloc(&nvs, sblock * cap);
+    if (e == hipSuccess) e = hipMemset(nk, 0, kblock * cap);
+    if (e == hipSuccess) e = hipMemset(nv, 0, kblock * cap);
+    if (e == hipSuccess && sblock) e = hipMemset(nks, 0, sblock * cap);
+    if (e == hipSuccess && sblock) e = hipMemset(nvs, 0, sblock * cap);
+    if (e == hipSuccess && capacity > 0) {
+      e = hipMemcpy(nk, k, kblock * capacity, hipMemcpyDeviceToDevice);
+      if (e == hipSuccess) e = hipMemcpy(nv, v, kblock * capacity, hipMemcpyDeviceToDevice);
+      if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, sblock * capacity, hipMemcpyDeviceToDevice);
+      if (e == hipSuccess && sblock) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
+    }
+    if (e != hipSuccess) {
+      for (void *p : {nk, nv, nks, nvs})
+        if (p) (void)hipFree(p);
+      return e;
+    }
+    for (void *p : {k, v, ks, vs})
+      if (p) (void)hipFree(p);
+    k = nk;
+    v = nv;
+    ks = nks;
+    vs = nvs;
+    for (int64_t i = cap - 1; i >= capacity; i--) free_list.push_back((int32_t)i);
+    refs.resize(cap, 0);
+    capacity = cap;
+    return hipSuccess;
+  }
+  // returns a pool index with refcount 1, growing the store when full
+  hipError_t take(int32_t &out) {
+    if (free_list.empty()) {
+      hipError_t e = allocate(capacity * 2);
+      if (e != hipSuccess) return e;
+    }
+    out = free_list.back();
+    free_list.pop_back();
+    refs[out] = 1;
+    return hipSuccess;
+  }
+  void release(int32_t idx) {
+    if (--refs[idx] == 0) free_list.push_back(idx);
+  }
+  hipError_t copy_block(int32_t src, int32_t dst) {
+    hipError_t e = hipMemcpy((char *)k + kblock * dst, (char *)k + kblock * src, kblock, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy((char *)v + kblock * dst, (char *)v + kblock * src, kblock, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess && sblock)
+      e = hipMemcpy((char *)ks + sblock * dst, (char *)ks + sblock * src, sblock, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess && sblock)
+      e = hipMemcpy((char *)vs + sblock * dst, (char *)vs + sblock * src, sblock, hipMemcpyDeviceToDevice);
+    return e;
+  }
+};
+
+// Scratch for the synchronous trait calls: small device buffers reused per call.
+struct TraitScratch {
+  void *buf = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t n) {
+    if (n <= bytes) return hipSuccess;
+    if (buf) (void)hipFree(buf);
+    buf = nullptr;
+    bytes = 0;
+    const size_t nb = align_up(std::max(n, (size_t)4096));
+    hipError_t e = hipMalloc(&buf, nb);
+    if (e == hipSuccess) bytes = nb;
+    return e;
+  }
+  ~TraitScratch() {
+    if (buf) (void)hipFree(buf);
+  }
+};
+
+}  // namespace
+
+struct llh_layer_cache {
+  llh_ctx *ctx = nullptr;
+  std::shared_ptr<BlockStore> store;
+  uint64_t id = 0;
+  uint64_t revision = 0;
+  size_t max_tokens = 0, kv_heads = 0, head_dim = 0;
+  int32_t format = 0;
+  size_t token_count = 0, tokens_seen = 0, window_start = 0;
+  std::vector<int32_t> table;  // pool index per ring block
+  std::vector<uint64_t> ids;   // BlockId per ring block
+  TraitScratch scratch;
+  std::mutex mu;
+
+  size_t vector_len() const { return kv_heads * head_dim; }
+};
+
+static uint64_t next_block_id() { return g_next_block_id.fetch_add(1); }
+
+extern "C" {
+
+int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, size_t head_dim, int32_t format,
+                           llh_layer_cache **out) {
+  if (!ctx || !out) return LLH_ERR_NULL;
+  *out = nullptr;
+  if (max_tokens == 0 || kv_heads == 0 || head_dim == 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "invalid KV cache shape");
+  if (format != LLH_KV_BF16 && format != LLH_KV_INT8)
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "unsupported KV cache format for the layer cache");
+  if (max_tokens > (size_t)INT32_MAX / 2 || kv_heads * head_dim > (1u << 20))
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV cache shape too large");
+  auto *c = new llh_layer_cache();
+  c->ctx = ctx;
+  c->max_tokens = max_tokens;
+  c->kv_heads = kv_heads;
+  c->head_dim = head_dim;
+  c->format = format;
+  c->id = g_next_cache_id.fetch_add(1);
+  const size_t nb = (max_tokens + kRingBlockTokens - 1) / kRingBlockTokens;
+  c->store = std::make_shared<BlockStore>();
+  c->store->ctx = ctx;
+  c->store->format = format;
+  c->store->kv_heads = (int32_t)kv_heads;
+  c->store->head_dim = (int32_t)head_dim;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = c->store->allocate((int64_t)nb * 2 + 2);
+  for (size_t i = 0; e == hipSuccess && i < nb; i++) {
+    int32_t idx;
+    e = c->store->take(idx);
+    c->table.push_back(idx);
+    c->ids.push_back(next_block_id());
+  }
+  if (e != hipSuccess) {
+    delete c;
+    return ctx->hip_fail(e, "layer cache allocation");
+  }
+  *out = c;
+  return LLH_OK;
+}
+
+int llh_layer_cache_destroy(llh_layer_cache *cache) {
+  if (!cache) return LLH_ERR_NULL;
+  {
+    std::lock_guard<std::mutex> g(cache->store->mu);
+    for (int32_t idx : cache->table) cache->store->release(idx);
+  }
+  (void)hipSetDevice(cache->ctx->device);
+  delete cache;
+  return LLH_OK;
+}
+
+int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out) {
+  if (!cache || !out) return LLH_ERR_NULL;
+  auto *src = const_cast<llh_layer_cache *>(cache);
+  std::lock_guard<std::mutex> g0(src->mu);
+  auto *c = new llh_layer_cache();
+  c->ctx = src->ctx;
+  c->store = src->store;
+  c->id = g_next_cache_id.fetch_add(1);
+  c->revision = src->revision;
+  c->max_tokens = src->max_tokens;
+  c->kv_heads = src->kv_heads;
+  c->head_dim = src->head_dim;
+  c->format = src->format;
+  c->token_count = src->token_count;
+  c->tokens_seen = src->tokens_seen;
+  c->window_start = src->window_start;
+  c->table = src->table;
+  c->ids = src->ids;
+  {
+    std::lock_guard<std::mutex> g(c->store->mu);
+    for (int32_t idx : c->table) c->store->refs[idx]++;
+  }
+  *out = c;
+  return LLH_OK;
+}
+
+int llh_layer_cache_clear(llh_layer_cache *cache) {
+  if (!cache) return LLH_ERR_NULL;
+  std::lock_guard<std::mutex> g(cache->mu);
+  cache->token_count = 0;
+  cache->tokens_seen = 0;
+  cache->window_start = 0;
+  cache->revision += 1;
+  return LLH_OK;
+}
+
+int llh_layer_cache_get_state(const llh_layer_cache *cache, llh_layer_cache_state *out) {
+  if (!cache || !out) return LLH_ERR_NULL;
+  out->id = cache->id;
+  out->revision = cache->revision;
+  out->max_tokens = cache->max_tokens;
+  out->kv_heads = cache->kv_heads;
+  out->head_dim = cache->head_dim;
+  out->token_count = cache->token_count;
+  out->tokens_seen = cache->tokens_seen;
+  out->window_start = cache->window_start;
+  out->block_count = cache->table.size();
+  out->format = cache->format;
+  out->block_tokens = kRingBlockTokens;
+  return LLH_OK;
+}
+
+int llh_layer_cache_block_ids(const llh_layer_cache *cache, uint64_t *h_out, size_t capacity, size_t *count) {
+  if (!cache || !count) return LLH_ERR_NULL;
+  *count = cache->ids.size();
+  if (h_out) std::memcpy(h_out, cache->ids.data(), std::min(capacity, cache->ids.size()) * sizeof(uint64_t));
+  return capacity >= cache->ids.size() || !h_out ? LLH_OK : LLH_ERR_CAPACITY;
+}
+
+// Runs of logical tokens contiguous in one device block, in logical order:
+// the closed form of append_active_block_run / remove_oldest_active_block_token
+// (layer.rs:1097-1162) for 16-token blocks.
+int llh_layer_cache_active_blocks(const llh_layer_cache *cache, llh_block_run *h_out, size_t capacity,
+                                  size_t *count) {
+  if (!cache || !count) return LLH_ERR_NULL;
+  std::vector<llh_block_run> runs;
+  for (size_t i = 0; i < cache->token_count; i++) {
+    const size_t phys = (cache->window_start + i) % cache->max_tokens;
+    const size_t bi = phys / kRingBlockTokens;
+    const size_t off = phys % kRingBlockTokens;
+    if (!runs.empty()) {
+      llh_block_run &r = runs.back();
+      if (r.block_index == bi && r.logical_token_start + r.token_count == i &&
+          r.physical_token_start + r.token_count == phys && r.block_token_start + r.token_count == off) {
+        r.token_count++;
+        continue;
+      }
+    }
+    runs.push_back(llh_block_run{cache->ids[bi], bi, i, phys, off, 1});
+  }
+  *count = runs.size();
+  if (h_out) std::memcpy(h_out, runs.data(), std::min(capacity, runs.size()) * sizeof(llh_block_run));
+  return capacity >= runs.size() || !h_out ? LLH_OK : LLH_ERR_CAPACITY;
+}
+
+static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key, const float *h_value, size_t len,
+                        bool sliding) {
+  if (!ctx || !cache || !h_key || !h_value) return LLH_ERR_NULL;
+  std::lock_guard<std::mutex> g(cache->mu);
+  if (len != cache->vector_len()) return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV row length does not match the cache");
+  if (cache->format == LLH_KV_INT8) {
+    for (size_t i = 0; i < len; i++)
+      if (!std::isfinite(h_key[i]) || !std::isfinite(h_value[i]))
+        return ctx->fail(LLH_ERR_NON_FINITE, "int8 KV cache rows must be finite");
+  }
+  const bool full = cache->token_count == cache->max_tokens;
+  if (full && !sliding) return ctx->fail(LLH_ERR_CAPACITY, "KV cache capacity exceeded");
+  const size_t phys = full ? cache->window_start : cache->token_count;
+  const size_t bi = phys / kRingBlockTokens;
+  const size_t off = phys % kRingBlockTokens;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
+  {
+    // copy-on-write: a block shared with a clone gets a fresh device block and id
+    BlockStore &bs = *cache->store;
+    std::lock_guard<std::mutex> gs(bs.mu);
+    const int32_t idx = cache->table[bi];
+    if (bs.refs[idx] > 1) {
+      int32_t fresh;
+      e = bs.take(fresh);
+      if (e == hipSuccess) e = bs.copy_block(idx, fresh);
+      if (e != hipSuccess) return ctx->hip_fail(e, "copy-on-write block");
+      bs.release(idx);
+      cache->table[bi] = fresh;
+      cache->ids[bi] = next_block_id();
+    }
+  }
+  const size_t row_bytes = len * sizeof(float);
+  e = cache->scratch.ensure(2 * row_bytes + 2 * sizeof(int64_t) + kAlign);
+  if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
+  char *sb = static_cast<char *>(cache->scratch.buf);
+  int64_t *d_slot = reinterpret_cast<int64_t *>(sb);
+  float *d_k = reinterpret_cast<float *>(sb + kAlign);
+  float *d_v = reinterpret_cast<float *>(sb + kAlign + row_bytes);
+  const int64_t slot = (int64_t)cache->table[bi] * kRingBlockTokens + (int64_t)off;
+  e = hipMemcpy(d_slot, &slot, sizeof(slot), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(d_k, h_key, row_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(d_v, h_value, row_bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return ctx->hip_fail(e, "row upload");
+  AppendArgs a{};
+  a.pool = cache->store->view();
+  a.k_dst = cache->store->k;
+  a.v_dst = cache->store->v;
+  a.ks_dst = cache->store->ks;
+  a.vs_dst = cache->store->vs;
+  a.slots = d_slot;
+  a.k = d_k;
+  a.v = d_v;
+  a.n = 1;
+  a.src_f32 = 1;
+  a.err = ctx->d_err;
+  e = launch_append(a, nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return ctx->hip_fail(e, "append");
+  ctx->append_calls++;
+  if (full) {
+    cache->window_start = (cache->window_start + 1) % cache->max_tokens;
+  } else {
+    cache->token_count += 1;
+  }
+  cache->tokens_seen += 1;
+  cache->revision += 1;
+  return LLH_OK;
+}
+
+int llh_append_kv_cache_sliding_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key, const float *h_value,
+                                    size_t len) {
+  return layer_append(ctx, cache, h_key, h_value, len, true);
+}
+
+int llh_append_kv_cache_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key, const float *h_value,
+                            size_t len) {
+  return layer_append(ctx, cache, h_key, h_value, len, false);
+}
+
+int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache_c, const float *h_query,
+                                              size_t query_len, size_t row_count, size_t num_attention_heads,
+                                              size_t num_key_value_heads, size_t head_dim, float score_scale,
+                                              float *h_output, size_t output_len) {
+  if (!ctx || !cache_c || !h_query || !h_output) return LLH_ERR_NULL;
+  auto *cache = const_cast<llh_layer_cache *>(cache_c);
+  std::lock_guard<std::mutex> g(cache->mu);
+  if (num_attention_heads == 0 || num_key_value_heads == 0 || head_dim == 0 ||
+      num_attention_heads % num_key_value_heads != 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "invalid attention head shape");
+  if (num_key_value_heads != cache->kv_heads || head_dim != cache->head_dim)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "attention shape does not match the KV cache");
+  const size_t qdim = num_attention_heads * head_dim;
+  if (query_len != qdim) return ctx->fail(LLH_ERR_INVALID_SHAPE, "query length does not match heads * head_dim");
+  if (output_len < qdim) return ctx->fail(LLH_ERR_INVALID_SHAPE, "attention output buffer too small");
+  if (row_count > cache->token_count)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "row count exceeds cache token count");
+  if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "softmax scores must be finite");
+  if (row_count == 0) {  // weighted sum of nothing (primitives.rs:1125-1128)
+    std::fill(h_output, h_output + qdim, 0.0f);
+    return LLH_OK;
+  }
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
+  const size_t nb = cache->table.size();
+  const size_t off_table = kAlign;                               // int32 [nb]
+  const size_t off_q = off_table + align_up(nb * sizeof(int32_t));
+  const size_t off_out = off_q + align_up(qdim * sizeof(float));
+  const size_t off_scores = off_out + align_up(qdim * sizeof(float));
+  const size_t need = off_scores + num_attention_heads * row_count * sizeof(float);
+  e = cache->scratch.ensure(need);
+  if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
+  char *sb = static_cast<char *>(cache->scratch.buf);
+  // header: err flag, start, end
+  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
+  const int32_t hdr[4] = {0, (int32_t)abs_start, (int32_t)(abs_start + (int64_t)row_count), 0};
+  e = hipMemcpy(sb, hdr, sizeof(hdr), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(sb + off_table, cache->table.data(), nb * sizeof(int32_t), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(sb + off_q, h_query, qdim * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return ctx->hip_fail(e, "attention upload");
+  GenericDecodeArgs a{};
+  a.pool = cache->store->view();
+  a.q = sb + off_q;
+  a.out = sb + off_out;
+  a.err = reinterpret_cast<int32_t *>(sb);
+  a.starts = reinterpret_cast<const int32_t *>(sb) + 1;
+  a.seq_lens = reinterpret_cast<const int32_t *>(sb) + 2;
+  a.tables = reinterpret_cast<const int32_t *>(sb + off_table);
+  a.scores = reinterpret_cast<float *>(sb + off_scores);
+  a.num_seqs = 1;
+  a.q_heads = (int32_t)num_attention_heads;
+  a.max_blocks = (int32_t)nb;
+  a.window = 0;
+  a.ring_tokens = (int32_t)cache->max_tokens;
+  a.score_stride = (int32_t)row_count;
+  a.scale = score_scale;
+  e = launch_decode_generic(a, 1, 1, nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  int32_t flags = 0;
+  if (e == hipSuccess) e = hipMemcpy(&flags, sb, sizeof(flags), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(h_output, sb + off_out, qdim * sizeof(float), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return ctx->hip_fail(e, "attention");
+  ctx->decode_calls++;
+  if (flags & kErrNonFinite) return ctx->fail(LLH_ERR_NON_FINITE, "softmax scores must be finite");
+  if (flags & kErrBadBlock) return ctx->fail(LLH_ERR_STALE, "KV cache block table is stale");
+  return LLH_OK;
+}
+
+int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache_c, int32_t tensor,
+                                               size_t row_count, size_t head_start, size_t head_len,
+                                               float *h_output, size_t output_len) {
+  if (!ctx || !cache_c || !h_output) return LLH_ERR_NULL;
+  auto *cache = const_cast<llh_layer_cache *>(cache_c);
+  std::lock_guard<std::mutex> g(cache->mu);
+  const size_t vl = cache->vector_len();
+  if (tensor != 0 && tensor != 1) return ctx->fail(LLH_ERR_INVALID_SHAPE, "tensor must be 0 (key) or 1 (value)");
+  if (row_count > cache->token_count)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "head row selection row count exceeds the cache");
+  if (head_start + head_len > vl) return ctx->fail(LLH_ERR_INVALID_SHAPE, "head row selection range exceeds row length");
+  if (output_len < row_count * head_len) return ctx->fail(LLH_ERR_INVALID_SHAPE, "head row selection output buffer too small");
+  if (row_count == 0 || head_len == 0) return LLH_OK;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
+  const size_t nb = cache->table.size();
+  const size_t off_table = kAlign;
+  const size_t off_out = off_table + align_up(nb * sizeof(int32_t));
+  e = cache->scratch.ensure(off_out + row_count * vl * sizeof(float));
+  if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
+  char *sb = static_cast<char *>(cache->scratch.buf);
+  const int32_t zero = 0;
+  e = hipMemcpy(sb, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(sb + off_table, cache->table.data(), nb * sizeof(int32_t), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return ctx->hip_fail(e, "upload");
+  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
+  GatherArgs a{};
+  a.pool = cache->store->view();
+  a.table = reinterpret_cast<const int32_t *>(sb + off_table);
+  a.max_blocks = (int32_t)nb;
+  a.lo = (int32_t)abs_start;
+  a.hi = (int32_t)(abs_start + (int64_t)row_count);
+  a.tensor = tensor;
+  a.ring_tokens = (int32_t)cache->max_tokens;
+  a.out = sb + off_out;
+  a.out_f32 = 1;
+  a.err = reinterpret_cast<int32_t *>(sb);
+  e = launch_gather(a, nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  std::vector<float> rows(row_count * vl);
+  if (e == hipSuccess) e = hipMemcpy(rows.data(), sb + off_out, rows.size() * sizeof(float), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return ctx->hip_fail(e, "select head rows");
+  for (size_t r = 0; r < row_count; r++)
+    std::memcpy(h_output + r * head_len, rows.data() + r * vl + head_start, head_len * sizeof(float));
+  return LLH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,289 @@
+// KV writes into the paged pool (quantise on write) and the bit-exact gather.
+//
+// write_blocks: whole blocks from token-major bf16 rows.  Replaces the
+//   per-append re-quantisation of a whole block in LayerInt8KvStore::update_block
+//   (crates/llm-kv-cache/src/format.rs:262-276) and the f32->f16 block upload
+//   of the Metal mirror (crates/llm-native-runtime/src/native_matvec.rs:384-465).
+// append: single token rows at absolute slots (the device half of
+//   append_kv_cache_sliding_f32, crates/llm-backend/src/core/native_matvec.rs:643-653).
+// gather: raw elements of a sequence's positions through its block table
+//   (select_head_rows_*, crates/llm-metal/src/device/shaders/generic.metal:310-360).
+//
+// Quantisation arithmetic matches the oracle bit for bit: int8 scale =
+// f16(absmax / 127) and codes = clamp(round_half_away(x / scale), -127, 127)
+// with the rounded scale (the symmetric rule of format.rs:702-737 at per
+// (token, head) granularity); fp8 scale = absmax / 448 per (block, head) and
+// codes are OCP e4m3fn, round to nearest even, saturating.
+#include "llh_internal.h"
+
+namespace llh {
+
+namespace {
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ int8_t quant_int8(float x, float s) {
+  if (s == 0.0f) return 0;
+  float c = roundf(__fdiv_rn(x, s));
+  c = fminf(fmaxf(c, -127.0f), 127.0f);
+  return (int8_t)c;
+}
+
+// OCP e4m3fn encode, round to nearest even, saturate to +-448, NaN -> 0x7f.
+__device__ __forceinline__ uint8_t encode_e4m3(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t au = u & 0x7fffffffu;
+  if (au > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+  if (__uint_as_float(au) >= 448.0f) return (uint8_t)(sign | 0x7eu);
+  const uint32_t exp = au >> 23;
+  uint32_t man = au & 0x7fffffu;
+  const int e = (int)exp - 127 + 7;
+  if (e <= 0) {
+    if (exp == 0) return (uint8_t)sign;
+    man |= 0x800000u;
+    const int shift = 21 - e;
+    if (shift > 24) return (uint8_t)sign;
+    uint32_t q = man >> shift;
+    const uint32_t rem = man & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint8_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)e << 3) | (man >> 20);
+  const uint32_t rem = man & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q++;
+  if (q > 0x7eu) q = 0x7eu;
+  return (uint8_t)(sign | q);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// One workgroup per (block i, kv head).  Source rows src[i][t][h][d].
+__global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs a) {
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  const int blk = a.blocks[i];
+  if (blk < 0 || (int64_t)blk >= a.pool.n_blocks) {
+    if (threadIdx.x == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  auto src_idx = [&](int t, int d) { return (((size_t)i * BT + t) * Hkv + h) * Dh + d; };
+  const int n = BT * Dh;
+  if (a.pool.format == kBf16) {
+    uint16_t *kd = reinterpret_cast<uint16_t *>(a.k_dst);
+    uint16_t *vd = reinterpret_cast<uint16_t *>(a.v_dst);
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const int t = e / Dh, d = e % Dh;
+      kd[(bh * BT + t) * Dh + d] = a.k[src_idx(t, d)];
+      vd[(bh * Dh + d) * BT + t] = a.v[src_idx(t, d)];
+    }
+    return;
+  }
+  if (a.pool.format == kInt8) {
+    // one wavefront per token row of this head
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int8_t *kd = reinterpret_cast<int8_t *>(a.k_dst);
+    int8_t *vd = reinterpret_cast<int8_t *>(a.v_dst);
+    uint16_t *ksd = reinterpret_cast<uint16_t *>(a.ks_dst);
+    uint16_t *vsd = reinterpret_cast<uint16_t *>(a.vs_dst);
+    for (int t = wave; t < BT; t += blockDim.x / 64) {
+      for (int tensor = 0; tensor < 2; tensor++) {
+        const uint16_t *src = tensor ? a.v : a.k;
+        float mx = 0.0f;
+        for (int d = lane; d < Dh; d += 64) mx = fmaxf(mx, fabsf(bf16_to_f32(src[src_idx(t, d)])));
+        mx = wave_max(mx);
+        const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
+        const float s = (float)s16;
+        for (int d = lane; d < Dh; d += 64) {
+          const int8_t code = quant_int8(bf16_to_f32(src[src_idx(t, d)]), s);
+          if (tensor)
+            vd[(bh * Dh + d) * BT + t] = code;
+          else
+            kd[(bh * BT + t) * Dh + d] = code;
+        }
+        if (lane == 0) (tensor ? vsd : ksd)[bh * BT + t] = __builtin_bit_cast(uint16_t, s16);
+      }
+    }
+    return;
+  }
+  // fp8: per (block, head) scale over all tokens of the block
+  __shared__ float red[256];
+  uint8_t *kd = reinterpret_cast<uint8_t *>(a.k_dst);
+  uint8_t *vd = reinterpret_cast<uint8_t *>(a.v_dst);
+  for (int tensor = 0; tensor < 2; tensor++) {
+    const uint16_t *src = tensor ? a.v : a.k;
+    float mx = 0.0f;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) mx = fmaxf(mx, fabsf(bf16_to_f32(src[src_idx(e / Dh, e % Dh)])));
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+      if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+      __syncthreads();
+    }
+    const float s = red[0] == 0.0f ? 0.0f : __fdiv_rn(red[0], 448.0f);
+    __syncthreads();
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const int t = e / Dh, d = e % Dh;
+      const uint8_t code = s == 0.0f ? 0 : encode_e4m3(__fdiv_rn(bf16_to_f32(src[src_idx(t, d)]), s));
+      if (tensor)
+        vd[(bh * Dh + d) * BT + t] = code;
+      else
+        kd[(bh * BT + t) * Dh + d] = code;
+    }
+    if (threadIdx.x == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[bh] = s;
+  }
+}
+
+// One wavefront per (token row i, kv head).
+template <typename ST>
+__global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  const int64_t slot = a.slots[i];
+  const int64_t blk = slot / BT;
+  const int off = (int)(slot % BT);
+  if (slot < 0 || blk >= a.pool.n_blocks) {
+    if (lane == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const ST *ks = reinterpret_cast<const ST *>(a.k) + ((size_t)i * Hkv + h) * Dh;
+  const ST *vs = reinterpret_cast<const ST *>(a.v) + ((size_t)i * Hkv + h) * Dh;
+  auto ld = [](const ST *p, int d) -> float {
+    if constexpr (sizeof(ST) == 4)
+      return p[d];
+    else
+      return bf16_to_f32(p[d]);
+  };
+  if (a.pool.format == kBf16) {
+    uint16_t *kd = reinterpret_cast<uint16_t *>(a.k_dst);
+    uint16_t *vd = reinterpret_cast<uint16_t *>(a.v_dst);
+    for (int d = lane; d < Dh; d += 64) {
+      kd[(bh * BT + off) * Dh + d] = f32_to_bf16_rne(ld(ks, d));
+      vd[(bh * Dh + d) * BT + off] = f32_to_bf16_rne(ld(vs, d));
+    }
+    return;
+  }
+  // int8 with per (token, head) fp16 scale
+  int8_t *kd = reinterpret_cast<int8_t *>(a.k_dst);
+  int8_t *vd = reinterpret_cast<int8_t *>(a.v_dst);
+  for (int tensor = 0; tensor < 2; tensor++) {
+    const ST *src = tensor ? vs : ks;
+    float mx = 0.0f;
+    bool finite = true;
+    for (int d = lane; d < Dh; d += 64) {
+      const float x = ld(src, d);
+      finite = finite && isfinite(x);
+      mx = fmaxf(mx, fabsf(x));
+    }
+    mx = wave_max(mx);
+    if (__any(!finite)) {
+      if (lane == 0) atomicOr(a.err, kErrNonFinite);
+      return;
+    }
+    const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
+    const float s = (float)s16;
+    for (int d = lane; d < Dh; d += 64) {
+      const int8_t code = quant_int8(ld(src, d), s);
+      if (tensor)
+        vd[(bh * Dh + d) * BT + off] = code;
+      else
+        kd[(bh * BT + off) * Dh + d] = code;
+    }
+    if (lane == 0)
+      reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[bh * BT + off] = __builtin_bit_cast(uint16_t, s16);
+  }
+}
+
+// One wavefront per (position, kv head): raw elements out[pos-lo][h][d].
+__global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
+  const int r = blockIdx.x;
+  const int h = blockIdx.y;
+  const int pos = a.lo + r;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  int slot_blk, off;
+  if (a.ring_tokens > 0) {
+    const int slot = pos % a.ring_tokens;
+    slot_blk = slot / BT;
+    off = slot % BT;
+  } else {
+    slot_blk = (pos / BT) % a.max_blocks;
+    off = pos % BT;
+  }
+  const int blk = slot_blk < a.max_blocks ? a.table[slot_blk] : -1;
+  if (blk < 0 || (int64_t)blk >= a.pool.n_blocks) {
+    if (threadIdx.x == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const size_t orow = ((size_t)r * Hkv + h) * Dh;
+  const void *base = a.tensor ? a.pool.v : a.pool.k;
+  const void *sc = a.tensor ? a.pool.v_scales : a.pool.k_scales;
+  for (int d = threadIdx.x; d < Dh; d += 64) {
+    const size_t idx = a.tensor ? (bh * Dh + d) * BT + off : (bh * BT + off) * Dh + d;
+    if (a.out_f32) {
+      float x;
+      if (a.pool.format == kBf16) {
+        x = bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
+      } else if (a.pool.format == kInt8) {
+        const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * BT + off]);
+        x = (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
+      } else {
+        x = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)reinterpret_cast<const uint8_t *>(base)[idx], false)[0] *
+            reinterpret_cast<const float *>(sc)[bh];
+      }
+      reinterpret_cast<float *>(a.out)[orow + d] = x;
+    } else if (a.pool.format == kBf16)
+      reinterpret_cast<uint16_t *>(a.out)[orow + d] = reinterpret_cast<const uint16_t *>(base)[idx];
+    else
+      reinterpret_cast<uint8_t *>(a.out)[orow + d] = reinterpret_cast<const uint8_t *>(base)[idx];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(write_blocks_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_append(const AppendArgs &a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  if (a.src_f32)
+    hipLaunchKernelGGL(append_kernel<float>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(append_kernel<uint16_t>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
+  if (a.hi <= a.lo) return hipSuccess;
+  hipLaunchKernelGGL(gather_kernel, dim3(a.hi - a.lo, a.pool.kv_heads), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace llh

@@ -1,0 +1,140 @@
+// Internal declarations shared by the HIP kernels and the host API of libllm_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace llh {
+
+constexpr int kFastHeadDim = 128;   // head_dim of the tuned kernels
+constexpr int kFastBlockTokens = 16;  // block_tokens of the tuned kernels
+constexpr int kDecodeThreads = 256;   // 4 wavefronts
+constexpr int kPrefillThreads = 256;  // 4 wavefronts, 32 query rows each
+
+enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2 };
+
+// Device error flags (bit set by kernels, read back by the host).
+enum ErrFlag : int32_t {
+  kErrBadBlock = 1,      // block table entry outside the pool
+  kErrTooManySplits = 2, // a sequence needed more split-K partials than the grid was sized for
+  kErrNonFinite = 4,     // non-finite score (softmax_f32 contract)
+};
+
+struct PoolView {
+  int32_t format;
+  int32_t block_tokens;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int64_t n_blocks;
+  const void *k;
+  const void *v;
+  const void *k_scales;
+  const void *v_scales;
+};
+
+// Split-K decode over the tuned shape (head_dim 128, 16-token blocks).
+struct DecodeArgs {
+  PoolView pool;
+  const uint16_t *q;        // [B][Hq][128] bf16
+  uint16_t *out;            // [B][Hq][128] bf16
+  const int32_t *seq_lens;  // [B]
+  const int32_t *tables;    // [B][max_blocks]
+  float *ws_o;              // [B][Hq][max_splits][128]
+  float2 *ws_ml;            // [B][Hq][max_splits]  (running max in log2 units, sum)
+  int32_t *counters;        // [B][Hkv] split arrival counters, zero between calls
+  int32_t *err;             // error flags
+  int32_t num_seqs;
+  int32_t q_heads;
+  int32_t max_blocks;
+  int32_t window;
+  int32_t split_blocks;     // blocks per split
+  int32_t max_splits;
+  float scale_log2e;        // score_scale * log2(e)
+};
+
+// Reference-order decode for any head_dim / block size / group size.
+struct GenericDecodeArgs {
+  PoolView pool;
+  const void *q;            // [B][Hq][D], f32 or bf16
+  void *out;                // [B][Hq][D], f32 or bf16
+  const int32_t *seq_lens;  // [B] end positions (exclusive)
+  const int32_t *starts;    // [B] first attended position, or null (then window rule)
+  const int32_t *tables;
+  float *scores;            // [B][Hq][score_stride] scratch
+  int32_t *err;
+  int32_t num_seqs;
+  int32_t q_heads;
+  int32_t max_blocks;
+  int32_t window;
+  int32_t ring_tokens;      // >0: position p lives in slot p % ring_tokens (ring cache mirror)
+  int32_t score_stride;
+  float scale;
+};
+
+struct PrefillArgs {
+  PoolView pool;
+  const uint16_t *q;        // [T][Hq][128]
+  uint16_t *out;            // [T][Hq][128]
+  const int32_t *chunk_starts;
+  const int32_t *context_lens;
+  const int32_t *tables;
+  int32_t *err;
+  int32_t num_seqs;
+  int32_t q_heads;
+  int32_t max_blocks;
+  int32_t window;
+  int32_t q_tiles;          // tiles of 128 rows per sequence in the grid
+  float scale_log2e;
+};
+
+struct WriteBlocksArgs {
+  PoolView pool;
+  void *k_dst;
+  void *v_dst;
+  void *ks_dst;
+  void *vs_dst;
+  const int32_t *blocks;    // [n]
+  const uint16_t *k;        // [n][BT][Hkv][D] bf16
+  const uint16_t *v;
+  int32_t n;
+  int32_t *err;
+};
+
+struct AppendArgs {
+  PoolView pool;
+  void *k_dst;
+  void *v_dst;
+  void *ks_dst;
+  void *vs_dst;
+  const int64_t *slots;     // [n] block * BT + offset
+  const void *k;            // [n][Hkv][D], bf16 or f32
+  const void *v;
+  int32_t n;
+  int32_t src_f32;
+  int32_t *err;
+};
+
+struct GatherArgs {
+  PoolView pool;
+  const int32_t *table;     // one sequence's row
+  int32_t max_blocks;
+  int32_t lo;
+  int32_t hi;
+  int32_t tensor;
+  int32_t ring_tokens;
+  int32_t out_f32;          // 1: dequantised f32 elements, 0: raw storage elements
+  void *out;
+  int32_t *err;
+};
+
+// launchers (return hipError_t of the launch)
+hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s);
+hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_f32, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
+hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
+hipError_t launch_append(const AppendArgs &a, hipStream_t s);
+hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
+hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);
+
+}  // namespace llh

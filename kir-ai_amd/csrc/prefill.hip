@@ -1,0 +1,274 @@
+// Chunked causal prefill over cached prefix blocks, on gfx950 MFMA.
+//
+// For each sequence, query row i of the chunk sits at position
+// pos = context_len - chunk_len + i and attends positions [lo(pos), pos]
+// (causal inside the chunk, full attention to the cached prefix, optional
+// sliding window).  This is the result of the reference's per-token
+// "append then attend" loop (crates/llm-backend/src/core/native_attention.rs:356-464)
+// computed as one dense pass.
+//
+// One workgroup = 128 query rows of one query head (4 wavefronts x 32 rows).
+// Key tiles of 64 positions (4 pool blocks) are staged in LDS; tiles wholly
+// outside the window or past the last query are never loaded, and only tiles
+// that straddle a boundary are masked.
+//
+// Per wavefront, with v_mfma_f32_32x32x16_bf16:
+//   S^T[key][query] = K Q^T       A = K rows (token-major pool layout)
+//                                 B = Q^T    (held in registers)
+//   O^T[dim][query] += V^T P^T    A = V^T    (the pool stores V dim-major)
+//                                 B = P^T    (exp'd S^T accumulators, packed to bf16)
+// The accumulator layout of S^T (lane = query column, 16 key rows per lane)
+// is exactly the B-operand layout P^T needs when the key order inside each
+// 16-key step is {4h..4h+3, 8+4h..8+4h+3} for lane half h; the V^T operand is
+// read from LDS with the same key order, so no transpose is ever done.
+// Softmax statistics are kept per query column in log2 units (online softmax).
+#include "llh_internal.h"
+
+namespace llh {
+
+namespace {
+
+constexpr int D = kFastHeadDim;
+constexpr int BT = kFastBlockTokens;
+constexpr int BM = 128;          // query rows per workgroup
+constexpr int BN = 64;           // key positions per tile
+constexpr int KBLK = BN / BT;    // pool blocks per tile
+constexpr int K_STRIDE = D + 8;  // bf16 elements per K row in LDS (272 B: conflict-free b128 reads)
+constexpr int V_STRIDE = BT + 4; // bf16 elements per V^T row in LDS (40 B: conflict-free b64 reads)
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+}
+
+__device__ __forceinline__ f32x16_t mfma32(const uint4 &a, const uint4 &b, const f32x16_t &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const PrefillArgs a) {
+  const int tile = blockIdx.x;
+  const int qh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int c0 = a.chunk_starts[b];
+  const int chunk = a.chunk_starts[b + 1] - c0;
+  const int ctx = a.context_lens[b];
+  const int i0 = tile * BM;
+  if (i0 >= chunk || chunk <= 0 || ctx < chunk) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;     // lane half
+  const int col = lane & 31;   // query column of this lane
+  const int Hq = a.q_heads;
+  const int Hkv = a.pool.kv_heads;
+  const int kvh = qh / (Hq / Hkv);
+  const int prefix = ctx - chunk;
+
+  // rows of this workgroup and of this wavefront
+  const int rows_wg = min(BM, chunk - i0);
+  const int qpos_first = prefix + i0;                 // position of the first row
+  const int qpos_last = prefix + i0 + rows_wg - 1;    // position of the last valid row
+  const int my_row = i0 + wave * 32 + col;            // chunk row of this lane's query
+  const bool row_ok = my_row < chunk;
+  const int my_pos = prefix + my_row;
+  const int my_lo = a.window > 0 ? max(0, my_pos - a.window + 1) : 0;
+
+  // ---- Q^T operand: 8 k-steps of 16 dims; lane holds dims 16ks + 8h .. +8 of its row ----
+  uint4 qb[8];
+  {
+    const uint16_t *qrow = a.q + ((size_t)(c0 + (row_ok ? my_row : 0)) * Hq + qh) * D;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      uint4 t = *reinterpret_cast<const uint4 *>(qrow + ks * 16 + h * 8);
+      if (!row_ok) t = make_uint4(0, 0, 0, 0);
+      qb[ks] = t;
+    }
+  }
+
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * K_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[KBLK * D * V_STRIDE];
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int j = 0; j < 16; j++) oacc[mt][j] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  // key range of the workgroup
+  const int klo = a.window > 0 ? max(0, qpos_first - a.window + 1) : 0;
+  const int khi = qpos_last + 1;  // exclusive
+  const int t_begin = (klo / BN) * BN;
+  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
+  // wavefront-level bounds for masking decisions
+  const int wrow0 = i0 + wave * 32;
+  const int wpos_first = prefix + wrow0;
+  const int wpos_last = prefix + min(wrow0 + 31, chunk - 1);
+  const int wlo_first = a.window > 0 ? max(0, wpos_first - a.window + 1) : 0;
+  const int wlo_last = a.window > 0 ? max(0, wpos_last - a.window + 1) : 0;
+  const bool wave_live = wrow0 < chunk;
+
+  for (int kt = t_begin; kt < khi; kt += BN) {
+    __syncthreads();  // previous tile fully consumed
+    // ---- stage K (token rows) and V^T (dim rows) of the 4 blocks into LDS ----
+#pragma unroll
+    for (int kb = 0; kb < KBLK; kb++) {
+      const int bpos = kt + kb * BT;
+      const bool inrange = bpos < ctx && bpos + BT > klo;
+      int phys = -1;
+      if (inrange) {
+        phys = table[(bpos / BT) % a.max_blocks];
+        if (phys < 0 || (int64_t)phys >= a.pool.n_blocks) {
+          if (tid == 0) atomicOr(a.err, kErrBadBlock);
+          phys = -1;
+        }
+      }
+      // K: 256 threads x 16 B = one 4 KiB block
+      {
+        const int r = tid >> 4;  // token in block
+        const int c16 = tid & 15;
+        uint4 t = make_uint4(0, 0, 0, 0);
+        if (phys >= 0 && bpos + r < ctx) {
+          const uint16_t *src = reinterpret_cast<const uint16_t *>(a.pool.k) +
+                                (((size_t)phys * Hkv + kvh) * BT + r) * D + c16 * 8;
+          t = *reinterpret_cast<const uint4 *>(src);
+        }
+        *reinterpret_cast<uint4 *>(&k_lds[(kb * BT + r) * K_STRIDE + c16 * 8]) = t;
+      }
+      // V^T: 256 threads x 16 B; thread -> dim tid/2, tokens 8*(tid&1) .. +8
+      {
+        const int d = tid >> 1;
+        const int half = tid & 1;
+        uint4 t = make_uint4(0, 0, 0, 0);
+        if (phys >= 0) {
+          const uint16_t *src = reinterpret_cast<const uint16_t *>(a.pool.v) +
+                                (((size_t)phys * Hkv + kvh) * D + d) * BT + half * 8;
+          t = *reinterpret_cast<const uint4 *>(src);
+          const int valid = ctx - (bpos + half * 8);  // tokens of this 8-run inside the context
+          if (valid < 8) {
+            uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+              if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+            t = make_uint4(w[0], w[1], w[2], w[3]);
+          }
+        }
+        uint16_t *dst = &v_lds[(kb * D + d) * V_STRIDE + half * 8];
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(t.x, t.y);
+        *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(t.z, t.w);
+      }
+    }
+    __syncthreads();
+    if (!wave_live) continue;
+    // tile entirely outside this wavefront's needs?
+    if (kt > wpos_last || kt + BN <= wlo_first) continue;
+
+    // ---- S^T = K Q^T for two 32-key sub-tiles ----
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) sacc[st][j] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ks++) {
+        const uint4 ka = *reinterpret_cast<const uint4 *>(&k_lds[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
+        sacc[st] = mfma32(ka, qb[ks], sacc[st]);
+      }
+    }
+
+    // ---- scale, mask, online softmax ----
+    const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        float s = sacc[st][j] * a.scale_log2e;
+        if (need_mask) {
+          const int kp = kt + st * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+          if (kp > my_pos || kp < my_lo || kp >= ctx || !row_ok) s = -INFINITY;
+        }
+        sacc[st][j] = s;
+        tmax = fmaxf(tmax, s);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float mref = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = fast_exp2(m_run - mref);
+    m_run = m_new;
+    float psum = 0.0f;
+    uint4 pb[4];  // P^T operands for the 4 16-key steps (one pool block each)
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      float p[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        p[j] = fast_exp2(sacc[st][j] - mref);
+        psum += p[j];
+      }
+      pb[2 * st + 0] = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
+                                  pack_bf16(p[6], p[7]));
+      pb[2 * st + 1] = make_uint4(pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]),
+                                  pack_bf16(p[14], p[15]));
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kb = 0; kb < KBLK; kb++) {
+#pragma unroll
+      for (int mt = 0; mt < 4; mt++) {
+        const uint16_t *vrow = &v_lds[(kb * D + mt * 32 + col) * V_STRIDE];
+        const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
+        const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
+        const uint4 va = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+        oacc[mt] = mfma32(va, pb[kb], oacc[mt]);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (!row_ok) return;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  uint16_t *orow = a.out + ((size_t)(c0 + my_row) * Hq + qh) * D;
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++) {
+#pragma unroll
+    for (int jq = 0; jq < 4; jq++) {
+      const int d0 = mt * 32 + jq * 8 + 4 * h;
+      const uint2 w = make_uint2(pack_bf16(oacc[mt][4 * jq + 0] * inv, oacc[mt][4 * jq + 1] * inv),
+                                 pack_bf16(oacc[mt][4 * jq + 2] * inv, oacc[mt][4 * jq + 3] * inv));
+      *reinterpret_cast<uint2 *>(orow + d0) = w;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
+  dim3 grid(a.q_tiles, a.q_heads, a.num_seqs);
+  hipLaunchKernelGGL(paged_prefill_kernel, grid, dim3(kPrefillThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace llh

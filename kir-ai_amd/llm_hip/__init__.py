@@ -1,0 +1,519 @@
+"""Python binding of libllm_hip (the C ABI in include/llm_hip.h).
+
+Two layers, both thin:
+
+* ``Context`` / ``KvPool``: the batched paged-attention hot path.  Device
+  buffers are torch tensors (torch is used for device memory and streams only);
+  calls are asynchronous on the current torch stream.
+* ``LayerKvCache`` / ``HipNativeMatvecBackend``: a mirror of kir-ai's
+  ``LayerKvCache`` (crates/llm-kv-cache/src/layer.rs) and of the attention
+  hooks of ``NativeMatvecBackend`` (crates/llm-backend/src/core/native_matvec.rs:619-668),
+  with the same method names, argument meaning and error behaviour, so tests
+  read like the reference's own.
+
+The shared library must exist: there is no fallback path.  Build it with
+``python kir-ai_amd/build.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libllm_hip.so")
+
+OK = 0
+NOT_HANDLED = 1
+ERR_INVALID_SHAPE = -1
+ERR_CAPACITY = -2
+ERR_NON_FINITE = -3
+ERR_UNSUPPORTED = -4
+ERR_DEVICE = -5
+ERR_STALE = -6
+ERR_NULL = -7
+
+KV_BF16 = 0
+KV_INT8 = 1
+KV_FP8_E4M3 = 2
+
+ERR_FLAG_BAD_BLOCK = 1
+ERR_FLAG_TOO_MANY_SPLITS = 2
+ERR_FLAG_NON_FINITE = 4
+
+_STATUS_NAMES = {
+    NOT_HANDLED: "not handled",
+    ERR_INVALID_SHAPE: "invalid shape",
+    ERR_CAPACITY: "capacity exceeded",
+    ERR_NON_FINITE: "non-finite value",
+    ERR_UNSUPPORTED: "unsupported format",
+    ERR_DEVICE: "device error",
+    ERR_STALE: "stale block table",
+    ERR_NULL: "null pointer",
+}
+
+
+class LlhError(RuntimeError):
+    """A non-OK status from the C ABI (MathError / KvCacheError in the reference)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+        self.message = message
+
+
+class DecodeDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("d_seq_lens", ctypes.c_void_p),
+        ("d_block_tables", ctypes.c_void_p),
+    ]
+
+
+class PrefillDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("total_q_rows", ctypes.c_int32),
+        ("max_chunk_len", ctypes.c_int32),
+        ("d_chunk_starts", ctypes.c_void_p),
+        ("d_context_lens", ctypes.c_void_p),
+        ("d_block_tables", ctypes.c_void_p),
+    ]
+
+
+class PoolInfo(ctypes.Structure):
+    _fields_ = [
+        ("format", ctypes.c_int32),
+        ("block_tokens", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("n_blocks", ctypes.c_int64),
+        ("d_k", ctypes.c_void_p),
+        ("d_v", ctypes.c_void_p),
+        ("d_k_scales", ctypes.c_void_p),
+        ("d_v_scales", ctypes.c_void_p),
+        ("k_bytes", ctypes.c_size_t),
+        ("scale_bytes", ctypes.c_size_t),
+    ]
+
+
+class Metrics(ctypes.Structure):
+    _fields_ = [
+        ("decode_calls", ctypes.c_uint64),
+        ("prefill_calls", ctypes.c_uint64),
+        ("append_calls", ctypes.c_uint64),
+        ("not_handled", ctypes.c_uint64),
+        ("device_errors", ctypes.c_uint64),
+        ("shape_errors", ctypes.c_uint64),
+    ]
+
+
+class LayerCacheState(ctypes.Structure):
+    _fields_ = [
+        ("id", ctypes.c_uint64),
+        ("revision", ctypes.c_uint64),
+        ("max_tokens", ctypes.c_uint64),
+        ("kv_heads", ctypes.c_uint64),
+        ("head_dim", ctypes.c_uint64),
+        ("token_count", ctypes.c_uint64),
+        ("tokens_seen", ctypes.c_uint64),
+        ("window_start", ctypes.c_uint64),
+        ("block_count", ctypes.c_uint64),
+        ("format", ctypes.c_int32),
+        ("block_tokens", ctypes.c_int32),
+    ]
+
+
+class BlockRun(ctypes.Structure):
+    _fields_ = [
+        ("block_id", ctypes.c_uint64),
+        ("block_index", ctypes.c_uint64),
+        ("logical_token_start", ctypes.c_uint64),
+        ("physical_token_start", ctypes.c_uint64),
+        ("block_token_start", ctypes.c_uint64),
+        ("token_count", ctypes.c_uint64),
+    ]
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_SZ = ctypes.c_size_t
+_FP = ctypes.POINTER(ctypes.c_float)
+
+# name -> (restype, argtypes); this is the full exported surface of include/llm_hip.h
+SIGNATURES = {
+    "llh_ctx_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_P)]),
+    "llh_ctx_destroy": (ctypes.c_int, [_P]),
+    "llh_ctx_last_error": (ctypes.c_char_p, [_P]),
+    "llh_ctx_reserve_workspace": (ctypes.c_int, [_P, _SZ]),
+    "llh_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
+    "llh_ctx_metrics": (ctypes.c_int, [_P, ctypes.POINTER(Metrics)]),
+    "llh_ctx_device_errors": (ctypes.c_int, [_P, ctypes.POINTER(_I32), _I32]),
+    "llh_kv_pool_create": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, ctypes.c_int64, ctypes.POINTER(_P)]),
+    "llh_kv_pool_destroy": (ctypes.c_int, [_P]),
+    "llh_kv_pool_get_info": (ctypes.c_int, [_P, ctypes.POINTER(PoolInfo)]),
+    "llh_kv_write_blocks": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
+    "llh_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
+    "llh_paged_decode": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
+    "llh_paged_prefill": (ctypes.c_int, [_P, _P, ctypes.POINTER(PrefillDesc), _P, _P, ctypes.c_float, _P]),
+    "llh_debug_gather": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _I32, _I32, _I32, _I32, _P, _P]),
+    "llh_debug_decode_fp8": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
+    "llh_layer_cache_create": (ctypes.c_int, [_P, _SZ, _SZ, _SZ, _I32, ctypes.POINTER(_P)]),
+    "llh_layer_cache_destroy": (ctypes.c_int, [_P]),
+    "llh_layer_cache_clone": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "llh_layer_cache_clear": (ctypes.c_int, [_P]),
+    "llh_layer_cache_get_state": (ctypes.c_int, [_P, ctypes.POINTER(LayerCacheState)]),
+    "llh_layer_cache_active_blocks": (ctypes.c_int, [_P, ctypes.POINTER(BlockRun), _SZ, ctypes.POINTER(_SZ)]),
+    "llh_layer_cache_block_ids": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64), _SZ, ctypes.POINTER(_SZ)]),
+    "llh_append_kv_cache_sliding_f32": (ctypes.c_int, [_P, _P, _FP, _FP, _SZ]),
+    "llh_append_kv_cache_f32": (ctypes.c_int, [_P, _P, _FP, _FP, _SZ]),
+    "llh_full_attention_cache_mix_f32_in_place": (
+        ctypes.c_int,
+        [_P, _P, _FP, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _FP, _SZ],
+    ),
+    "llh_select_kv_cache_head_rows_f32_in_place": (ctypes.c_int, [_P, _P, _I32, _SZ, _SZ, _SZ, _FP, _SZ]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Loads libllm_hip.so; raises if it was not built (no silent fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python kir-ai_amd/build.py`")
+    # torch ships its own libamdhip64.so.7; loading torch first makes this library
+    # bind to that same runtime (same soname), so the process has one HIP runtime.
+    import torch  # noqa: F401
+
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _f32_ptr(a: np.ndarray):
+    return a.ctypes.data_as(_FP)
+
+
+def _ptr(t) -> int:
+    """Device pointer of a torch tensor (or None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+class Context:
+    """An llh_ctx on one HIP device."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = _P()
+        st = self.lib.llh_ctx_create(device, ctypes.byref(h))
+        if st != OK:
+            raise LlhError(st, f"llh_ctx_create({device}) failed")
+        self.handle = h
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.llh_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter teardown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, st: int) -> int:
+        if st < 0:
+            raise LlhError(st, self.lib.llh_ctx_last_error(self.handle).decode())
+        return st
+
+    def last_error(self) -> str:
+        return self.lib.llh_ctx_last_error(self.handle).decode()
+
+    def metrics(self) -> dict:
+        m = Metrics()
+        self.check(self.lib.llh_ctx_metrics(self.handle, ctypes.byref(m)))
+        return {f: getattr(m, f) for f, _ in Metrics._fields_}
+
+    def device_errors(self, reset: bool = True) -> int:
+        flags = _I32()
+        self.check(self.lib.llh_ctx_device_errors(self.handle, ctypes.byref(flags), 1 if reset else 0))
+        return flags.value
+
+    def reserve_workspace(self, nbytes: int) -> None:
+        self.check(self.lib.llh_ctx_reserve_workspace(self.handle, nbytes))
+
+    def pool(self, fmt: int, block_tokens: int, kv_heads: int, head_dim: int, n_blocks: int) -> "KvPool":
+        return KvPool(self, fmt, block_tokens, kv_heads, head_dim, n_blocks)
+
+    # ---- batched hot path ----
+    @staticmethod
+    def decode_desc(seq_lens, block_tables, num_q_heads: int, max_seq_len: int, window: int = 0) -> DecodeDesc:
+        return DecodeDesc(
+            num_seqs=seq_lens.shape[0],
+            num_q_heads=num_q_heads,
+            max_blocks_per_seq=block_tables.shape[1],
+            max_seq_len=max_seq_len,
+            window=window,
+            reserved=0,
+            d_seq_lens=_ptr(seq_lens),
+            d_block_tables=_ptr(block_tables),
+        )
+
+    def paged_decode(self, pool: "KvPool", desc: DecodeDesc, q, out, score_scale: float, stream=None) -> None:
+        self.check(
+            self.lib.llh_paged_decode(
+                self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out), score_scale, _stream(stream)
+            )
+        )
+
+    def paged_prefill(self, pool: "KvPool", desc: PrefillDesc, q, out, score_scale: float, stream=None) -> None:
+        self.check(
+            self.lib.llh_paged_prefill(
+                self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out), score_scale, _stream(stream)
+            )
+        )
+
+    def write_blocks(self, pool: "KvPool", blocks, k, v, stream=None) -> None:
+        self.check(
+            self.lib.llh_kv_write_blocks(
+                self.handle, pool.handle, _ptr(blocks), _ptr(k), _ptr(v), blocks.shape[0], _stream(stream)
+            )
+        )
+
+    def append(self, pool: "KvPool", slots, k, v, stream=None) -> None:
+        self.check(
+            self.lib.llh_kv_append(self.handle, pool.handle, _ptr(slots), _ptr(k), _ptr(v), slots.shape[0],
+                                   _stream(stream))
+        )
+
+    def gather(self, pool: "KvPool", desc: DecodeDesc, seq: int, lo: int, hi: int, tensor: int, out,
+               stream=None) -> None:
+        self.check(
+            self.lib.llh_debug_gather(self.handle, pool.handle, ctypes.byref(desc), seq, lo, hi, tensor, _ptr(out),
+                                      _stream(stream))
+        )
+
+    def decode_fp8(self, codes, out, stream=None) -> None:
+        self.check(self.lib.llh_debug_decode_fp8(self.handle, _ptr(codes), _ptr(out), codes.numel(), _stream(stream)))
+
+    def layer_cache(self, max_tokens: int, kv_heads: int, head_dim: int, fmt: int = KV_BF16) -> "LayerKvCache":
+        return LayerKvCache.new_with_config(self, max_tokens, kv_heads, head_dim, fmt)
+
+
+class KvPool:
+    """A device-resident paged KV pool (llh_kv_pool)."""
+
+    def __init__(self, ctx: Context, fmt: int, block_tokens: int, kv_heads: int, head_dim: int, n_blocks: int):
+        self.ctx = ctx
+        h = _P()
+        ctx.check(ctx.lib.llh_kv_pool_create(ctx.handle, fmt, block_tokens, kv_heads, head_dim, n_blocks,
+                                             ctypes.byref(h)))
+        self.handle = h
+        info = PoolInfo()
+        ctx.check(ctx.lib.llh_kv_pool_get_info(h, ctypes.byref(info)))
+        self.info = info
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.ctx.lib.llh_kv_pool_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def raw(self) -> dict:
+        """Copies K, V (and scales) to host numpy arrays of raw storage bytes."""
+        import torch
+
+        i = self.info
+        torch.cuda.synchronize()
+
+        def dl(ptr: int, nbytes: int) -> np.ndarray:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=f"cuda:{self.ctx.device}")
+            _memcpy_d2d(buf.data_ptr(), ptr, nbytes)
+            return buf.cpu().numpy()
+
+        out = {"k": dl(i.d_k, i.k_bytes), "v": dl(i.d_v, i.k_bytes)}
+        if i.scale_bytes:
+            out["k_scales"] = dl(i.d_k_scales, i.scale_bytes)
+            out["v_scales"] = dl(i.d_v_scales, i.scale_bytes)
+        return out
+
+
+def _memcpy_d2d(dst: int, src: int, nbytes: int) -> None:
+    """hipMemcpy device-to-device of raw pointers (used to read a pool back)."""
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
+    hip.hipMemcpy.restype = ctypes.c_int
+    hip.hipMemcpy.argtypes = [_P, _P, _SZ, ctypes.c_int]
+    st = hip.hipMemcpy(dst, src, nbytes, 3)  # hipMemcpyDeviceToDevice
+    if st != 0:
+        raise LlhError(ERR_DEVICE, f"hipMemcpy failed with {st}")
+
+
+class LayerKvCache:
+    """Mirror of kir-ai's LayerKvCache over device blocks (crates/llm-kv-cache/src/layer.rs)."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    @classmethod
+    def new(cls, ctx: Context, max_tokens: int, key_value_heads: int, head_dim: int) -> "LayerKvCache":
+        return cls.new_with_config(ctx, max_tokens, key_value_heads, head_dim, KV_BF16)
+
+    @classmethod
+    def new_with_config(cls, ctx: Context, max_tokens: int, key_value_heads: int, head_dim: int,
+                        fmt: int) -> "LayerKvCache":
+        h = _P()
+        ctx.check(ctx.lib.llh_layer_cache_create(ctx.handle, max_tokens, key_value_heads, head_dim, fmt,
+                                                 ctypes.byref(h)))
+        return cls(ctx, h)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.ctx.lib.llh_layer_cache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def clone(self) -> "LayerKvCache":
+        h = _P()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_clone(self.handle, ctypes.byref(h)))
+        return LayerKvCache(self.ctx, h)
+
+    def clear(self) -> None:
+        self.ctx.check(self.ctx.lib.llh_layer_cache_clear(self.handle))
+
+    def state(self) -> LayerCacheState:
+        s = LayerCacheState()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_get_state(self.handle, ctypes.byref(s)))
+        return s
+
+    def id(self) -> int:
+        return self.state().id
+
+    def revision(self) -> int:
+        return self.state().revision
+
+    def token_count(self) -> int:
+        return self.state().token_count
+
+    def next_position(self) -> int:
+        return self.state().tokens_seen
+
+    def max_tokens(self) -> int:
+        return self.state().max_tokens
+
+    def vector_len(self) -> int:
+        s = self.state()
+        return s.kv_heads * s.head_dim
+
+    def append_sliding(self, key: Sequence[float], value: Sequence[float]) -> None:
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        if k.size != v.size:
+            raise LlhError(ERR_INVALID_SHAPE, "key and value lengths differ")
+        self.ctx.check(self.ctx.lib.llh_append_kv_cache_sliding_f32(self.ctx.handle, self.handle, _f32_ptr(k),
+                                                                    _f32_ptr(v), k.size))
+
+    def append(self, key: Sequence[float], value: Sequence[float]) -> None:
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        if k.size != v.size:
+            raise LlhError(ERR_INVALID_SHAPE, "key and value lengths differ")
+        self.ctx.check(self.ctx.lib.llh_append_kv_cache_f32(self.ctx.handle, self.handle, _f32_ptr(k), _f32_ptr(v),
+                                                            k.size))
+
+    def block_ids(self) -> list:
+        n = _SZ()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_block_ids(self.handle, None, 0, ctypes.byref(n)))
+        arr = (ctypes.c_uint64 * max(1, n.value))()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_block_ids(self.handle, arr, n.value, ctypes.byref(n)))
+        return list(arr[: n.value])
+
+    def active_blocks(self) -> list:
+        n = _SZ()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_active_blocks(self.handle, None, 0, ctypes.byref(n)))
+        arr = (BlockRun * max(1, n.value))()
+        self.ctx.check(self.ctx.lib.llh_layer_cache_active_blocks(self.handle, arr, n.value, ctypes.byref(n)))
+        return [{f: getattr(r, f) for f, _ in BlockRun._fields_} for r in arr[: n.value]]
+
+    def keys(self) -> np.ndarray:
+        return HipNativeMatvecBackend(self.ctx).select_kv_cache_head_rows_f32(
+            self, 0, self.token_count(), 0, self.vector_len())
+
+    def values(self) -> np.ndarray:
+        return HipNativeMatvecBackend(self.ctx).select_kv_cache_head_rows_f32(
+            self, 1, self.token_count(), 0, self.vector_len())
+
+
+class HipNativeMatvecBackend:
+    """The attention hooks of NativeMatvecBackend (native_matvec.rs:619-668) on the device."""
+
+    KEY = 0
+    VALUE = 1
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+
+    def append_kv_cache_sliding_f32(self, cache: LayerKvCache, key, value) -> None:
+        cache.append_sliding(key, value)
+
+    def full_attention_cache_mix_f32_in_place(self, cache: LayerKvCache, query, row_count: int,
+                                              num_attention_heads: int, num_key_value_heads: int, head_dim: int,
+                                              score_scale: float, output: np.ndarray) -> bool:
+        q = np.ascontiguousarray(query, dtype=np.float32)
+        if output.dtype != np.float32 or not output.flags["C_CONTIGUOUS"]:
+            raise LlhError(ERR_INVALID_SHAPE, "output must be a contiguous float32 array")
+        st = self.ctx.lib.llh_full_attention_cache_mix_f32_in_place(
+            self.ctx.handle, cache.handle, _f32_ptr(q), q.size, row_count, num_attention_heads,
+            num_key_value_heads, head_dim, float(score_scale), _f32_ptr(output), output.size)
+        if st == NOT_HANDLED:
+            return False
+        self.ctx.check(st)
+        return True
+
+    def select_kv_cache_head_rows_f32(self, cache: LayerKvCache, tensor: int, row_count: int, head_start: int,
+                                      head_len: int) -> np.ndarray:
+        out = np.zeros(row_count * head_len, dtype=np.float32)
+        self.select_kv_cache_head_rows_f32_in_place(cache, tensor, row_count, head_start, head_len, out)
+        return out
+
+    def select_kv_cache_head_rows_f32_in_place(self, cache: LayerKvCache, tensor: int, row_count: int,
+                                               head_start: int, head_len: int, output: np.ndarray) -> None:
+        self.ctx.check(self.ctx.lib.llh_select_kv_cache_head_rows_f32_in_place(
+            self.ctx.handle, cache.handle, tensor, row_count, head_start, head_len, _f32_ptr(output), output.size))

@@ -1,0 +1,201 @@
+"""Paged GQA decode on the GPU vs the CPU oracle (2, 4, 5 and edge cases).
+
+Every case runs the HIP kernel through the C ABI (llh_paged_decode) and compares
+with the oracle's restatement of the reference per-head loop
+(crates/llm-backend/src/core/native_attention.rs:707-773) run on the pool the
+GPU actually holds, at the BASELINE bar: bf16 output within max-abs 2e-2 and
+mean-abs 2e-3 of the fp32 reference rounded to bf16.  The kernel's sticky error
+flags must stay clear (no out-of-pool block touched, no split overflow).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import llm_hip
+import oracle
+from helpers import assert_parity, from_dev_bf16, rows_bf16, to_dev
+from llm_hip import workloads
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+BT = 16
+
+
+def build_case(ctx, batch, Hq, Hkv, fmt, seed, head_dim=D):
+    bt = batch.block_tokens
+    ids, src_k = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 1, b, lo, hi, Hkv, head_dim),
+                                         Hkv, head_dim)
+    _, src_v = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, Hkv, head_dim),
+                                       Hkv, head_dim)
+    pool = ctx.pool(fmt, bt, Hkv, head_dim, batch.n_blocks)
+    if ids.size:
+        ctx.write_blocks(pool, to_dev(ids), to_dev(src_k), to_dev(src_v))
+    q = oracle.normal_bf16(seed + 3, batch.seq_lens.size * Hq * head_dim)
+    return pool, q
+
+
+def run_decode(ctx, pool, batch, q, Hq, window, scale, head_dim=D, max_seq_len=None):
+    import torch
+
+    B = batch.seq_lens.size
+    d_lens, d_tab, d_q = to_dev(batch.seq_lens), to_dev(batch.tables), to_dev(q)
+    d_out = torch.full((B * Hq * head_dim,), 0x7FC0, dtype=torch.int16, device="cuda")  # NaN fill
+    msl = int(batch.seq_lens.max()) if max_seq_len is None else max_seq_len
+    desc = ctx.decode_desc(d_lens, d_tab, Hq, msl, window)
+    ctx.paged_decode(pool, desc, d_q, d_out, scale)
+    torch.cuda.synchronize()
+    return from_dev_bf16(d_out)
+
+
+def oracle_decode(pool, batch, fmt, Hq, Hkv, window, q, scale, head_dim=D):
+    opool = oracle.Pool.from_raw(fmt, batch.block_tokens, Hkv, head_dim, batch.n_blocks, pool.raw())
+    st, ref = opool.decode(Hq, batch.seq_lens, batch.tables, window, q, scale, threads=16)
+    assert st == oracle.OK
+    return ref
+
+
+def check(ctx, batch, Hq, Hkv, fmt=llm_hip.KV_BF16, window=0, seed=1, head_dim=D, what=""):
+    scale = 1.0 / math.sqrt(head_dim)
+    pool, q = build_case(ctx, batch, Hq, Hkv, fmt, seed, head_dim)
+    out = run_decode(ctx, pool, batch, q, Hq, window, scale, head_dim)
+    assert ctx.device_errors() == 0, ctx.last_error()
+    ref = oracle_decode(pool, batch, fmt, Hq, Hkv, window, q, scale, head_dim)
+    return assert_parity(out, ref, what=what)
+
+
+def identity_batch(lens, block_tokens=BT):
+    lens = np.asarray(lens, dtype=np.int32)
+    nblk = (lens + block_tokens - 1) // block_tokens
+    mb = max(1, int(nblk.max()))
+    tables = np.full((lens.size, mb), -1, dtype=np.int32)
+    cur = 0
+    for b, n in enumerate(nblk):
+        tables[b, :n] = np.arange(cur, cur + n)
+        cur += n
+    return workloads.PagedBatch(lens, tables, max(cur, 1), block_tokens, np.zeros(lens.size, np.int32))
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16])
+def test_decode_c1_identity_table(ctx, fmt):
+    """B=1, L=512, Hq16/Hkv8, D128, 16-token blocks, identity table."""
+    check(ctx, identity_batch([512]), 16, 8, fmt, seed=workloads.SEED_BASE + 0, what="C1")
+
+
+def test_decode_c2_full_size(ctx):
+    """B=32, L~U[256,4096], permuted pool +10% free blocks."""
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
+    assert batch.n_blocks == math.ceil(1.1 * int(np.sum((lens + 15) // 16)))
+    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what="C2")
+
+
+@pytest.mark.parametrize("lens", [[1], [15, 16, 17], [31, 33, 255, 256, 257], [1000, 4095, 4096, 4097]])
+def test_decode_ragged_lengths(ctx, lens):
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=len(lens))
+    check(ctx, batch, 16, 8, seed=7, what=f"lens={lens}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+def test_decode_gqa_groups(ctx, Hq, Hkv):
+    lens = [300, 700, 1200]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq * 10 + Hkv)
+    check(ctx, batch, Hq, Hkv, seed=11, what=f"Hq={Hq} Hkv={Hkv}")
+
+
+def test_decode_c4_sliding_window_skips_blocks(ctx):
+    """configs[3] decode: 4 x 32768 positions, window 4096, shuffled blocks.
+    Blocks wholly before the window are not in the pool (table entry -1): any
+    access would raise the bad-block flag, so a clear flag proves they are skipped."""
+    L, W = 32768, 4096
+    lens = [L] * 4
+    first = [(L - W) // BT] * 4
+    batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 3, resident_from=first)
+    check(ctx, batch, 16, 8, window=W, seed=workloads.SEED_BASE + 3, what="C4 decode")
+
+
+@pytest.mark.parametrize("W,lens", [(1, [5, 16, 17]), (17, [16, 17, 40, 100]), (100, [50, 99, 100, 101, 333])])
+def test_decode_window_edges(ctx, W, lens):
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=W)
+    check(ctx, batch, 16, 8, window=W, seed=W + 1, what=f"W={W}")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_c5_quantized(ctx, fmt):
+    """configs[4] shape (Hq32/Hkv8, L=8192) at 16 of the 64 sequences; bench.py runs all 64."""
+    lens = [8192] * 16
+    batch = workloads.paged_batch(lens, BT, 0.0, workloads.SEED_BASE + 4)
+    check(ctx, batch, 32, 8, fmt, seed=workloads.SEED_BASE + 4, what=f"C5 fmt={fmt}")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_quantized_ragged_window(ctx, fmt):
+    lens = [1, 17, 250, 1025, 3000]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=fmt)
+    check(ctx, batch, 16, 8, fmt, window=0, seed=21, what=f"fmt={fmt}")
+    check(ctx, batch, 16, 8, fmt, window=333, seed=22, what=f"fmt={fmt} W=333")
+
+
+def test_decode_empty_sequence_is_zero(ctx):
+    """R = 0 gives a zero output (weighted sum of nothing, primitives.rs:1125-1128)."""
+    batch = workloads.paged_batch([0, 20], BT, 0.10, seed=3)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 5)
+    out = run_decode(ctx, pool, batch, q, 16, 0, 0.125)
+    assert ctx.device_errors() == 0
+    assert np.all(oracle.bf16_to_f32(out[: 16 * D]) == 0.0)
+    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, 16, 8, 0, q, 0.125)
+    assert_parity(out, ref, what="empty + 20")
+
+
+@pytest.mark.parametrize("head_dim,bt,Hq,Hkv", [(64, 8, 8, 2), (32, 16, 6, 3), (128, 32, 16, 8)])
+def test_decode_generic_shapes(ctx, head_dim, bt, Hq, Hkv):
+    """Shapes outside the tuned kernel run the reference-order kernel."""
+    batch = workloads.paged_batch([5, 77, 300], bt, 0.10, seed=head_dim)
+    check(ctx, batch, Hq, Hkv, seed=31, head_dim=head_dim, what=f"D={head_dim} BT={bt}")
+
+
+def test_decode_bad_block_raises_flag(ctx):
+    batch = workloads.paged_batch([64, 64], BT, 0.10, seed=9)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 9)
+    bad = workloads.PagedBatch(batch.seq_lens, batch.tables.copy(), batch.n_blocks, BT, batch.first_block)
+    bad.tables[1, 2] = batch.n_blocks + 5  # outside the pool: the kernel's bounds check turns it into a flag
+    run_decode(ctx, pool, bad, q, 16, 0, 0.1)
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
+
+
+def test_decode_max_seq_len_bound_raises_flag(ctx):
+    batch = workloads.paged_batch([2000], BT, 0.10, seed=10)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 10)
+    run_decode(ctx, pool, batch, q, 16, 0, 0.1, max_seq_len=100)
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_TOO_MANY_SPLITS
+
+
+def test_decode_repeated_calls_are_identical(ctx):
+    """Split counters return to zero after every call: repeat calls give identical bits."""
+    lens = workloads.uniform_lengths(8, 256, 4096, 99)
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=99)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 99)
+    outs = [run_decode(ctx, pool, batch, q, 16, 0, 0.09) for _ in range(3)]
+    assert ctx.device_errors() == 0
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+
+
+def test_decode_shape_errors(ctx):
+    import torch
+
+    batch = workloads.paged_batch([10], BT, 0.10, seed=1)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 1)
+    d_lens, d_tab = to_dev(batch.seq_lens), to_dev(batch.tables)
+    d_q, d_out = to_dev(q), torch.empty(16 * D, dtype=torch.int16, device="cuda")
+    desc = ctx.decode_desc(d_lens, d_tab, 12, 10)  # 12 q heads is not a multiple of 8 kv heads
+    with pytest.raises(llm_hip.LlhError) as e:
+        ctx.paged_decode(pool, desc, d_q, d_out, 0.1)
+    assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+    desc = ctx.decode_desc(d_lens, d_tab, 16, 10, window=-1)
+    with pytest.raises(llm_hip.LlhError):
+        ctx.paged_decode(pool, desc, d_q, d_out, 0.1)
+    desc = ctx.decode_desc(d_lens, d_tab, 16, 10)
+    with pytest.raises(llm_hip.LlhError) as e:
+        ctx.paged_decode(pool, desc, d_q, d_out, float("nan"))
+    assert e.value.status == llm_hip.ERR_NON_FINITE
