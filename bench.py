@@ -190,9 +190,7 @@ def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos
     starts = torch.tensor([i * chunk for i in range(B + 1)], dtype=torch.int32, device="cuda")
     clens = torch.tensor(lens, dtype=torch.int32, device="cuda")
     tab = torch.from_numpy(batch.tables).cuda()
-    desc = llm_hip.PrefillDesc(num_seqs=B, num_q_heads=Hq, max_blocks_per_seq=batch.max_blocks, window=window,
-                               total_q_rows=B * chunk, max_chunk_len=chunk, d_chunk_starts=starts.data_ptr(),
-                               d_context_lens=clens.data_ptr(), d_block_tables=tab.data_ptr())
+    desc = ctx.prefill_desc(starts, clens, tab, Hq, chunk, window, total_q_rows=B * chunk)
     keep = (pool, q, out, starts, clens, tab)
     scale = 1.0 / math.sqrt(D)
 

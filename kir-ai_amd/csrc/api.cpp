@@ -60,6 +60,7 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window) {
     split = 4;
     while (split < 32 && work / (split * 2) >= 4096) split *= 2;
   }
+  split = std::min(std::max(split, 4), 256);  // a wavefront reads its table entries from <= 64 lanes
   SplitPlan p;
   p.split_blocks = split;
   p.est_blocks = est_blocks;

@@ -6,10 +6,18 @@
 // crates/llm-backend/src/core/native_attention.rs:731-771, with the window rule
 // of crates/llm-backend/src/core/qwen/ops/cache.rs:116-121).
 //
-// Tuned kernel (head_dim 128, 16-token blocks): one workgroup per
-// (split, kv head, sequence).  A split is `split_blocks` consecutive blocks of
-// the attended range; the four wavefronts take its blocks round-robin.  Every
-// K/V byte of the kv head is read once and serves all G = Hq/Hkv query heads.
+// Tuned path (head_dim 128, 16-token blocks), two launches:
+//   1. paged_decode_kernel: one workgroup per (split, kv head, sequence).  A
+//      split is `split_blocks` consecutive blocks of the attended range; the
+//      four wavefronts take its blocks round-robin, double-buffering the loads
+//      of the next block behind the math of the current one.  Every K/V byte of
+//      the kv head is read once and serves all G = Hq/Hkv query heads.  A
+//      single-split sequence writes its output directly; otherwise each split
+//      writes (max, sum, unnormalised output) partials.
+//   2. decode_merge_kernel: log-sum-exp merge of the partials.
+// The launch boundary makes the partials visible to the merge: no device-scope
+// fence runs inside a workgroup (on gfx950 such a fence writes back and
+// invalidates the whole L2 of the XCD, and those serialise).
 // The path is HBM-bound and uses no MFMA.
 //
 // Lane roles inside a wavefront, per 16-token block (K: token rows, V: dim rows):
@@ -21,8 +29,7 @@
 //             512 contiguous bytes per instruction.
 // Each group keeps its own online-softmax state (running max in log2 units,
 // sum, 8 output dims per lane per head); groups, wavefronts and splits are
-// merged by log-sum-exp.  The last workgroup of a (sequence, kv head) to finish
-// merges the split partials, so one launch produces the output.
+// merged by log-sum-exp.
 #include "llh_internal.h"
 
 namespace llh {
@@ -77,18 +84,241 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Per-block online-softmax update for one query head of one token group.
-// s[4] are scores (log2 units, -inf when masked), w[4] the weights used for V
-// (p, or p * value scale); returns p via the array.
-__device__ __forceinline__ void online_update(float &m, float &l, float s[4], float &alpha, float p[4]) {
-  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  mx = fmaxf(mx, m);
-  const float mref = (mx == -INFINITY) ? 0.0f : mx;
-  alpha = fast_exp2(m - mref);
+// Raw registers of one block for one wavefront.
+template <int FMT>
+struct BlockRegs;
+
+template <>
+struct BlockRegs<kBf16> {
+  uint4 k[4];
+  uint2 v[8];
+  bool valid;
+};
+
+template <int FMT>
+struct BlockRegs {
+  uint4 k[2];
+  uint32_t v[8];
+  uint2 ks;   // int8: fp16 scales of tokens 4g..4g+3
+  uint2 vs;
+  float ksb;  // fp8: per (block, head) scales
+  float vsb;
+  bool valid;
+};
+
+// Issues the loads of block `phys` (wave-uniform) into r.
+template <int FMT>
+__device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kvh, int lane, BlockRegs<FMT> &r) {
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  r.valid = phys >= 0 && (int64_t)phys < a.pool.n_blocks;
+  if (!r.valid) return;
+  constexpr int kBlockBytes = (FMT == kBf16 ? 2 : 1) * BT * D;
+  const size_t bh = (size_t)phys * a.pool.kv_heads + kvh;
+  const char *kb = reinterpret_cast<const char *>(a.pool.k) + bh * kBlockBytes;
+  const char *vb = reinterpret_cast<const char *>(a.pool.v) + bh * kBlockBytes;
+  if constexpr (FMT == kBf16) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[i] - mref);
-  l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-  m = mx;
+    for (int i = 0; i < 4; i++) r.k[i] = *reinterpret_cast<const uint4 *>(kb + (4 * g + i) * (D * 2) + c * 16);
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.v[j] = *reinterpret_cast<const uint2 *>(vb + (16 * j + c) * (BT * 2) + g * 8);
+  } else {
+    const int hf = (lane >> 3) & 1;
+    const int c8 = lane & 7;
+#pragma unroll
+    for (int i = 0; i < 2; i++) r.k[i] = *reinterpret_cast<const uint4 *>(kb + (4 * g + 2 * i + hf) * D + c8 * 16);
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.v[j] = *reinterpret_cast<const uint32_t *>(vb + (16 * j + c) * BT + g * 4);
+    if constexpr (FMT == kInt8) {
+      r.ks = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales) + bh * BT + 4 * g);
+      r.vs = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) + bh * BT + 4 * g);
+    } else {
+      r.ksb = reinterpret_cast<const float *>(a.pool.k_scales)[bh];
+      r.vsb = reinterpret_cast<const float *>(a.pool.v_scales)[bh];
+    }
+  }
+}
+
+// Per-group online-softmax state for G query heads.
+template <int G>
+struct SoftmaxState {
+  float m[G];
+  float l[G];
+  float wsum[G];  // int8 only: running sum of p * value scale (offset-128 correction)
+  float o[G][8];
+};
+
+template <int G, int FMT>
+__device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
+                                              int lane, const uint32_t (&qw)[G][4], const float (&qf)[G][16],
+                                              const float (&qsum)[G], SoftmaxState<G> &st) {
+  if (!r.valid) {
+    if (lane == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const int g = lane >> 4;
+  const int pos0 = jb * BT + 4 * g;
+  const bool partial = (jb * BT < lo) || (jb * BT + BT > len);
+  bool ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len);
+
+  float s[G][4];
+  float vf[8][4];  // V values of dims 16j + c, tokens 4g .. 4g+3
+  float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+
+  if constexpr (FMT == kBf16) {
+    uint2 vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) vr[j] = r.v[j];
+    if (partial) {
+      const uint32_t mx = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
+      const uint32_t my = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        vr[j].x &= mx;
+        vr[j].y &= my;
+      }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float acc = dot2_bf16(r.k[i].x, qw[gi][0], 0.0f);
+        acc = dot2_bf16(r.k[i].y, qw[gi][1], acc);
+        acc = dot2_bf16(r.k[i].z, qw[gi][2], acc);
+        acc = dot2_bf16(r.k[i].w, qw[gi][3], acc);
+        s[gi][i] = row_sum16(acc) * a.scale_log2e;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      vf[j][0] = bf16_lo(vr[j].x);
+      vf[j][1] = bf16_hi(vr[j].x);
+      vf[j][2] = bf16_lo(vr[j].y);
+      vf[j][3] = bf16_hi(vr[j].y);
+    }
+  } else {
+    // int8 / fp8: K token rows of 128 bytes; lane (g, half hf, c8) holds tokens
+    // 4g + 2i + hf (i = 0, 1) at dims 16*c8 .. +16.  V dim rows of 16 bytes;
+    // lane holds the 4 bytes of tokens 4g..4g+3 for dims 16j + c.
+    const int hf = (lane >> 3) & 1;
+    uint32_t vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) vr[j] = r.v[j];
+    if (partial) {
+      const uint32_t mk = (ok[0] ? 0xffu : 0u) | (ok[1] ? 0xff00u : 0u) | (ok[2] ? 0xff0000u : 0u) |
+                          (ok[3] ? 0xff000000u : 0u);
+#pragma unroll
+      for (int j = 0; j < 8; j++) vr[j] &= mk;
+    }
+    float kscale_own[2];
+    if constexpr (FMT == kInt8) {
+      const float k4[4] = {f16_bits_to_f32(r.ks.x & 0xffffu), f16_bits_to_f32(r.ks.x >> 16),
+                           f16_bits_to_f32(r.ks.y & 0xffffu), f16_bits_to_f32(r.ks.y >> 16)};
+      vsc[0] = f16_bits_to_f32(r.vs.x & 0xffffu);
+      vsc[1] = f16_bits_to_f32(r.vs.x >> 16);
+      vsc[2] = f16_bits_to_f32(r.vs.y & 0xffffu);
+      vsc[3] = f16_bits_to_f32(r.vs.y >> 16);
+      kscale_own[0] = hf ? k4[1] : k4[0];
+      kscale_own[1] = hf ? k4[3] : k4[2];
+      // codes as unsigned bytes u = code + 128 (xor 0x80); f32(u) is one convert
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t u = vr[j] ^ 0x80808080u;
+#pragma unroll
+        for (int i = 0; i < 4; i++) vf[j][i] = (float)((u >> (8 * i)) & 0xffu);
+      }
+    } else {
+      kscale_own[0] = r.ksb;
+      kscale_own[1] = r.ksb;
+      vsc[0] = vsc[1] = vsc[2] = vsc[3] = r.vsb;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], false);
+        const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], true);
+        vf[j][0] = lo2[0];
+        vf[j][1] = lo2[1];
+        vf[j][2] = hi2[0];
+        vf[j][3] = hi2[1];
+      }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      float own[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          if constexpr (FMT == kInt8) {
+            const uint32_t u = w[k] ^ 0x80808080u;
+#pragma unroll
+            for (int n = 0; n < 4; n++) acc += qf[gi][4 * k + n] * (float)((u >> (8 * n)) & 0xffu);
+          } else {
+            const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
+            const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
+            acc += qf[gi][4 * k + 0] * lo2[0];
+            acc += qf[gi][4 * k + 1] * lo2[1];
+            acc += qf[gi][4 * k + 2] * hi2[0];
+            acc += qf[gi][4 * k + 3] * hi2[1];
+          }
+        }
+        if constexpr (FMT == kInt8) acc -= 128.0f * qsum[gi];
+        own[i] = row_sum8(acc) * kscale_own[i] * a.scale_log2e;
+      }
+      const float oth0 = dpp<0x140>(own[0]);  // row_mirror swaps the two 8-lane halves
+      const float oth1 = dpp<0x140>(own[1]);
+      s[gi][0] = hf ? oth0 : own[0];
+      s[gi][1] = hf ? own[0] : oth0;
+      s[gi][2] = hf ? oth1 : own[1];
+      s[gi][3] = hf ? own[1] : oth1;
+    }
+  }
+
+  if (partial) {
+#pragma unroll
+    for (int gi = 0; gi < G; gi++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (!ok[i]) s[gi][i] = -INFINITY;
+  }
+
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    float mx = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
+    mx = fmaxf(mx, st.m[gi]);
+    const float mref = (mx == -INFINITY) ? 0.0f : mx;
+    const float alpha = fast_exp2(st.m[gi] - mref);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
+    st.l[gi] = st.l[gi] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    st.m[gi] = mx;
+    float w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = (FMT == kBf16) ? p[i] : (ok[i] ? p[i] * vsc[i] : 0.0f);
+    if constexpr (FMT == kInt8) st.wsum[gi] = st.wsum[gi] * alpha + ((w[0] + w[1]) + (w[2] + w[3]));
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      float acc = st.o[gi][j] * alpha;
+      acc += w[0] * vf[j][0];
+      acc += w[1] * vf[j][1];
+      acc += w[2] * vf[j][2];
+      acc += w[3] * vf[j][3];
+      st.o[gi][j] = acc;
+    }
+  }
+}
+
+__device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, int &lo, int &first_blk, int &n_blk,
+                                          int &n_splits) {
+  len = a.seq_lens[b];
+  lo = a.window > 0 ? max(0, len - a.window) : 0;
+  first_blk = lo / BT;
+  n_blk = len > lo ? (len - 1) / BT - first_blk + 1 : 0;
+  n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
 }
 
 template <int G, int FMT>
@@ -96,13 +326,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  const int Hkv = a.pool.kv_heads;
-
-  const int len = a.seq_lens[b];
-  const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-  const int first_blk = lo / BT;
-  const int n_blk = len > lo ? (len - 1) / BT - first_blk + 1 : 0;
-  const int n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
+  int len, lo, first_blk, n_blk, n_splits;
+  seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
   if (n_splits > a.max_splits) {
     if (threadIdx.x == 0 && split == 0) atomicOr(a.err, kErrTooManySplits);
     return;
@@ -121,9 +346,16 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     return;
   }
 
+  // ---- this wavefront's blocks and their pool indices (one load, read back per block) ----
+  const int blk_begin = first_blk + split * a.split_blocks;
+  const int blk_end = min(blk_begin + a.split_blocks, first_blk + n_blk);
+  const int nbw = max(0, (blk_end - blk_begin - wave + 3) / 4);  // <= split_blocks / 4 <= 64
+  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
+  const int my_entry = lane < nbw ? table[(blk_begin + wave + 4 * lane) % a.max_blocks] : -1;
+
   // ---- query ----
-  uint32_t qw[G][4];     // bf16 pairs, dims 8c..8c+7 (bf16 K path)
-  float qf[G][16];       // f32 dims 16*(lane&7) .. +16 (int8/fp8 K path)
+  uint32_t qw[G][4];  // bf16 pairs, dims 8c..8c+7 (bf16 K path)
+  float qf[G][16];    // f32 dims 16*(lane&7) .. +16 (int8/fp8 K path)
   float qsum[G];
   if constexpr (FMT == kBf16) {
 #pragma unroll
@@ -133,6 +365,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       qw[gi][1] = t.y;
       qw[gi][2] = t.z;
       qw[gi][3] = t.w;
+      qsum[gi] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) qf[gi][k] = 0.0f;
     }
   } else {
     const int c8 = lane & 7;
@@ -149,191 +384,30 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
         s += qf[gi][2 * k] + qf[gi][2 * k + 1];
       }
       qsum[gi] = s;
+#pragma unroll
+      for (int k = 0; k < 4; k++) qw[gi][k] = 0u;
     }
   }
 
-  float m[G], l[G], wsum[G], o[G][8];
+  SoftmaxState<G> st;
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    m[gi] = -INFINITY;
-    l[gi] = 0.0f;
-    wsum[gi] = 0.0f;
+    st.m[gi] = -INFINITY;
+    st.l[gi] = 0.0f;
+    st.wsum[gi] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) o[gi][j] = 0.0f;
+    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
   }
 
-  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const int blk_begin = first_blk + split * a.split_blocks;
-  const int blk_end = min(blk_begin + a.split_blocks, first_blk + n_blk);
-  constexpr int kBlockBytes = (FMT == kBf16 ? 2 : 1) * BT * D;
-
-  for (int jb = blk_begin + wave; jb < blk_end; jb += 4) {
-    const int phys = table[jb % a.max_blocks];
-    if (phys < 0 || (int64_t)phys >= a.pool.n_blocks) {
-      if (lane == 0) atomicOr(a.err, kErrBadBlock);
-      continue;
-    }
-    const size_t bh = (size_t)phys * Hkv + kvh;
-    const char *kb = reinterpret_cast<const char *>(a.pool.k) + bh * kBlockBytes;
-    const char *vb = reinterpret_cast<const char *>(a.pool.v) + bh * kBlockBytes;
-    const int pos0 = jb * BT + 4 * g;
-    const bool partial = (jb * BT < lo) || (jb * BT + BT > len);
-    bool ok[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len);
-
-    float s[G][4];
-    float vf[8][4];  // V values of dims 16j + c, tokens 4g .. 4g+3
-    float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-
-    if constexpr (FMT == kBf16) {
-      uint4 kr[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) kr[i] = *reinterpret_cast<const uint4 *>(kb + (4 * g + i) * (D * 2) + c * 16);
-      uint2 vr[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) vr[j] = *reinterpret_cast<const uint2 *>(vb + (16 * j + c) * (BT * 2) + g * 8);
-      if (partial) {
-        const uint32_t mx = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
-        const uint32_t my = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          vr[j].x &= mx;
-          vr[j].y &= my;
-        }
-      }
-#pragma unroll
-      for (int gi = 0; gi < G; gi++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          float acc = dot2_bf16(kr[i].x, qw[gi][0], 0.0f);
-          acc = dot2_bf16(kr[i].y, qw[gi][1], acc);
-          acc = dot2_bf16(kr[i].z, qw[gi][2], acc);
-          acc = dot2_bf16(kr[i].w, qw[gi][3], acc);
-          s[gi][i] = row_sum16(acc) * a.scale_log2e;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        vf[j][0] = bf16_lo(vr[j].x);
-        vf[j][1] = bf16_hi(vr[j].x);
-        vf[j][2] = bf16_lo(vr[j].y);
-        vf[j][3] = bf16_hi(vr[j].y);
-      }
-    } else {
-      // int8 / fp8: K token rows of 128 bytes; lane (g, half hf, c8) holds tokens
-      // 4g + 2i + hf (i = 0, 1) at dims 16*c8 .. +16.  V dim rows of 16 bytes;
-      // lane holds the 4 bytes of tokens 4g..4g+3 for dims 16j + c.
-      const int hf = (lane >> 3) & 1;
-      const int c8 = lane & 7;
-      uint4 kr[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++) kr[i] = *reinterpret_cast<const uint4 *>(kb + (4 * g + 2 * i + hf) * D + c8 * 16);
-      uint32_t vr[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) vr[j] = *reinterpret_cast<const uint32_t *>(vb + (16 * j + c) * BT + g * 4);
-      if (partial) {
-        const uint32_t mk = (ok[0] ? 0xffu : 0u) | (ok[1] ? 0xff00u : 0u) | (ok[2] ? 0xff0000u : 0u) |
-                            (ok[3] ? 0xff000000u : 0u);
-#pragma unroll
-        for (int j = 0; j < 8; j++) vr[j] &= mk;
-      }
-      float kscale_own[2];
-      if constexpr (FMT == kInt8) {
-        const uint16_t *ksp = reinterpret_cast<const uint16_t *>(a.pool.k_scales) + bh * BT + 4 * g;
-        const uint16_t *vsp = reinterpret_cast<const uint16_t *>(a.pool.v_scales) + bh * BT + 4 * g;
-        const uint2 ks = *reinterpret_cast<const uint2 *>(ksp);
-        const uint2 vs = *reinterpret_cast<const uint2 *>(vsp);
-        const float k4[4] = {f16_bits_to_f32(ks.x & 0xffffu), f16_bits_to_f32(ks.x >> 16),
-                             f16_bits_to_f32(ks.y & 0xffffu), f16_bits_to_f32(ks.y >> 16)};
-        vsc[0] = f16_bits_to_f32(vs.x & 0xffffu);
-        vsc[1] = f16_bits_to_f32(vs.x >> 16);
-        vsc[2] = f16_bits_to_f32(vs.y & 0xffffu);
-        vsc[3] = f16_bits_to_f32(vs.y >> 16);
-        kscale_own[0] = hf ? k4[1] : k4[0];
-        kscale_own[1] = hf ? k4[3] : k4[2];
-        // codes as unsigned bytes u = code + 128 (xor 0x80); f32(u) is one convert
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const uint32_t u = vr[j] ^ 0x80808080u;
-#pragma unroll
-          for (int i = 0; i < 4; i++) vf[j][i] = (float)((u >> (8 * i)) & 0xffu);
-        }
-      } else {
-        const float ksb = reinterpret_cast<const float *>(a.pool.k_scales)[bh];
-        const float vsb = reinterpret_cast<const float *>(a.pool.v_scales)[bh];
-        kscale_own[0] = ksb;
-        kscale_own[1] = ksb;
-        vsc[0] = vsc[1] = vsc[2] = vsc[3] = vsb;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], false);
-          const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], true);
-          vf[j][0] = lo2[0];
-          vf[j][1] = lo2[1];
-          vf[j][2] = hi2[0];
-          vf[j][3] = hi2[1];
-        }
-      }
-#pragma unroll
-      for (int gi = 0; gi < G; gi++) {
-        float own[2];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-          const uint32_t w[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-          float acc = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 4; k++) {
-            if constexpr (FMT == kInt8) {
-              const uint32_t u = w[k] ^ 0x80808080u;
-#pragma unroll
-              for (int n = 0; n < 4; n++) acc += qf[gi][4 * k + n] * (float)((u >> (8 * n)) & 0xffu);
-            } else {
-              const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
-              const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
-              acc += qf[gi][4 * k + 0] * lo2[0];
-              acc += qf[gi][4 * k + 1] * lo2[1];
-              acc += qf[gi][4 * k + 2] * hi2[0];
-              acc += qf[gi][4 * k + 3] * hi2[1];
-            }
-          }
-          if constexpr (FMT == kInt8) acc -= 128.0f * qsum[gi];
-          own[i] = row_sum8(acc) * kscale_own[i] * a.scale_log2e;
-        }
-        const float oth0 = dpp<0x140>(own[0]);  // row_mirror swaps the two 8-lane halves
-        const float oth1 = dpp<0x140>(own[1]);
-        s[gi][0] = hf ? oth0 : own[0];
-        s[gi][1] = hf ? own[0] : oth0;
-        s[gi][2] = hf ? oth1 : own[1];
-        s[gi][3] = hf ? own[1] : oth1;
-      }
-    }
-
-    if (partial) {
-#pragma unroll
-      for (int gi = 0; gi < G; gi++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (!ok[i]) s[gi][i] = -INFINITY;
-    }
-
-#pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-      float p[4], alpha;
-      online_update(m[gi], l[gi], s[gi], alpha, p);
-      float w[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) w[i] = (FMT == kBf16) ? p[i] : (ok[i] ? p[i] * vsc[i] : 0.0f);
-      if constexpr (FMT == kInt8) wsum[gi] = wsum[gi] * alpha + ((w[0] + w[1]) + (w[2] + w[3]));
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        float acc = o[gi][j] * alpha;
-        acc += w[0] * vf[j][0];
-        acc += w[1] * vf[j][1];
-        acc += w[2] * vf[j][2];
-        acc += w[3] * vf[j][3];
-        o[gi][j] = acc;
-      }
+  // ---- double-buffered block loop: loads of block k+1 overlap the math of block k ----
+  BlockRegs<FMT> ra, rb;
+  if (nbw > 0) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, 0), kvh, lane, ra);
+  for (int k = 0; k < nbw; k += 2) {
+    if (k + 1 < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, k + 1), kvh, lane, rb);
+    compute_block<G, FMT>(a, ra, blk_begin + wave + 4 * k, lo, len, lane, qw, qf, qsum, st);
+    if (k + 1 < nbw) {
+      if (k + 2 < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, k + 2), kvh, lane, ra);
+      compute_block<G, FMT>(a, rb, blk_begin + wave + 4 * (k + 1), lo, len, lane, qw, qf, qsum, st);
     }
   }
 
@@ -345,25 +419,25 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   for (int gi = 0; gi < G; gi++) {
     if constexpr (FMT == kInt8) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) o[gi][j] -= 128.0f * wsum[gi];
+      for (int j = 0; j < 8; j++) st.o[gi][j] -= 128.0f * st.wsum[gi];
     }
-    float mm = fmaxf(m[gi], __shfl_xor(m[gi], 16));
+    float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
     mm = fmaxf(mm, __shfl_xor(mm, 32));
     const float mref = (mm == -INFINITY) ? 0.0f : mm;
-    const float f = fast_exp2(m[gi] - mref);
-    float ll = l[gi] * f;
+    const float f = fast_exp2(st.m[gi] - mref);
+    float ll = st.l[gi] * f;
     ll += __shfl_xor(ll, 16);
     ll += __shfl_xor(ll, 32);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      float v = o[gi][j] * f;
+      float v = st.o[gi][j] * f;
       v += __shfl_xor(v, 16);
       v += __shfl_xor(v, 32);
-      o[gi][j] = v;
+      st.o[gi][j] = v;
     }
     if (g == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) s_o[wave][gi][16 * j + c] = o[gi][j];
+      for (int j = 0; j < 8; j++) s_o[wave][gi][16 * j + c] = st.o[gi][j];
       if (c == 0) {
         s_m[wave][gi] = mm;
         s_l[wave][gi] = ll;
@@ -372,8 +446,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   }
   __syncthreads();
 
-  // ---- merge the four wavefronts; write output or the split partial ----
-  const size_t part0 = qrow0 * a.max_splits;  // partial row of (b, first q head of group, split 0)
+  // ---- merge the four wavefronts; write the output or this split's partial ----
   for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
     const int gi = idx / D;
     const int d = idx % D;
@@ -389,42 +462,34 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     if (n_splits == 1) {
       a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
     } else {
-      const size_t row = part0 + (size_t)gi * a.max_splits + split;
+      const size_t row = (qrow0 + gi) * a.max_splits + split;
       a.ws_o[row * D + d] = oo;
       if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
     }
   }
-  if (n_splits == 1) return;
+}
 
-  // ---- last workgroup of this (sequence, kv head) merges the splits ----
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&a.counters[(size_t)b * Hkv + kvh], 1);
-    s_last = (prev == n_splits - 1);
+// Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
+// dim) per (query head, sequence) whose sequence used more than one split.
+__global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  int len, lo, first_blk, n_blk, n_splits;
+  seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
+  if (n_splits <= 1 || n_splits > a.max_splits) return;
+  const int d = threadIdx.x;
+  const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
+  float mm = -INFINITY;
+  for (int sp = 0; sp < n_splits; sp++) mm = fmaxf(mm, a.ws_ml[row0 + sp].x);
+  const float mref = (mm == -INFINITY) ? 0.0f : mm;
+  float ll = 0.0f, oo = 0.0f;
+  for (int sp = 0; sp < n_splits; sp++) {
+    const float2 ml = a.ws_ml[row0 + sp];
+    const float f = fast_exp2(ml.x - mref);
+    ll += ml.y * f;
+    oo += a.ws_o[(row0 + sp) * D + d] * f;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (tid == 0) a.counters[(size_t)b * Hkv + kvh] = 0;
-  for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-    const int gi = idx / D;
-    const int d = idx % D;
-    const size_t row0 = part0 + (size_t)gi * a.max_splits;
-    float mm = -INFINITY;
-    for (int sp = 0; sp < n_splits; sp++) mm = fmaxf(mm, __builtin_nontemporal_load(&a.ws_ml[row0 + sp].x));
-    const float mref = (mm == -INFINITY) ? 0.0f : mm;
-    float ll = 0.0f, oo = 0.0f;
-    for (int sp = 0; sp < n_splits; sp++) {
-      const float mx = __builtin_nontemporal_load(&a.ws_ml[row0 + sp].x);
-      const float lx = __builtin_nontemporal_load(&a.ws_ml[row0 + sp].y);
-      const float f = fast_exp2(mx - mref);
-      ll += lx * f;
-      oo += __builtin_nontemporal_load(&a.ws_o[(row0 + sp) * D + d]) * f;
-    }
-    a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
-  }
+  a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / ll);
 }
 
 // ---------------------------------------------------------------------------
@@ -568,6 +633,9 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s) 
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
   dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
   hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.max_splits <= 1) return e;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }
 

@@ -275,7 +275,8 @@ class Context:
     # ---- batched hot path ----
     @staticmethod
     def decode_desc(seq_lens, block_tables, num_q_heads: int, max_seq_len: int, window: int = 0) -> DecodeDesc:
-        return DecodeDesc(
+        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers)."""
+        d = DecodeDesc(
             num_seqs=seq_lens.shape[0],
             num_q_heads=num_q_heads,
             max_blocks_per_seq=block_tables.shape[1],
@@ -285,6 +286,28 @@ class Context:
             d_seq_lens=_ptr(seq_lens),
             d_block_tables=_ptr(block_tables),
         )
+        d._keep = (seq_lens, block_tables)
+        return d
+
+    @staticmethod
+    def prefill_desc(chunk_starts, context_lens, block_tables, num_q_heads: int, max_chunk_len: int,
+                     window: int = 0, total_q_rows: Optional[int] = None) -> PrefillDesc:
+        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers)."""
+        if total_q_rows is None:
+            total_q_rows = int(chunk_starts[-1].item())
+        d = PrefillDesc(
+            num_seqs=context_lens.shape[0],
+            num_q_heads=num_q_heads,
+            max_blocks_per_seq=block_tables.shape[1],
+            window=window,
+            total_q_rows=total_q_rows,
+            max_chunk_len=max_chunk_len,
+            d_chunk_starts=_ptr(chunk_starts),
+            d_context_lens=_ptr(context_lens),
+            d_block_tables=_ptr(block_tables),
+        )
+        d._keep = (chunk_starts, context_lens, block_tables)
+        return d
 
     def paged_decode(self, pool: "KvPool", desc: DecodeDesc, q, out, score_scale: float, stream=None) -> None:
         self.check(
