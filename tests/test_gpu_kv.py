@@ -1,0 +1,171 @@
+"""KV writes into the paged pool and the block-table gather, bit-exact against the oracle.
+
+* gather: llh_debug_gather through permuted tables == the oracle's gather of the
+  same pool bytes (bf16, int8, fp8), including ranges that start mid-block and
+  ring-style tables (position p in table[(p / 16) % max_blocks]).
+* quantise on write: int8 codes/fp16 scales per (token, head) and fp8 codes/f32
+  scales per (block, head) == the oracle's quantisers on the same bf16 input.
+* append == whole-block write, bit for bit; fp8 decode table == the OCP table.
+"""
+import numpy as np
+import pytest
+
+import llm_hip
+import oracle
+from helpers import rows_bf16, to_dev
+from llm_hip import workloads
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+BT = 16
+
+
+def write_case(ctx, fmt, lens, Hkv, seed, head_dim=D, free=0.1):
+    batch = workloads.paged_batch(lens, BT, free, seed)
+    ids, sk = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 1, b, lo, hi, Hkv, head_dim), Hkv,
+                                      head_dim)
+    _, sv = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, Hkv, head_dim), Hkv,
+                                    head_dim)
+    pool = ctx.pool(fmt, BT, Hkv, head_dim, batch.n_blocks)
+    ctx.write_blocks(pool, to_dev(ids), to_dev(sk), to_dev(sv))
+    return batch, pool, ids, sk, sv
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_gather_is_bit_exact(ctx, fmt):
+    import torch
+
+    Hkv = 4
+    batch, pool, _, _, _ = write_case(ctx, fmt, [3, 16, 33, 700], Hkv, 100 + fmt)
+    opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, batch.n_blocks, pool.raw())
+    d_lens, d_tab = to_dev(batch.seq_lens), to_dev(batch.tables)
+    desc = ctx.decode_desc(d_lens, d_tab, Hkv, int(batch.seq_lens.max()))
+    esz = 2 if fmt == llm_hip.KV_BF16 else 1
+    for b, L in enumerate(batch.seq_lens):
+        for lo, hi in ((0, int(L)), (int(L) // 3, int(L))):
+            for tensor in (0, 1):
+                out = torch.zeros((hi - lo) * Hkv * D * esz, dtype=torch.uint8, device="cuda")
+                ctx.gather(pool, desc, b, lo, hi, tensor, out)
+                torch.cuda.synchronize()
+                st, ref = opool.gather_raw(batch.tables[b], lo, hi, tensor)
+                assert st == oracle.OK
+                assert np.array_equal(out.cpu().numpy(), ref.view(np.uint8)), (fmt, b, lo, hi, tensor)
+    assert ctx.device_errors() == 0
+
+
+def test_gather_bf16_returns_the_written_rows(ctx):
+    import torch
+
+    Hkv = 2
+    batch, pool, _, _, _ = write_case(ctx, llm_hip.KV_BF16, [77], Hkv, 7)
+    desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(batch.tables), Hkv, 77)
+    out = torch.zeros(77 * Hkv * D, dtype=torch.int16, device="cuda")
+    ctx.gather(pool, desc, 0, 0, 77, 0, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), rows_bf16(8, 0, 0, 77, Hkv, D).ravel())
+
+
+def test_gather_ring_table(ctx):
+    """A 3-block ring serving positions 40..87 (table index (p / 16) % 3)."""
+    import torch
+
+    Hkv = 1
+    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, 5)
+    ring = np.array([[4, 0, 2]], np.int32)
+    rows = rows_bf16(9, 0, 0, 96, Hkv, D)
+    ids, src = [], []
+    for j in range(3, 6):  # positions 48..95 -> ring slots 0, 1, 2
+        ids.append(ring[0, j % 3])
+        src.append(rows[j * BT:(j + 1) * BT])
+    ctx.write_blocks(pool, to_dev(np.array(ids, np.int32)), to_dev(np.stack(src)), to_dev(np.stack(src)))
+    desc = ctx.decode_desc(to_dev(np.array([96], np.int32)), to_dev(ring), 1, 96)
+    out = torch.zeros(40 * D, dtype=torch.int16, device="cuda")
+    ctx.gather(pool, desc, 0, 50, 90, 0, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), rows[50:90].ravel())
+
+
+def test_int8_quantise_on_write_is_bit_exact(ctx):
+    Hkv = 4
+    batch, pool, ids, sk, sv = write_case(ctx, llm_hip.KV_INT8, [40, 17], Hkv, 200)
+    raw = pool.raw()
+    k = raw["k"].view(np.int8).reshape(batch.n_blocks, Hkv, BT, D)
+    v = raw["v"].view(np.int8).reshape(batch.n_blocks, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.uint16).reshape(batch.n_blocks, Hkv, BT)
+    vs = raw["v_scales"].view(np.uint16).reshape(batch.n_blocks, Hkv, BT)
+    for i, blk in enumerate(ids):
+        for h in range(Hkv):
+            for t in range(BT):
+                st, codes, s16 = oracle.quantize_int8_head(oracle.bf16_to_f32(sk[i, t, h]))
+                assert st == oracle.OK
+                assert np.array_equal(k[blk, h, t], codes) and ks[blk, h, t] == s16
+                st, codes, s16 = oracle.quantize_int8_head(oracle.bf16_to_f32(sv[i, t, h]))
+                assert np.array_equal(v[blk, h, :, t], codes) and vs[blk, h, t] == s16
+
+
+def test_fp8_quantise_on_write_is_bit_exact(ctx):
+    Hkv = 4
+    batch, pool, ids, sk, sv = write_case(ctx, llm_hip.KV_FP8_E4M3, [40, 17], Hkv, 300)
+    raw = pool.raw()
+    k = raw["k"].reshape(batch.n_blocks, Hkv, BT, D)
+    v = raw["v"].reshape(batch.n_blocks, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.float32).reshape(batch.n_blocks, Hkv)
+    vs = raw["v_scales"].view(np.float32).reshape(batch.n_blocks, Hkv)
+    for i, blk in enumerate(ids):
+        for h in range(Hkv):
+            st, codes, s = oracle.quantize_fp8_block(oracle.bf16_to_f32(sk[i, :, h, :]))
+            assert st == oracle.OK
+            assert np.array_equal(k[blk, h], codes.reshape(BT, D)) and ks[blk, h] == np.float32(s)
+            st, codes, s = oracle.quantize_fp8_block(oracle.bf16_to_f32(sv[i, :, h, :]))
+            assert np.array_equal(v[blk, h], codes.reshape(BT, D).T) and vs[blk, h] == np.float32(s)
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_append_equals_block_write(ctx, fmt):
+    import torch
+
+    Hkv = 8
+    batch, pool_w, ids, sk, sv = write_case(ctx, fmt, [48, 32], Hkv, 400, free=0.0)
+    pool_a = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
+    slots = []
+    rows_k, rows_v = [], []
+    for i, blk in enumerate(ids):
+        for t in range(BT):
+            slots.append(int(blk) * BT + t)
+            rows_k.append(sk[i, t])
+            rows_v.append(sv[i, t])
+    order = np.random.default_rng(1).permutation(len(slots))  # append order does not matter
+    ctx.append(pool_a, to_dev(np.array(slots, np.int64)[order]), to_dev(np.stack(rows_k)[order]),
+               to_dev(np.stack(rows_v)[order]))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0
+    ra, rw = pool_a.raw(), pool_w.raw()
+    for key in rw:
+        assert np.array_equal(ra[key], rw[key]), key
+
+
+def test_append_rejects_fp8_and_flags_bad_slots(ctx):
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_FP8_E4M3, BT, 2, D, 2)
+    z = torch.zeros(2 * D, dtype=torch.int16, device="cuda")
+    with pytest.raises(llm_hip.LlhError) as e:
+        ctx.append(pool, torch.zeros(1, dtype=torch.int64, device="cuda"), z, z)
+    assert e.value.status == llm_hip.ERR_UNSUPPORTED
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 2, D, 2)
+    ctx.append(pool, torch.tensor([2 * BT + 1], dtype=torch.int64, device="cuda"), z, z)
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
+
+
+def test_fp8_decode_table(ctx):
+    import torch
+
+    codes = torch.arange(256, dtype=torch.uint8, device="cuda")
+    out = torch.zeros(256, dtype=torch.float32, device="cuda")
+    ctx.decode_fp8(codes, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = oracle.fp8_decode_table()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan) and np.array_equal(got[~nan], ref[~nan])

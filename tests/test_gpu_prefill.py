@@ -1,0 +1,134 @@
+"""Chunked causal prefill over cached prefix blocks (MFMA) vs the oracle.
+
+Row i of a chunk sits at position prefix + i and attends [lo, pos]: the result
+of the reference's per-token "append then attend" loop
+(crates/llm-backend/src/core/native_attention.rs:400-461).  At the BASELINE
+sizes the oracle checks sampled rows (tile edges included) and every row is
+checked against the decode kernel at that row's position (a separate kernel
+with a separate reduction order); small ragged cases are checked in full.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import llm_hip
+import oracle
+from helpers import assert_parity, from_dev_bf16, rows_bf16, to_dev
+from llm_hip import workloads
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+BT = 16
+
+
+def build(ctx, prefix, chunk, Hq, Hkv, window, seed, resident_from=None):
+    import torch
+
+    ctxlen = [p + c for p, c in zip(prefix, chunk)]
+    first = None if resident_from is None else [r // BT for r in resident_from]
+    batch = workloads.paged_batch(ctxlen, BT, 0.10, seed, first)
+    ids, sk = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 1, b, lo, hi, Hkv, D), Hkv, D)
+    _, sv = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, Hkv, D), Hkv, D)
+    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks)
+    ctx.write_blocks(pool, to_dev(ids), to_dev(sk), to_dev(sv))
+    starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
+    q = oracle.normal_bf16(seed + 3, int(starts[-1]) * Hq * D)
+    d_starts, d_lens, d_tab = to_dev(starts), to_dev(batch.seq_lens), to_dev(batch.tables)
+    desc = ctx.prefill_desc(d_starts, d_lens, d_tab, Hq, max(chunk), window, total_q_rows=int(starts[-1]))
+    d_q = to_dev(q)
+    d_out = torch.full((int(starts[-1]) * Hq * D,), 0x7FC0, dtype=torch.int16, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    ctx.paged_prefill(pool, desc, d_q, d_out, scale)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    return batch, pool, starts, q, from_dev_bf16(d_out), scale
+
+
+def decode_every_row(ctx, batch, pool, starts, prefix, chunk, q, Hq, window, scale):
+    """Each prefill row as one decode sequence of length pos + 1 sharing its parent's table."""
+    import torch
+
+    lens, tabs = [], []
+    for b in range(len(chunk)):
+        for i in range(chunk[b]):
+            lens.append(prefix[b] + i + 1)
+            tabs.append(batch.tables[b])
+    lens = np.array(lens, np.int32)
+    tabs = np.stack(tabs).astype(np.int32)
+    d_lens, d_tab = to_dev(lens), to_dev(tabs)
+    desc = ctx.decode_desc(d_lens, d_tab, Hq, int(lens.max()), window)
+    d_out = torch.empty(lens.size * Hq * D, dtype=torch.int16, device="cuda")
+    ctx.paged_decode(pool, desc, to_dev(q), d_out, scale)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0
+    return from_dev_bf16(d_out)
+
+
+def oracle_rows(pool, batch, starts, Hq, Hkv, window, q, scale, rows_per_seq):
+    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks, pool.raw())
+    out = np.zeros(int(starts[-1]) * Hq * D, np.float32)
+    picked = []
+    for b in range(batch.seq_lens.size):
+        for r in rows_per_seq[b]:
+            st = opool.prefill_rows(b, Hq, starts, batch.seq_lens, batch.tables, window, q, scale, r, r + 1, out,
+                                    threads=16)
+            assert st == oracle.OK
+            picked.append(int(starts[b]) + r)
+    return out.reshape(-1, Hq * D), picked
+
+
+def sample_rows(chunk):
+    base = {0, 1, 31, 32, 63, 64, 127, 128, 129, 255, 256, 383, 384, chunk - 2, chunk - 1}
+    return sorted(r for r in base if 0 <= r < chunk)
+
+
+@pytest.mark.parametrize("case", ["C3", "C4"])
+def test_prefill_baseline_configs(ctx, case):
+    if case == "C3":  # configs[2]: 8 x (1536 cached + 512 new), Hq32/Hkv4, causal in chunk
+        prefix, chunk, Hq, Hkv, W, res = [1536] * 8, [512] * 8, 32, 4, 0, None
+    else:  # configs[3] prefill: 4 x (31744 + 1024), window 4096, blocks before the window absent
+        prefix, chunk, Hq, Hkv, W = [31744] * 4, [1024] * 4, 16, 8, 4096
+        res = [31744 - W + 1] * 4
+    seed = workloads.SEED_BASE + (2 if case == "C3" else 3)
+    batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, W, seed, res)
+    ref, picked = oracle_rows(pool, batch, starts, Hq, Hkv, W, q, scale, [sample_rows(c) for c in chunk])
+    got = out.reshape(-1, Hq * D)
+    assert_parity(got[picked], ref[picked], what=f"{case} sampled rows vs oracle")
+    dec = decode_every_row(ctx, batch, pool, starts, prefix, chunk, q, Hq, W, scale)
+    assert_parity(out, oracle.bf16_to_f32(dec), what=f"{case} all rows vs decode kernel")
+
+
+@pytest.mark.parametrize("W", [0, 37, 200])
+def test_prefill_ragged_full_oracle(ctx, W):
+    prefix = [0, 17, 1000, 3, 64]
+    chunk = [1, 5, 130, 300, 64]
+    Hq, Hkv = 16, 8
+    batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, W, 50 + W)
+    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks, pool.raw())
+    st, ref = opool.prefill(Hq, starts, batch.seq_lens, batch.tables, W, q, scale, threads=16)
+    assert st == oracle.OK
+    assert_parity(out, ref, what=f"ragged W={W}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (32, 4), (16, 1)])
+def test_prefill_gqa_groups(ctx, Hq, Hkv):
+    prefix, chunk = [40, 0], [100, 129]
+    batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, 0, Hq + Hkv)
+    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks, pool.raw())
+    st, ref = opool.prefill(Hq, starts, batch.seq_lens, batch.tables, 0, q, scale, threads=16)
+    assert st == oracle.OK
+    assert_parity(out, ref, what=f"Hq={Hq} Hkv={Hkv}")
+
+
+def test_prefill_rejects_quantized_pool(ctx):
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_INT8, BT, 8, D, 4)
+    z = torch.zeros(2, dtype=torch.int32, device="cuda")
+    desc = ctx.prefill_desc(z, z[:1], z.view(1, 2), 16, 1, 0, total_q_rows=1)
+    with pytest.raises(llm_hip.LlhError) as e:
+        ctx.paged_prefill(pool, desc, torch.zeros(16 * D, dtype=torch.int16, device="cuda"),
+                          torch.zeros(16 * D, dtype=torch.int16, device="cuda"), 0.1)
+    assert e.value.status == llm_hip.ERR_UNSUPPORTED

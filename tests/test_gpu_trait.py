@@ -1,0 +1,234 @@
+"""The NativeMatvecBackend attention hooks over the device LayerKvCache mirror,
+on the reference's own test cases (tests/golden/known_answers.json).
+
+These read like the reference tests they come from: a LayerKvCache is built
+with append/append_sliding, then full_attention_cache_mix_f32_in_place runs
+on the GPU (the reference-order kernel) and is compared with the closed form
+or with reference_attention, at the reference's tolerances (1e-4 for exact
+inputs, 1e-2 for the 257-row f16-mirror case, 3e-2 for int8).  K/V are stored
+as bf16 (or int8 with fp16 per (token, head) scales), so inputs that are not
+exact in bf16 use the reference's mirror tolerances.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import llm_hip
+import oracle
+from llm_hip import HipNativeMatvecBackend, LayerKvCache
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KA = json.load(open(os.path.join(HERE, "golden", "known_answers.json")))
+
+
+def mix(ctx, cache, query, row_count, hq, hkv, d, scale):
+    out = np.zeros(hq * d, np.float32)
+    handled = HipNativeMatvecBackend(ctx).full_attention_cache_mix_f32_in_place(cache, query, row_count, hq, hkv, d,
+                                                                                scale, out)
+    assert handled
+    return out
+
+
+def test_full_attention_cache_mix_matches_reference_values(ctx):
+    c = KA["two_head_closed_form"]
+    cache = LayerKvCache.new(ctx, 8, 1, 2)
+    keys = np.array(c["keys"], np.float32).reshape(2, 2)
+    vals = np.array(c["values"], np.float32).reshape(2, 2)
+    for k, v in zip(keys, vals):
+        cache.append_sliding(k, v)
+    out = mix(ctx, cache, c["query"], 2, 2, 1, 2, 1.0)
+    assert np.max(np.abs(out - np.array(c["expected"]))) < c["tolerance"]
+
+
+def test_full_attention_cache_mix_int8_matches_reference_values(ctx):
+    """primitives/tests.rs:413-466 with the device int8 layout (fp16 scale per (token, head))."""
+    c = KA["int8_closed_form"]
+    cache = LayerKvCache.new_with_config(ctx, 8, 1, 2, llm_hip.KV_INT8)
+    cache.append_sliding([1.0, 0.0], [10.0, 0.0])
+    cache.append_sliding([0.0, 1.0], [0.0, 10.0])
+    out = mix(ctx, cache, c["query"], 2, 2, 1, 2, 1.0)
+    # |error| <= 10 * (f16 rounding of 10/127) ~ 5e-3; the reference's f32 scales give 1e-4
+    assert np.max(np.abs(out - np.array(c["expected"]))) < 1e-2
+
+
+def test_sequence_is_causal(ctx):
+    c = KA["causal_sequence"]
+    cache = LayerKvCache.new(ctx, 8, 1, 1)
+    outs = []
+    backend = HipNativeMatvecBackend(ctx)
+    for q, k, v in zip(c["queries"], c["keys"], c["values"]):
+        backend.append_kv_cache_sliding_f32(cache, k, v)
+        outs.append(mix(ctx, cache, q, cache.token_count(), 1, 1, 1, c["scale"])[0])
+    assert abs(outs[0] - c["expected_first"]) < 1e-5
+    assert outs[1] > c["second_greater_than"] and abs(outs[1] - c["second_closed_form"]) < 1e-4
+
+
+def test_uses_caller_score_scale(ctx):
+    c = KA["score_scale"]
+    cache = LayerKvCache.new(ctx, 8, 1, 1)
+    for k, v in zip(c["keys"], c["values"]):
+        cache.append_sliding(k, v)
+    assert abs(mix(ctx, cache, [1.0], 2, 1, 1, 1, 0.0)[0] - c["scale_zero_second"]) < 1e-4
+    assert mix(ctx, cache, [1.0], 2, 1, 1, 1, 1.0)[0] > c["scale_one_second_greater_than"]
+
+
+def test_cache_sequence_reads_first_source_rows(ctx):
+    c = KA["source_counts"]
+    cache = LayerKvCache.new(ctx, 8, 1, 1)
+    for k, v in zip(c["cache_keys"], c["cache_values"]):
+        cache.append_sliding(k, v)
+    first = mix(ctx, cache, c["queries"][0], c["source_counts"][0], 1, 1, 1, c["scale"])[0]
+    second = mix(ctx, cache, c["queries"][1], c["source_counts"][1], 1, 1, 1, c["scale"])[0]
+    assert cache.token_count() == 2
+    assert abs(first - c["expected_first"]) < 1e-5 and second > c["second_greater_than"]
+
+
+def test_small_cache_uses_sliding_window(ctx):
+    c = KA["sliding_window_two"]
+    cache = LayerKvCache.new(ctx, c["max_tokens"], 1, 2)
+    out = None
+    for v in c["values"]:
+        cache.append_sliding([1.0, 0.0], v)
+        out = mix(ctx, cache, [math.sqrt(2.0), 0.0], cache.token_count(), 1, 1, 2, 1.0 / math.sqrt(2.0))
+    assert cache.token_count() == 2
+    assert np.array_equal(cache.values(), np.ravel(c["expected_ring_values"]).astype(np.float32))
+    assert np.max(np.abs(out - np.array(c["expected_attention"]))) < 1e-6
+    assert np.max(np.abs(out * 0.5 - np.array(c["expected_after_gate"]))) < 1e-6
+
+
+@pytest.mark.parametrize("fmt,tol", [(llm_hip.KV_BF16, "tolerance_f16_mirror"), (llm_hip.KV_INT8, "tolerance_int8")])
+def test_block_mirror_attention_matches_cpu_reference_across_blocks(ctx, fmt, tol):
+    """native_matvec.rs:2065-2184: 257 rows span two device blocks."""
+    c = KA["cross_block_257_rows"]
+    n = c["row_count"]
+    cache = LayerKvCache.new_with_config(ctx, n, 1, 2, fmt)
+    keys = np.array([[t / n, 1.0 - t / (n * 2.0)] for t in range(n)], np.float32)
+    vals = np.array([[(t % 7) - 3.0, (t % 11) * 0.25 - 1.0] for t in range(n)], np.float32)
+    for k, v in zip(keys, vals):
+        cache.append(k, v)
+    assert len(cache.active_blocks()) >= 2
+    out = mix(ctx, cache, c["query"], n, 1, 1, 2, c["scale"])
+    q = np.array(c["query"], np.float32)
+    s = (q[0] * keys[:, 0] + q[1] * keys[:, 1]) * np.float32(c["scale"])
+    w = np.exp(s - s.max())
+    ref = (w[:, None] * vals).sum(0) / w.sum()
+    assert np.max(np.abs(out - ref)) < c[tol]
+
+
+def test_active_blocks_after_sliding_wrap(ctx):
+    c = KA["active_blocks_after_wrap"]
+    cache = LayerKvCache.new(ctx, c["max_tokens"], 1, 1)
+    for k, v in zip(c["keys"], c["values"]):
+        cache.append_sliding(k, v)
+    assert list(cache.keys()) == c["expected_keys"]
+    runs = cache.active_blocks()
+    assert [(r["logical_token_start"], r["physical_token_start"], r["token_count"]) for r in runs] == \
+           [(e["logical_token_start"], e["physical_token_start"], e["token_count"]) for e in c["expected_runs"]]
+
+
+@pytest.mark.parametrize("max_tokens", [1, 5, 16, 33, 50])
+def test_ring_state_and_runs_follow_the_reference(ctx, max_tokens):
+    """Random-length append_sliding sequences: keys(), token_count, next_position,
+    window start and active runs equal the oracle's LayerKvCache restatement."""
+    rng = np.random.default_rng(max_tokens)
+    cache = LayerKvCache.new(ctx, max_tokens, 2, 4)
+    ring = oracle.Ring(max_tokens, 8, 16)
+    for n in range(int(rng.integers(1, 3 * max_tokens + 4))):
+        k = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal(8).astype(np.float32)))
+        v = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal(8).astype(np.float32)))
+        cache.append_sliding(k, v)
+        ring.append_sliding(k, v)
+    s = cache.state()
+    assert (s.token_count, s.tokens_seen, s.window_start) == (ring.token_count, ring.tokens_seen, ring.window_start)
+    assert np.array_equal(cache.keys(), ring.logical_rows(0))
+    assert np.array_equal(cache.values(), ring.logical_rows(1))
+    got = [(r["block_index"], r["logical_token_start"], r["physical_token_start"], r["block_token_start"],
+            r["token_count"]) for r in cache.active_blocks()]
+    assert got == ring.active_runs()
+    ids = cache.block_ids()
+    assert all(r["block_id"] == ids[r["block_index"]] for r in cache.active_blocks())
+
+
+def test_clone_write_forks_block_identity(ctx):
+    """int8_cache_format.rs:62-135: writing through a clone forks block identity;
+    the original's rows are untouched."""
+    cache = LayerKvCache.new_with_config(ctx, 2, 1, 2, llm_hip.KV_INT8)
+    cache.append_sliding([1.0, 2.0], [0.5, 1.0])
+    prefix_id = cache.block_ids()[0]
+    cache.append_sliding([3.0, 4.0], [1.5, 2.0])
+    cache.append_sliding([5.0, 6.0], [2.5, 3.0])
+    assert np.max(np.abs(cache.values() - np.array([1.5, 2.0, 2.5, 3.0], np.float32))) < 0.03
+    clone = cache.clone()
+    assert clone.id() != cache.id()
+    assert np.array_equal(clone.keys(), cache.keys())
+    clone.append_sliding([7.0, 8.0], [3.5, 4.0])
+    assert clone.block_ids()[0] != cache.block_ids()[0]
+    assert clone.block_ids()[0] != prefix_id
+    assert np.max(np.abs(cache.keys() - np.array([3.0, 4.0, 5.0, 6.0], np.float32))) < 0.03
+    assert np.max(np.abs(clone.keys() - np.array([5.0, 6.0, 7.0, 8.0], np.float32))) < 0.05
+    # the original now owns its block alone: writing keeps its identity
+    before = cache.block_ids()[0]
+    cache.append_sliding([9.0, 9.0], [9.0, 9.0])
+    assert cache.block_ids()[0] == before
+
+
+def test_errors_follow_the_reference(ctx):
+    backend = HipNativeMatvecBackend(ctx)
+    cache = LayerKvCache.new(ctx, 2, 1, 2)
+    with pytest.raises(llm_hip.LlhError) as e:
+        cache.append_sliding([1.0], [1.0])  # wrong row length
+    assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+    cache.append([1.0, 0.0], [1.0, 1.0])
+    cache.append([0.0, 1.0], [2.0, 2.0])
+    with pytest.raises(llm_hip.LlhError) as e:
+        cache.append([0.0, 1.0], [2.0, 2.0])  # strict append on a full cache
+    assert e.value.status == llm_hip.ERR_CAPACITY
+    out = np.zeros(2, np.float32)
+    with pytest.raises(llm_hip.LlhError) as e:
+        backend.full_attention_cache_mix_f32_in_place(cache, [1.0, 0.0], 3, 1, 1, 2, 1.0, out)  # rows > tokens
+    assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+    with pytest.raises(llm_hip.LlhError):
+        backend.full_attention_cache_mix_f32_in_place(cache, [1.0, 0.0], 2, 1, 1, 2, 1.0, np.zeros(1, np.float32))
+    with pytest.raises(llm_hip.LlhError):
+        backend.full_attention_cache_mix_f32_in_place(cache, [1.0, 0.0, 1.0, 0.0], 2, 2, 2, 2, 1.0,
+                                                      np.zeros(4, np.float32))  # kv heads != cache
+    assert np.all(mix(ctx, cache, [1.0, 0.0], 0, 1, 1, 2, 1.0) == 0.0)  # no rows -> zero output
+    q8 = LayerKvCache.new_with_config(ctx, 2, 1, 2, llm_hip.KV_INT8)
+    with pytest.raises(llm_hip.LlhError) as e:
+        q8.append_sliding([float("nan"), 0.0], [1.0, 1.0])
+    assert e.value.status == llm_hip.ERR_NON_FINITE
+    with pytest.raises(llm_hip.LlhError) as e:
+        LayerKvCache.new(ctx, 0, 1, 2)
+    assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+    with pytest.raises(llm_hip.LlhError) as e:
+        LayerKvCache.new_with_config(ctx, 4, 1, 2, llm_hip.KV_FP8_E4M3)
+    assert e.value.status == llm_hip.ERR_UNSUPPORTED
+
+
+def test_non_finite_scores_are_an_error(ctx):
+    """softmax_f32's "scores must be finite" (math.rs:485-489) surfaces as ERR_NON_FINITE."""
+    cache = LayerKvCache.new(ctx, 4, 1, 1)
+    cache.append_sliding([1e30], [1.0])
+    out = np.zeros(1, np.float32)
+    with pytest.raises(llm_hip.LlhError) as e:
+        HipNativeMatvecBackend(ctx).full_attention_cache_mix_f32_in_place(cache, [1e30], 1, 1, 1, 1, 1.0, out)
+    assert e.value.status == llm_hip.ERR_NON_FINITE
+
+
+def test_select_head_rows_and_revision(ctx):
+    cache = LayerKvCache.new(ctx, 3, 2, 2)
+    rows = [[1.0, 2.0, 3.0, 4.0], [5.0, 6.0, 7.0, 8.0], [9.0, 10.0, 11.0, 12.0], [13.0, 14.0, 15.0, 16.0]]
+    for i, r in enumerate(rows):
+        cache.append_sliding(r, [-x for x in r])
+        assert cache.revision() == i + 1 and cache.next_position() == i + 1
+    sel = HipNativeMatvecBackend(ctx).select_kv_cache_head_rows_f32(cache, 0, 3, 2, 2)
+    assert list(sel) == [7.0, 8.0, 11.0, 12.0, 15.0, 16.0]
+    sel = HipNativeMatvecBackend(ctx).select_kv_cache_head_rows_f32(cache, 1, 2, 0, 2)
+    assert list(sel) == [-5.0, -6.0, -9.0, -10.0]
+    cache.clear()
+    assert cache.token_count() == 0 and cache.next_position() == 0 and cache.revision() == 5
