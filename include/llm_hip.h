@@ -156,7 +156,7 @@ typedef struct llh_decode_desc {
   int32_t max_blocks_per_seq; /* row stride of d_block_tables */
   int32_t max_seq_len;        /* host-known bound on d_seq_lens (sizes the grid) */
   int32_t window;             /* 0 = full attention; else attend [max(0, len - window), len) */
-  int32_t reserved;
+  int32_t total_tokens_hint;  /* host-known sum of attended tokens (sizes split-K); 0 = unknown */
   const int32_t *d_seq_lens;     /* [num_seqs] tokens incl. the new one (appended first, native_attention.rs:307-309) */
   const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] pool block indices */
 } llh_decode_desc;

@@ -42,23 +42,36 @@ int env_int(const char *name, int dflt) {
 }
 
 // Split-K sizing for the tuned decode kernel.  `est_blocks` bounds the blocks
-// any sequence attends.  Splits of 4..32 blocks keep the grid at roughly 4096
-// workgroups so every CU gets several.
+// any one sequence attends (it sizes the grid and the partial buffer).  The
+// split size is the power of two in [4, 256] that brings the number of
+// non-empty workgroups closest to ~4096 (16 per CU on 256 CUs), measured best
+// on MI355X for both short bf16 and long int8 contexts.  The total work comes
+// from the caller's hint when given, else from the max_seq_len bound.
 struct SplitPlan {
   int split_blocks;
   int max_splits;
   int est_blocks;
 };
 
-SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window) {
+SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, int total_tokens_hint) {
   int span = max_seq_len;
   if (window > 0) span = std::min(span, window);
   const int est_blocks = (span + kFastBlockTokens - 1) / kFastBlockTokens + 1;
   int split = env_int("LLH_DECODE_SPLIT_BLOCKS", 0);
   if (split <= 0) {
-    const long long work = (long long)num_seqs * kv_heads * est_blocks;
+    long long blocks = (long long)num_seqs * est_blocks;
+    if (total_tokens_hint > 0) blocks = (long long)total_tokens_hint / kFastBlockTokens + num_seqs;
+    const double target = 4096.0;
+    double best = 1e30;
     split = 4;
-    while (split < 32 && work / (split * 2) >= 4096) split *= 2;
+    for (int s = 4; s <= 256; s *= 2) {
+      const double wgs = (double)kv_heads * (double)(blocks + (long long)num_seqs * (s / 2)) / s;
+      const double cost = wgs > target ? wgs / target : target / wgs;
+      if (cost < best) {
+        best = cost;
+        split = s;
+      }
+    }
   }
   split = std::min(std::max(split, 4), 256);  // a wavefront reads its table entries from <= 64 lanes
   SplitPlan p;
@@ -345,7 +358,8 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   hipStream_t s = static_cast<hipStream_t>(stream);
   ctx->decode_calls++;
   if (fast) {
-    const SplitPlan plan = plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window);
+    const SplitPlan plan =
+        plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint);
     const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
     const size_t ml_off = kCounterBytes;
     const size_t o_off = ml_off + align_up(rows * sizeof(float2));
@@ -368,6 +382,7 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     a.window = desc->window;
     a.split_blocks = plan.split_blocks;
     a.max_splits = plan.max_splits;
+    a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
     a.scale_log2e = score_scale * 1.4426950408889634f;
     hipError_t e = launch_decode(a, group, desc->max_seq_len, s);
     if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");

@@ -6,18 +6,21 @@
 // crates/llm-backend/src/core/native_attention.rs:731-771, with the window rule
 // of crates/llm-backend/src/core/qwen/ops/cache.rs:116-121).
 //
-// Tuned path (head_dim 128, 16-token blocks), two launches:
-//   1. paged_decode_kernel: one workgroup per (split, kv head, sequence).  A
-//      split is `split_blocks` consecutive blocks of the attended range; the
-//      four wavefronts take its blocks round-robin, double-buffering the loads
-//      of the next block behind the math of the current one.  Every K/V byte of
-//      the kv head is read once and serves all G = Hq/Hkv query heads.  A
-//      single-split sequence writes its output directly; otherwise each split
-//      writes (max, sum, unnormalised output) partials.
-//   2. decode_merge_kernel: log-sum-exp merge of the partials.
-// The launch boundary makes the partials visible to the merge: no device-scope
-// fence runs inside a workgroup (on gfx950 such a fence writes back and
-// invalidates the whole L2 of the XCD, and those serialise).
+// Tuned path (head_dim 128, 16-token blocks): paged_decode_kernel, one
+// workgroup per (split, kv head, sequence).  A split is `split_blocks`
+// consecutive blocks of the attended range; the four wavefronts take its blocks
+// round-robin, double-buffering the loads of the next block behind the math of
+// the current one.  Every K/V byte of the kv head is read once and serves all
+// G = Hq/Hkv query heads.  A single-split sequence writes its output directly;
+// otherwise each split writes (max, sum, unnormalised output) partials that a
+// second launch (decode_merge_kernel) merges by log-sum-exp.  With fused_merge
+// set, the last workgroup of the (sequence, kv head) to arrive merges instead:
+// partials then cross XCDs (each has its own L2) through agent-scope atomic
+// stores and loads, which the compiler makes coherent per access, with no
+// device-scope fence (on gfx950 such a fence writes back and invalidates the
+// whole L2 of the XCD, and those serialise across workgroups).  Measured on
+// MI355X the second launch is faster: the fused variant makes every
+// workgroup wait for its write-through stores before it can retire.
 // The path is HBM-bound and uses no MFMA.
 //
 // Lane roles inside a wavefront, per 16-token block (K: token rows, V: dim rows):
@@ -144,42 +147,75 @@ template <int G>
 struct SoftmaxState {
   float m[G];
   float l[G];
-  float wsum[G];  // int8 only: running sum of p * value scale (offset-128 correction)
   float o[G][8];
 };
 
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // round to nearest even
+}
+
+// Two signed int8 codes (bytes b, b+1 of w) as a packed bf16 pair (exact).
+__device__ __forceinline__ uint32_t i8x2_to_bf16(uint32_t w, int b) {
+  return pack_bf16((float)(int8_t)(w >> (8 * b)), (float)(int8_t)(w >> (8 * b + 8)));
+}
+
+// Two OCP e4m3 codes (bytes 2*HI, 2*HI+1 of w) as a packed bf16 pair (exact).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
+// The V elements of dim 16j + c for tokens 4g..4g+3 as two packed bf16 pairs:
+// (token 0, token 1) and (token 2, token 3); masked tokens are zero.
+template <int FMT>
+__device__ __forceinline__ void v_pairs(const BlockRegs<FMT> &r, const uint32_t (&vmask)[2], int j, uint32_t &p01,
+                                        uint32_t &p23) {
+  if constexpr (FMT == kBf16) {
+    p01 = r.v[j].x & vmask[0];
+    p23 = r.v[j].y & vmask[1];
+  } else if constexpr (FMT == kInt8) {
+    const uint32_t w = r.v[j] & vmask[0];
+    p01 = i8x2_to_bf16(w, 0);
+    p23 = i8x2_to_bf16(w, 2);
+  } else {
+    const uint32_t w = r.v[j] & vmask[0];
+    p01 = fp8x2_to_bf16<false>(w);
+    p23 = fp8x2_to_bf16<true>(w);
+  }
+}
+
+// One 16-token block for the G query heads of this wavefront's kv head.
+// q . k and p . v both run on packed bf16 dot2 with fp32 accumulation: K, V and
+// q are exact in bf16 (int8 and e4m3 codes convert exactly); the softmax
+// weights p (times the value scale for int8/fp8) are rounded to bf16 for the
+// p . v products, the softmax denominator sums them in fp32.
 template <int G, int FMT>
 __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
-                                              int lane, const uint32_t (&qw)[G][4], const float (&qf)[G][16],
-                                              const float (&qsum)[G], SoftmaxState<G> &st) {
+                                              int lane, const uint32_t (&qw)[G][8], SoftmaxState<G> &st) {
   if (!r.valid) {
     if (lane == 0) atomicOr(a.err, kErrBadBlock);
     return;
   }
   const int g = lane >> 4;
-  const int pos0 = jb * BT + 4 * g;
   const bool partial = (jb * BT < lo) || (jb * BT + BT > len);
-  bool ok[4];
+  bool ok[4] = {true, true, true, true};
+  uint32_t vmask[2] = {0xffffffffu, 0xffffffffu};  // zero V of tokens outside [lo, len) (slots may hold garbage)
+  if (partial) {
+    const int pos0 = jb * BT + 4 * g;
 #pragma unroll
-  for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len);
+    for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len);
+    if constexpr (FMT == kBf16) {
+      vmask[0] = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
+      vmask[1] = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
+    } else {
+      vmask[0] = (ok[0] ? 0xffu : 0u) | (ok[1] ? 0xff00u : 0u) | (ok[2] ? 0xff0000u : 0u) | (ok[3] ? 0xff000000u : 0u);
+    }
+  }
 
   float s[G][4];
-  float vf[8][4];  // V values of dims 16j + c, tokens 4g .. 4g+3
   float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
 
   if constexpr (FMT == kBf16) {
-    uint2 vr[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) vr[j] = r.v[j];
-    if (partial) {
-      const uint32_t mx = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
-      const uint32_t my = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        vr[j].x &= mx;
-        vr[j].y &= my;
-      }
-    }
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
 #pragma unroll
@@ -191,27 +227,11 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
         s[gi][i] = row_sum16(acc) * a.scale_log2e;
       }
     }
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      vf[j][0] = bf16_lo(vr[j].x);
-      vf[j][1] = bf16_hi(vr[j].x);
-      vf[j][2] = bf16_lo(vr[j].y);
-      vf[j][3] = bf16_hi(vr[j].y);
-    }
   } else {
     // int8 / fp8: K token rows of 128 bytes; lane (g, half hf, c8) holds tokens
     // 4g + 2i + hf (i = 0, 1) at dims 16*c8 .. +16.  V dim rows of 16 bytes;
     // lane holds the 4 bytes of tokens 4g..4g+3 for dims 16j + c.
     const int hf = (lane >> 3) & 1;
-    uint32_t vr[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) vr[j] = r.v[j];
-    if (partial) {
-      const uint32_t mk = (ok[0] ? 0xffu : 0u) | (ok[1] ? 0xff00u : 0u) | (ok[2] ? 0xff0000u : 0u) |
-                          (ok[3] ? 0xff000000u : 0u);
-#pragma unroll
-      for (int j = 0; j < 8; j++) vr[j] &= mk;
-    }
     float kscale_own[2];
     if constexpr (FMT == kInt8) {
       const float k4[4] = {f16_bits_to_f32(r.ks.x & 0xffffu), f16_bits_to_f32(r.ks.x >> 16),
@@ -220,60 +240,43 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
       vsc[1] = f16_bits_to_f32(r.vs.x >> 16);
       vsc[2] = f16_bits_to_f32(r.vs.y & 0xffffu);
       vsc[3] = f16_bits_to_f32(r.vs.y >> 16);
-      kscale_own[0] = hf ? k4[1] : k4[0];
-      kscale_own[1] = hf ? k4[3] : k4[2];
-      // codes as unsigned bytes u = code + 128 (xor 0x80); f32(u) is one convert
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint32_t u = vr[j] ^ 0x80808080u;
-#pragma unroll
-        for (int i = 0; i < 4; i++) vf[j][i] = (float)((u >> (8 * i)) & 0xffu);
-      }
+      kscale_own[0] = (hf ? k4[1] : k4[0]) * a.scale_log2e;
+      kscale_own[1] = (hf ? k4[3] : k4[2]) * a.scale_log2e;
     } else {
-      kscale_own[0] = r.ksb;
-      kscale_own[1] = r.ksb;
+      kscale_own[0] = kscale_own[1] = r.ksb * a.scale_log2e;
       vsc[0] = vsc[1] = vsc[2] = vsc[3] = r.vsb;
+    }
+    float own[G][2];
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], false);
-        const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(vr[j], true);
-        vf[j][0] = lo2[0];
-        vf[j][1] = lo2[1];
-        vf[j][2] = hi2[0];
-        vf[j][3] = hi2[1];
+    for (int i = 0; i < 2; i++) {
+      const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
+      uint32_t kp[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if constexpr (FMT == kInt8) {
+          kp[2 * k] = i8x2_to_bf16(w[k], 0);
+          kp[2 * k + 1] = i8x2_to_bf16(w[k], 2);
+        } else {
+          kp[2 * k] = fp8x2_to_bf16<false>(w[k]);
+          kp[2 * k + 1] = fp8x2_to_bf16<true>(w[k]);
+        }
+      }
+#pragma unroll
+      for (int gi = 0; gi < G; gi++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
+        own[gi][i] = row_sum8(acc) * kscale_own[i];
       }
     }
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-      float own[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          if constexpr (FMT == kInt8) {
-            const uint32_t u = w[k] ^ 0x80808080u;
-#pragma unroll
-            for (int n = 0; n < 4; n++) acc += qf[gi][4 * k + n] * (float)((u >> (8 * n)) & 0xffu);
-          } else {
-            const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
-            const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
-            acc += qf[gi][4 * k + 0] * lo2[0];
-            acc += qf[gi][4 * k + 1] * lo2[1];
-            acc += qf[gi][4 * k + 2] * hi2[0];
-            acc += qf[gi][4 * k + 3] * hi2[1];
-          }
-        }
-        if constexpr (FMT == kInt8) acc -= 128.0f * qsum[gi];
-        own[i] = row_sum8(acc) * kscale_own[i] * a.scale_log2e;
-      }
-      const float oth0 = dpp<0x140>(own[0]);  // row_mirror swaps the two 8-lane halves
-      const float oth1 = dpp<0x140>(own[1]);
-      s[gi][0] = hf ? oth0 : own[0];
-      s[gi][1] = hf ? own[0] : oth0;
-      s[gi][2] = hf ? oth1 : own[1];
-      s[gi][3] = hf ? own[1] : oth1;
+      const float oth0 = dpp<0x140>(own[gi][0]);  // row_mirror swaps the two 8-lane halves
+      const float oth1 = dpp<0x140>(own[gi][1]);
+      s[gi][0] = hf ? oth0 : own[gi][0];
+      s[gi][1] = hf ? own[gi][0] : oth0;
+      s[gi][2] = hf ? oth1 : own[gi][1];
+      s[gi][3] = hf ? own[gi][1] : oth1;
     }
   }
 
@@ -285,31 +288,47 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
         if (!ok[i]) s[gi][i] = -INFINITY;
   }
 
+  // online softmax per head: running max (log2 units), sum, bf16 weights for V
+  float alpha[G];
+  uint32_t w01[G], w23[G];
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
     float mx = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
     mx = fmaxf(mx, st.m[gi]);
     const float mref = (mx == -INFINITY) ? 0.0f : mx;
-    const float alpha = fast_exp2(st.m[gi] - mref);
+    alpha[gi] = fast_exp2(st.m[gi] - mref);
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
-    st.l[gi] = st.l[gi] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    st.l[gi] = st.l[gi] * alpha[gi] + ((p[0] + p[1]) + (p[2] + p[3]));
     st.m[gi] = mx;
-    float w[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) w[i] = (FMT == kBf16) ? p[i] : (ok[i] ? p[i] * vsc[i] : 0.0f);
-    if constexpr (FMT == kInt8) st.wsum[gi] = st.wsum[gi] * alpha + ((w[0] + w[1]) + (w[2] + w[3]));
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      float acc = st.o[gi][j] * alpha;
-      acc += w[0] * vf[j][0];
-      acc += w[1] * vf[j][1];
-      acc += w[2] * vf[j][2];
-      acc += w[3] * vf[j][3];
-      st.o[gi][j] = acc;
+    if constexpr (FMT == kBf16) {
+      w01[gi] = pack_bf16(p[0], p[1]);
+      w23[gi] = pack_bf16(p[2], p[3]);
+    } else {
+      w01[gi] = pack_bf16(ok[0] ? p[0] * vsc[0] : 0.0f, ok[1] ? p[1] * vsc[1] : 0.0f);
+      w23[gi] = pack_bf16(ok[2] ? p[2] * vsc[2] : 0.0f, ok[3] ? p[3] * vsc[3] : 0.0f);
     }
   }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    uint32_t v01, v23;
+    v_pairs<FMT>(r, vmask, j, v01, v23);
+#pragma unroll
+    for (int gi = 0; gi < G; gi++)
+      st.o[gi][j] = dot2_bf16(v23, w23[gi], dot2_bf16(v01, w01[gi], st.o[gi][j] * alpha[gi]));
+  }
+}
+
+// Blocks in flight per wavefront (register budget: one bf16 block is 32 VGPRs).
+constexpr int pipeline_stages(int G, int FMT) {
+#ifdef LLH_DECODE_STAGES
+  return LLH_DECODE_STAGES;
+#else
+  // measured on MI355X (C2 bf16, C5 int8/fp8): 2 and 3 stages tie, 4 and more lose
+  // occupancy (2 waves per SIMD) and run 20-40% slower
+  return (void)G, (void)FMT, 2;
+#endif
 }
 
 __device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, int &lo, int &first_blk, int &n_blk,
@@ -353,39 +372,28 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
   const int my_entry = lane < nbw ? table[(blk_begin + wave + 4 * lane) % a.max_blocks] : -1;
 
-  // ---- query ----
-  uint32_t qw[G][4];  // bf16 pairs, dims 8c..8c+7 (bf16 K path)
-  float qf[G][16];    // f32 dims 16*(lane&7) .. +16 (int8/fp8 K path)
-  float qsum[G];
-  if constexpr (FMT == kBf16) {
+  // ---- query: packed bf16 pairs (bf16 K: dims 8c..8c+7; int8/fp8 K: dims 16*(lane&7)..+16) ----
+  uint32_t qw[G][8];
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) {
+  for (int gi = 0; gi < G; gi++) {
+    if constexpr (FMT == kBf16) {
       const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c * 8);
       qw[gi][0] = t.x;
       qw[gi][1] = t.y;
       qw[gi][2] = t.z;
       qw[gi][3] = t.w;
-      qsum[gi] = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 16; k++) qf[gi][k] = 0.0f;
-    }
-  } else {
-    const int c8 = lane & 7;
-#pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c8 * 16);
+      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
+    } else {
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 7) * 16);
       const uint4 t0 = src[0], t1 = src[1];
-      const uint32_t w[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
-      float s = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        qf[gi][2 * k] = bf16_lo(w[k]);
-        qf[gi][2 * k + 1] = bf16_hi(w[k]);
-        s += qf[gi][2 * k] + qf[gi][2 * k + 1];
-      }
-      qsum[gi] = s;
-#pragma unroll
-      for (int k = 0; k < 4; k++) qw[gi][k] = 0u;
+      qw[gi][0] = t0.x;
+      qw[gi][1] = t0.y;
+      qw[gi][2] = t0.z;
+      qw[gi][3] = t0.w;
+      qw[gi][4] = t1.x;
+      qw[gi][5] = t1.y;
+      qw[gi][6] = t1.z;
+      qw[gi][7] = t1.w;
     }
   }
 
@@ -394,20 +402,25 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   for (int gi = 0; gi < G; gi++) {
     st.m[gi] = -INFINITY;
     st.l[gi] = 0.0f;
-    st.wsum[gi] = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
   }
 
-  // ---- double-buffered block loop: loads of block k+1 overlap the math of block k ----
-  BlockRegs<FMT> ra, rb;
-  if (nbw > 0) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, 0), kvh, lane, ra);
-  for (int k = 0; k < nbw; k += 2) {
-    if (k + 1 < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, k + 1), kvh, lane, rb);
-    compute_block<G, FMT>(a, ra, blk_begin + wave + 4 * k, lo, len, lane, qw, qf, qsum, st);
-    if (k + 1 < nbw) {
-      if (k + 2 < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, k + 2), kvh, lane, ra);
-      compute_block<G, FMT>(a, rb, blk_begin + wave + 4 * (k + 1), lo, len, lane, qw, qf, qsum, st);
+  // ---- block pipeline: loads run STAGES-1 blocks ahead of the math ----
+  constexpr int STAGES = pipeline_stages(G, FMT);
+  BlockRegs<FMT> r[STAGES];
+#pragma unroll
+  for (int sidx = 0; sidx < STAGES - 1; sidx++)
+    if (sidx < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, sidx), kvh, lane, r[sidx]);
+  for (int k0 = 0; k0 < nbw; k0 += STAGES) {
+#pragma unroll
+    for (int sidx = 0; sidx < STAGES; sidx++) {
+      const int k = k0 + sidx;
+      if (k < nbw) {
+        const int kn = k + STAGES - 1;
+        if (kn < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, kn), kvh, lane, r[(sidx + STAGES - 1) % STAGES]);
+        compute_block<G, FMT>(a, r[sidx], blk_begin + wave + 4 * k, lo, len, lane, qw, st);
+      }
     }
   }
 
@@ -417,10 +430,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   __shared__ float s_l[4][G];
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    if constexpr (FMT == kInt8) {
-#pragma unroll
-      for (int j = 0; j < 8; j++) st.o[gi][j] -= 128.0f * st.wsum[gi];
-    }
     float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
     mm = fmaxf(mm, __shfl_xor(mm, 32));
     const float mref = (mm == -INFINITY) ? 0.0f : mm;
@@ -447,6 +456,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   __syncthreads();
 
   // ---- merge the four wavefronts; write the output or this split's partial ----
+  const bool fused = a.fused_merge != 0;
   for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
     const int gi = idx / D;
     const int d = idx % D;
@@ -463,9 +473,71 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
     } else {
       const size_t row = (qrow0 + gi) * a.max_splits + split;
-      a.ws_o[row * D + d] = oo;
-      if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
+      if (fused) {
+        // agent-scope atomic stores: coherent across XCDs without any L2 writeback
+        __hip_atomic_store(&a.ws_o[row * D + d], oo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+          const uint64_t ml = (uint64_t)__float_as_uint(mm) | ((uint64_t)__float_as_uint(ll) << 32);
+          __hip_atomic_store(reinterpret_cast<uint64_t *>(&a.ws_ml[row]), ml, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        a.ws_o[row * D + d] = oo;
+        if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
+      }
     }
+  }
+  if (n_splits == 1 || !fused) return;
+
+  // ---- the last workgroup of this (sequence, kv head) to arrive merges the splits ----
+  // Every wave waits until its partial stores have completed, the barrier
+  // collects the waves, then one lane counts the arrival (agent-scope atomic).
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int s_last;
+  __syncthreads();
+  int32_t *counter = &a.counters[(size_t)b * a.pool.kv_heads + kvh];
+  if (tid == 0) s_last = atomicAdd(counter, 1) == n_splits - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
+    const int gi = idx / D;
+    const int d = idx % D;
+    const size_t row0 = (qrow0 + gi) * a.max_splits;
+    float m_sp[8], l_sp[8], o_sp[8];
+    float mm = -INFINITY, ll = 0.0f, oo = 0.0f;
+    for (int sp0 = 0; sp0 < n_splits; sp0 += 8) {
+      const int cnt = min(8, n_splits - sp0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        if (i < cnt) {
+          const uint64_t ml = __hip_atomic_load(reinterpret_cast<const uint64_t *>(&a.ws_ml[row0 + sp0 + i]),
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          m_sp[i] = __uint_as_float((uint32_t)ml);
+          l_sp[i] = __uint_as_float((uint32_t)(ml >> 32));
+          o_sp[i] = __hip_atomic_load(&a.ws_o[(row0 + sp0 + i) * D + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          m_sp[i] = -INFINITY;
+          l_sp[i] = 0.0f;
+          o_sp[i] = 0.0f;
+        }
+      }
+      float cm = mm;
+#pragma unroll
+      for (int i = 0; i < 8; i++) cm = fmaxf(cm, m_sp[i]);
+      const float mref = (cm == -INFINITY) ? 0.0f : cm;
+      const float f0 = fast_exp2(mm - mref);
+      ll *= f0;
+      oo *= f0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float f = fast_exp2(m_sp[i] - mref);
+        ll += l_sp[i] * f;
+        oo += o_sp[i] * f;
+      }
+      mm = cm;
+    }
+    a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
   }
 }
 
@@ -479,15 +551,30 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   if (n_splits <= 1 || n_splits > a.max_splits) return;
   const int d = threadIdx.x;
   const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
-  float mm = -INFINITY;
-  for (int sp = 0; sp < n_splits; sp++) mm = fmaxf(mm, a.ws_ml[row0 + sp].x);
-  const float mref = (mm == -INFINITY) ? 0.0f : mm;
-  float ll = 0.0f, oo = 0.0f;
-  for (int sp = 0; sp < n_splits; sp++) {
-    const float2 ml = a.ws_ml[row0 + sp];
-    const float f = fast_exp2(ml.x - mref);
-    ll += ml.y * f;
-    oo += a.ws_o[(row0 + sp) * D + d] * f;
+  float mm = -INFINITY, ll = 0.0f, oo = 0.0f;
+  for (int sp0 = 0; sp0 < n_splits; sp0 += 8) {
+    const int cnt = min(8, n_splits - sp0);
+    float2 ml[8];
+    float o_sp[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      ml[i] = i < cnt ? a.ws_ml[row0 + sp0 + i] : make_float2(-INFINITY, 0.0f);
+      o_sp[i] = i < cnt ? a.ws_o[(row0 + sp0 + i) * D + d] : 0.0f;
+    }
+    float cm = mm;
+#pragma unroll
+    for (int i = 0; i < 8; i++) cm = fmaxf(cm, ml[i].x);
+    const float mref = (cm == -INFINITY) ? 0.0f : cm;
+    const float f0 = fast_exp2(mm - mref);
+    ll *= f0;
+    oo *= f0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float f = fast_exp2(ml[i].x - mref);
+      ll += ml[i].y * f;
+      oo += o_sp[i] * f;
+    }
+    mm = cm;
   }
   a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / ll);
 }
@@ -624,7 +711,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(const GenericDecode
 
 __global__ void decode_fp8_kernel(const uint8_t *codes, float *out, int32_t n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)codes[i], false)[0];
+  if (i < n) out[i] = bf16_lo(fp8x2_to_bf16<false>((uint32_t)codes[i]));
 }
 
 template <int G, int FMT>
@@ -634,7 +721,7 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s) 
   dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
   hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.max_splits <= 1) return e;
+  if (e != hipSuccess || a.max_splits <= 1 || a.fused_merge) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }

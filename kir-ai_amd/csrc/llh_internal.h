@@ -50,6 +50,7 @@ struct DecodeArgs {
   int32_t window;
   int32_t split_blocks;     // blocks per split
   int32_t max_splits;
+  int32_t fused_merge;      // 1: last workgroup merges the splits; 0: second launch merges
   float scale_log2e;        // score_scale * log2(e)
 };
 

@@ -70,7 +70,7 @@ class DecodeDesc(ctypes.Structure):
         ("max_blocks_per_seq", ctypes.c_int32),
         ("max_seq_len", ctypes.c_int32),
         ("window", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("total_tokens_hint", ctypes.c_int32),
         ("d_seq_lens", ctypes.c_void_p),
         ("d_block_tables", ctypes.c_void_p),
     ]
@@ -274,15 +274,17 @@ class Context:
 
     # ---- batched hot path ----
     @staticmethod
-    def decode_desc(seq_lens, block_tables, num_q_heads: int, max_seq_len: int, window: int = 0) -> DecodeDesc:
-        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers)."""
+    def decode_desc(seq_lens, block_tables, num_q_heads: int, max_seq_len: int, window: int = 0,
+                    total_tokens_hint: int = 0) -> DecodeDesc:
+        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers).
+        total_tokens_hint: the sum of attended tokens if the caller knows it (sizes split-K)."""
         d = DecodeDesc(
             num_seqs=seq_lens.shape[0],
             num_q_heads=num_q_heads,
             max_blocks_per_seq=block_tables.shape[1],
             max_seq_len=max_seq_len,
             window=window,
-            reserved=0,
+            total_tokens_hint=total_tokens_hint,
             d_seq_lens=_ptr(seq_lens),
             d_block_tables=_ptr(block_tables),
         )

@@ -83,12 +83,44 @@ def test_decode_c1_identity_table(ctx, fmt):
     check(ctx, identity_batch([512]), 16, 8, fmt, seed=workloads.SEED_BASE + 0, what="C1")
 
 
-def test_decode_c2_full_size(ctx):
+@pytest.fixture(params=["fused", "kernel"])
+def merge_mode(request, monkeypatch):
+    """Split partials merged by the last workgroup (default) or by a second launch."""
+    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1" if request.param == "fused" else "0")
+    return request.param
+
+
+def test_decode_c2_full_size(ctx, merge_mode):
     """B=32, L~U[256,4096], permuted pool +10% free blocks."""
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
     assert batch.n_blocks == math.ceil(1.1 * int(np.sum((lens + 15) // 16)))
-    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what="C2")
+    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 merge={merge_mode}")
+
+
+@pytest.mark.parametrize("split_blocks", [4, 8, 64])
+def test_decode_split_sizes(ctx, merge_mode, split_blocks, monkeypatch):
+    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", str(split_blocks))
+    lens = workloads.uniform_lengths(12, 1, 5000, 17)
+    batch = workloads.paged_batch(lens, BT, 0.10, 17)
+    check(ctx, batch, 32, 8, seed=17, what=f"split={split_blocks} merge={merge_mode}")
+
+
+def test_decode_fused_merge_is_deterministic(ctx, monkeypatch):
+    """Many splits per sequence and many repeated calls: the last-arriving workgroup
+    merges in split order, so every call must give identical bits; a stale partial
+    read across XCDs would show up as a difference."""
+    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1")
+    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", "4")
+    lens = workloads.uniform_lengths(32, 256, 4096, 23)
+    batch = workloads.paged_batch(lens, BT, 0.10, 23)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 23)
+    first = run_decode(ctx, pool, batch, q, 16, 0, 0.088)
+    for _ in range(30):
+        assert np.array_equal(run_decode(ctx, pool, batch, q, 16, 0, 0.088), first)
+    assert ctx.device_errors() == 0
+    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, 16, 8, 0, q, 0.088)
+    assert_parity(first, ref, what="fused merge, split 4")
 
 
 @pytest.mark.parametrize("lens", [[1], [15, 16, 17], [31, 33, 255, 256, 257], [1000, 4095, 4096, 4097]])
