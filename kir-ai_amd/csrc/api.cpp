@@ -47,6 +47,8 @@ int env_int(const char *name, int dflt) {
 // non-empty workgroups closest to ~4096 (16 per CU on 256 CUs), measured best
 // on MI355X for both short bf16 and long int8 contexts.  The total work comes
 // from the caller's hint when given, else from the max_seq_len bound.
+constexpr int kMaxDecodeSplits = 1024;  // partials one merge workgroup combines
+
 struct SplitPlan {
   int split_blocks;
   int max_splits;
@@ -73,7 +75,8 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
       }
     }
   }
-  split = std::min(std::max(split, 4), 256);  // a wavefront reads its table entries from <= 64 lanes
+  split = std::min(std::max(split, 4), 64);  // a wavefront reads its table entries from <= 64 lanes
+  while ((est_blocks + split - 1) / split > kMaxDecodeSplits && split < 64) split *= 2;
   SplitPlan p;
   p.split_blocks = split;
   p.est_blocks = est_blocks;
@@ -360,6 +363,8 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   if (fast) {
     const SplitPlan plan =
         plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint);
+    if (plan.max_splits > kMaxDecodeSplits)
+      return ctx->fail(LLH_ERR_INVALID_SHAPE, "context too long for one decode call (over 4M attended tokens)");
     const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
     const size_t ml_off = kCounterBytes;
     const size_t o_off = ml_off + align_up(rows * sizeof(float2));
@@ -383,6 +388,7 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     a.split_blocks = plan.split_blocks;
     a.max_splits = plan.max_splits;
     a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
+    a.wave_splits = env_int("LLH_DECODE_WAVE_SPLITS", 0) ? 1 : 0;
     a.scale_log2e = score_scale * 1.4426950408889634f;
     hipError_t e = launch_decode(a, group, desc->max_seq_len, s);
     if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");

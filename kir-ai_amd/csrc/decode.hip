@@ -342,6 +342,9 @@ __device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, 
 
 template <int G, int FMT>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeArgs a) {
+  // consecutive workgroups are consecutive splits of one (kv head, sequence):
+  // they share its query rows and block-table row in L2 (measured faster on
+  // MI355X than dispatching all first splits first)
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -541,42 +544,168 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   }
 }
 
+// Wavefront-granular variant: every wavefront is an independent work item
+// (its own split of `split_blocks` consecutive blocks, its own partial), with
+// no LDS merge and no barrier.  Workgroup (kv head, sequence, z) holds splits
+// 4z .. 4z+3.
+template <int G, int FMT>
+__global__ __launch_bounds__(kDecodeThreads) void paged_decode_wave_kernel(const DecodeArgs a) {
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int split = blockIdx.z * 4 + (tid >> 6);
+  int len, lo, first_blk, n_blk, n_splits;
+  seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
+  if (n_splits > a.max_splits) {
+    if (tid == 0 && blockIdx.z == 0) atomicOr(a.err, kErrTooManySplits);
+    return;
+  }
+  if (split >= max(n_splits, 1)) return;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G;
+  if (n_blk == 0) {
+    for (int idx = lane; idx < G * D; idx += 64) a.out[qrow0 * D + idx] = 0;
+    return;
+  }
+  const int blk_begin = first_blk + split * a.split_blocks;
+  const int nb = min(a.split_blocks, first_blk + n_blk - blk_begin);  // <= 64
+  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
+  const int my_entry = lane < nb ? table[(blk_begin + lane) % a.max_blocks] : -1;
+
+  uint32_t qw[G][8];
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    if constexpr (FMT == kBf16) {
+      const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c * 8);
+      qw[gi][0] = t.x;
+      qw[gi][1] = t.y;
+      qw[gi][2] = t.z;
+      qw[gi][3] = t.w;
+      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
+    } else {
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 7) * 16);
+      const uint4 t0 = src[0], t1 = src[1];
+      qw[gi][0] = t0.x;
+      qw[gi][1] = t0.y;
+      qw[gi][2] = t0.z;
+      qw[gi][3] = t0.w;
+      qw[gi][4] = t1.x;
+      qw[gi][5] = t1.y;
+      qw[gi][6] = t1.z;
+      qw[gi][7] = t1.w;
+    }
+  }
+  SoftmaxState<G> st;
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    st.m[gi] = -INFINITY;
+    st.l[gi] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
+  }
+  constexpr int STAGES = pipeline_stages(G, FMT);
+  BlockRegs<FMT> r[STAGES];
+#pragma unroll
+  for (int sidx = 0; sidx < STAGES - 1; sidx++)
+    if (sidx < nb) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, sidx), kvh, lane, r[sidx]);
+  for (int k0 = 0; k0 < nb; k0 += STAGES) {
+#pragma unroll
+    for (int sidx = 0; sidx < STAGES; sidx++) {
+      const int k = k0 + sidx;
+      if (k < nb) {
+        const int kn = k + STAGES - 1;
+        if (kn < nb)
+          load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, kn), kvh, lane, r[(sidx + STAGES - 1) % STAGES]);
+        compute_block<G, FMT>(a, r[sidx], blk_begin + k, lo, len, lane, qw, st);
+      }
+    }
+  }
+  // merge the four token groups; afterwards every group holds the totals, and
+  // group g stores dims 16j + c for j = 2g, 2g + 1
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
+    mm = fmaxf(mm, __shfl_xor(mm, 32));
+    const float mref = (mm == -INFINITY) ? 0.0f : mm;
+    const float f = fast_exp2(st.m[gi] - mref);
+    float ll = st.l[gi] * f;
+    ll += __shfl_xor(ll, 16);
+    ll += __shfl_xor(ll, 32);
+    float o2[2];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      float v = st.o[gi][j] * f;
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (j == 2 * g) o2[0] = v;
+      if (j == 2 * g + 1) o2[1] = v;
+    }
+    if (n_splits == 1) {
+      const float inv = 1.0f / ll;
+      a.out[(qrow0 + gi) * D + 16 * (2 * g) + c] = f32_to_bf16_rne(o2[0] * inv);
+      a.out[(qrow0 + gi) * D + 16 * (2 * g + 1) + c] = f32_to_bf16_rne(o2[1] * inv);
+    } else {
+      const size_t row = (qrow0 + gi) * a.max_splits + split;
+      a.ws_o[row * D + 16 * (2 * g) + c] = o2[0];
+      a.ws_o[row * D + 16 * (2 * g + 1) + c] = o2[1];
+      if (lane == 0) a.ws_ml[row] = make_float2(mm, ll);
+    }
+  }
+}
+
 // Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
 // dim) per (query head, sequence) whose sequence used more than one split.
+// The (max, sum) pairs of all splits are read in one round into LDS; then each
+// lane's partial outputs are loaded 16 splits at a time.
+constexpr int kMergeMaxSplits = 1024;
+
 __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   int len, lo, first_blk, n_blk, n_splits;
   seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
-  if (n_splits <= 1 || n_splits > a.max_splits) return;
+  if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMergeMaxSplits) return;
+  __shared__ float s_f[kMergeMaxSplits];
+  __shared__ float s_red[2];
   const int d = threadIdx.x;
   const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
-  float mm = -INFINITY, ll = 0.0f, oo = 0.0f;
-  for (int sp0 = 0; sp0 < n_splits; sp0 += 8) {
-    const int cnt = min(8, n_splits - sp0);
-    float2 ml[8];
-    float o_sp[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      ml[i] = i < cnt ? a.ws_ml[row0 + sp0 + i] : make_float2(-INFINITY, 0.0f);
-      o_sp[i] = i < cnt ? a.ws_o[(row0 + sp0 + i) * D + d] : 0.0f;
-    }
-    float cm = mm;
-#pragma unroll
-    for (int i = 0; i < 8; i++) cm = fmaxf(cm, ml[i].x);
-    const float mref = (cm == -INFINITY) ? 0.0f : cm;
-    const float f0 = fast_exp2(mm - mref);
-    ll *= f0;
-    oo *= f0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float f = fast_exp2(ml[i].x - mref);
-      ll += ml[i].y * f;
-      oo += o_sp[i] * f;
-    }
-    mm = cm;
+  float lm = -INFINITY;
+  for (int sp = d; sp < n_splits; sp += D) {
+    const float2 ml = a.ws_ml[row0 + sp];
+    s_f[sp] = ml.x;
+    lm = fmaxf(lm, ml.x);
   }
-  a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / ll);
+  // max over the workgroup (two wavefronts)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lm = fmaxf(lm, __shfl_xor(lm, o));
+  if ((d & 63) == 0) s_red[d >> 6] = lm;
+  __syncthreads();
+  const float mm = fmaxf(s_red[0], s_red[1]);
+  const float mref = (mm == -INFINITY) ? 0.0f : mm;
+  float ll = 0.0f;
+  for (int sp = d; sp < n_splits; sp += D) {
+    const float f = fast_exp2(s_f[sp] - mref);
+    ll += a.ws_ml[row0 + sp].y * f;
+    s_f[sp] = f;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ll += __shfl_xor(ll, o);
+  __syncthreads();
+  if ((d & 63) == 0) s_red[d >> 6] = ll;
+  __syncthreads();
+  const float l_tot = s_red[0] + s_red[1];
+  float oo = 0.0f;
+  for (int sp0 = 0; sp0 < n_splits; sp0 += 16) {
+    float o_sp[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) o_sp[i] = sp0 + i < n_splits ? a.ws_o[(row0 + sp0 + i) * D + d] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      if (sp0 + i < n_splits) oo += o_sp[i] * s_f[sp0 + i];
+  }
+  a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / l_tot);
 }
 
 // ---------------------------------------------------------------------------
@@ -718,10 +847,15 @@ template <int G, int FMT>
 hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s) {
   const int max_blk = (max_seq_len + BT - 1) / BT + 1;
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
-  dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
+  if (a.wave_splits) {
+    dim3 grid(a.pool.kv_heads, a.num_seqs, (min(grid_x, a.max_splits) + 3) / 4);
+    hipLaunchKernelGGL((paged_decode_wave_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
+  } else {
+    dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
+    hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
+  }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.max_splits <= 1 || a.fused_merge) return e;
+  if (e != hipSuccess || a.max_splits <= 1 || (a.fused_merge && !a.wave_splits)) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }

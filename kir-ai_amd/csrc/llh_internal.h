@@ -51,6 +51,7 @@ struct DecodeArgs {
   int32_t split_blocks;     // blocks per split
   int32_t max_splits;
   int32_t fused_merge;      // 1: last workgroup merges the splits; 0: second launch merges
+  int32_t wave_splits;      // 1: one split per wavefront (no workgroup merge); 0: one split per workgroup
   float scale_log2e;        // score_scale * log2(e)
 };
 
