@@ -107,14 +107,20 @@ class DecodeWorkload:
         self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
 
 
-def time_steps(fn, steps: int, warmup: int):
-    """Mean ms per step from HIP events recorded on the launch stream."""
+def time_steps(fn, steps: int, warmup: int, kernel_timing=None):
+    """Mean ms per step from HIP events recorded on the launch stream.
+
+    With kernel_timing = (ctx, kind), the library also records HIP events around
+    its main kernel in every timed step (same stream); returns (step ms, kernel ms)."""
     import torch
 
     stream = torch.cuda.Stream()  # default priority
     for _ in range(warmup):
         fn(stream)
     torch.cuda.synchronize()
+    if kernel_timing:
+        kernel_timing[0].kernel_time(kernel_timing[1], reset=True)
+        kernel_timing[0].set_kernel_timing(True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -122,7 +128,12 @@ def time_steps(fn, steps: int, warmup: int):
         fn(stream)
     e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    step_ms = e0.elapsed_time(e1) / steps
+    if not kernel_timing:
+        return step_ms
+    kernel_timing[0].set_kernel_timing(False)
+    total, n = kernel_timing[0].kernel_time(kernel_timing[1], reset=True)
+    return step_ms, total / max(n, 1)
 
 
 def cpu_baseline_decode(w: DecodeWorkload, budget_s: float):
@@ -244,19 +255,37 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         copies[state["i"] % len(copies)].step(stream)
         state["i"] += 1
 
+    # step time over all timed steps, then the decode kernel alone (library-recorded events)
     ms = time_steps(step, steps, warmup)
+    _, kms = time_steps(step, steps, 0, kernel_timing=(ctx, "decode"))
     if ctx.device_errors() != 0:
         raise RuntimeError(f"{name}: device error flags set during timing")
     gbs = nbytes / (ms * 1e-3) / 1e9
     return first, {
         "config": name,
         "us_per_step": round(ms * 1e3, 2),
+        "kernel_us": round(kms * 1e3, 2),
+        "kernel_gbs": round(nbytes / (kms * 1e-3) / 1e9, 1),
         "hbm_gbs": round(gbs, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
         "bytes_per_step": nbytes,
         "rotating_copies": len(copies),
     }
+
+
+def traffic_from_profile(alg_bytes: int):
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_c2_bf16.md")
+    try:
+        for line in open(path):
+            cells = [c.strip() for c in line.split("|")]
+            if len(cells) > 9 and cells[1] == "C2" and "paged_decode_kernel" in cells[2]:
+                return int((float(cells[7]) + float(cells[8])) * 1024)
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def main() -> int:
@@ -292,7 +321,8 @@ def main() -> int:
                            seed=workloads.SEED_BASE + 1)
     ms = c2["us_per_step"] / 1e3
     value = c2["hbm_gbs"]
-    log(f"C2: {c2['us_per_step']} us/step, {value} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+    log(f"C2: {c2['us_per_step']} us/step, {value} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of 8 TB/s); "
+        f"decode kernel {c2['kernel_us']} us = {c2['kernel_gbs']} GB/s")
 
     copy = None
     if args.copy_mb > 0:
@@ -331,10 +361,11 @@ def main() -> int:
                 ("C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096)):
             step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res)
             pms = time_steps(step, sec_steps, args.warmup)
+            _, pkms = time_steps(step, sec_steps, 0, kernel_timing=(ctx, "prefill"))
             if ctx.device_errors() != 0:
                 raise RuntimeError(f"{name}: device error flags set")
             tf = flops / (pms * 1e-3) / 1e12
-            r = {"config": name, "us_per_step": round(pms * 1e3, 2), "tflops": round(tf, 1),
+            r = {"config": name, "us_per_step": round(pms * 1e3, 2), "kernel_us": round(pkms * 1e3, 2), "tflops": round(tf, 1),
                  "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
                  "flops_per_step": flops}
             secondary.append(r)
@@ -369,11 +400,13 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": value,
+            "kernel": "paged_decode_kernel<2, bf16> (split-K partials; the merge launch is excluded)",
+            "achieved": c2["kernel_gbs"],
+            "kernel_us": c2["kernel_us"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profile(c2["bytes_per_step"]),
         },
         "cpu_baseline": cpu,
         "copy_ceiling": copy,

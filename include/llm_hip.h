@@ -90,6 +90,13 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
  * outside the pool, 2 = a sequence longer than the call's max_seq_len allows,
  * 4 = a non-finite score. */
 int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset);
+/* Kernel timing for measurement: while enabled, each llh_paged_decode /
+ * llh_paged_prefill call records a pair of HIP events on its stream around its
+ * main kernel (the split-K decode kernel, not the merge; the prefill kernel).
+ * llh_ctx_kernel_time waits for the recorded events and returns the summed
+ * duration and count for kind 0 = decode, 1 = prefill (reset clears them). */
+int llh_ctx_set_kernel_timing(llh_ctx *ctx, int32_t enable);
+int llh_ctx_kernel_time(llh_ctx *ctx, int32_t kind, double *total_ms, int64_t *count, int32_t reset);
 
 /* ------------------------------------------------------------------ */
 /* paged KV pool (device resident)                                    */

@@ -98,6 +98,37 @@ struct llh_ctx {
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
       shape_errors{0};
+  // kernel timing (measurement only)
+  std::atomic<int> timing{0};
+  std::mutex timing_mu;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[2];
+  std::vector<hipEvent_t> event_pool;
+  double timed_ms[2] = {0.0, 0.0};
+  int64_t timed_n[2] = {0, 0};
+
+  hipEvent_t take_event() {
+    if (!event_pool.empty()) {
+      hipEvent_t e = event_pool.back();
+      event_pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+  // records the start event of `kind` on stream s; returns the pair index or -1
+  std::pair<hipEvent_t, hipEvent_t> timing_begin(hipStream_t s) {
+    if (!timing.load()) return {nullptr, nullptr};
+    std::lock_guard<std::mutex> g(timing_mu);
+    hipEvent_t a = take_event(), b = take_event();
+    if (!a || !b || hipEventRecord(a, s) != hipSuccess) return {nullptr, nullptr};
+    return {a, b};
+  }
+  void timing_end(int kind, std::pair<hipEvent_t, hipEvent_t> ev, hipStream_t s) {
+    if (!ev.first) return;
+    std::lock_guard<std::mutex> g(timing_mu);
+    if (hipEventRecord(ev.second, s) == hipSuccess) pending[kind].push_back(ev);
+  }
 
   int fail(int status, const std::string &msg) {
     {
@@ -172,6 +203,12 @@ int llh_ctx_destroy(llh_ctx *ctx) {
   if (!ctx) return LLH_ERR_NULL;
   (void)hipSetDevice(ctx->device);
   (void)hipDeviceSynchronize();
+  for (auto &list : ctx->pending)
+    for (auto &ev : list) {
+      (void)hipEventDestroy(ev.first);
+      (void)hipEventDestroy(ev.second);
+    }
+  for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->d_err) (void)hipFree(ctx->d_err);
   delete ctx;
@@ -216,6 +253,36 @@ int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset) {
   if (e == hipSuccess) e = hipMemcpy(flags, ctx->d_err, sizeof(int32_t), hipMemcpyDeviceToHost);
   if (e == hipSuccess && reset) e = hipMemset(ctx->d_err, 0, sizeof(int32_t));
   if (e != hipSuccess) return ctx->hip_fail(e, "device error flags");
+  return LLH_OK;
+}
+
+int llh_ctx_set_kernel_timing(llh_ctx *ctx, int32_t enable) {
+  if (!ctx) return LLH_ERR_NULL;
+  ctx->timing.store(enable ? 1 : 0);
+  return LLH_OK;
+}
+
+int llh_ctx_kernel_time(llh_ctx *ctx, int32_t kind, double *total_ms, int64_t *count, int32_t reset) {
+  if (!ctx || !total_ms || !count) return LLH_ERR_NULL;
+  if (kind != 0 && kind != 1) return ctx->fail(LLH_ERR_INVALID_SHAPE, "timing kind must be 0 (decode) or 1 (prefill)");
+  std::lock_guard<std::mutex> g(ctx->timing_mu);
+  for (auto &ev : ctx->pending[kind]) {
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(ev.second);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.first, ev.second);
+    if (e != hipSuccess) return ctx->hip_fail(e, "kernel timing");
+    ctx->timed_ms[kind] += ms;
+    ctx->timed_n[kind] += 1;
+    ctx->event_pool.push_back(ev.first);
+    ctx->event_pool.push_back(ev.second);
+  }
+  ctx->pending[kind].clear();
+  *total_ms = ctx->timed_ms[kind];
+  *count = ctx->timed_n[kind];
+  if (reset) {
+    ctx->timed_ms[kind] = 0.0;
+    ctx->timed_n[kind] = 0;
+  }
   return LLH_OK;
 }
 
@@ -390,7 +457,17 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
     a.wave_splits = env_int("LLH_DECODE_WAVE_SPLITS", 0) ? 1 : 0;
     a.scale_log2e = score_scale * 1.4426950408889634f;
-    hipError_t e = launch_decode(a, group, desc->max_seq_len, s);
+    struct TimingHook {
+      llh_ctx *ctx;
+      std::pair<hipEvent_t, hipEvent_t> ev;
+    } th{ctx, {nullptr, nullptr}};
+    hipError_t e = launch_decode(a, group, desc->max_seq_len, s, &th, [](void *u, int phase, hipStream_t st) {
+      auto *t = static_cast<TimingHook *>(u);
+      if (phase == 0)
+        t->ev = t->ctx->timing_begin(st);
+      else
+        t->ctx->timing_end(0, t->ev, st);
+    });
     if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");
     return LLH_OK;
   }
@@ -452,7 +529,9 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   a.q_tiles = std::max(1, (desc->max_chunk_len + 127) / 128);
   a.scale_log2e = score_scale * 1.4426950408889634f;
   ctx->prefill_calls++;
+  auto ev = ctx->timing_begin(static_cast<hipStream_t>(stream));
   hipError_t e = launch_prefill(a, static_cast<hipStream_t>(stream));
+  ctx->timing_end(1, ev, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "prefill launch");
   return LLH_OK;
 }

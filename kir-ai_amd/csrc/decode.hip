@@ -844,9 +844,10 @@ __global__ void decode_fp8_kernel(const uint8_t *codes, float *out, int32_t n) {
 }
 
 template <int G, int FMT>
-hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s) {
+hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   const int max_blk = (max_seq_len + BT - 1) / BT + 1;
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
+  if (hook) hook(hu, 0, s);
   if (a.wave_splits) {
     dim3 grid(a.pool.kv_heads, a.num_seqs, (min(grid_x, a.max_splits) + 3) / 4);
     hipLaunchKernelGGL((paged_decode_wave_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
@@ -855,36 +856,37 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s) 
     hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
   }
   hipError_t e = hipGetLastError();
+  if (hook) hook(hu, 1, s);
   if (e != hipSuccess || a.max_splits <= 1 || (a.fused_merge && !a.wave_splits)) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }
 
 template <int G>
-hipError_t launch_decode_fmt(const DecodeArgs &a, int max_seq_len, hipStream_t s) {
+hipError_t launch_decode_fmt(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   switch (a.pool.format) {
     case kBf16:
-      return launch_decode_t<G, kBf16>(a, max_seq_len, s);
+      return launch_decode_t<G, kBf16>(a, max_seq_len, s, hu, hook);
     case kInt8:
-      return launch_decode_t<G, kInt8>(a, max_seq_len, s);
+      return launch_decode_t<G, kInt8>(a, max_seq_len, s, hu, hook);
     case kFp8:
-      return launch_decode_t<G, kFp8>(a, max_seq_len, s);
+      return launch_decode_t<G, kFp8>(a, max_seq_len, s, hu, hook);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s) {
+hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   switch (group) {
     case 1:
-      return launch_decode_fmt<1>(a, max_seq_len, s);
+      return launch_decode_fmt<1>(a, max_seq_len, s, hu, hook);
     case 2:
-      return launch_decode_fmt<2>(a, max_seq_len, s);
+      return launch_decode_fmt<2>(a, max_seq_len, s, hu, hook);
     case 4:
-      return launch_decode_fmt<4>(a, max_seq_len, s);
+      return launch_decode_fmt<4>(a, max_seq_len, s, hu, hook);
     case 8:
-      return launch_decode_fmt<8>(a, max_seq_len, s);
+      return launch_decode_fmt<8>(a, max_seq_len, s, hu, hook);
   }
   return hipErrorInvalidValue;
 }

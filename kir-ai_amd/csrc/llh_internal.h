@@ -131,7 +131,11 @@ struct GatherArgs {
 };
 
 // launchers (return hipError_t of the launch)
-hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s);
+// `hook(user, 0, s)` runs just before and `hook(user, 1, s)` just after the main
+// decode kernel is enqueued (before the merge): kernel timing records events there.
+typedef void (*LaunchHook)(void *user, int phase, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s, void *hook_user = nullptr,
+                         LaunchHook hook = nullptr);
 hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_f32, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);

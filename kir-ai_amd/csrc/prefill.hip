@@ -8,9 +8,18 @@
 // computed as one dense pass.
 //
 // One workgroup = 128 query rows of one query head (4 wavefronts x 32 rows).
-// Key tiles of 64 positions (4 pool blocks) are staged in LDS; tiles wholly
-// outside the window or past the last query are never loaded, and only tiles
-// that straddle a boundary are masked.
+// Key tiles of 64 positions (4 pool blocks) are staged in LDS, double
+// buffered: while the wavefronts run the MFMAs of tile t, every lane already
+// holds its share of tile t+1 in registers, and stores it to the other buffer
+// afterwards (one barrier per tile).  Tiles wholly outside the window or past
+// the last query are never loaded, and only tiles that straddle a boundary are
+// masked.
+//
+// Work mapping: workgroups are dispatched round-robin over the 8 XCDs, each
+// with its own L2.  The launch maps workgroup L to logical work item
+// w = (L % 8) * ceil(N / 8) + L / 8, and logical items run (sequence, kv head,
+// query tile, query head in group) with the head fastest, so each XCD works on
+// few (sequence, kv head) pairs at a time and their K/V tiles stay in its L2.
 //
 // Per wavefront, with v_mfma_f32_32x32x16_bf16:
 //   S^T[key][query] = K Q^T       A = K rows (token-major pool layout)
@@ -35,19 +44,15 @@ constexpr int BN = 64;           // key positions per tile
 constexpr int KBLK = BN / BT;    // pool blocks per tile
 constexpr int K_STRIDE = D + 8;  // bf16 elements per K row in LDS (272 B: conflict-free b128 reads)
 constexpr int V_STRIDE = BT + 4; // bf16 elements per V^T row in LDS (40 B: conflict-free b64 reads)
+constexpr int K_TILE = BN * K_STRIDE;        // bf16 elements of one K tile in LDS
+constexpr int V_TILE = KBLK * D * V_STRIDE;  // bf16 elements of one V^T tile in LDS
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
 }
 
 __device__ __forceinline__ f32x16_t mfma32(const uint4 &a, const uint4 &b, const f32x16_t &c) {
@@ -57,10 +62,77 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4 &a, const uint4 &b, const
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const PrefillArgs a) {
-  const int tile = blockIdx.x;
-  const int qh = blockIdx.y;
-  const int b = blockIdx.z;
+// One lane's share of a key tile: for each of the 4 blocks, 16 B of K (token
+// tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..).
+struct TileRegs {
+  uint4 k[KBLK];
+  uint4 v[KBLK];
+};
+
+__device__ __forceinline__ void load_tile(const PrefillArgs &a, const int32_t *table, int kvh, int kt, int ctx,
+                                          int klo, int tid, TileRegs &r) {
+  const int Hkv = a.pool.kv_heads;
+#pragma unroll
+  for (int kb = 0; kb < KBLK; kb++) {
+    const int bpos = kt + kb * BT;
+    int phys = -1;
+    if (bpos < ctx && bpos + BT > klo) {
+      phys = table[(bpos / BT) % a.max_blocks];
+      if (phys < 0 || (int64_t)phys >= a.pool.n_blocks) {
+        if (tid == 0) atomicOr(a.err, kErrBadBlock);
+        phys = -1;
+      }
+    }
+    const int r_tok = tid >> 4;
+    uint4 tk = make_uint4(0, 0, 0, 0);
+    if (phys >= 0 && bpos + r_tok < ctx)
+      tk = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.k) +
+                                            (((size_t)phys * Hkv + kvh) * BT + r_tok) * D + (tid & 15) * 8);
+    r.k[kb] = tk;
+    const int d = tid >> 1;
+    const int half = tid & 1;
+    uint4 tv = make_uint4(0, 0, 0, 0);
+    if (phys >= 0) {
+      tv = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v) +
+                                            (((size_t)phys * Hkv + kvh) * D + d) * BT + half * 8);
+      const int valid = ctx - (bpos + half * 8);  // tokens of this 8-run inside the context
+      if (valid < 8) {
+        uint32_t w[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+        tv = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    r.v[kb] = tv;
+  }
+}
+
+__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, const TileRegs &r) {
+#pragma unroll
+  for (int kb = 0; kb < KBLK; kb++) {
+    *reinterpret_cast<uint4 *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[kb];
+    uint16_t *dst = &v_lds[(kb * D + (tid >> 1)) * V_STRIDE + (tid & 1) * 8];
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(r.v[kb].x, r.v[kb].y);
+    *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(r.v[kb].z, r.v[kb].w);
+  }
+}
+
+__global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const PrefillArgs a) {
+  // ---- XCD-aware logical work item ----
+  const int Hq = a.q_heads;
+  const int Hkv = a.pool.kv_heads;
+  const int G = Hq / Hkv;
+  const int n_items = a.q_tiles * Hq * a.num_seqs;
+  const int per_xcd = (n_items + 7) / 8;
+  const int w = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (w >= n_items) return;
+  const int gi = w % G;
+  const int tile = (w / G) % a.q_tiles;
+  const int kvh = (w / (G * a.q_tiles)) % Hkv;
+  const int b = w / (G * a.q_tiles * Hkv);
+  const int qh = kvh * G + gi;
+
   const int c0 = a.chunk_starts[b];
   const int chunk = a.chunk_starts[b + 1] - c0;
   const int ctx = a.context_lens[b];
@@ -72,9 +144,6 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const Pr
   const int wave = tid >> 6;
   const int h = lane >> 5;     // lane half
   const int col = lane & 31;   // query column of this lane
-  const int Hq = a.q_heads;
-  const int Hkv = a.pool.kv_heads;
-  const int kvh = qh / (Hq / Hkv);
   const int prefix = ctx - chunk;
 
   // rows of this workgroup and of this wavefront
@@ -98,8 +167,8 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const Pr
     }
   }
 
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * K_STRIDE];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[KBLK * D * V_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][K_TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][V_TILE];
 
   f32x16_t oacc[4];
 #pragma unroll
@@ -122,128 +191,93 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const Pr
   const int wlo_last = a.window > 0 ? max(0, wpos_last - a.window + 1) : 0;
   const bool wave_live = wrow0 < chunk;
 
-  for (int kt = t_begin; kt < khi; kt += BN) {
-    __syncthreads();  // previous tile fully consumed
-    // ---- stage K (token rows) and V^T (dim rows) of the 4 blocks into LDS ----
+  TileRegs next;
+  load_tile(a, table, kvh, t_begin, ctx, klo, tid, next);
+  store_tile(k_lds[0], v_lds[0], tid, next);
+  __syncthreads();
+
+  int buf = 0;
+  for (int kt = t_begin; kt < khi; kt += BN, buf ^= 1) {
+    const bool has_next = kt + BN < khi;
+    if (has_next) load_tile(a, table, kvh, kt + BN, ctx, klo, tid, next);  // in flight during the math
+
+    // tile needed by this wavefront?
+    if (wave_live && kt <= wpos_last && kt + BN > wlo_first) {
+      const uint16_t *kl = k_lds[buf];
+      const uint16_t *vl = v_lds[buf];
+      // ---- S^T = K Q^T for two 32-key sub-tiles ----
+      f32x16_t sacc[2];
 #pragma unroll
-    for (int kb = 0; kb < KBLK; kb++) {
-      const int bpos = kt + kb * BT;
-      const bool inrange = bpos < ctx && bpos + BT > klo;
-      int phys = -1;
-      if (inrange) {
-        phys = table[(bpos / BT) % a.max_blocks];
-        if (phys < 0 || (int64_t)phys >= a.pool.n_blocks) {
-          if (tid == 0) atomicOr(a.err, kErrBadBlock);
-          phys = -1;
+      for (int st = 0; st < 2; st++) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) sacc[st][j] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+          const uint4 ka = *reinterpret_cast<const uint4 *>(&kl[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
+          sacc[st] = mfma32(ka, qb[ks], sacc[st]);
         }
       }
-      // K: 256 threads x 16 B = one 4 KiB block
-      {
-        const int r = tid >> 4;  // token in block
-        const int c16 = tid & 15;
-        uint4 t = make_uint4(0, 0, 0, 0);
-        if (phys >= 0 && bpos + r < ctx) {
-          const uint16_t *src = reinterpret_cast<const uint16_t *>(a.pool.k) +
-                                (((size_t)phys * Hkv + kvh) * BT + r) * D + c16 * 8;
-          t = *reinterpret_cast<const uint4 *>(src);
-        }
-        *reinterpret_cast<uint4 *>(&k_lds[(kb * BT + r) * K_STRIDE + c16 * 8]) = t;
-      }
-      // V^T: 256 threads x 16 B; thread -> dim tid/2, tokens 8*(tid&1) .. +8
-      {
-        const int d = tid >> 1;
-        const int half = tid & 1;
-        uint4 t = make_uint4(0, 0, 0, 0);
-        if (phys >= 0) {
-          const uint16_t *src = reinterpret_cast<const uint16_t *>(a.pool.v) +
-                                (((size_t)phys * Hkv + kvh) * D + d) * BT + half * 8;
-          t = *reinterpret_cast<const uint4 *>(src);
-          const int valid = ctx - (bpos + half * 8);  // tokens of this 8-run inside the context
-          if (valid < 8) {
-            uint32_t w[4] = {t.x, t.y, t.z, t.w};
+
+      // ---- scale, mask, online softmax ----
+      const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
+      float tmax = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-              if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-            t = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int st = 0; st < 2; st++) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          float s = sacc[st][j] * a.scale_log2e;
+          if (need_mask) {
+            const int kp = kt + st * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+            if (kp > my_pos || kp < my_lo || kp >= ctx || !row_ok) s = -INFINITY;
           }
+          sacc[st][j] = s;
+          tmax = fmaxf(tmax, s);
         }
-        uint16_t *dst = &v_lds[(kb * D + d) * V_STRIDE + half * 8];
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(t.x, t.y);
-        *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(t.z, t.w);
       }
-    }
-    __syncthreads();
-    if (!wave_live) continue;
-    // tile entirely outside this wavefront's needs?
-    if (kt > wpos_last || kt + BN <= wlo_first) continue;
-
-    // ---- S^T = K Q^T for two 32-key sub-tiles ----
-    f32x16_t sacc[2];
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      const float mref = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = fast_exp2(m_run - mref);
+      m_run = m_new;
+      float psum = 0.0f;
+      uint4 pb[4];  // P^T operands for the 4 16-key steps (one pool block each)
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
+      for (int st = 0; st < 2; st++) {
+        float p[16];
 #pragma unroll
-      for (int j = 0; j < 16; j++) sacc[st][j] = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < 8; ks++) {
-        const uint4 ka = *reinterpret_cast<const uint4 *>(&k_lds[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
-        sacc[st] = mfma32(ka, qb[ks], sacc[st]);
-      }
-    }
-
-    // ---- scale, mask, online softmax ----
-    const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < 2; st++) {
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        float s = sacc[st][j] * a.scale_log2e;
-        if (need_mask) {
-          const int kp = kt + st * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
-          if (kp > my_pos || kp < my_lo || kp >= ctx || !row_ok) s = -INFINITY;
+        for (int j = 0; j < 16; j++) {
+          p[j] = fast_exp2(sacc[st][j] - mref);
+          psum += p[j];
         }
-        sacc[st][j] = s;
-        tmax = fmaxf(tmax, s);
+        pb[2 * st + 0] = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
+                                    pack_bf16(p[6], p[7]));
+        pb[2 * st + 1] = make_uint4(pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]),
+                                    pack_bf16(p[14], p[15]));
       }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float mref = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - mref);
-    m_run = m_new;
-    float psum = 0.0f;
-    uint4 pb[4];  // P^T operands for the 4 16-key steps (one pool block each)
+      l_run = l_run * alpha + psum;
+      if (__any(alpha != 1.0f)) {  // the running max moved for some row: rescale the outputs
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
-      float p[16];
+        for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
-        p[j] = fast_exp2(sacc[st][j] - mref);
-        psum += p[j];
+          for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
       }
-      pb[2 * st + 0] = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
-                                  pack_bf16(p[6], p[7]));
-      pb[2 * st + 1] = make_uint4(pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]),
-                                  pack_bf16(p[14], p[15]));
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-      for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
 
-    // ---- O^T += V^T P^T ----
+      // ---- O^T += V^T P^T ----
 #pragma unroll
-    for (int kb = 0; kb < KBLK; kb++) {
+      for (int kb = 0; kb < KBLK; kb++) {
 #pragma unroll
-      for (int mt = 0; mt < 4; mt++) {
-        const uint16_t *vrow = &v_lds[(kb * D + mt * 32 + col) * V_STRIDE];
-        const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
-        const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
-        const uint4 va = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-        oacc[mt] = mfma32(va, pb[kb], oacc[mt]);
+        for (int mt = 0; mt < 4; mt++) {
+          const uint16_t *vrow = &vl[(kb * D + mt * 32 + col) * V_STRIDE];
+          const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
+          const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
+          const uint4 va = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+          oacc[mt] = mfma32(va, pb[kb], oacc[mt]);
+        }
       }
     }
+
+    if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next);
+    __syncthreads();  // next tile visible; this tile no longer read
   }
 
   // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
@@ -256,9 +290,9 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const Pr
 #pragma unroll
     for (int jq = 0; jq < 4; jq++) {
       const int d0 = mt * 32 + jq * 8 + 4 * h;
-      const uint2 w = make_uint2(pack_bf16(oacc[mt][4 * jq + 0] * inv, oacc[mt][4 * jq + 1] * inv),
-                                 pack_bf16(oacc[mt][4 * jq + 2] * inv, oacc[mt][4 * jq + 3] * inv));
-      *reinterpret_cast<uint2 *>(orow + d0) = w;
+      const uint2 w2 = make_uint2(pack_bf16(oacc[mt][4 * jq + 0] * inv, oacc[mt][4 * jq + 1] * inv),
+                                  pack_bf16(oacc[mt][4 * jq + 2] * inv, oacc[mt][4 * jq + 3] * inv));
+      *reinterpret_cast<uint2 *>(orow + d0) = w2;
     }
   }
 }
@@ -266,8 +300,9 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const Pr
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
-  dim3 grid(a.q_tiles, a.q_heads, a.num_seqs);
-  hipLaunchKernelGGL(paged_prefill_kernel, grid, dim3(kPrefillThreads), 0, s, a);
+  const int n_items = a.q_tiles * a.q_heads * a.num_seqs;
+  const int grid = (n_items + 7) / 8 * 8;
+  hipLaunchKernelGGL(paged_prefill_kernel, dim3(grid), dim3(kPrefillThreads), 0, s, a);
   return hipGetLastError();
 }
 

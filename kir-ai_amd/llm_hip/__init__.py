@@ -158,6 +158,9 @@ SIGNATURES = {
     "llh_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "llh_ctx_metrics": (ctypes.c_int, [_P, ctypes.POINTER(Metrics)]),
     "llh_ctx_device_errors": (ctypes.c_int, [_P, ctypes.POINTER(_I32), _I32]),
+    "llh_ctx_set_kernel_timing": (ctypes.c_int, [_P, _I32]),
+    "llh_ctx_kernel_time": (ctypes.c_int, [_P, _I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
+                                           _I32]),
     "llh_kv_pool_create": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, ctypes.c_int64, ctypes.POINTER(_P)]),
     "llh_kv_pool_destroy": (ctypes.c_int, [_P]),
     "llh_kv_pool_get_info": (ctypes.c_int, [_P, ctypes.POINTER(PoolInfo)]),
@@ -265,6 +268,16 @@ class Context:
         flags = _I32()
         self.check(self.lib.llh_ctx_device_errors(self.handle, ctypes.byref(flags), 1 if reset else 0))
         return flags.value
+
+    def set_kernel_timing(self, enable: bool) -> None:
+        self.check(self.lib.llh_ctx_set_kernel_timing(self.handle, 1 if enable else 0))
+
+    def kernel_time(self, kind: str, reset: bool = True) -> tuple[float, int]:
+        """(summed ms, count) of the timed main kernels: kind 'decode' or 'prefill'."""
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        self.check(self.lib.llh_ctx_kernel_time(self.handle, {"decode": 0, "prefill": 1}[kind], ctypes.byref(ms),
+                                                ctypes.byref(n), 1 if reset else 0))
+        return ms.value, n.value
 
     def reserve_workspace(self, nbytes: int) -> None:
         self.check(self.lib.llh_ctx_reserve_workspace(self.handle, nbytes))
