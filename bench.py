@@ -301,7 +301,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (the batch shards by sequence with "
-              "no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "no communication). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import numpy as np

@@ -6,7 +6,7 @@
  * trait (crates/llm-backend/src/core/native_matvec.rs:222-769) into the Metal
  * implementation (crates/llm-native-runtime/src/native_matvec.rs:3026-4566).
  * A Rust shim binds the functions below with `extern "C"` and adds a
- * `NativeTextMatvecBackend::Hip` arm (see INTEGRATION.md for the binding).
+ * `NativeTextMatvecBackend::Hip` arm that forwards the trait methods here.
  *
  * Conventions
  *   - Every function returns an int status (llh_status); none aborts.

@@ -85,7 +85,8 @@ def test_decode_c1_identity_table(ctx, fmt):
 
 @pytest.fixture(params=["fused", "kernel"])
 def merge_mode(request, monkeypatch):
-    """Split partials merged by the last workgroup (default) or by a second launch."""
+    """Split partials merged by the last-arriving workgroup (LLH_DECODE_FUSED_MERGE=1) or by a
+    second launch (the default)."""
     monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1" if request.param == "fused" else "0")
     return request.param
 
