@@ -50,6 +50,7 @@ constexpr int V_TILE = KBLK * D * V_STRIDE;  // bf16 elements of one V^T tile in
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;  // native vector: stays in registers
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
@@ -63,58 +64,70 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4 &a, const uint4 &b, const
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // One lane's share of a key tile: for each of the 4 blocks, 16 B of K (token
-// tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..).
+// tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..),
+// plus a (wavefront-uniform) bit per block: 1 = the block is needed and valid.
 struct TileRegs {
-  uint4 k[KBLK];
-  uint4 v[KBLK];
+  u32x4_t k[KBLK];
+  u32x4_t v[KBLK];
 };
 
-__device__ __forceinline__ void load_tile(const PrefillArgs &a, const int32_t *table, int kvh, int kt, int ctx,
-                                          int klo, int tid, TileRegs &r) {
+// Block-table entries of the tile starting at kt: lane kb of every wavefront
+// holds the entry of the tile's block kb (lanes repeat mod KBLK).  Always an
+// in-bounds table read (the index is taken mod max_blocks), issued one tile
+// ahead so the table read never sits on the critical path.
+__device__ __forceinline__ int fetch_entries(const PrefillArgs &a, const int32_t *table, int kt, int lane) {
+  return table[(kt / BT + (lane & (KBLK - 1))) % a.max_blocks];
+}
+
+// Issues the tile's K/V loads.  Every load is unconditional (blocks that are not
+// needed, or whose entry is outside the pool, read block 0 and are zeroed when
+// stored to LDS), so no branch or conditional memory operation sits between
+// the prefetch and the math that overlaps it.  `bad` collects needed blocks
+// with an out-of-pool entry (flagged once, at the end of the kernel).
+__device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries, int kvh, int kt, int ctx, int klo,
+                                              int tid, TileRegs &r, bool &bad) {
   const int Hkv = a.pool.kv_heads;
+  uint32_t use_mask = 0;
 #pragma unroll
   for (int kb = 0; kb < KBLK; kb++) {
     const int bpos = kt + kb * BT;
-    int phys = -1;
-    if (bpos < ctx && bpos + BT > klo) {
-      phys = table[(bpos / BT) % a.max_blocks];
-      if (phys < 0 || (int64_t)phys >= a.pool.n_blocks) {
-        if (tid == 0) atomicOr(a.err, kErrBadBlock);
-        phys = -1;
-      }
-    }
-    const int r_tok = tid >> 4;
-    uint4 tk = make_uint4(0, 0, 0, 0);
-    if (phys >= 0 && bpos + r_tok < ctx)
-      tk = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.k) +
-                                            (((size_t)phys * Hkv + kvh) * BT + r_tok) * D + (tid & 15) * 8);
-    r.k[kb] = tk;
-    const int d = tid >> 1;
-    const int half = tid & 1;
-    uint4 tv = make_uint4(0, 0, 0, 0);
-    if (phys >= 0) {
-      tv = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v) +
-                                            (((size_t)phys * Hkv + kvh) * D + d) * BT + half * 8);
-      const int valid = ctx - (bpos + half * 8);  // tokens of this 8-run inside the context
-      if (valid < 8) {
-        uint32_t w[4] = {tv.x, tv.y, tv.z, tv.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-          if (e >= valid) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-        tv = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    r.v[kb] = tv;
+    const bool needed = bpos < ctx && bpos + BT > klo;
+    const int phys = __builtin_amdgcn_readlane(entries, kb);
+    const bool ok = phys >= 0 && (int64_t)phys < a.pool.n_blocks;
+    bad |= needed && !ok;
+    const bool use = needed && ok;
+    use_mask |= use ? (1u << kb) : 0u;
+    const size_t base = ((size_t)(use ? phys : 0) * Hkv + kvh) * (BT * D);
+    r.k[kb] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
+                                               (tid >> 4) * D + (tid & 15) * 8);
+    r.v[kb] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
+                                               (tid >> 1) * BT + (tid & 1) * 8);
   }
+  return use_mask;
 }
 
-__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, const TileRegs &r) {
+// Stores a tile to LDS.  K rows are stored as loaded (keys that are not
+// attended are masked to -inf in the scores, whatever K holds); V^T is zeroed
+// for unused blocks and for tokens at or past the context end, because
+// P = 0 times a non-finite V would still poison the accumulators.
+__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, const TileRegs &r,
+                                           uint32_t use_mask, int kt, int ctx) {
+  const bool tail = kt + BN > ctx;  // the tile reaches the end of the context (uniform)
 #pragma unroll
   for (int kb = 0; kb < KBLK; kb++) {
-    *reinterpret_cast<uint4 *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[kb];
+    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[kb];
+    u32x4_t v = r.v[kb];
+    if (!(use_mask & (1u << kb))) v = u32x4_t{0u, 0u, 0u, 0u};
+    if (tail) {
+      const int valid = ctx - (kt + kb * BT + (tid & 1) * 8);  // tokens of this 8-run inside the context
+      v[0] &= (valid > 0 ? 0x0000ffffu : 0u) | (valid > 1 ? 0xffff0000u : 0u);
+      v[1] &= (valid > 2 ? 0x0000ffffu : 0u) | (valid > 3 ? 0xffff0000u : 0u);
+      v[2] &= (valid > 4 ? 0x0000ffffu : 0u) | (valid > 5 ? 0xffff0000u : 0u);
+      v[3] &= (valid > 6 ? 0x0000ffffu : 0u) | (valid > 7 ? 0xffff0000u : 0u);
+    }
     uint16_t *dst = &v_lds[(kb * D + (tid >> 1)) * V_STRIDE + (tid & 1) * 8];
-    *reinterpret_cast<uint2 *>(dst) = make_uint2(r.v[kb].x, r.v[kb].y);
-    *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(r.v[kb].z, r.v[kb].w);
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(v[0], v[1]);
+    *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(v[2], v[3]);
   }
 }
 
@@ -192,14 +205,18 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const bool wave_live = wrow0 < chunk;
 
   TileRegs next;
-  load_tile(a, table, kvh, t_begin, ctx, klo, tid, next);
-  store_tile(k_lds[0], v_lds[0], tid, next);
+  bool bad = false;
+  uint32_t use_next = load_tile(a, fetch_entries(a, table, t_begin, lane), kvh, t_begin, ctx, klo, tid, next, bad);
+  int ent_next = fetch_entries(a, table, t_begin + BN, lane);
+  store_tile(k_lds[0], v_lds[0], tid, next, use_next, t_begin, ctx);
   __syncthreads();
 
   int buf = 0;
   for (int kt = t_begin; kt < khi; kt += BN, buf ^= 1) {
     const bool has_next = kt + BN < khi;
-    if (has_next) load_tile(a, table, kvh, kt + BN, ctx, klo, tid, next);  // in flight during the math
+    if (has_next) use_next = load_tile(a, ent_next, kvh, kt + BN, ctx, klo, tid, next, bad);  // in flight during the math
+    // entries of the tile after next, issued behind this tile's loads
+    ent_next = fetch_entries(a, table, kt + 2 * BN, lane);
 
     // tile needed by this wavefront?
     if (wave_live && kt <= wpos_last && kt + BN > wlo_first) {
@@ -219,20 +236,39 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
       }
 
       // ---- scale, mask, online softmax ----
+      // Unmasked tiles keep raw scores: the row max is taken on them and the
+      // scale (log2 units) is folded into the exp2 argument, fma(s, c, -m).
+      // Masked tiles are scaled first, then masked with -inf (c_exp = 1).
       const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
+      const float c = a.scale_log2e;
+      float c_exp = c;
       float tmax = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int st = 0; st < 2; st++) {
+        for (int st = 0; st < 2; st++) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-          float s = sacc[st][j] * a.scale_log2e;
-          if (need_mask) {
+          for (int j = 0; j < 16; j++) {
+            float s = sacc[st][j] * c;
             const int kp = kt + st * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
             if (kp > my_pos || kp < my_lo || kp >= ctx || !row_ok) s = -INFINITY;
+            sacc[st][j] = s;
+            tmax = fmaxf(tmax, s);
           }
-          sacc[st][j] = s;
-          tmax = fmaxf(tmax, s);
         }
+        c_exp = 1.0f;
+      } else if (c >= 0.0f) {  // c * max(s) == max(c * s) for c >= 0, exactly
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[st][j]);
+        tmax *= c;
+      } else {
+        float tmin = INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) tmin = fminf(tmin, sacc[st][j]);
+        tmax = tmin * c;
       }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
       const float m_new = fmaxf(m_run, tmax);
@@ -246,7 +282,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         float p[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-          p[j] = fast_exp2(sacc[st][j] - mref);
+          p[j] = fast_exp2(__builtin_fmaf(sacc[st][j], c_exp, -mref));
           psum += p[j];
         }
         pb[2 * st + 0] = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
@@ -276,11 +312,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
       }
     }
 
-    if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next);
+    if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
     __syncthreads();  // next tile visible; this tile no longer read
   }
 
   // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
+  if (bad && tid == 0) atomicOr(a.err, kErrBadBlock);  // a needed block was missing: its keys read as zeros
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
