@@ -56,12 +56,26 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
 }
 
-__device__ __forceinline__ f32x16_t mfma32(const uint4 &a, const uint4 &b, const f32x16_t &c) {
+__device__ __forceinline__ f32x16_t mfma32(const u32x4_t &a, const u32x4_t &b, const f32x16_t &c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                   0, 0, 0);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value of lane (l ^ 32): v_permlane32_swap exchanges the two 32-lane halves
+// of a pair of registers in the VALU, no LDS round trip.
+__device__ __forceinline__ float xor32_other(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  // r[0] holds the low half's values in both halves and r[1] the high half's
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// acc + lo + hi of a packed bf16 pair, exactly (dot product with (1, 1) in f32)
+__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
 
 // One lane's share of a key tile: for each of the 4 blocks, 16 B of K (token
 // tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..),
@@ -169,13 +183,13 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const int my_lo = a.window > 0 ? max(0, my_pos - a.window + 1) : 0;
 
   // ---- Q^T operand: 8 k-steps of 16 dims; lane holds dims 16ks + 8h .. +8 of its row ----
-  uint4 qb[8];
+  u32x4_t qb[8];
   {
     const uint16_t *qrow = a.q + ((size_t)(c0 + (row_ok ? my_row : 0)) * Hq + qh) * D;
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
-      uint4 t = *reinterpret_cast<const uint4 *>(qrow + ks * 16 + h * 8);
-      if (!row_ok) t = make_uint4(0, 0, 0, 0);
+      u32x4_t t = *reinterpret_cast<const u32x4_t *>(qrow + ks * 16 + h * 8);
+      if (!row_ok) t = u32x4_t{0u, 0u, 0u, 0u};
       qb[ks] = t;
     }
   }
@@ -230,7 +244,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         for (int j = 0; j < 16; j++) sacc[st][j] = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-          const uint4 ka = *reinterpret_cast<const uint4 *>(&kl[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
+          const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
           sacc[st] = mfma32(ka, qb[ks], sacc[st]);
         }
       }
@@ -270,33 +284,41 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           for (int j = 0; j < 16; j++) tmin = fminf(tmin, sacc[st][j]);
         tmax = tmin * c;
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m_run, tmax);
-      const float mref = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = fast_exp2(m_run - mref);
-      m_run = m_new;
-      float psum = 0.0f;
-      uint4 pb[4];  // P^T operands for the 4 16-key steps (one pool block each)
-#pragma unroll
-      for (int st = 0; st < 2; st++) {
-        float p[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-          p[j] = fast_exp2(__builtin_fmaf(sacc[st][j], c_exp, -mref));
-          psum += p[j];
-        }
-        pb[2 * st + 0] = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
-                                    pack_bf16(p[6], p[7]));
-        pb[2 * st + 1] = make_uint4(pack_bf16(p[8], p[9]), pack_bf16(p[10], p[11]), pack_bf16(p[12], p[13]),
-                                    pack_bf16(p[14], p[15]));
-      }
-      l_run = l_run * alpha + psum;
-      if (__any(alpha != 1.0f)) {  // the running max moved for some row: rescale the outputs
+      tmax = fmaxf(tmax, xor32_other(tmax));
+      // Lazy rescale: the reference max m_run only moves when a row's max grows
+      // by more than 8 (log2 units), so p <= 2^8 and the accumulators are
+      // rescaled on few tiles.  The result is the same softmax (any reference
+      // max gives it) with no risk of overflow in f32 / bf16.
+      const float m_cand = fmaxf(m_run, tmax);
+      const bool grow = m_cand > m_run + 8.0f;  // true on the first finite tile
+      if (__any(grow)) {
+        const float alpha = grow ? fast_exp2(m_run - m_cand) : 1.0f;  // 0 when m_run = -inf
+        m_run = grow ? m_cand : m_run;
+        l_run *= alpha;
 #pragma unroll
         for (int mt = 0; mt < 4; mt++)
 #pragma unroll
           for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
       }
+      const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
+      u32x4_t pb[4];  // P^T operands for the 4 16-key steps (one pool block each)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        float p[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) p[j] = fast_exp2(__builtin_fmaf(sacc[st][j], c_exp, -mref));
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+          pb[2 * st + q] = u32x4_t{pack_bf16(p[8 * q + 0], p[8 * q + 1]), pack_bf16(p[8 * q + 2], p[8 * q + 3]),
+                                   pack_bf16(p[8 * q + 4], p[8 * q + 5]), pack_bf16(p[8 * q + 6], p[8 * q + 7])};
+      }
+      // row sums of exactly the bf16 weights that enter P V (dot2 with (1, 1))
+      float psum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < KBLK; kb++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) psum = dot2_ones(pb[kb][e], psum);
+      l_run += psum;
 
       // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -306,8 +328,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           const uint16_t *vrow = &vl[(kb * D + mt * 32 + col) * V_STRIDE];
           const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
           const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
-          const uint4 va = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-          oacc[mt] = mfma32(va, pb[kb], oacc[mt]);
+          oacc[mt] = mfma32(u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y}, pb[kb], oacc[mt]);
         }
       }
     }
@@ -318,7 +339,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 
   // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
   if (bad && tid == 0) atomicOr(a.err, kErrBadBlock);  // a needed block was missing: its keys read as zeros
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = l_run + xor32_other(l_run);
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   uint16_t *orow = a.out + ((size_t)(c0 + my_row) * Hq + qh) * D;
