@@ -279,6 +279,123 @@ int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cac
                                                size_t row_count, size_t head_start, size_t head_len,
                                                float *h_output, size_t output_len);
 
+/* ------------------------------------------------------------------ */
+/* paged block allocator: BlockPool, session block tables, prefixes   */
+/* ------------------------------------------------------------------ */
+/*
+ * kir-ai's BlockPool (crates/llm-kv-cache/src/block_pool.rs:38-318,344-896)
+ * over the blocks of a device KV pool: block i of the allocator is block i of
+ * the llh_kv_pool, so session tables map straight to the int32 rows of
+ * llh_decode_desc / llh_prefill_desc.  Every entry point takes the pool's
+ * mutex.  Functions that return Option / bool in the reference report through
+ * an out parameter (0 id = None; 0/1 flag) and return LLH_OK.
+ */
+typedef struct llh_block_pool llh_block_pool;
+
+/* SHA-256 (FIPS 180-4) of a byte string. */
+int llh_sha256(const void *data, size_t len, uint8_t out[32]);
+/* cache_block_chain_hash (crates/llm-kv-cache/src/block.rs:8-33): SHA-256 of
+ * "kir-ai-kv-block-chain/v1" || u64le(len) || model_id || u64le(len) ||
+ * cache_context || previous_hash[32] || u64le(n) || u32le token ids. */
+int llh_cache_block_chain_hash(const char *model_id, size_t model_len, const char *cache_context,
+                               size_t context_len, const uint8_t previous_hash[32], const uint32_t *token_ids,
+                               size_t n, uint8_t out[32]);
+
+/* BlockPool::new(block_count, block_capacity_tokens, vector_len)
+ * (block_pool.rs:151-163, 345-370): bookkeeping only, no payload. */
+int llh_block_pool_create_host(size_t block_count, size_t block_capacity_tokens, size_t vector_len,
+                               llh_block_pool **out);
+/* A BlockPool over every block of a device pool (capacity = the pool's
+ * block_tokens, vector_len = kv_heads * head_dim).  The pool must outlive it. */
+int llh_block_pool_create(llh_ctx *ctx, llh_kv_pool *pool, llh_block_pool **out);
+int llh_block_pool_destroy(llh_block_pool *bp);
+const char *llh_block_pool_last_error(const llh_block_pool *bp);
+
+/* total_blocks / free_blocks / allocated_blocks / session_count (block_pool.rs:165-179,193-195) */
+typedef struct llh_block_pool_counts {
+  uint64_t total_blocks;
+  uint64_t free_blocks;
+  uint64_t allocated_blocks;
+  uint64_t sessions;
+} llh_block_pool_counts;
+int llh_block_pool_get_counts(const llh_block_pool *bp, llh_block_pool_counts *out);
+
+/* PagedKvCacheMetricsSnapshot (block_pool.rs:99-122) */
+typedef struct llh_paged_kv_metrics {
+  uint64_t total_blocks, resident_blocks, active_blocks, blocks_in_use, free_blocks, free_list_blocks;
+  double pool_utilization_pct;
+  uint64_t sessions, session_block_tables, shared_blocks, refcount_total;
+  double avg_refcount;
+  uint64_t max_refcount, max_refcount_seen, total_refcount_increments, total_cow_clones, cow_bytes_saved;
+  uint64_t blocks_evicted_lru, sessions_evicted_lru, eviction_high_water_mark, pool_high_water_blocks;
+} llh_paged_kv_metrics;
+int llh_block_pool_metrics(const llh_block_pool *bp, llh_paged_kv_metrics *out);
+
+/* CacheBlock metadata (block.rs:36-53) and its device pool index.
+ * payload_bytes: bytes of the block's K and V (f32 for host-only pools, as the
+ * reference counts them; device bytes incl. scales for device pools). */
+typedef struct llh_cache_block_info {
+  uint64_t block_id;
+  int64_t pool_index;
+  uint64_t revision, capacity_tokens, vector_len, token_count, ref_count, last_access, payload_bytes;
+  int32_t has_content_hash;
+  uint8_t content_hash[32];
+} llh_cache_block_info;
+/* LLH_ERR_STALE for an id this pool does not hold. */
+int llh_block_pool_block_info(const llh_block_pool *bp, uint64_t block_id, llh_cache_block_info *out);
+
+/* allocate / deallocate (= release) / retain / touch / lru_block (block_pool.rs:669-728) */
+int llh_block_pool_allocate(llh_block_pool *bp, uint64_t *block_id);
+int llh_block_pool_release(llh_block_pool *bp, uint64_t block_id, int32_t *released);
+int llh_block_pool_retain(llh_block_pool *bp, uint64_t block_id, int32_t *retained);
+int llh_block_pool_touch(llh_block_pool *bp, uint64_t block_id, int32_t *touched);
+int llh_block_pool_lru_block(const llh_block_pool *bp, uint64_t *block_id);
+/* CacheBlock::set_content_hash via block_mut (block_pool.rs:730-737): only on
+ * a block with ref_count 1 (else LLH_ERR_INVALID_SHAPE); hash NULL clears. */
+int llh_block_pool_set_content_hash(llh_block_pool *bp, uint64_t block_id, const uint8_t *hash);
+
+/* sessions (block_pool.rs:197-227, 433-481) */
+int llh_block_pool_create_session(llh_block_pool *bp, uint64_t *session_id);
+int llh_block_pool_release_session(llh_block_pool *bp, uint64_t session_id, int32_t *released);
+/* evicts least-recently-used sessions when no block is free */
+int llh_block_pool_allocate_for_session(llh_block_pool *bp, uint64_t session_id, uint64_t *block_id);
+int llh_block_pool_append_block_to_session(llh_block_pool *bp, uint64_t session_id, uint64_t block_id);
+int llh_block_pool_read_session_block(llh_block_pool *bp, uint64_t session_id, size_t index, uint64_t *block_id);
+typedef struct llh_session_info {
+  uint64_t session_id, created_at, last_access, block_count, owned_block_count;
+} llh_session_info;
+int llh_block_pool_session_info(const llh_block_pool *bp, uint64_t session_id, llh_session_info *out);
+/* The session's table as BlockIds and device pool indices (either may be NULL). */
+int llh_block_pool_session_blocks(const llh_block_pool *bp, uint64_t session_id, uint64_t *h_ids,
+                                  int32_t *h_pool_indices, size_t capacity, size_t *count);
+int llh_block_pool_lru_session(const llh_block_pool *bp, uint64_t *session_id);
+
+/* prefix registry keyed by the terminal chain hash (block_pool.rs:483-519) */
+int llh_block_pool_register_prefix(llh_block_pool *bp, const uint8_t prefix_hash[32], const uint64_t *block_ids,
+                                   size_t n);
+int llh_block_pool_lookup_prefix(const llh_block_pool *bp, const uint8_t prefix_hash[32], uint64_t *h_ids,
+                                 size_t capacity, size_t *count, int32_t *found);
+int llh_block_pool_attach_prefix_to_session(llh_block_pool *bp, uint64_t session_id, const uint8_t prefix_hash[32],
+                                            uint64_t *h_ids, size_t capacity, size_t *count, int32_t *found);
+/* copy_on_write_session_block (block_pool.rs:521-603): a shared block is
+ * cloned (device payload copy for device pools) into a fresh block that
+ * replaces it in this session's table. */
+int llh_block_pool_copy_on_write_session_block(llh_block_pool *bp, uint64_t session_id, size_t index,
+                                               uint64_t *block_id);
+
+/* payload, device pools only */
+/* CacheBlock::append (block.rs:250-272) through block_mut: one token row to
+ * the block's next slot (quantised on write for int8); exclusive blocks only. */
+int llh_block_pool_append_f32(llh_block_pool *bp, uint64_t block_id, const float *h_key, const float *h_value,
+                              size_t len);
+/* Records n rows the caller wrote with llh_kv_append at slots
+ * pool_index * block_tokens + token_count + i (token_count, hash, revision). */
+int llh_block_pool_commit_tokens(llh_block_pool *bp, uint64_t block_id, size_t n);
+/* CacheBlock::keys() / values() (block.rs:300-306): token_count rows of
+ * vector_len f32 (dequantised); tensor 0 = K, 1 = V. */
+int llh_block_pool_read_rows_f32(llh_block_pool *bp, uint64_t block_id, int32_t tensor, float *h_out,
+                                 size_t capacity, size_t *count);
+
 #ifdef __cplusplus
 }
 #endif

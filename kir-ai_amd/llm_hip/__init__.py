@@ -144,10 +144,54 @@ class BlockRun(ctypes.Structure):
     ]
 
 
+class BlockPoolCounts(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("total_blocks", "free_blocks", "allocated_blocks", "sessions")]
+
+
+class PagedKvMetrics(ctypes.Structure):
+    """PagedKvCacheMetricsSnapshot (crates/llm-kv-cache/src/block_pool.rs:99-122)."""
+    _fields_ = (
+        [(n, ctypes.c_uint64) for n in ("total_blocks", "resident_blocks", "active_blocks", "blocks_in_use",
+                                         "free_blocks", "free_list_blocks")]
+        + [("pool_utilization_pct", ctypes.c_double)]
+        + [(n, ctypes.c_uint64) for n in ("sessions", "session_block_tables", "shared_blocks", "refcount_total")]
+        + [("avg_refcount", ctypes.c_double)]
+        + [(n, ctypes.c_uint64) for n in ("max_refcount", "max_refcount_seen", "total_refcount_increments",
+                                         "total_cow_clones", "cow_bytes_saved", "blocks_evicted_lru",
+                                         "sessions_evicted_lru", "eviction_high_water_mark",
+                                         "pool_high_water_blocks")]
+    )
+
+
+class CacheBlockInfo(ctypes.Structure):
+    _fields_ = [
+        ("block_id", ctypes.c_uint64),
+        ("pool_index", ctypes.c_int64),
+        ("revision", ctypes.c_uint64),
+        ("capacity_tokens", ctypes.c_uint64),
+        ("vector_len", ctypes.c_uint64),
+        ("token_count", ctypes.c_uint64),
+        ("ref_count", ctypes.c_uint64),
+        ("last_access", ctypes.c_uint64),
+        ("payload_bytes", ctypes.c_uint64),
+        ("has_content_hash", ctypes.c_int32),
+        ("content_hash", ctypes.c_uint8 * 32),
+    ]
+
+    def content_hash_bytes(self) -> Optional[bytes]:
+        return bytes(self.content_hash) if self.has_content_hash else None
+
+
+class SessionInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("session_id", "created_at", "last_access", "block_count",
+                                              "owned_block_count")]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _SZ = ctypes.c_size_t
 _FP = ctypes.POINTER(ctypes.c_float)
+_U64 = ctypes.c_uint64
 
 # name -> (restype, argtypes); this is the full exported surface of include/llm_hip.h
 SIGNATURES = {
@@ -184,6 +228,37 @@ SIGNATURES = {
         [_P, _P, _FP, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _FP, _SZ],
     ),
     "llh_select_kv_cache_head_rows_f32_in_place": (ctypes.c_int, [_P, _P, _I32, _SZ, _SZ, _SZ, _FP, _SZ]),
+    "llh_sha256": (ctypes.c_int, [_P, _SZ, _P]),
+    "llh_cache_block_chain_hash": (ctypes.c_int, [ctypes.c_char_p, _SZ, ctypes.c_char_p, _SZ, _P, _P, _SZ, _P]),
+    "llh_block_pool_create_host": (ctypes.c_int, [_SZ, _SZ, _SZ, ctypes.POINTER(_P)]),
+    "llh_block_pool_create": (ctypes.c_int, [_P, _P, ctypes.POINTER(_P)]),
+    "llh_block_pool_destroy": (ctypes.c_int, [_P]),
+    "llh_block_pool_last_error": (ctypes.c_char_p, [_P]),
+    "llh_block_pool_get_counts": (ctypes.c_int, [_P, ctypes.POINTER(BlockPoolCounts)]),
+    "llh_block_pool_metrics": (ctypes.c_int, [_P, ctypes.POINTER(PagedKvMetrics)]),
+    "llh_block_pool_block_info": (ctypes.c_int, [_P, _U64, ctypes.POINTER(CacheBlockInfo)]),
+    "llh_block_pool_allocate": (ctypes.c_int, [_P, ctypes.POINTER(_U64)]),
+    "llh_block_pool_release": (ctypes.c_int, [_P, _U64, ctypes.POINTER(_I32)]),
+    "llh_block_pool_retain": (ctypes.c_int, [_P, _U64, ctypes.POINTER(_I32)]),
+    "llh_block_pool_touch": (ctypes.c_int, [_P, _U64, ctypes.POINTER(_I32)]),
+    "llh_block_pool_lru_block": (ctypes.c_int, [_P, ctypes.POINTER(_U64)]),
+    "llh_block_pool_set_content_hash": (ctypes.c_int, [_P, _U64, _P]),
+    "llh_block_pool_create_session": (ctypes.c_int, [_P, ctypes.POINTER(_U64)]),
+    "llh_block_pool_release_session": (ctypes.c_int, [_P, _U64, ctypes.POINTER(_I32)]),
+    "llh_block_pool_allocate_for_session": (ctypes.c_int, [_P, _U64, ctypes.POINTER(_U64)]),
+    "llh_block_pool_append_block_to_session": (ctypes.c_int, [_P, _U64, _U64]),
+    "llh_block_pool_read_session_block": (ctypes.c_int, [_P, _U64, _SZ, ctypes.POINTER(_U64)]),
+    "llh_block_pool_session_info": (ctypes.c_int, [_P, _U64, ctypes.POINTER(SessionInfo)]),
+    "llh_block_pool_session_blocks": (ctypes.c_int, [_P, _U64, _P, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "llh_block_pool_lru_session": (ctypes.c_int, [_P, ctypes.POINTER(_U64)]),
+    "llh_block_pool_register_prefix": (ctypes.c_int, [_P, _P, _P, _SZ]),
+    "llh_block_pool_lookup_prefix": (ctypes.c_int, [_P, _P, _P, _SZ, ctypes.POINTER(_SZ), ctypes.POINTER(_I32)]),
+    "llh_block_pool_attach_prefix_to_session": (
+        ctypes.c_int, [_P, _U64, _P, _P, _SZ, ctypes.POINTER(_SZ), ctypes.POINTER(_I32)]),
+    "llh_block_pool_copy_on_write_session_block": (ctypes.c_int, [_P, _U64, _SZ, ctypes.POINTER(_U64)]),
+    "llh_block_pool_append_f32": (ctypes.c_int, [_P, _U64, _FP, _FP, _SZ]),
+    "llh_block_pool_commit_tokens": (ctypes.c_int, [_P, _U64, _SZ]),
+    "llh_block_pool_read_rows_f32": (ctypes.c_int, [_P, _U64, _I32, _FP, _SZ, ctypes.POINTER(_SZ)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -555,3 +630,230 @@ class HipNativeMatvecBackend:
                                                head_start: int, head_len: int, output: np.ndarray) -> None:
         self.ctx.check(self.ctx.lib.llh_select_kv_cache_head_rows_f32_in_place(
             self.ctx.handle, cache.handle, tensor, row_count, head_start, head_len, _f32_ptr(output), output.size))
+
+
+# ---------------------------------------------------------------------------
+# BlockPool mirror (crates/llm-kv-cache/src/block_pool.rs, block.rs:8-33)
+# ---------------------------------------------------------------------------
+
+def sha256(data: bytes) -> bytes:
+    """SHA-256 computed by the library (FIPS 180-4)."""
+    lib = load_library()
+    out = (ctypes.c_uint8 * 32)()
+    buf = ctypes.create_string_buffer(bytes(data), len(data) or 1)
+    st = lib.llh_sha256(ctypes.cast(buf, _P), len(data), out)
+    if st != OK:
+        raise LlhError(st, "sha256")
+    return bytes(out)
+
+
+def cache_block_chain_hash(model_id: str, cache_context: str, previous_hash: bytes, token_ids) -> bytes:
+    """cache_block_chain_hash (crates/llm-kv-cache/src/block.rs:8-28)."""
+    lib = load_library()
+    m, c = model_id.encode(), cache_context.encode()
+    prev = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(previous_hash))
+    toks = np.ascontiguousarray(np.asarray(token_ids, dtype=np.uint32))
+    out = (ctypes.c_uint8 * 32)()
+    st = lib.llh_cache_block_chain_hash(m, len(m), c, len(c), prev, toks.ctypes.data_as(_P) if toks.size else None,
+                                        toks.size, out)
+    if st != OK:
+        raise LlhError(st, "chain hash")
+    return bytes(out)
+
+
+class BlockPool:
+    """kir-ai's BlockPool with the reference's method names.  ``new`` makes a
+    bookkeeping-only pool (BlockPool::new(block_count, capacity, vector_len));
+    ``over`` makes one over a device KvPool whose blocks carry the payload.
+    Option results are None, bool results are bool, errors raise LlhError."""
+
+    def __init__(self, handle, ctx: Optional[Context] = None, kv_pool: Optional["KvPool"] = None):
+        self._lib = load_library()
+        self._h = handle
+        self._ctx = ctx
+        self._kv_pool = kv_pool  # keeps the device pool alive
+
+    @classmethod
+    def new(cls, block_count: int, block_capacity_tokens: int, vector_len: int) -> "BlockPool":
+        lib = load_library()
+        h = _P()
+        st = lib.llh_block_pool_create_host(block_count, block_capacity_tokens, vector_len, ctypes.byref(h))
+        if st != OK:
+            raise LlhError(st, "BlockPool::new")
+        return cls(h)
+
+    @classmethod
+    def over(cls, ctx: Context, kv_pool: "KvPool") -> "BlockPool":
+        h = _P()
+        ctx.check(ctx.lib.llh_block_pool_create(ctx.handle, kv_pool.handle, ctypes.byref(h)))
+        return cls(h, ctx, kv_pool)
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.llh_block_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int) -> None:
+        if st != OK:
+            raise LlhError(st, (self._lib.llh_block_pool_last_error(self._h) or b"").decode())
+
+    def _u64_out(self, fn, *args) -> Optional[int]:
+        v = _U64()
+        self._check(fn(self._h, *args, ctypes.byref(v)))
+        return v.value or None
+
+    def _flag(self, fn, *args) -> bool:
+        v = _I32()
+        self._check(fn(self._h, *args, ctypes.byref(v)))
+        return bool(v.value)
+
+    def _counts(self) -> BlockPoolCounts:
+        c = BlockPoolCounts()
+        self._check(self._lib.llh_block_pool_get_counts(self._h, ctypes.byref(c)))
+        return c
+
+    def total_blocks(self) -> int:
+        return self._counts().total_blocks
+
+    def free_blocks(self) -> int:
+        return self._counts().free_blocks
+
+    def allocated_blocks(self) -> int:
+        return self._counts().allocated_blocks
+
+    def session_count(self) -> int:
+        return self._counts().sessions
+
+    def metrics_snapshot(self) -> PagedKvMetrics:
+        m = PagedKvMetrics()
+        self._check(self._lib.llh_block_pool_metrics(self._h, ctypes.byref(m)))
+        return m
+
+    def block(self, block_id: int) -> Optional[CacheBlockInfo]:
+        info = CacheBlockInfo()
+        st = self._lib.llh_block_pool_block_info(self._h, block_id, ctypes.byref(info))
+        if st == ERR_STALE:
+            return None
+        self._check(st)
+        return info
+
+    def allocate(self) -> Optional[int]:
+        return self._u64_out(self._lib.llh_block_pool_allocate)
+
+    def deallocate(self, block_id: int) -> bool:
+        return self.release(block_id)
+
+    def release(self, block_id: int) -> bool:
+        return self._flag(self._lib.llh_block_pool_release, block_id)
+
+    def retain(self, block_id: int) -> bool:
+        return self._flag(self._lib.llh_block_pool_retain, block_id)
+
+    def touch(self, block_id: int) -> Optional[bool]:
+        return True if self._flag(self._lib.llh_block_pool_touch, block_id) else None
+
+    def lru_block(self) -> Optional[int]:
+        return self._u64_out(self._lib.llh_block_pool_lru_block)
+
+    def set_content_hash(self, block_id: int, content_hash: Optional[bytes]) -> None:
+        buf = None if content_hash is None else (ctypes.c_uint8 * 32).from_buffer_copy(bytes(content_hash))
+        self._check(self._lib.llh_block_pool_set_content_hash(self._h, block_id, buf))
+
+    def create_session(self) -> int:
+        return self._u64_out(self._lib.llh_block_pool_create_session)
+
+    def release_session(self, session_id: int) -> bool:
+        return self._flag(self._lib.llh_block_pool_release_session, session_id)
+
+    def allocate_for_session(self, session_id: int) -> Optional[int]:
+        return self._u64_out(self._lib.llh_block_pool_allocate_for_session, session_id)
+
+    def append_block_to_session(self, session_id: int, block_id: int) -> None:
+        self._check(self._lib.llh_block_pool_append_block_to_session(self._h, session_id, block_id))
+
+    def read_session_block(self, session_id: int, index: int) -> Optional[int]:
+        return self._u64_out(self._lib.llh_block_pool_read_session_block, session_id, index)
+
+    def session(self, session_id: int) -> Optional[SessionInfo]:
+        info = SessionInfo()
+        st = self._lib.llh_block_pool_session_info(self._h, session_id, ctypes.byref(info))
+        if st == ERR_STALE:
+            return None
+        self._check(st)
+        return info
+
+    def session_blocks(self, session_id: int) -> tuple[list, np.ndarray]:
+        """(BlockIds, int32 device pool indices) of the session's table, in order."""
+        n = _SZ()
+        self._check(self._lib.llh_block_pool_session_blocks(self._h, session_id, None, None, 0, ctypes.byref(n)))
+        ids = (_U64 * max(1, n.value))()
+        idx = np.zeros(n.value, np.int32)
+        self._check(self._lib.llh_block_pool_session_blocks(self._h, session_id, ids,
+                                                            idx.ctypes.data_as(_P) if n.value else None,
+                                                            n.value, ctypes.byref(n)))
+        return list(ids)[: n.value], idx
+
+    def lru_session(self) -> Optional[int]:
+        return self._u64_out(self._lib.llh_block_pool_lru_session)
+
+    def register_prefix(self, prefix_hash: bytes, block_ids) -> None:
+        h = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(prefix_hash))
+        ids = (_U64 * max(1, len(block_ids)))(*block_ids)
+        self._check(self._lib.llh_block_pool_register_prefix(self._h, h, ids, len(block_ids)))
+
+    def _ids_query(self, fn, *args) -> Optional[list]:
+        n, found = _SZ(), _I32()
+        cap = self.total_blocks()
+        ids = (_U64 * max(1, cap))()
+        self._check(fn(self._h, *args, ids, cap, ctypes.byref(n), ctypes.byref(found)))
+        return list(ids)[: n.value] if found.value else None
+
+    def lookup_prefix(self, prefix_hash: bytes) -> Optional[list]:
+        h = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(prefix_hash))
+        return self._ids_query(self._lib.llh_block_pool_lookup_prefix, h)
+
+    def attach_prefix_to_session(self, session_id: int, prefix_hash: bytes) -> Optional[list]:
+        h = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(prefix_hash))
+        n, found = _SZ(), _I32()
+        cap = self.total_blocks()
+        ids = (_U64 * max(1, cap))()
+        self._check(self._lib.llh_block_pool_attach_prefix_to_session(self._h, session_id, h, ids, cap,
+                                                                      ctypes.byref(n), ctypes.byref(found)))
+        return list(ids)[: n.value] if found.value else None
+
+    def copy_on_write_session_block(self, session_id: int, index: int) -> int:
+        return self._u64_out(self._lib.llh_block_pool_copy_on_write_session_block, session_id, index)
+
+    # payload (device pools)
+    def append(self, block_id: int, key, value) -> None:
+        """CacheBlock::append through block_mut (exclusive blocks only)."""
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        if k.size != v.size:
+            raise LlhError(ERR_INVALID_SHAPE, "key and value rows differ in length")
+        self._check(self._lib.llh_block_pool_append_f32(self._h, block_id, _f32_ptr(k), _f32_ptr(v), k.size))
+
+    def commit_tokens(self, block_id: int, n: int) -> None:
+        self._check(self._lib.llh_block_pool_commit_tokens(self._h, block_id, n))
+
+    def rows(self, block_id: int, tensor: int) -> np.ndarray:
+        """CacheBlock::keys() (tensor 0) / values() (tensor 1): [token_count, vector_len] f32."""
+        n = _SZ()
+        self._check(self._lib.llh_block_pool_read_rows_f32(self._h, block_id, tensor, None, 0, ctypes.byref(n)))
+        out = np.zeros(max(1, n.value), np.float32)
+        self._check(self._lib.llh_block_pool_read_rows_f32(self._h, block_id, tensor, _f32_ptr(out), n.value,
+                                                          ctypes.byref(n)))
+        info = self.block(block_id)
+        return out[: n.value].reshape(info.token_count, info.vector_len)
+
+    def keys(self, block_id: int) -> np.ndarray:
+        return self.rows(block_id, 0)
+
+    def values(self, block_id: int) -> np.ndarray:
+        return self.rows(block_id, 1)

@@ -405,3 +405,23 @@ def quantize_fp8_block(x: np.ndarray) -> tuple[int, np.ndarray, float]:
     s = ctypes.c_float()
     st = lib().orc_quantize_fp8_block(_p(a), a.size, _p(codes), ctypes.addressof(s))
     return st, codes, s.value
+
+
+def chain_hash(model_id: str, cache_context: str, previous_hash: bytes, token_ids) -> bytes:
+    """cache_block_chain_hash restated (crates/llm-kv-cache/src/block.rs:8-33): SHA-256
+    (Python's hashlib, an independent implementation) over the domain tag
+    "kir-ai-kv-block-chain/v1", the u64-LE length-prefixed model id and cache
+    context, the 32-byte previous hash, the u64-LE token count and the u32-LE ids."""
+    import hashlib
+    import struct
+
+    m, c = model_id.encode(), cache_context.encode()
+    h = hashlib.sha256()
+    h.update(b"kir-ai-kv-block-chain/v1")
+    h.update(struct.pack("<Q", len(m)) + m)
+    h.update(struct.pack("<Q", len(c)) + c)
+    h.update(bytes(previous_hash))
+    h.update(struct.pack("<Q", len(token_ids)))
+    for t in token_ids:
+        h.update(struct.pack("<I", int(t)))
+    return h.digest()

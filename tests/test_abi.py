@@ -45,6 +45,10 @@ STRUCTS = {
     "llh_metrics": llm_hip.Metrics,
     "llh_layer_cache_state": llm_hip.LayerCacheState,
     "llh_block_run": llm_hip.BlockRun,
+    "llh_block_pool_counts": llm_hip.BlockPoolCounts,
+    "llh_paged_kv_metrics": llm_hip.PagedKvMetrics,
+    "llh_cache_block_info": llm_hip.CacheBlockInfo,
+    "llh_session_info": llm_hip.SessionInfo,
 }
 
 
@@ -86,6 +90,8 @@ def test_host_only_entry_points():
     assert lib.llh_kv_pool_destroy(None) == llm_hip.ERR_NULL
     assert lib.llh_layer_cache_destroy(None) == llm_hip.ERR_NULL
     assert lib.llh_paged_decode(None, None, None, None, None, 0.0, None) == llm_hip.ERR_NULL
+    assert lib.llh_block_pool_destroy(None) == llm_hip.ERR_NULL
+    assert lib.llh_block_pool_create(None, None, None) == llm_hip.ERR_NULL
     out = ctypes.c_void_p()
     assert lib.llh_ctx_create(0, None) == llm_hip.ERR_NULL
     # workspace sizing is host arithmetic
