@@ -195,6 +195,25 @@ typedef struct llh_prefill_desc {
 int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
                       void *d_out, float score_scale, void *stream);
 
+/* Output projection after attention, on the device: the batched form of
+ * bf16_matvecs_row_major_f32_flat_inputs (native_matvec.rs:264-272) with the
+ * reference's per-row dot (crates/llm-backend/src/core/safetensors/math.rs:66-72).
+ * out[i][r] = sum_c W[r][c] * x[i][c]; W bf16 [rows][cols] row-major, x [n][cols]
+ * bf16 (x_f32 = 0) or f32 (x_f32 = 1, rounded to bf16 for the MFMA), out f32
+ * [n][rows], f32 accumulation.  cols must be a multiple of 128 and W, x 16-byte
+ * aligned, else LLH_ERR_UNSUPPORTED. */
+int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, const void *d_x, int32_t x_f32,
+                        int32_t n, float *d_out, void *stream);
+
+/* full_attention_cache_mix_bf16_output_projection_f32_in_place
+ * (native_matvec.rs:671-685), batched: one llh_paged_decode step whose bf16
+ * attention output stays in the context workspace, then out[b] = W_o attn[b]
+ * on the same stream.  W_o bf16 [rows][num_q_heads * head_dim]; out f32
+ * [num_seqs][rows]. */
+int llh_paged_decode_output_projection(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
+                                       const void *d_q, const void *d_w_o, int32_t rows, float *d_out,
+                                       float score_scale, void *stream);
+
 /* Bit-exact gather of positions [lo, hi) of sequence `seq` through its block
  * table into d_out [hi-lo][kv_heads][head_dim] raw elements (2 bytes bf16,
  * 1 byte int8/fp8); tensor 0 = K, 1 = V.  The gather half of
@@ -271,6 +290,18 @@ int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cach
                                               size_t query_len, size_t row_count, size_t num_attention_heads,
                                               size_t num_key_value_heads, size_t head_dim, float score_scale,
                                               float *h_output, size_t output_len);
+
+/* NativeMatvecBackend::full_attention_cache_mix_bf16_output_projection_f32_in_place
+ * (native_matvec.rs:671-685; Metal form crates/llm-native-runtime/src/native_matvec.rs:4418-4492):
+ * attention as above, then the o_proj matvec on the device.  d_w_o: device bf16
+ * [w_rows][w_cols] (the safetensors tensor, uploaded once by the caller).
+ * h_output receives w_rows f32 values.  LLH_NOT_HANDLED (the trait's Ok(false))
+ * when w_cols != heads * head_dim, output_len < w_rows, or w_cols is not a
+ * multiple of 128. */
+int llh_full_attention_cache_mix_bf16_output_projection_f32_in_place(
+    llh_ctx *ctx, const llh_layer_cache *cache, const float *h_query, size_t query_len, size_t row_count,
+    size_t num_attention_heads, size_t num_key_value_heads, size_t head_dim, float score_scale, const void *d_w_o,
+    int32_t w_rows, int32_t w_cols, float *h_output, size_t output_len);
 
 /* NativeMatvecBackend::select_kv_cache_head_rows_f32_in_place
  * (native_matvec.rs:619-641): rows [0, row_count) of one head slice

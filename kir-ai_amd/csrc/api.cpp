@@ -317,14 +317,20 @@ static int check_desc_common(llh_ctx *ctx, const llh_kv_pool *pool, int32_t num_
   return LLH_OK;
 }
 
-int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q, void *d_out,
-                     float score_scale, void *stream) {
+}  // extern "C"
+
+// One decode step.  With d_out == nullptr the bf16 output goes to a buffer of
+// `extra_bytes` placed after the call's own workspace regions (returned in
+// *extra_ptr), so a following kernel on the stream can consume it without any
+// allocation.
+static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                             void *d_out, float score_scale, void *stream, size_t extra_bytes, void **extra_ptr) {
   if (!ctx || !pool || !desc) return LLH_ERR_NULL;
   int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
   if (st != LLH_OK) return st;
   if (desc->num_seqs == 0) return LLH_OK;
   if (desc->max_seq_len < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "max_seq_len must be >= 0");
-  if (!d_q || !d_out || !desc->d_seq_lens || !desc->d_block_tables)
+  if (!d_q || (!d_out && !extra_ptr) || !desc->d_seq_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   const PoolView &pv = pool->view;
@@ -342,9 +348,12 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
     const size_t ml_off = kCounterBytes;
     const size_t o_off = ml_off + align_up(rows * sizeof(float2));
-    st = ctx->ensure_ws(o_off + rows * kFastHeadDim * sizeof(float));
+    const size_t need = align_up(o_off + rows * kFastHeadDim * sizeof(float));
+    st = ctx->ensure_ws(need + extra_bytes);
     if (st != LLH_OK) return st;
     char *ws = static_cast<char *>(ctx->ws);
+    if (extra_ptr) *extra_ptr = ws + need;
+    if (!d_out) d_out = ws + need;
     DecodeArgs a{};
     a.pool = pv;
     a.q = static_cast<const uint16_t *>(d_q);
@@ -382,8 +391,11 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   const int span = desc->window > 0 ? std::min(desc->window, desc->max_seq_len) : desc->max_seq_len;
   const int stride = std::max(1, span);
   const size_t off = kCounterBytes;
-  st = ctx->ensure_ws(off + (size_t)desc->num_seqs * desc->num_q_heads * stride * sizeof(float));
+  const size_t need = align_up(off + (size_t)desc->num_seqs * desc->num_q_heads * stride * sizeof(float));
+  st = ctx->ensure_ws(need + extra_bytes);
   if (st != LLH_OK) return st;
+  if (extra_ptr) *extra_ptr = static_cast<char *>(ctx->ws) + need;
+  if (!d_out) d_out = static_cast<char *>(ctx->ws) + need;
   GenericDecodeArgs g{};
   g.pool = pv;
   g.q = d_q;
@@ -402,6 +414,78 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   g.scale = score_scale;
   hipError_t e = launch_decode_generic(g, 0, 0, s);
   if (e != hipSuccess) return ctx->hip_fail(e, "generic decode launch");
+  return LLH_OK;
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int check_projection(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, float *d_out) {
+  if (!d_w || !d_out) return ctx->fail(LLH_ERR_NULL, "null device pointer in projection call");
+  if (rows <= 0 || cols <= 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "projection rows and columns must be > 0");
+  if (cols % kMatvecColsMultiple != 0 || !aligned16(d_w)) {
+    ctx->not_handled++;
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "projection takes 16-byte aligned weights with columns a multiple of 128");
+  }
+  return LLH_OK;
+}
+
+extern "C" {
+
+int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q, void *d_out,
+                     float score_scale, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (!d_out && desc->num_seqs > 0) return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
+  return paged_decode_impl(ctx, pool, desc, d_q, d_out, score_scale, stream, 0, nullptr);
+}
+
+int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, const void *d_x, int32_t x_f32,
+                        int32_t n, float *d_out, void *stream) {
+  if (!ctx) return LLH_ERR_NULL;
+  if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "input count must be >= 0");
+  if (n == 0) return LLH_OK;
+  int st = check_projection(ctx, d_w, rows, cols, d_out);
+  if (st != LLH_OK) return st;
+  if (!d_x) return ctx->fail(LLH_ERR_NULL, "null device pointer in projection call");
+  if (!aligned16(d_x)) return ctx->fail(LLH_ERR_UNSUPPORTED, "projection inputs must be 16-byte aligned");
+  MatvecArgs a{};
+  a.w = static_cast<const uint16_t *>(d_w);
+  a.x = d_x;
+  a.out = d_out;
+  a.rows = rows;
+  a.cols = cols;
+  a.n = n;
+  a.ldx = cols;
+  a.ldo = rows;
+  a.x_f32 = x_f32 ? 1 : 0;
+  hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
+  return LLH_OK;
+}
+
+int llh_paged_decode_output_projection(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
+                                       const void *d_q, const void *d_w_o, int32_t rows, float *d_out,
+                                       float score_scale, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (desc->num_seqs <= 0) return desc->num_seqs == 0 ? LLH_OK : ctx->fail(LLH_ERR_INVALID_SHAPE, "num_seqs < 0");
+  const int32_t cols = desc->num_q_heads * pool->view.head_dim;
+  int st = check_projection(ctx, d_w_o, rows, cols, d_out);
+  if (st != LLH_OK) return st;
+  const size_t attn_bytes = align_up((size_t)desc->num_seqs * cols * sizeof(uint16_t));
+  void *attn = nullptr;
+  st = paged_decode_impl(ctx, pool, desc, d_q, nullptr, score_scale, stream, attn_bytes, &attn);
+  if (st != LLH_OK) return st;
+  MatvecArgs a{};
+  a.w = static_cast<const uint16_t *>(d_w_o);
+  a.x = attn;
+  a.out = d_out;
+  a.rows = rows;
+  a.cols = cols;
+  a.n = desc->num_seqs;
+  a.ldx = cols;
+  a.ldo = rows;
+  a.x_f32 = 0;
+  hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
   return LLH_OK;
 }
 
@@ -821,10 +905,15 @@ int llh_append_kv_cache_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h
   return layer_append(ctx, cache, h_key, h_value, len, false);
 }
 
-int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache_c, const float *h_query,
-                                              size_t query_len, size_t row_count, size_t num_attention_heads,
-                                              size_t num_key_value_heads, size_t head_dim, float score_scale,
-                                              float *h_output, size_t output_len) {
+}  // extern "C"
+
+// Attention over the first row_count logical rows of a layer cache, f32 in and
+// out.  With d_w != nullptr the f32 attention output is projected on the
+// device by W [w_rows][heads * head_dim] bf16 and h_output receives the w_rows
+// projected values instead.
+static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const float *h_query, size_t query_len,
+                          size_t row_count, size_t num_attention_heads, size_t num_key_value_heads, size_t head_dim,
+                          float score_scale, const void *d_w, int32_t w_rows, float *h_output, size_t output_len) {
   if (!ctx || !cache_c || !h_query || !h_output) return LLH_ERR_NULL;
   auto *cache = const_cast<llh_layer_cache *>(cache_c);
   std::lock_guard<std::mutex> g(cache->mu);
@@ -835,12 +924,13 @@ int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cach
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "attention shape does not match the KV cache");
   const size_t qdim = num_attention_heads * head_dim;
   if (query_len != qdim) return ctx->fail(LLH_ERR_INVALID_SHAPE, "query length does not match heads * head_dim");
-  if (output_len < qdim) return ctx->fail(LLH_ERR_INVALID_SHAPE, "attention output buffer too small");
+  if (!d_w && output_len < qdim) return ctx->fail(LLH_ERR_INVALID_SHAPE, "attention output buffer too small");
+  const size_t out_len = d_w ? (size_t)w_rows : qdim;
   if (row_count > cache->token_count)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "row count exceeds cache token count");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "softmax scores must be finite");
-  if (row_count == 0) {  // weighted sum of nothing (primitives.rs:1125-1128)
-    std::fill(h_output, h_output + qdim, 0.0f);
+  if (row_count == 0) {  // weighted sum of nothing (primitives.rs:1125-1128), projected: still zero
+    std::fill(h_output, h_output + out_len, 0.0f);
     return LLH_OK;
   }
   hipError_t e = hipSetDevice(ctx->device);
@@ -850,7 +940,8 @@ int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cach
   const size_t off_q = off_table + align_up(nb * sizeof(int32_t));
   const size_t off_out = off_q + align_up(qdim * sizeof(float));
   const size_t off_scores = off_out + align_up(qdim * sizeof(float));
-  const size_t need = off_scores + num_attention_heads * row_count * sizeof(float);
+  const size_t off_proj = off_scores + align_up(num_attention_heads * row_count * sizeof(float));
+  const size_t need = off_proj + (d_w ? (size_t)w_rows * sizeof(float) : 0);
   e = cache->scratch.ensure(need);
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
   char *sb = static_cast<char *>(cache->scratch.buf);
@@ -878,15 +969,59 @@ int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cach
   a.score_stride = (int32_t)row_count;
   a.scale = score_scale;
   e = launch_decode_generic(a, 1, 1, nullptr);
+  if (e == hipSuccess && d_w) {
+    MatvecArgs m{};
+    m.w = static_cast<const uint16_t *>(d_w);
+    m.x = sb + off_out;
+    m.out = reinterpret_cast<float *>(sb + off_proj);
+    m.rows = w_rows;
+    m.cols = (int32_t)qdim;
+    m.n = 1;
+    m.ldx = (int32_t)qdim;
+    m.ldo = w_rows;
+    m.x_f32 = 1;
+    e = launch_matvec_bf16(m, nullptr);
+  }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   int32_t flags = 0;
   if (e == hipSuccess) e = hipMemcpy(&flags, sb, sizeof(flags), hipMemcpyDeviceToHost);
-  if (e == hipSuccess) e = hipMemcpy(h_output, sb + off_out, qdim * sizeof(float), hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    e = hipMemcpy(h_output, sb + (d_w ? off_proj : off_out), out_len * sizeof(float), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return ctx->hip_fail(e, "attention");
   ctx->decode_calls++;
   if (flags & kErrNonFinite) return ctx->fail(LLH_ERR_NON_FINITE, "softmax scores must be finite");
   if (flags & kErrBadBlock) return ctx->fail(LLH_ERR_STALE, "KV cache block table is stale");
   return LLH_OK;
+}
+
+
+extern "C" {
+
+int llh_full_attention_cache_mix_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache_c, const float *h_query,
+                                              size_t query_len, size_t row_count, size_t num_attention_heads,
+                                              size_t num_key_value_heads, size_t head_dim, float score_scale,
+                                              float *h_output, size_t output_len) {
+  return cache_mix_impl(ctx, cache_c, h_query, query_len, row_count, num_attention_heads, num_key_value_heads,
+                        head_dim, score_scale, nullptr, 0, h_output, output_len);
+}
+
+// full_attention_cache_mix_bf16_output_projection_f32_in_place
+// (crates/llm-backend/src/core/native_matvec.rs:671-685; Metal form
+// crates/llm-native-runtime/src/native_matvec.rs:4418-4492): shapes the fused
+// path does not take return LLH_NOT_HANDLED (the trait's Ok(false)).
+int llh_full_attention_cache_mix_bf16_output_projection_f32_in_place(
+    llh_ctx *ctx, const llh_layer_cache *cache_c, const float *h_query, size_t query_len, size_t row_count,
+    size_t num_attention_heads, size_t num_key_value_heads, size_t head_dim, float score_scale, const void *d_w_o,
+    int32_t w_rows, int32_t w_cols, float *h_output, size_t output_len) {
+  if (!ctx || !cache_c || !h_query || !h_output || !d_w_o) return LLH_ERR_NULL;
+  const size_t attention_dim = num_attention_heads * head_dim;
+  if (w_rows <= 0 || w_cols <= 0 || (size_t)w_cols != attention_dim || output_len < (size_t)w_rows ||
+      w_cols % kMatvecColsMultiple != 0 || !aligned16(d_w_o)) {
+    ctx->not_handled++;
+    return LLH_NOT_HANDLED;
+  }
+  return cache_mix_impl(ctx, cache_c, h_query, query_len, row_count, num_attention_heads, num_key_value_heads,
+                        head_dim, score_scale, d_w_o, w_rows, h_output, output_len);
 }
 
 int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cache *cache_c, int32_t tensor,

@@ -11,6 +11,8 @@ constexpr int kFastHeadDim = 128;   // head_dim of the tuned kernels
 constexpr int kFastBlockTokens = 16;  // block_tokens of the tuned kernels
 constexpr int kDecodeThreads = 256;   // 4 wavefronts
 constexpr int kPrefillThreads = 256;  // 4 wavefronts, 32 query rows each
+constexpr int kMatvecWaves = 8;       // wavefronts (K slices) per output-projection workgroup
+constexpr int kMatvecColsMultiple = kMatvecWaves * 16;  // cols the projection kernel takes
 
 enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2 };
 
@@ -130,6 +132,18 @@ struct GatherArgs {
   int32_t *err;
 };
 
+struct MatvecArgs {
+  const uint16_t *w;        // [rows][cols] bf16, row-major
+  const void *x;            // [n][ldx] bf16 or f32
+  float *out;               // [n][ldo] f32
+  int32_t rows;
+  int32_t cols;             // multiple of kMatvecColsMultiple
+  int32_t n;
+  int32_t ldx;
+  int32_t ldo;
+  int32_t x_f32;
+};
+
 // launchers (return hipError_t of the launch)
 // `hook(user, 0, s)` runs just before and `hook(user, 1, s)` just after the main
 // decode kernel is enqueued (before the merge): kernel timing records events there.
@@ -142,5 +156,6 @@ hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);
+hipError_t launch_matvec_bf16(const MatvecArgs &a, hipStream_t s);
 
 }  // namespace llh

@@ -228,6 +228,11 @@ SIGNATURES = {
         [_P, _P, _FP, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _FP, _SZ],
     ),
     "llh_select_kv_cache_head_rows_f32_in_place": (ctypes.c_int, [_P, _P, _I32, _SZ, _SZ, _SZ, _FP, _SZ]),
+    "llh_matvec_bf16_f32": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _I32, _P, _P]),
+    "llh_paged_decode_output_projection": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, _I32, _P,
+                                                          ctypes.c_float, _P]),
+    "llh_full_attention_cache_mix_bf16_output_projection_f32_in_place": (
+        ctypes.c_int, [_P, _P, _FP, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P, _I32, _I32, _FP, _SZ]),
     "llh_sha256": (ctypes.c_int, [_P, _SZ, _P]),
     "llh_cache_block_chain_hash": (ctypes.c_int, [ctypes.c_char_p, _SZ, ctypes.c_char_p, _SZ, _P, _P, _SZ, _P]),
     "llh_block_pool_create_host": (ctypes.c_int, [_SZ, _SZ, _SZ, ctypes.POINTER(_P)]),
@@ -405,6 +410,20 @@ class Context:
                 self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out), score_scale, _stream(stream)
             )
         )
+
+    def matvec_bf16(self, w, rows: int, cols: int, x, n: int, out, stream=None) -> None:
+        """out[n][rows] f32 = x[n][cols] (bf16 or f32 tensor) times W[rows][cols]^T (bf16)."""
+        import torch
+
+        self.check(self.lib.llh_matvec_bf16_f32(self.handle, _ptr(w), rows, cols, _ptr(x),
+                                                1 if x.dtype == torch.float32 else 0, n, _ptr(out),
+                                                _stream(stream)))
+
+    def paged_decode_output_projection(self, pool: "KvPool", desc: DecodeDesc, q, w_o, rows: int, out,
+                                       score_scale: float, stream=None) -> None:
+        self.check(self.lib.llh_paged_decode_output_projection(
+            self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(w_o), rows, _ptr(out), score_scale,
+            _stream(stream)))
 
     def paged_prefill(self, pool: "KvPool", desc: PrefillDesc, q, out, score_scale: float, stream=None) -> None:
         self.check(
@@ -615,6 +634,23 @@ class HipNativeMatvecBackend:
         st = self.ctx.lib.llh_full_attention_cache_mix_f32_in_place(
             self.ctx.handle, cache.handle, _f32_ptr(q), q.size, row_count, num_attention_heads,
             num_key_value_heads, head_dim, float(score_scale), _f32_ptr(output), output.size)
+        if st == NOT_HANDLED:
+            return False
+        self.ctx.check(st)
+        return True
+
+    def full_attention_cache_mix_bf16_output_projection_f32_in_place(
+            self, cache: LayerKvCache, query, row_count: int, num_attention_heads: int, num_key_value_heads: int,
+            head_dim: int, score_scale: float, weight, output: np.ndarray) -> bool:
+        """``weight``: device bf16 tensor [rows][cols] (the o_proj tensor, already resident)."""
+        q = np.ascontiguousarray(query, dtype=np.float32)
+        if output.dtype != np.float32 or not output.flags["C_CONTIGUOUS"]:
+            raise LlhError(ERR_INVALID_SHAPE, "output must be a contiguous float32 array")
+        rows, cols = weight.shape
+        st = self.ctx.lib.llh_full_attention_cache_mix_bf16_output_projection_f32_in_place(
+            self.ctx.handle, cache.handle, _f32_ptr(q), q.size, row_count, num_attention_heads,
+            num_key_value_heads, head_dim, float(score_scale), _ptr(weight), rows, cols, _f32_ptr(output),
+            output.size)
         if st == NOT_HANDLED:
             return False
         self.ctx.check(st)

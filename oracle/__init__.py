@@ -96,6 +96,7 @@ _SIGS = {
     "orc_uniform_int": (_I64, [_U64, _U64, _I64, _I64]),
     "orc_permutation": (None, [_U64, _I32, _P]),
     "orc_matvec_row_major": (None, [_P, _P, _SZ, _SZ, _P]),
+    "orc_matvec_bf16_f32": (None, [_P, _SZ, _SZ, _P, _P]),
     "orc_softmax": (ctypes.c_int, [_P, _SZ, _P]),
     "orc_weighted_sum": (None, [_P, _P, _SZ, _SZ, _P]),
     "orc_select_head_rows": (None, [_P, _SZ, _SZ, _SZ, _SZ, _P]),
@@ -425,3 +426,14 @@ def chain_hash(model_id: str, cache_context: str, previous_hash: bytes, token_id
     for t in token_ids:
         h.update(struct.pack("<I", int(t)))
     return h.digest()
+
+
+def matvec_bf16_f32(w_bf16: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """bf16_matvec_row_major_f32: w [rows][cols] bf16 bits, x [cols] f32 -> [rows] f32."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    rows, cols = w.shape
+    xx = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    assert xx.size == cols
+    out = np.zeros(rows, np.float32)
+    lib().orc_matvec_bf16_f32(w.ctypes.data_as(ctypes.c_void_p), rows, cols, _p(xx), _p(out))
+    return out

@@ -184,6 +184,21 @@ void orc_matvec_row_major(const float *x, const float *w, size_t rows, size_t co
   }
 }
 
+/* bf16_dot_f32_scalar (crates/llm-backend/src/core/safetensors/math.rs:66-72) per row:
+ * out[r] = sum_c bf16(w[r][c]) * x[c], products and sum in f32, in column order
+ * (the row matvec of bf16_matvec_rows_f32_in_place, safetensors.rs:915-966). */
+void orc_matvec_bf16_f32(const uint16_t *w, size_t rows, size_t cols, const float *x, float *out) {
+  for (size_t r = 0; r < rows; r++) {
+    const uint16_t *row = w + r * cols;
+    float acc = 0.0f;
+    for (size_t c = 0; c < cols; c++) {
+      float prod = orc_bf16_to_f32(row[c]) * x[c];
+      acc = acc + prod;
+    }
+    out[r] = acc;
+  }
+}
+
 /* math.rs:476-505 softmax_f32_in_place */
 int orc_softmax(const float *scores, size_t n, float *out) {
   if (n == 0) return ORC_OK;

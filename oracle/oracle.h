@@ -74,6 +74,8 @@ void orc_permutation(uint64_t seed, int32_t n, int32_t *out);
 /* ---------------- reference math (math.rs) ---------------- */
 /* matvec_row_major_f32_in_place: out[r] = sum_c w[r*cols+c]*x[c], sequential */
 void orc_matvec_row_major(const float *x, const float *w, size_t rows, size_t cols, float *out);
+/* safetensors/math.rs:66-72 bf16_dot_f32_scalar, one per row: f32 input, bf16 row-major weights */
+void orc_matvec_bf16_f32(const uint16_t *w, size_t rows, size_t cols, const float *x, float *out);
 /* softmax_f32_in_place: error on non-finite input or invalid denominator */
 int orc_softmax(const float *scores, size_t n, float *out);
 /* weighted_sum_f32_in_place */

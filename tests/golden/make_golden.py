@@ -121,6 +121,12 @@ KNOWN_ANSWERS = {
         "values_rule": "value[t] = [(t % 7) - 3, (t % 11) * 0.25 - 1]",
         "tolerance_f16_mirror": 1e-2, "tolerance_int8": 3e-2,
     },
+    "bf16_matvec": {
+        "source": "crates/llm-backend/src/core/tests/safetensors_loader/shard_store.rs:16-51",
+        "rows": 2, "cols": 3, "weight": [1.0, 2.0, 3.0, 4.0, 5.0, 6.0],
+        "inputs": [[1.0, 2.0, 3.0], [3.0, 2.0, 1.0]],
+        "expected": [[14.0, 32.0], [10.0, 28.0]],
+    },
 }
 
 

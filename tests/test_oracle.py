@@ -491,3 +491,23 @@ def test_strict_append_capacity_error():
     r.append([2.0], [2.0])
     with pytest.raises(OverflowError):
         r.append([3.0], [3.0])
+
+
+def test_bf16_matvec_known_answer():
+    """crates/llm-backend/src/core/tests/safetensors_loader/shard_store.rs:16-51."""
+    ka = KA["bf16_matvec"]
+    w = oracle.f32_to_bf16(np.array(ka["weight"], np.float32)).reshape(ka["rows"], ka["cols"])
+    for x, exp in zip(ka["inputs"], ka["expected"]):
+        assert oracle.matvec_bf16_f32(w, np.array(x, np.float32)).tolist() == exp
+
+
+def test_bf16_matvec_matches_float64():
+    rng = np.random.default_rng(11)
+    rows, cols = 37, 300
+    w = oracle.f32_to_bf16(rng.standard_normal((rows, cols)).astype(np.float32))
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = oracle.matvec_bf16_f32(w, x)
+    ref = oracle.bf16_to_f32(w.ravel()).reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+    assert np.max(np.abs(got - ref)) < 1e-4
+    # a transposed operand or a dropped row fails this
+    assert not np.allclose(got[:-1], ref[1:], atol=1e-2)
