@@ -657,9 +657,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_wave_kernel(const
 
 // Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
 // dim) per (query head, sequence) whose sequence used more than one split.
-// The (max, sum) pairs of all splits are read in one round into LDS; then each
-// lane's partial outputs are loaded 16 splits at a time.
+// Up to 32 splits, each lane loads every (max, sum) pair and its partial of
+// every split in one round and combines them in registers; beyond that the
+// pairs go through LDS and the partials are loaded 16 splits at a time.
 constexpr int kMergeMaxSplits = 1024;
+constexpr int kMergeOneRound = 32;  // splits merged from one round of loads
 
 __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   const int h = blockIdx.x;
@@ -667,10 +669,35 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   int len, lo, first_blk, n_blk, n_splits;
   seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
   if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMergeMaxSplits) return;
-  __shared__ float s_f[kMergeMaxSplits];
-  __shared__ float s_red[2];
   const int d = threadIdx.x;
   const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
+  if (n_splits <= kMergeOneRound) {
+    // one memory round trip: every (max, sum) pair and this lane's partial of
+    // every split are in flight together, then combined in registers
+    float2 ml[kMergeOneRound];
+    float o_sp[kMergeOneRound];
+#pragma unroll
+    for (int i = 0; i < kMergeOneRound; i++) {
+      const bool live = i < n_splits;
+      ml[i] = live ? a.ws_ml[row0 + i] : make_float2(-INFINITY, 0.0f);
+      o_sp[i] = live ? a.ws_o[(row0 + i) * D + d] : 0.0f;
+    }
+    float mm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kMergeOneRound; i++) mm = fmaxf(mm, ml[i].x);
+    const float mref = (mm == -INFINITY) ? 0.0f : mm;
+    float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMergeOneRound; i++) {
+      const float f = fast_exp2(ml[i].x - mref);
+      ll += ml[i].y * f;
+      oo += o_sp[i] * f;
+    }
+    a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / ll);
+    return;
+  }
+  __shared__ float s_f[kMergeMaxSplits];
+  __shared__ float s_red[2];
   float lm = -INFINITY;
   for (int sp = d; sp < n_splits; sp += D) {
     const float2 ml = a.ws_ml[row0 + sp];
