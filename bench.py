@@ -256,7 +256,9 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         state["i"] += 1
 
     # step time over all timed steps, then the decode kernel alone (library-recorded events)
+    streamed0 = ctx.metrics()["stream_decode_calls"]
     ms = time_steps(step, steps, warmup)
+    streamed = ctx.metrics()["stream_decode_calls"] - streamed0
     _, kms = time_steps(step, steps, 0, kernel_timing=(ctx, "decode"))
     if ctx.device_errors() != 0:
         raise RuntimeError(f"{name}: device error flags set during timing")
@@ -271,6 +273,7 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
         "bytes_per_step": nbytes,
         "rotating_copies": len(copies),
+        "kernel": "paged_decode_stream_kernel" if streamed == steps + warmup else "paged_decode_kernel (split-K)",
     }
 
 
@@ -400,7 +403,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_kernel<2, bf16> (split-K partials; the merge launch is excluded)",
+            "kernel": f"{c2['kernel']}, G=2, bf16 (the merge launch is excluded)",
             "achieved": c2["kernel_gbs"],
             "kernel_us": c2["kernel_us"],
             "peak": HBM_PEAK_GBS,

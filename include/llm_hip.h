@@ -83,6 +83,7 @@ typedef struct llh_metrics {
   uint64_t not_handled;
   uint64_t device_errors;
   uint64_t shape_errors;
+  uint64_t stream_decode_calls; /* decode calls that ran the persistent stream kernel */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Waits for the device, then reads (and optionally clears) the sticky error
@@ -92,7 +93,8 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset);
 /* Kernel timing for measurement: while enabled, each llh_paged_decode /
  * llh_paged_prefill call records a pair of HIP events on its stream around its
- * main kernel (the split-K decode kernel, not the merge; the prefill kernel).
+ * main kernel (the split-K or stream decode kernel, not the merge; the prefill
+ * kernel).
  * llh_ctx_kernel_time waits for the recorded events and returns the summed
  * duration and count for kind 0 = decode, 1 = prefill (reset clears them). */
 int llh_ctx_set_kernel_timing(llh_ctx *ctx, int32_t enable);

@@ -83,6 +83,42 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
   return p;
 }
 
+// Persistent stream decode (bf16 pools): two workgroups of four wavefronts per
+// compute unit, the best grid measured on MI355X for C2 (one and three per CU
+// run 2-8% slower).  It is chosen when the step has at least
+// kStreamMinUnitsPerWave units (block x kv head) per wavefront and its
+// 32-bit partition arithmetic (units * wavefronts < 2^31) is exact; smaller
+// steps (C1, C4 decode) and quantised pools, whose kernels are bound by their
+// per-block arithmetic rather than by memory, use split-K.  LLH_DECODE_KERNEL
+// = "split" | "stream" overrides the choice, LLH_DECODE_STREAM_WGS the grid.
+constexpr int kStreamWgsPerCu = 2;
+constexpr int kStreamMaxWgs = 1024;
+constexpr int kStreamMinUnitsPerWave = 8;
+
+int stream_grid(const llh_ctx *ctx) {
+  const int wgs = env_int("LLH_DECODE_STREAM_WGS", 0);
+  return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : kStreamWgsPerCu * ctx->cus));
+}
+
+// Returns the stream grid (workgroups) for this step, or 0 for split-K.
+int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int est_blocks, int total_tokens_hint) {
+  const char *force = std::getenv("LLH_DECODE_KERNEL");
+  const bool want_split = force && std::strcmp(force, "split") == 0;
+  const bool want_stream = force && std::strcmp(force, "stream") == 0;
+  if (want_split) return 0;
+  const int wgs = stream_grid(ctx);
+  const long long waves = 4LL * wgs;
+  const long long max_units_seq = (long long)kv_heads * est_blocks;
+  const long long max_units = max_units_seq * num_seqs;
+  if (2LL * num_seqs >= waves || max_units_seq * waves >= (1LL << 31) || max_units >= (1LL << 31)) return 0;
+  if (want_stream) return wgs;
+  if (format != LLH_KV_BF16) return 0;
+  const long long units = total_tokens_hint > 0
+                              ? (long long)kv_heads * ((long long)total_tokens_hint / kFastBlockTokens + num_seqs)
+                              : max_units;
+  return units >= kStreamMinUnitsPerWave * waves ? wgs : 0;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -98,10 +134,12 @@ int llh_ctx_create(int device, llh_ctx **out) {
   auto *ctx = new llh_ctx();
   ctx->device = device;
   if (hipSetDevice(device) != hipSuccess || hipMalloc(&ctx->d_err, sizeof(int32_t)) != hipSuccess ||
-      hipMemset(ctx->d_err, 0, sizeof(int32_t)) != hipSuccess) {
+      hipMemset(ctx->d_err, 0, sizeof(int32_t)) != hipSuccess ||
+      hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
     delete ctx;
     return LLH_ERR_DEVICE;
   }
+  ctx->cus = std::max(1, ctx->cus);
   *out = ctx;
   return LLH_OK;
 }
@@ -139,7 +177,11 @@ size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t
   const size_t max_splits = (size_t)(est_blocks + 3) / 4;
   const size_t rows = (size_t)num_seqs * num_q_heads * max_splits;
   const size_t generic = (size_t)num_seqs * num_q_heads * std::max(1, max_seq_len) * sizeof(float);
-  return std::max(align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic);
+  // stream kernel: two partial slots per wavefront of the largest grid, G <= 8 rows each
+  const size_t srows = (size_t)2 * 4 * kStreamMaxWgs * std::min(num_q_heads, 8);
+  const size_t stream = align_up(srows * sizeof(float2)) + align_up(srows * kFastHeadDim * sizeof(float)) +
+                        align_up((size_t)num_seqs * num_q_heads * 2 * sizeof(int32_t));
+  return std::max({align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic, stream});
 }
 
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
@@ -150,6 +192,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->not_handled = ctx->not_handled.load();
   out->device_errors = ctx->device_errors.load();
   out->shape_errors = ctx->shape_errors.load();
+  out->stream_decode_calls = ctx->stream_decode_calls.load();
   return LLH_OK;
 }
 
@@ -343,12 +386,17 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   if (fast) {
     const SplitPlan plan =
         plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint);
-    if (plan.max_splits > kMaxDecodeSplits)
+    const int stream_wgs =
+        plan_stream(ctx, pv.format, desc->num_seqs, pv.kv_heads, plan.est_blocks, desc->total_tokens_hint);
+    if (!stream_wgs && plan.max_splits > kMaxDecodeSplits)
       return ctx->fail(LLH_ERR_INVALID_SHAPE, "context too long for one decode call (over 4M attended tokens)");
-    const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
+    // partial rows: split-K [B][Hq][max_splits]; stream [2 * waves][G]
+    const size_t rows = stream_wgs ? (size_t)2 * 4 * stream_wgs * group
+                                   : (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
     const size_t ml_off = kCounterBytes;
     const size_t o_off = ml_off + align_up(rows * sizeof(float2));
-    const size_t need = align_up(o_off + rows * kFastHeadDim * sizeof(float));
+    const size_t desc_off = align_up(o_off + rows * kFastHeadDim * sizeof(float));
+    const size_t need = align_up(desc_off + (stream_wgs ? (size_t)desc->num_seqs * pv.kv_heads * 2 * sizeof(int32_t) : 0));
     st = ctx->ensure_ws(need + extra_bytes);
     if (st != LLH_OK) return st;
     char *ws = static_cast<char *>(ctx->ws);
@@ -372,6 +420,10 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     a.max_splits = plan.max_splits;
     a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
     a.wave_splits = env_int("LLH_DECODE_WAVE_SPLITS", 0) ? 1 : 0;
+    a.stream_wgs = stream_wgs;
+    a.max_seq_len = desc->max_seq_len;
+    a.seg_desc = stream_wgs ? reinterpret_cast<int32_t *>(ws + desc_off) : nullptr;
+    if (stream_wgs) ctx->stream_decode_calls++;
     a.scale_log2e = score_scale * 1.4426950408889634f;
     struct TimingHook {
       llh_ctx *ctx;

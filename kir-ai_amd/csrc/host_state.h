@@ -31,13 +31,14 @@ uint64_t next_block_id();
 
 struct llh_ctx {
   int device = 0;
+  int cus = 256;  // compute units of the device (sizes the persistent decode grid)
   std::mutex mu;
   std::string last_error;
   void *ws = nullptr;
   size_t ws_bytes = 0;
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
-      shape_errors{0};
+      shape_errors{0}, stream_decode_calls{0};
   // kernel timing (measurement only)
   std::atomic<int> timing{0};
   std::mutex timing_mu;

@@ -54,6 +54,9 @@ struct DecodeArgs {
   int32_t max_splits;
   int32_t fused_merge;      // 1: last workgroup merges the splits; 0: second launch merges
   int32_t wave_splits;      // 1: one split per wavefront (no workgroup merge); 0: one split per workgroup
+  int32_t stream_wgs;       // >0: persistent stream kernel over this many workgroups (split fields unused)
+  int32_t max_seq_len;      // host bound on seq_lens (stream kernel: longer lengths raise kErrTooManySplits)
+  int32_t *seg_desc;        // stream kernel: [B][Hkv][2] (first partial slot, partial count; 0 = written)
   float scale_log2e;        // score_scale * log2(e)
 };
 

@@ -114,6 +114,7 @@ class Metrics(ctypes.Structure):
         ("not_handled", ctypes.c_uint64),
         ("device_errors", ctypes.c_uint64),
         ("shape_errors", ctypes.c_uint64),
+        ("stream_decode_calls", ctypes.c_uint64),
     ]
 
 

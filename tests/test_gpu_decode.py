@@ -8,6 +8,7 @@ mean-abs 2e-3 of the fp32 reference rounded to bf16.  The kernel's sticky error
 flags must stay clear (no out-of-pool block touched, no split overflow).
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -44,8 +45,15 @@ def run_decode(ctx, pool, batch, q, Hq, window, scale, head_dim=D, max_seq_len=N
     d_out = torch.full((B * Hq * head_dim,), 0x7FC0, dtype=torch.int16, device="cuda")  # NaN fill
     msl = int(batch.seq_lens.max()) if max_seq_len is None else max_seq_len
     desc = ctx.decode_desc(d_lens, d_tab, Hq, msl, window)
+    before = ctx.metrics()["stream_decode_calls"]
     ctx.paged_decode(pool, desc, d_q, d_out, scale)
     torch.cuda.synchronize()
+    streamed = ctx.metrics()["stream_decode_calls"] - before
+    forced = os.environ.get("LLH_DECODE_KERNEL")
+    if forced == "stream" and head_dim == D and batch.block_tokens == BT:
+        assert streamed == 1, "the stream kernel did not run"
+    if forced == "split":
+        assert streamed == 0, "the stream kernel ran under LLH_DECODE_KERNEL=split"
     return from_dev_bf16(d_out)
 
 
@@ -85,18 +93,33 @@ def test_decode_c1_identity_table(ctx, fmt):
 
 @pytest.fixture(params=["fused", "kernel"])
 def merge_mode(request, monkeypatch):
-    """Split partials merged by the last-arriving workgroup (LLH_DECODE_FUSED_MERGE=1) or by a
+    """Split-K partials merged by the last-arriving workgroup (LLH_DECODE_FUSED_MERGE=1) or by a
     second launch (the default)."""
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
     monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1" if request.param == "fused" else "0")
     return request.param
 
 
-def test_decode_c2_full_size(ctx, merge_mode):
+@pytest.fixture(params=["split", "stream"])
+def decode_kernel(request, monkeypatch):
+    """Both tuned decode kernels: split-K (one workgroup per split) and the persistent stream
+    kernel (LLH_DECODE_KERNEL forces the choice the library otherwise makes by batch size)."""
+    monkeypatch.setenv("LLH_DECODE_KERNEL", request.param)
+    return request.param
+
+
+def test_decode_c2_full_size(ctx, decode_kernel):
     """B=32, L~U[256,4096], permuted pool +10% free blocks."""
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
     assert batch.n_blocks == math.ceil(1.1 * int(np.sum((lens + 15) // 16)))
-    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 merge={merge_mode}")
+    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 kernel={decode_kernel}")
+
+
+def test_decode_c2_fused_merge(ctx, merge_mode):
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
+    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 split-K merge={merge_mode}")
 
 
 @pytest.mark.parametrize("split_blocks", [4, 8, 64])
@@ -125,19 +148,19 @@ def test_decode_fused_merge_is_deterministic(ctx, monkeypatch):
 
 
 @pytest.mark.parametrize("lens", [[1], [15, 16, 17], [31, 33, 255, 256, 257], [1000, 4095, 4096, 4097]])
-def test_decode_ragged_lengths(ctx, lens):
+def test_decode_ragged_lengths(ctx, decode_kernel, lens):
     batch = workloads.paged_batch(lens, BT, 0.10, seed=len(lens))
-    check(ctx, batch, 16, 8, seed=7, what=f"lens={lens}")
+    check(ctx, batch, 16, 8, seed=7, what=f"lens={lens} {decode_kernel}")
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
-def test_decode_gqa_groups(ctx, Hq, Hkv):
+def test_decode_gqa_groups(ctx, decode_kernel, Hq, Hkv):
     lens = [300, 700, 1200]
     batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq * 10 + Hkv)
     check(ctx, batch, Hq, Hkv, seed=11, what=f"Hq={Hq} Hkv={Hkv}")
 
 
-def test_decode_c4_sliding_window_skips_blocks(ctx):
+def test_decode_c4_sliding_window_skips_blocks(ctx, decode_kernel):
     """configs[3] decode: 4 x 32768 positions, window 4096, shuffled blocks.
     Blocks wholly before the window are not in the pool (table entry -1): any
     access would raise the bad-block flag, so a clear flag proves they are skipped."""
@@ -149,13 +172,13 @@ def test_decode_c4_sliding_window_skips_blocks(ctx):
 
 
 @pytest.mark.parametrize("W,lens", [(1, [5, 16, 17]), (17, [16, 17, 40, 100]), (100, [50, 99, 100, 101, 333])])
-def test_decode_window_edges(ctx, W, lens):
+def test_decode_window_edges(ctx, decode_kernel, W, lens):
     batch = workloads.paged_batch(lens, BT, 0.10, seed=W)
     check(ctx, batch, 16, 8, window=W, seed=W + 1, what=f"W={W}")
 
 
 @pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
-def test_decode_c5_quantized(ctx, fmt):
+def test_decode_c5_quantized(ctx, decode_kernel, fmt):
     """configs[4] shape (Hq32/Hkv8, L=8192) at 16 of the 64 sequences; bench.py runs all 64."""
     lens = [8192] * 16
     batch = workloads.paged_batch(lens, BT, 0.0, workloads.SEED_BASE + 4)
@@ -163,14 +186,14 @@ def test_decode_c5_quantized(ctx, fmt):
 
 
 @pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
-def test_decode_quantized_ragged_window(ctx, fmt):
+def test_decode_quantized_ragged_window(ctx, decode_kernel, fmt):
     lens = [1, 17, 250, 1025, 3000]
     batch = workloads.paged_batch(lens, BT, 0.10, seed=fmt)
     check(ctx, batch, 16, 8, fmt, window=0, seed=21, what=f"fmt={fmt}")
     check(ctx, batch, 16, 8, fmt, window=333, seed=22, what=f"fmt={fmt} W=333")
 
 
-def test_decode_empty_sequence_is_zero(ctx):
+def test_decode_empty_sequence_is_zero(ctx, decode_kernel):
     """R = 0 gives a zero output (weighted sum of nothing, primitives.rs:1125-1128)."""
     batch = workloads.paged_batch([0, 20], BT, 0.10, seed=3)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 5)
@@ -188,7 +211,7 @@ def test_decode_generic_shapes(ctx, head_dim, bt, Hq, Hkv):
     check(ctx, batch, Hq, Hkv, seed=31, head_dim=head_dim, what=f"D={head_dim} BT={bt}")
 
 
-def test_decode_bad_block_raises_flag(ctx):
+def test_decode_bad_block_raises_flag(ctx, decode_kernel):
     batch = workloads.paged_batch([64, 64], BT, 0.10, seed=9)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 9)
     bad = workloads.PagedBatch(batch.seq_lens, batch.tables.copy(), batch.n_blocks, BT, batch.first_block)
@@ -197,14 +220,14 @@ def test_decode_bad_block_raises_flag(ctx):
     assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
 
 
-def test_decode_max_seq_len_bound_raises_flag(ctx):
+def test_decode_max_seq_len_bound_raises_flag(ctx, decode_kernel):
     batch = workloads.paged_batch([2000], BT, 0.10, seed=10)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 10)
     run_decode(ctx, pool, batch, q, 16, 0, 0.1, max_seq_len=100)
     assert ctx.device_errors() & llm_hip.ERR_FLAG_TOO_MANY_SPLITS
 
 
-def test_decode_repeated_calls_are_identical(ctx):
+def test_decode_repeated_calls_are_identical(ctx, decode_kernel):
     """Split counters return to zero after every call: repeat calls give identical bits."""
     lens = workloads.uniform_lengths(8, 256, 4096, 99)
     batch = workloads.paged_batch(lens, BT, 0.10, seed=99)
@@ -232,3 +255,62 @@ def test_decode_shape_errors(ctx):
     with pytest.raises(llm_hip.LlhError) as e:
         ctx.paged_decode(pool, desc, d_q, d_out, float("nan"))
     assert e.value.status == llm_hip.ERR_NON_FINITE
+
+
+# ---- the persistent stream kernel's partition -------------------------------------------------
+
+@pytest.mark.parametrize("wgs", [1, 2, 3, 7, 16, 64])
+def test_stream_small_grids_cut_segments_everywhere(ctx, wgs, monkeypatch):
+    """Small grids put wavefront boundaries at every possible place relative to the
+    (kv head, block) segments: ranges that start on a segment's last block, span several
+    kv heads, or hold one unit; each cut segment is merged from its partials."""
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+    monkeypatch.setenv("LLH_DECODE_STREAM_WGS", str(wgs))
+    lens = [1, 16, 17, 250, 4096, 33, 1000][: max(1, min(7, 2 * wgs - 1))]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=40 + wgs)
+    check(ctx, batch, 16, 8, seed=41 + wgs, what=f"stream wgs={wgs}")
+
+
+def test_stream_many_partials_per_segment(ctx, monkeypatch):
+    """Few long sequences on a large grid: ~64 partials per segment, merged in rounds of 16."""
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+    monkeypatch.setenv("LLH_DECODE_STREAM_WGS", "512")
+    batch = workloads.paged_batch([4096] * 4, BT, 0.10, seed=44)
+    check(ctx, batch, 16, 8, seed=45, what="stream 4 x 4096")
+
+
+def test_stream_batch_over_64(ctx, decode_kernel):
+    """Batches beyond one wavefront's 64 lanes take the chunked length scan."""
+    lens = workloads.uniform_lengths(150, 0, 700, 46)
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=46)
+    check(ctx, batch, 16, 8, seed=47, what=f"B=150 {decode_kernel}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (64, 8), (32, 4)])
+def test_stream_group_sizes(ctx, Hq, Hkv, monkeypatch):
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+    lens = workloads.uniform_lengths(24, 1, 3000, Hq)
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq + Hkv)
+    check(ctx, batch, Hq, Hkv, seed=48, what=f"stream Hq={Hq} Hkv={Hkv}")
+
+
+def test_stream_is_the_default_for_large_bf16_batches(ctx, monkeypatch):
+    """Without an override the library picks the stream kernel for C2 and split-K for C1:
+    both give the same result as the forced choice, bit for bit."""
+    monkeypatch.delenv("LLH_DECODE_KERNEL", raising=False)
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 50)
+    before = ctx.metrics()["stream_decode_calls"]
+    auto = run_decode(ctx, pool, batch, q, 16, 0, 0.088)
+    assert ctx.metrics()["stream_decode_calls"] == before + 1
+    c1 = identity_batch([512])
+    c1pool, c1q = build_case(ctx, c1, 16, 8, llm_hip.KV_BF16, 51)
+    run_decode(ctx, c1pool, c1, c1q, 16, 0, 0.088)
+    assert ctx.metrics()["stream_decode_calls"] == before + 1  # C1 stays on split-K
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+    assert np.array_equal(run_decode(ctx, pool, batch, q, 16, 0, 0.088), auto)
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
+    split = run_decode(ctx, pool, batch, q, 16, 0, 0.088)
+    assert not np.array_equal(split, auto)  # different summation order: proves the choice
+    assert ctx.device_errors() == 0
