@@ -277,15 +277,15 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     }
 
 
-def traffic_from_profile(alg_bytes: int):
-    """HBM bytes per launch of the decode kernel from the committed rocprofv3 --pmc summary
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch of the C2 decode kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
     path = os.path.join(ROOT, "profiles", "decode_c2_bf16.md")
     try:
         for line in open(path):
             cells = [c.strip() for c in line.split("|")]
-            if len(cells) > 9 and cells[1] == "C2" and "paged_decode_kernel" in cells[2]:
-                return int((float(cells[7]) + float(cells[8])) * 1024)
+            if len(cells) > 11 and cells[1] == "C2" and cells[2].strip("`").startswith(kernel):
+                return int(float(cells[10]))
     except (OSError, ValueError):
         pass
     return None
@@ -409,7 +409,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profile(c2["bytes_per_step"]),
+            "traffic": traffic_from_profile(c2["kernel"].split(" ")[0]),
         },
         "cpu_baseline": cpu,
         "copy_ceiling": copy,
