@@ -86,6 +86,12 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// Value of lane (l ^ 15) within its 16-lane row: every lane is written, so no
+// old value is needed (mov_dpp leaves the destination's prior bits unused).
+__device__ __forceinline__ float row_mirror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+}
+
 // Sum over the 16 lanes of a DPP row; every lane receives the total.
 __device__ __forceinline__ float row_sum16(float v) {
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -293,8 +299,8 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     }
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-      const float oth0 = dpp<0x140>(own[gi][0]);  // row_mirror swaps the two 8-lane halves
-      const float oth1 = dpp<0x140>(own[gi][1]);
+      const float oth0 = row_mirror(own[gi][0]);  // swaps the two 8-lane halves of a row
+      const float oth1 = row_mirror(own[gi][1]);
       s[gi][0] = hf ? oth0 : own[gi][0];
       s[gi][1] = hf ? own[gi][0] : oth0;
       s[gi][2] = hf ? oth1 : own[gi][1];
@@ -308,28 +314,51 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
 #pragma unroll
       for (int i = 0; i < 4; i++)
         if (!ok[i]) s[gi][i] = -INFINITY;
+    // slots outside [lo, len) may hold any scale bits: zero their weights' scale
+    // (their V codes are masked too) so that 0 * garbage cannot reach the sums
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (!ok[i]) vsc[i] = 0.0f;
   }
 
-  // online softmax per head: running max (log2 units), sum, bf16 weights for V
-  float alpha[G];
+  // Online softmax per head with a lazy reference max (log2 units): st.m only
+  // moves when a score exceeds it by more than 8, so the weights stay <= 2^8 and
+  // the accumulators are rescaled on few blocks (a wavefront-uniform branch).
+  // Any reference max gives the same softmax; the partials carry theirs.
+  bool grow[G];
+  bool any_grow = false;
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
+    grow[gi] = tmax > st.m[gi] + 8.0f;  // true on the first block with a finite score
+    any_grow |= grow[gi];
+  }
+  if (__any(any_grow)) {
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
+      const float nm = grow[gi] ? tmax : st.m[gi];
+      const float alpha = grow[gi] ? fast_exp2(st.m[gi] - nm) : 1.0f;  // 0 when st.m = -inf
+      st.m[gi] = nm;
+      st.l[gi] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; j++) st.o[gi][j] *= alpha;
+    }
+  }
   uint32_t w01[G], w23[G];
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    float mx = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
-    mx = fmaxf(mx, st.m[gi]);
-    const float mref = (mx == -INFINITY) ? 0.0f : mx;
-    alpha[gi] = fast_exp2(st.m[gi] - mref);
+    const float mref = (st.m[gi] == -INFINITY) ? 0.0f : st.m[gi];
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
-    st.l[gi] = st.l[gi] * alpha[gi] + ((p[0] + p[1]) + (p[2] + p[3]));
-    st.m[gi] = mx;
+    st.l[gi] += (p[0] + p[1]) + (p[2] + p[3]);
     if constexpr (FMT == kBf16) {
       w01[gi] = pack_bf16(p[0], p[1]);
       w23[gi] = pack_bf16(p[2], p[3]);
     } else {
-      w01[gi] = pack_bf16(ok[0] ? p[0] * vsc[0] : 0.0f, ok[1] ? p[1] * vsc[1] : 0.0f);
-      w23[gi] = pack_bf16(ok[2] ? p[2] * vsc[2] : 0.0f, ok[3] ? p[3] * vsc[3] : 0.0f);
+      w01[gi] = pack_bf16(p[0] * vsc[0], p[1] * vsc[1]);
+      w23[gi] = pack_bf16(p[2] * vsc[2], p[3] * vsc[3]);
     }
   }
 #pragma unroll
@@ -337,8 +366,7 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     uint32_t v01, v23;
     v_pairs<FMT>(r, vmask, j, v01, v23);
 #pragma unroll
-    for (int gi = 0; gi < G; gi++)
-      st.o[gi][j] = dot2_bf16(v23, w23[gi], dot2_bf16(v01, w01[gi], st.o[gi][j] * alpha[gi]));
+    for (int gi = 0; gi < G; gi++) st.o[gi][j] = dot2_bf16(v23, w23[gi], dot2_bf16(v01, w01[gi], st.o[gi][j]));
   }
 }
 
