@@ -573,7 +573,11 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   a.scale_log2e = score_scale * 1.4426950408889634f;
   ctx->prefill_calls++;
   auto ev = ctx->timing_begin(static_cast<hipStream_t>(stream));
-  hipError_t e = launch_prefill(a, static_cast<hipStream_t>(stream));
+  // two query heads of a kv head per workgroup share its K/V tile stream when the group is even
+  const int group = desc->num_q_heads / pv.kv_heads;
+  const int hpw_env = env_int("LLH_PREFILL_HEADS_PER_WG", 0);
+  const int hpw = (hpw_env == 1 || group % 2 != 0) ? 1 : 2;
+  hipError_t e = launch_prefill(a, hpw, static_cast<hipStream_t>(stream));
   ctx->timing_end(1, ev, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "prefill launch");
   return LLH_OK;

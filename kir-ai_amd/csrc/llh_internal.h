@@ -154,7 +154,8 @@ typedef void (*LaunchHook)(void *user, int phase, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s, void *hook_user = nullptr,
                          LaunchHook hook = nullptr);
 hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_f32, hipStream_t s);
-hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
+// heads_per_wg: query heads of one kv head that share a workgroup's K/V tiles (1 or 2; 2 needs an even group)
+hipError_t launch_prefill(const PrefillArgs &a, int heads_per_wg, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);

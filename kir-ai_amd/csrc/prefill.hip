@@ -11,7 +11,9 @@
 // Key tiles of 64 positions (4 pool blocks) are staged in LDS, double
 // buffered: while the wavefronts run the MFMAs of tile t, every lane already
 // holds its share of tile t+1 in registers, and stores it to the other buffer
-// afterwards (one barrier per tile).  Tiles wholly outside the window or past
+// afterwards (one barrier per tile).  When a kv head's group is even, one
+// workgroup of 8 wavefronts runs two of its query heads over the same K/V
+// tiles (half the tile loads and LDS stores per FLOP).  Tiles wholly outside the window or past
 // the last query are never loaded, and only tiles that straddle a boundary are
 // masked.
 //
@@ -80,9 +82,10 @@ __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
 // One lane's share of a key tile: for each of the 4 blocks, 16 B of K (token
 // tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..),
 // plus a (wavefront-uniform) bit per block: 1 = the block is needed and valid.
+template <int NB>
 struct TileRegs {
-  u32x4_t k[KBLK];
-  u32x4_t v[KBLK];
+  u32x4_t k[NB];
+  u32x4_t v[NB];
 };
 
 // Block-table entries of the tile starting at kt: lane kb of every wavefront
@@ -98,24 +101,26 @@ __device__ __forceinline__ int fetch_entries(const PrefillArgs &a, const int32_t
 // stored to LDS), so no branch or conditional memory operation sits between
 // the prefetch and the math that overlaps it.  `bad` collects needed blocks
 // with an out-of-pool entry (flagged once, at the end of the kernel).
+template <int NB>
 __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries, int kvh, int kt, int ctx, int klo,
-                                              int tid, TileRegs &r, bool &bad) {
+                                              int tid, int kb0, TileRegs<NB> &r, bool &bad) {
   const int Hkv = a.pool.kv_heads;
   uint32_t use_mask = 0;
 #pragma unroll
-  for (int kb = 0; kb < KBLK; kb++) {
+  for (int i = 0; i < NB; i++) {
+    const int kb = kb0 + i;
     const int bpos = kt + kb * BT;
     const bool needed = bpos < ctx && bpos + BT > klo;
     const int phys = __builtin_amdgcn_readlane(entries, kb);
     const bool ok = phys >= 0 && (int64_t)phys < a.pool.n_blocks;
     bad |= needed && !ok;
     const bool use = needed && ok;
-    use_mask |= use ? (1u << kb) : 0u;
+    use_mask |= use ? (1u << i) : 0u;
     const size_t base = ((size_t)(use ? phys : 0) * Hkv + kvh) * (BT * D);
-    r.k[kb] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
-                                               (tid >> 4) * D + (tid & 15) * 8);
-    r.v[kb] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
-                                               (tid >> 1) * BT + (tid & 1) * 8);
+    r.k[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
+                                              (tid >> 4) * D + (tid & 15) * 8);
+    r.v[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
+                                              (tid >> 1) * BT + (tid & 1) * 8);
   }
   return use_mask;
 }
@@ -124,14 +129,16 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
 // attended are masked to -inf in the scores, whatever K holds); V^T is zeroed
 // for unused blocks and for tokens at or past the context end, because
 // P = 0 times a non-finite V would still poison the accumulators.
-__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, const TileRegs &r,
+template <int NB>
+__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, int kb0, const TileRegs<NB> &r,
                                            uint32_t use_mask, int kt, int ctx) {
   const bool tail = kt + BN > ctx;  // the tile reaches the end of the context (uniform)
 #pragma unroll
-  for (int kb = 0; kb < KBLK; kb++) {
-    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[kb];
-    u32x4_t v = r.v[kb];
-    if (!(use_mask & (1u << kb))) v = u32x4_t{0u, 0u, 0u, 0u};
+  for (int i = 0; i < NB; i++) {
+    const int kb = kb0 + i;
+    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[i];
+    u32x4_t v = r.v[i];
+    if (!(use_mask & (1u << i))) v = u32x4_t{0u, 0u, 0u, 0u};
     if (tail) {
       const int valid = ctx - (kt + kb * BT + (tid & 1) * 8);  // tokens of this 8-run inside the context
       v[0] &= (valid > 0 ? 0x0000ffffu : 0u) | (valid > 1 ? 0xffff0000u : 0u);
@@ -145,20 +152,20 @@ __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int
   }
 }
 
-__global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const PrefillArgs a) {
+template <int HPW>
+__global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_kernel(const PrefillArgs a) {
   // ---- XCD-aware logical work item ----
   const int Hq = a.q_heads;
   const int Hkv = a.pool.kv_heads;
-  const int G = Hq / Hkv;
-  const int n_items = a.q_tiles * Hq * a.num_seqs;
+  const int GW = Hq / Hkv / HPW;  // workgroups per (kv head, query tile)
+  const int n_items = a.q_tiles * Hkv * GW * a.num_seqs;
   const int per_xcd = (n_items + 7) / 8;
   const int w = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (w >= n_items) return;
-  const int gi = w % G;
-  const int tile = (w / G) % a.q_tiles;
-  const int kvh = (w / (G * a.q_tiles)) % Hkv;
-  const int b = w / (G * a.q_tiles * Hkv);
-  const int qh = kvh * G + gi;
+  const int tile = (w / GW) % a.q_tiles;
+  const int kvh = (w / (GW * a.q_tiles)) % Hkv;
+  const int b = w / (GW * a.q_tiles * Hkv);
+  const int qh = (kvh * GW + w % GW) * HPW + (threadIdx.x >> 8);  // this wavefront's query head
 
   const int c0 = a.chunk_starts[b];
   const int chunk = a.chunk_starts[b + 1] - c0;
@@ -167,8 +174,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   if (i0 >= chunk || chunk <= 0 || ctx < chunk) return;
 
   const int tid = threadIdx.x;
+  const int ltid = tid & (kPrefillThreads - 1);  // thread index within the head's 4 wavefronts
+  const int kb0 = (tid / kPrefillThreads) * (KBLK / HPW);  // first tile block this thread loads
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = ltid >> 6;
   const int h = lane >> 5;     // lane half
   const int col = lane & 31;   // query column of this lane
   const int prefix = ctx - chunk;
@@ -218,17 +227,19 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const int wlo_last = a.window > 0 ? max(0, wpos_last - a.window + 1) : 0;
   const bool wave_live = wrow0 < chunk;
 
-  TileRegs next;
+  TileRegs<KBLK / HPW> next;
   bool bad = false;
-  uint32_t use_next = load_tile(a, fetch_entries(a, table, t_begin, lane), kvh, t_begin, ctx, klo, tid, next, bad);
+  uint32_t use_next =
+      load_tile(a, fetch_entries(a, table, t_begin, lane), kvh, t_begin, ctx, klo, ltid, kb0, next, bad);
   int ent_next = fetch_entries(a, table, t_begin + BN, lane);
-  store_tile(k_lds[0], v_lds[0], tid, next, use_next, t_begin, ctx);
+  store_tile(k_lds[0], v_lds[0], ltid, kb0, next, use_next, t_begin, ctx);
   __syncthreads();
 
   int buf = 0;
   for (int kt = t_begin; kt < khi; kt += BN, buf ^= 1) {
     const bool has_next = kt + BN < khi;
-    if (has_next) use_next = load_tile(a, ent_next, kvh, kt + BN, ctx, klo, tid, next, bad);  // in flight during the math
+    if (has_next)  // in flight during the math
+      use_next = load_tile(a, ent_next, kvh, kt + BN, ctx, klo, ltid, kb0, next, bad);
     // entries of the tile after next, issued behind this tile's loads
     ent_next = fetch_entries(a, table, kt + 2 * BN, lane);
 
@@ -333,7 +344,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
       }
     }
 
-    if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
+    if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], ltid, kb0, next, use_next, kt + BN, ctx);
     __syncthreads();  // next tile visible; this tile no longer read
   }
 
@@ -357,10 +368,13 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 
 }  // namespace
 
-hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
-  const int n_items = a.q_tiles * a.q_heads * a.num_seqs;
+hipError_t launch_prefill(const PrefillArgs &a, int heads_per_wg, hipStream_t s) {
+  const int n_items = a.q_tiles * (a.q_heads / heads_per_wg) * a.num_seqs;
   const int grid = (n_items + 7) / 8 * 8;
-  hipLaunchKernelGGL(paged_prefill_kernel, dim3(grid), dim3(kPrefillThreads), 0, s, a);
+  if (heads_per_wg == 2)
+    hipLaunchKernelGGL(paged_prefill_kernel<2>, dim3(grid), dim3(2 * kPrefillThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(paged_prefill_kernel<1>, dim3(grid), dim3(kPrefillThreads), 0, s, a);
   return hipGetLastError();
 }
 

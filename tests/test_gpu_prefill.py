@@ -112,8 +112,9 @@ def test_prefill_ragged_full_oracle(ctx, W):
     assert_parity(out, ref, what=f"ragged W={W}")
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (32, 4), (16, 1)])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (32, 4), (16, 1), (12, 4)])
 def test_prefill_gqa_groups(ctx, Hq, Hkv):
+    """Groups of 1 and 3 run one query head per workgroup, even groups two."""
     prefix, chunk = [40, 0], [100, 129]
     batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, 0, Hq + Hkv)
     opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks, pool.raw())
@@ -132,3 +133,15 @@ def test_prefill_rejects_quantized_pool(ctx):
         ctx.paged_prefill(pool, desc, torch.zeros(16 * D, dtype=torch.int16, device="cuda"),
                           torch.zeros(16 * D, dtype=torch.int16, device="cuda"), 0.1)
     assert e.value.status == llm_hip.ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("W", [0, 300])
+def test_prefill_two_heads_per_workgroup_match_one(ctx, W, monkeypatch):
+    """Two query heads sharing a workgroup's K/V tiles give the same bits as one head
+    per workgroup: the per-wavefront arithmetic is identical, only the tile loads are shared."""
+    prefix, chunk = [0, 300, 1500], [77, 256, 512]
+    monkeypatch.setenv("LLH_PREFILL_HEADS_PER_WG", "1")
+    one = build(ctx, prefix, chunk, 16, 4, W, 60 + W)[4]
+    monkeypatch.delenv("LLH_PREFILL_HEADS_PER_WG")
+    two = build(ctx, prefix, chunk, 16, 4, W, 60 + W)[4]
+    assert np.array_equal(one, two)
