@@ -429,6 +429,77 @@ int llh_block_pool_commit_tokens(llh_block_pool *bp, uint64_t block_id, size_t n
 int llh_block_pool_read_rows_f32(llh_block_pool *bp, uint64_t block_id, int32_t tensor, float *h_out,
                                  size_t capacity, size_t *count);
 
+/* ---------------------------------------------------------------------------
+ * Prefix cache: the driver-side longest-prefix lookup over token ids
+ * (NativeTextPrefixCache, crates/llm-native-runtime/src/native_text/prefix_cache.rs:20-336).
+ * Entries are keyed by (namespace, exact token sequence) -- the namespace is
+ * the caller's serialisation of NativeTextPrefixCacheNamespace
+ * (prefix_cache.rs:59-80), compared byte for byte.  A payload is a hidden row
+ * (f32) plus opaque 64-bit state handles (here: BlockPool block ids holding the
+ * prefix's K/V); its size is 4 * n_hidden + state_bytes (the reference's
+ * prefix_cache_entry_bytes).  A successful store takes the cache's own
+ * reference to the handles (`retain`, like the reference cloning the caller's
+ * caches into the payload), each hit takes one more for the caller (the
+ * reference's Arc clone of the hit payload, prefix_cache.rs:256-275), and the
+ * cache's reference goes (`release`) when the entry is evicted, replaced or the
+ * cache destroyed.  Callbacks run outside the cache's lock.
+ * ------------------------------------------------------------------------- */
+typedef struct llh_prefix_cache llh_prefix_cache;
+typedef void (*llh_prefix_retain_fn)(void *user, const uint64_t *states, size_t n_states);
+typedef void (*llh_prefix_release_fn)(void *user, const uint64_t *states, size_t n_states);
+/* lookup_compatible's predicate (prefix_cache.rs:223-229): nonzero = reusable */
+typedef int (*llh_prefix_compatible_fn)(void *user, const uint64_t *states, size_t n_states);
+
+typedef struct llh_prefix_hit {
+  uint64_t token_count; /* 0 = miss */
+  uint64_t n_hidden;
+  uint64_t n_states;
+  uint64_t byte_len;
+} llh_prefix_hit;
+
+/* NativeTextPrefixCacheCounters (prefix_cache.rs:170-196); every counter saturates */
+typedef struct llh_prefix_cache_counters {
+  uint64_t hits, misses, stores, evictions, rejected, reused_tokens;
+  uint64_t prefill_chunks, prefill_tokens, checkpoint_stores, checkpoint_store_tokens;
+  uint64_t checkpoint_reuse_hits, checkpoint_reused_tokens, shared_prefix_hits, shared_prefix_reused_tokens;
+  uint64_t hit_tokens, miss_tokens, avoided_prefill_tokens, entries_scanned, namespace_entries_scanned;
+  uint64_t hit_clone_bytes, bytes_stored, bytes_evicted, resident_bytes, resident_entries;
+} llh_prefix_cache_counters;
+
+enum {
+  LLH_PREFIX_RECORD_PREFILL_CHUNK = 0,        /* record_prefill_chunk (prefix_cache.rs:556-561) */
+  LLH_PREFIX_RECORD_CHECKPOINT_STORE = 1,     /* record_checkpoint_store */
+  LLH_PREFIX_RECORD_CHECKPOINT_REUSE = 2,     /* record_checkpoint_reuse */
+  LLH_PREFIX_RECORD_SHARED_PREFIX_REUSE = 3,  /* record_shared_prefix_reuse */
+  LLH_PREFIX_RECORD_HIT = 4,                  /* record_hit for a hit served elsewhere (disk tier) */
+  LLH_PREFIX_RECORD_MISS_TOKENS = 5           /* record_miss_tokens */
+};
+
+/* NativeTextPrefixCache::new (prefix_cache.rs:204-209) */
+int llh_prefix_cache_create(uint64_t max_bytes, llh_prefix_retain_fn retain, llh_prefix_release_fn release,
+                            void *user, llh_prefix_cache **out);
+int llh_prefix_cache_destroy(llh_prefix_cache *pc);
+/* store (prefix_cache.rs:256-336): *stored = 0 for an empty token list or an
+ * entry over the whole budget (counted as rejected) */
+int llh_prefix_cache_store(llh_prefix_cache *pc, const char *ns, size_t ns_len, const uint32_t *tokens,
+                           size_t n_tokens, const float *hidden, size_t n_hidden, const uint64_t *states,
+                           size_t n_states, uint64_t state_bytes, int32_t *stored);
+/* lookup_compatible (prefix_cache.rs:223-254); compatible = NULL accepts any
+ * entry (lookup).  Copies up to hidden_cap / states_cap values out. */
+int llh_prefix_cache_lookup(llh_prefix_cache *pc, const char *ns, size_t ns_len, const uint32_t *tokens,
+                            size_t n_tokens, llh_prefix_compatible_fn compatible, void *compat_user,
+                            llh_prefix_hit *hit, float *hidden_out, size_t hidden_cap, uint64_t *states_out,
+                            size_t states_cap);
+/* driver-side counters (NativeTextPrefixCacheMetrics::record_*) */
+int llh_prefix_cache_record(llh_prefix_cache *pc, int32_t kind, uint64_t tokens);
+int llh_prefix_cache_metrics(llh_prefix_cache *pc, llh_prefix_cache_counters *out);
+/* introspection for tests: namespace buckets, entries and indexed lengths of
+ * one namespace, resident bytes; the index-th entry in LRU order (oldest first) */
+int llh_prefix_cache_shape(llh_prefix_cache *pc, const char *ns, size_t ns_len, uint64_t *namespaces,
+                           uint64_t *entries_in_ns, uint64_t *indexed_in_ns, uint64_t *used_bytes);
+int llh_prefix_cache_lru_entry(llh_prefix_cache *pc, size_t index, char *ns_out, size_t ns_cap, size_t *ns_len,
+                               uint32_t *tokens_out, size_t tokens_cap, size_t *n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@ The shared library must exist: there is no fallback path.  Build it with
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 import os
 from typing import Optional, Sequence
 
@@ -188,6 +189,32 @@ class SessionInfo(ctypes.Structure):
                                               "owned_block_count")]
 
 
+class PrefixHit(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("token_count", "n_hidden", "n_states", "byte_len")]
+
+
+PREFIX_COUNTER_FIELDS = (
+    "hits", "misses", "stores", "evictions", "rejected", "reused_tokens", "prefill_chunks", "prefill_tokens",
+    "checkpoint_stores", "checkpoint_store_tokens", "checkpoint_reuse_hits", "checkpoint_reused_tokens",
+    "shared_prefix_hits", "shared_prefix_reused_tokens", "hit_tokens", "miss_tokens", "avoided_prefill_tokens",
+    "entries_scanned", "namespace_entries_scanned", "hit_clone_bytes", "bytes_stored", "bytes_evicted",
+    "resident_bytes", "resident_entries")
+
+
+class PrefixCacheCounters(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in PREFIX_COUNTER_FIELDS]
+
+
+PREFIX_HANDLES_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t)
+PREFIX_COMPATIBLE_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.c_size_t)
+PREFIX_RECORD_PREFILL_CHUNK = 0
+PREFIX_RECORD_CHECKPOINT_STORE = 1
+PREFIX_RECORD_CHECKPOINT_REUSE = 2
+PREFIX_RECORD_SHARED_PREFIX_REUSE = 3
+PREFIX_RECORD_HIT = 4
+PREFIX_RECORD_MISS_TOKENS = 5
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _SZ = ctypes.c_size_t
@@ -265,6 +292,18 @@ SIGNATURES = {
     "llh_block_pool_append_f32": (ctypes.c_int, [_P, _U64, _FP, _FP, _SZ]),
     "llh_block_pool_commit_tokens": (ctypes.c_int, [_P, _U64, _SZ]),
     "llh_block_pool_read_rows_f32": (ctypes.c_int, [_P, _U64, _I32, _FP, _SZ, ctypes.POINTER(_SZ)]),
+    "llh_prefix_cache_create": (ctypes.c_int, [_U64, PREFIX_HANDLES_FN, PREFIX_HANDLES_FN, _P, ctypes.POINTER(_P)]),
+    "llh_prefix_cache_destroy": (ctypes.c_int, [_P]),
+    "llh_prefix_cache_store": (ctypes.c_int, [_P, ctypes.c_char_p, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, _U64,
+                                              ctypes.POINTER(_I32)]),
+    "llh_prefix_cache_lookup": (ctypes.c_int, [_P, ctypes.c_char_p, _SZ, _P, _SZ, PREFIX_COMPATIBLE_FN, _P,
+                                               ctypes.POINTER(PrefixHit), _P, _SZ, _P, _SZ]),
+    "llh_prefix_cache_record": (ctypes.c_int, [_P, _I32, _U64]),
+    "llh_prefix_cache_metrics": (ctypes.c_int, [_P, ctypes.POINTER(PrefixCacheCounters)]),
+    "llh_prefix_cache_shape": (ctypes.c_int, [_P, ctypes.c_char_p, _SZ, ctypes.POINTER(_U64), ctypes.POINTER(_U64),
+                                              ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "llh_prefix_cache_lru_entry": (ctypes.c_int, [_P, _SZ, _P, _SZ, ctypes.POINTER(_SZ), _P, _SZ,
+                                                  ctypes.POINTER(_SZ)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -894,3 +933,120 @@ class BlockPool:
 
     def values(self, block_id: int) -> np.ndarray:
         return self.rows(block_id, 1)
+
+
+@dataclass
+class PrefixCacheHitResult:
+    """NativeTextPrefixCacheHit (prefix_cache.rs:162-167): the reused token count, the cached
+    hidden row and the state handles (the caller now holds a reference to them)."""
+    token_count: int
+    hidden: np.ndarray
+    states: np.ndarray
+    byte_len: int
+
+
+class PrefixCache:
+    """ctypes mirror of the native prefix cache (NativeTextPrefixCache,
+    crates/llm-native-runtime/src/native_text/prefix_cache.rs:20-336).
+
+    `retain` / `release` receive the payload's state handles (a numpy uint64 array):
+    release when the cache drops a payload, retain for each hit."""
+
+    def __init__(self, max_bytes: int, retain=None, release=None):
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+
+        def wrap(fn):
+            if fn is None:
+                return PREFIX_HANDLES_FN()
+            return PREFIX_HANDLES_FN(lambda _u, p, n: fn(np.ctypeslib.as_array(p, (n,)).copy() if n else
+                                                          np.zeros(0, np.uint64)))
+
+        self._retain = wrap(retain)
+        self._release = wrap(release)
+        st = self._lib.llh_prefix_cache_create(max_bytes, self._retain, self._release, None, ctypes.byref(h))
+        if st != OK:
+            raise LlhError(st, "llh_prefix_cache_create")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            self._lib.llh_prefix_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _ns(namespace) -> bytes:
+        return namespace if isinstance(namespace, bytes) else str(namespace).encode()
+
+    def _check(self, st: int, what: str):
+        if st != OK:
+            raise LlhError(st, what)
+
+    def store(self, namespace, tokens, hidden, states, state_bytes: int) -> bool:
+        ns = self._ns(namespace)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        hd = np.ascontiguousarray(hidden, dtype=np.float32)
+        sv = np.ascontiguousarray(states, dtype=np.uint64)
+        out = _I32()
+        self._check(self._lib.llh_prefix_cache_store(self._h, ns, len(ns), t.ctypes.data, t.size, hd.ctypes.data,
+                                                     hd.size, sv.ctypes.data, sv.size, int(state_bytes),
+                                                     ctypes.byref(out)), "llh_prefix_cache_store")
+        return bool(out.value)
+
+    def lookup(self, namespace, tokens, compatible=None, max_hidden: int = 1 << 16, max_states: int = 1 << 16):
+        """lookup / lookup_compatible: the longest stored prefix of `tokens` that `compatible`
+        (a function of the state handles) accepts, or None."""
+        ns = self._ns(namespace)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        hit = PrefixHit()
+        hidden = np.zeros(max_hidden, np.float32)
+        states = np.zeros(max_states, np.uint64)
+        cb = PREFIX_COMPATIBLE_FN() if compatible is None else PREFIX_COMPATIBLE_FN(
+            lambda _u, p, n: 1 if compatible(np.ctypeslib.as_array(p, (n,)).copy() if n else np.zeros(0, np.uint64))
+            else 0)
+        self._check(self._lib.llh_prefix_cache_lookup(self._h, ns, len(ns), t.ctypes.data, t.size, cb, None,
+                                                      ctypes.byref(hit), hidden.ctypes.data, hidden.size,
+                                                      states.ctypes.data, states.size), "llh_prefix_cache_lookup")
+        if hit.token_count == 0:
+            return None
+        return PrefixCacheHitResult(int(hit.token_count), hidden[: hit.n_hidden].copy(),
+                                    states[: hit.n_states].copy(), int(hit.byte_len))
+
+    def record(self, kind: int, tokens: int):
+        self._check(self._lib.llh_prefix_cache_record(self._h, kind, int(tokens)), "llh_prefix_cache_record")
+
+    def metrics(self) -> dict:
+        c = PrefixCacheCounters()
+        self._check(self._lib.llh_prefix_cache_metrics(self._h, ctypes.byref(c)), "llh_prefix_cache_metrics")
+        return {f: int(getattr(c, f)) for f in PREFIX_COUNTER_FIELDS}
+
+    def shape(self, namespace=b"") -> dict:
+        ns = self._ns(namespace)
+        a, b, c, d = _U64(), _U64(), _U64(), _U64()
+        self._check(self._lib.llh_prefix_cache_shape(self._h, ns, len(ns), ctypes.byref(a), ctypes.byref(b),
+                                                     ctypes.byref(c), ctypes.byref(d)), "llh_prefix_cache_shape")
+        return {"namespaces": a.value, "entries": b.value, "indexed": c.value, "used_bytes": d.value}
+
+    def lru_order(self) -> list:
+        """(namespace, tokens) of every resident entry, least recently used first."""
+        out = []
+        i = 0
+        while True:
+            nl, nt = _SZ(), _SZ()
+            st = self._lib.llh_prefix_cache_lru_entry(self._h, i, None, 0, ctypes.byref(nl), None, 0, ctypes.byref(nt))
+            if st != OK:
+                break
+            nsb = ctypes.create_string_buffer(max(1, nl.value))
+            toks = np.zeros(max(1, nt.value), np.uint32)
+            self._check(self._lib.llh_prefix_cache_lru_entry(self._h, i, nsb, nl.value, ctypes.byref(nl),
+                                                             toks.ctypes.data, nt.value, ctypes.byref(nt)),
+                        "llh_prefix_cache_lru_entry")
+            out.append((nsb.raw[: nl.value].decode(), [int(x) for x in toks[: nt.value]]))
+            i += 1
+        return out
