@@ -44,7 +44,8 @@ typedef enum llh_status {
   LLH_ERR_UNSUPPORTED = -4,   /* KvCacheError::UnsupportedFormat */
   LLH_ERR_DEVICE = -5,        /* HIP runtime failure: caller may record a fallback (native_matvec.rs:2979-2999) */
   LLH_ERR_STALE = -6,         /* block id / revision mismatch (layer.rs:1001-1009) */
-  LLH_ERR_NULL = -7           /* NULL handle or pointer */
+  LLH_ERR_NULL = -7,          /* NULL handle or pointer */
+  LLH_ERR_INTEGRITY = -8      /* NativeTextDiskCacheError::Integrity (native_text/disk_cache.rs:262-270) */
 } llh_status;
 
 /* KV storage formats (crates/llm-kv-cache/src/format.rs:5-21 plus the two
@@ -151,6 +152,12 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
  * fp8 pools return LLH_ERR_UNSUPPORTED (their scale is per block: use llh_kv_write_blocks). */
 int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k,
                   const void *d_v, int32_t n, void *stream);
+/* llh_kv_append from f32 rows (d_k, d_v [n][kv_heads][head_dim] f32): the
+ * restore side of a disk block, whose tensors are f32 (codec.rs:72-99); the
+ * bf16 rounding is round-to-nearest-even, so rows exported from a bf16 pool
+ * come back bit for bit. */
+int llh_kv_append_f32(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const float *d_k,
+                      const float *d_v, int32_t n, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* batched paged attention (the hot path)                             */
@@ -499,6 +506,123 @@ int llh_prefix_cache_shape(llh_prefix_cache *pc, const char *ns, size_t ns_len, 
                            uint64_t *entries_in_ns, uint64_t *indexed_in_ns, uint64_t *used_bytes);
 int llh_prefix_cache_lru_entry(llh_prefix_cache *pc, size_t index, char *ns_out, size_t ns_cap, size_t *ns_len,
                                uint32_t *tokens_out, size_t tokens_cap, size_t *n_tokens);
+
+/* ---------------------------------------------------------------------------
+ * On-disk prefix KV blocks (the SSD tier behind the prefix cache,
+ * crates/llm-native-runtime/src/native_text/disk_cache.rs, disk_cache/io.rs,
+ * disk_cache/codec.rs, disk_cache/hashing.rs).  A block file is a safetensors
+ * archive: u64le header length, a JSON header with "__metadata__":{"kir_ai":
+ * <block metadata JSON>} and one F32 tensor per name ("hidden",
+ * "layers.<i>.full.keys", ...), tensors in name order.  The encoder writes the
+ * bytes the reference writes for the same content.  Hashes are lowercase hex
+ * SHA-256, 64 characters plus NUL.  Errors other than NULL arguments are
+ * LLH_ERR_INTEGRITY with the reference's message in llh_disk_last_error().
+ * K/V travel as f32 rows: llh_kv_export_rows_f32 reads them out of a device
+ * pool, llh_kv_append writes them back.
+ * ------------------------------------------------------------------------- */
+enum {
+  LLH_DISK_LAYER_QWEN_FULL = 0, /* "qwen_full_attention", tensors layers.<i>.full.{keys,values} */
+  LLH_DISK_LAYER_GEMMA = 1,     /* "gemma_attention", tensors layers.<i>.attention.{keys,values} */
+  LLH_DISK_LAYER_OTHER = 2      /* "qwen_linear_attention": recurrent state, not paged KV (read side only) */
+};
+
+/* NativeTextDiskCacheBlockDescriptor (disk_cache.rs:165-217) */
+typedef struct llh_disk_block_descriptor {
+  char model_hash[65];
+  char snapshot_hash[65];
+  char model_family[64];
+  char namespace_hash[65];
+  char previous_block_hash[65];
+  char block_hash[65];
+  uint64_t block_start;
+  uint64_t token_count;
+  uint32_t cache_layout_version;
+  uint32_t n_layers; /* filled by llh_disk_block_read_descriptor only */
+} llh_disk_block_descriptor;
+
+/* NativeTextDiskCacheIdentity (disk_cache.rs:93-147); allowed_namespace_hash may be NULL */
+typedef struct llh_disk_identity {
+  const char *model_hash;
+  const char *snapshot_hash;
+  const char *model_family;
+  const char *allowed_namespace_hash;
+} llh_disk_identity;
+
+/* One full-attention layer of a block (NativeTextDiskFullAttentionLayout,
+ * codec.rs:43-55): keys / values are token_count x key_value_heads x head_dim f32 */
+typedef struct llh_disk_layer {
+  int32_t kind; /* LLH_DISK_LAYER_QWEN_FULL or LLH_DISK_LAYER_GEMMA */
+  uint64_t revision, max_tokens, key_value_heads, head_dim, token_count, tokens_seen;
+  const float *keys;
+  const float *values;
+} llh_disk_layer;
+
+typedef struct llh_disk_layer_info {
+  int32_t kind;
+  uint64_t revision, max_tokens, key_value_heads, head_dim, token_count, tokens_seen;
+  uint64_t n_values; /* f32 values per tensor */
+} llh_disk_layer_info;
+
+typedef struct llh_disk_block llh_disk_block;
+
+/* message of the calling thread's last LLH_ERR_INTEGRITY from this family */
+const char *llh_disk_last_error(void);
+/* hash_components (hashing.rs:178-190): label, then (name, value-or-NULL) pairs --
+ * the snapshot, model and namespace hashes (hashing.rs:32-128) are this with
+ * their labels and component lists */
+int llh_disk_hash_components(const char *label, size_t n, const char *const *names, const char *const *values,
+                             char out_hex[65]);
+/* native_text_disk_block_hash (hashing.rs:130-150) */
+int llh_disk_block_hash(const char *model_hash, const char *namespace_hash, const char *previous_block_hash,
+                        uint64_t block_start, const uint64_t *tokens, size_t n_tokens, char out_hex[65]);
+/* native_text_disk_previous_block_hash (hashing.rs:152-176) */
+int llh_disk_previous_block_hash(const char *model_hash, const char *namespace_hash, uint64_t block_start,
+                                 uint64_t block_token_count, const uint64_t *prefix_tokens, size_t n_prefix,
+                                 char out_hex[65]);
+/* NativeTextDiskCacheBlockDescriptor::new (disk_cache.rs:176-217): the block is
+ * prefix_tokens[block_start..] */
+int llh_disk_block_descriptor_new(const llh_disk_identity *identity, const char *namespace_hash,
+                                  uint32_t cache_layout_version, uint64_t block_start, const uint64_t *prefix_tokens,
+                                  size_t n_prefix, llh_disk_block_descriptor *out);
+/* path_for_descriptor (disk_cache.rs:527-534) below the cache root:
+ * <model_hash>/<namespace_hash>/<block_hash[0:2]>/<block_hash>.safetensors */
+int llh_disk_block_path(const llh_disk_block_descriptor *desc, char *out, size_t capacity, size_t *length);
+/* NativeTextDiskCacheBlock::encode (io.rs:40-69).  out = NULL reports the size
+ * in *length; a short buffer is LLH_ERR_CAPACITY. */
+int llh_disk_block_encode(const llh_disk_block_descriptor *desc, const float *hidden, size_t n_hidden,
+                          const llh_disk_layer *layers, size_t n_layers, uint8_t *out, size_t capacity,
+                          size_t *length);
+/* Parses a block file (header, metadata, tensor table: io.rs:195-204); the
+ * handle keeps its own copy of the bytes. */
+int llh_disk_block_open(const uint8_t *bytes, size_t length, llh_disk_block **out);
+int llh_disk_block_close(llh_disk_block *blk);
+/* decode_descriptor (io.rs:105-121): the metadata's descriptor, after the codec / layout check */
+int llh_disk_block_read_descriptor(const llh_disk_block *blk, llh_disk_block_descriptor *out);
+/* the checks of NativeTextDiskCacheBlock::decode (io.rs:71-103), in its order */
+int llh_disk_block_validate(const llh_disk_block *blk, const llh_disk_block_descriptor *expected,
+                            const llh_disk_identity *identity);
+/* the hidden row: *count values, up to capacity copied (out may be NULL) */
+int llh_disk_block_hidden(const llh_disk_block *blk, float *out, size_t capacity, size_t *count);
+/* decode_layer_kv_snapshot (codec.rs:101-130) for layer `index`; up to
+ * capacity values of each tensor copied.  LLH_ERR_UNSUPPORTED for a linear
+ * attention layer, LLH_ERR_INVALID_SHAPE past the last layer. */
+int llh_disk_block_layer(const llh_disk_block *blk, size_t index, llh_disk_layer_info *info, float *keys,
+                         float *values, size_t capacity);
+
+/* The checks that join consecutive blocks of one prefix
+ * (validate_contiguous_disk_blocks and assemble_layer_kv_prefix_state_blocks,
+ * codec.rs:252-322): block starts contiguous from 0, the same layer kinds and
+ * KV shapes in every block, the joined rows within each layer's max_tokens.
+ * *total_tokens = the prefix length. */
+int llh_disk_blocks_assemble_check(const llh_disk_block *const *blocks, size_t n, uint64_t *total_tokens);
+
+/* Reads n token rows (K and V, kv_heads x head_dim each) of a device pool as
+ * f32 into d_k / d_v: row i is token slot d_slots[i] (pool block * block_tokens
+ * + offset).  Dequantises int8 / fp8 with the block's scales -- the
+ * LayerKvCacheSnapshot keys()/values() view the disk encoder consumes
+ * (codec.rs:72-99). */
+int llh_kv_export_rows_f32(llh_ctx *ctx, const llh_kv_pool *pool, const int64_t *d_slots, int64_t n, float *d_k,
+                           float *d_v, void *stream);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <cmath>
 #include <cstdio>
@@ -320,8 +321,8 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
   return LLH_OK;
 }
 
-int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
-                  int32_t n, void *stream) {
+static int kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
+                     int32_t n, int32_t src_f32, void *stream) {
   if (!ctx || !pool) return LLH_ERR_NULL;
   if (pool->view.format == LLH_KV_FP8_E4M3)
     return ctx->fail(LLH_ERR_UNSUPPORTED, "fp8 pools carry per-block scales: write whole blocks");
@@ -338,11 +339,39 @@ int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const
   a.k = d_k;
   a.v = d_v;
   a.n = n;
-  a.src_f32 = 0;
+  a.src_f32 = src_f32;
   a.err = ctx->d_err;
   ctx->append_calls++;
   hipError_t e = launch_append(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "append launch");
+  return LLH_OK;
+}
+
+int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
+                  int32_t n, void *stream) {
+  return kv_append(ctx, pool, d_slots, d_k, d_v, n, 0, stream);
+}
+
+int llh_kv_append_f32(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const float *d_k, const float *d_v,
+                      int32_t n, void *stream) {
+  return kv_append(ctx, pool, d_slots, d_k, d_v, n, 1, stream);
+}
+
+int llh_kv_export_rows_f32(llh_ctx *ctx, const llh_kv_pool *pool, const int64_t *d_slots, int64_t n, float *d_k,
+                           float *d_v, void *stream) {
+  if (!ctx || !pool) return LLH_ERR_NULL;
+  if (n < 0 || n > INT32_MAX) return ctx->fail(LLH_ERR_INVALID_SHAPE, "row count out of range");
+  if (n == 0) return LLH_OK;
+  if (!d_slots || !d_k || !d_v) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  ExportArgs a{};
+  a.pool = pool->view;
+  a.slots = d_slots;
+  a.k = d_k;
+  a.v = d_v;
+  a.n = (int32_t)n;
+  a.err = ctx->d_err;
+  hipError_t e = launch_export_rows(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "export launch");
   return LLH_OK;
 }
 

@@ -216,6 +216,40 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
   }
 }
 
+__device__ __forceinline__ float load_f32(const PoolView &p, const void *base, const void *sc, size_t bh, size_t idx,
+                                          int off) {
+  if (p.format == kBf16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
+  if (p.format == kInt8) {
+    const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + off]);
+    return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
+  }
+  return __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)reinterpret_cast<const uint8_t *>(base)[idx], false)[0] *
+         reinterpret_cast<const float *>(sc)[bh];
+}
+
+// One wavefront per (slot, kv head): K and V of that token as f32 rows
+// k[i][h][d], v[i][h][d] (V is stored d-major within a block).
+__global__ __launch_bounds__(64) void export_rows_kernel(const ExportArgs a) {
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  const int64_t slot = a.slots[i];
+  const int64_t blk = slot / BT;
+  const int off = (int)(slot % BT);
+  if (slot < 0 || blk >= a.pool.n_blocks) {
+    if (threadIdx.x == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const size_t orow = ((size_t)i * Hkv + h) * Dh;
+  for (int d = threadIdx.x; d < Dh; d += 64) {
+    a.k[orow + d] = load_f32(a.pool, a.pool.k, a.pool.k_scales, bh, (bh * BT + off) * Dh + d, off);
+    a.v[orow + d] = load_f32(a.pool, a.pool.v, a.pool.v_scales, bh, (bh * Dh + d) * BT + off, off);
+  }
+}
+
 // One wavefront per (position, kv head): raw elements out[pos-lo][h][d].
 __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
   const int r = blockIdx.x;
@@ -244,19 +278,9 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
   const void *sc = a.tensor ? a.pool.v_scales : a.pool.k_scales;
   for (int d = threadIdx.x; d < Dh; d += 64) {
     const size_t idx = a.tensor ? (bh * Dh + d) * BT + off : (bh * BT + off) * Dh + d;
-    if (a.out_f32) {
-      float x;
-      if (a.pool.format == kBf16) {
-        x = bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
-      } else if (a.pool.format == kInt8) {
-        const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * BT + off]);
-        x = (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
-      } else {
-        x = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)reinterpret_cast<const uint8_t *>(base)[idx], false)[0] *
-            reinterpret_cast<const float *>(sc)[bh];
-      }
-      reinterpret_cast<float *>(a.out)[orow + d] = x;
-    } else if (a.pool.format == kBf16)
+    if (a.out_f32)
+      reinterpret_cast<float *>(a.out)[orow + d] = load_f32(a.pool, base, sc, bh, idx, off);
+    else if (a.pool.format == kBf16)
       reinterpret_cast<uint16_t *>(a.out)[orow + d] = reinterpret_cast<const uint16_t *>(base)[idx];
     else
       reinterpret_cast<uint8_t *>(a.out)[orow + d] = reinterpret_cast<const uint8_t *>(base)[idx];
@@ -264,6 +288,12 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
 }
 
 }  // namespace
+
+hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
+  if (a.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(export_rows_kernel, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;

@@ -135,6 +135,15 @@ struct GatherArgs {
   int32_t *err;
 };
 
+struct ExportArgs {
+  PoolView pool;
+  const int64_t *slots;     // [n] block * BT + offset
+  float *k;                 // [n][Hkv][D] f32
+  float *v;
+  int32_t n;
+  int32_t *err;
+};
+
 struct MatvecArgs {
   const uint16_t *w;        // [rows][cols] bf16, row-major
   const void *x;            // [n][ldx] bf16 or f32
@@ -159,6 +168,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int heads_per_wg, hipStream_t s)
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
+hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s);
 hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);
 hipError_t launch_matvec_bf16(const MatvecArgs &a, hipStream_t s);
 

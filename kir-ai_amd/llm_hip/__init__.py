@@ -34,6 +34,7 @@ ERR_UNSUPPORTED = -4
 ERR_DEVICE = -5
 ERR_STALE = -6
 ERR_NULL = -7
+ERR_INTEGRITY = -8
 
 KV_BF16 = 0
 KV_INT8 = 1
@@ -52,6 +53,7 @@ _STATUS_NAMES = {
     ERR_DEVICE: "device error",
     ERR_STALE: "stale block table",
     ERR_NULL: "null pointer",
+    ERR_INTEGRITY: "disk cache integrity",
 }
 
 
@@ -215,6 +217,35 @@ PREFIX_RECORD_SHARED_PREFIX_REUSE = 3
 PREFIX_RECORD_HIT = 4
 PREFIX_RECORD_MISS_TOKENS = 5
 
+DISK_LAYER_QWEN_FULL = 0
+DISK_LAYER_GEMMA = 1
+DISK_LAYER_OTHER = 2
+
+
+class DiskBlockDescriptor(ctypes.Structure):
+    _fields_ = [("model_hash", ctypes.c_char * 65), ("snapshot_hash", ctypes.c_char * 65),
+                ("model_family", ctypes.c_char * 64), ("namespace_hash", ctypes.c_char * 65),
+                ("previous_block_hash", ctypes.c_char * 65), ("block_hash", ctypes.c_char * 65),
+                ("block_start", ctypes.c_uint64), ("token_count", ctypes.c_uint64),
+                ("cache_layout_version", ctypes.c_uint32), ("n_layers", ctypes.c_uint32)]
+
+
+class DiskIdentity(ctypes.Structure):
+    _fields_ = [("model_hash", ctypes.c_char_p), ("snapshot_hash", ctypes.c_char_p),
+                ("model_family", ctypes.c_char_p), ("allowed_namespace_hash", ctypes.c_char_p)]
+
+
+class DiskLayer(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32)] + [(n, ctypes.c_uint64) for n in (
+        "revision", "max_tokens", "key_value_heads", "head_dim", "token_count", "tokens_seen")] + [
+        ("keys", ctypes.POINTER(ctypes.c_float)), ("values", ctypes.POINTER(ctypes.c_float))]
+
+
+class DiskLayerInfo(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32)] + [(n, ctypes.c_uint64) for n in (
+        "revision", "max_tokens", "key_value_heads", "head_dim", "token_count", "tokens_seen", "n_values")]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _SZ = ctypes.c_size_t
@@ -238,6 +269,8 @@ SIGNATURES = {
     "llh_kv_pool_get_info": (ctypes.c_int, [_P, ctypes.POINTER(PoolInfo)]),
     "llh_kv_write_blocks": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
     "llh_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
+    "llh_kv_append_f32": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
+    "llh_kv_export_rows_f32": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, _P, _P]),
     "llh_paged_decode": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
     "llh_paged_prefill": (ctypes.c_int, [_P, _P, ctypes.POINTER(PrefillDesc), _P, _P, ctypes.c_float, _P]),
     "llh_debug_gather": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _I32, _I32, _I32, _I32, _P, _P]),
@@ -304,6 +337,23 @@ SIGNATURES = {
                                               ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
     "llh_prefix_cache_lru_entry": (ctypes.c_int, [_P, _SZ, _P, _SZ, ctypes.POINTER(_SZ), _P, _SZ,
                                                   ctypes.POINTER(_SZ)]),
+    "llh_disk_last_error": (ctypes.c_char_p, []),
+    "llh_disk_hash_components": (ctypes.c_int, [ctypes.c_char_p, _SZ, _P, _P, _P]),
+    "llh_disk_block_hash": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _U64, _P, _SZ, _P]),
+    "llh_disk_previous_block_hash": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _U64, _U64, _P, _SZ, _P]),
+    "llh_disk_block_descriptor_new": (ctypes.c_int, [ctypes.POINTER(DiskIdentity), ctypes.c_char_p, ctypes.c_uint32,
+                                                     _U64, _P, _SZ, ctypes.POINTER(DiskBlockDescriptor)]),
+    "llh_disk_block_path": (ctypes.c_int, [ctypes.POINTER(DiskBlockDescriptor), _P, _SZ, ctypes.POINTER(_SZ)]),
+    "llh_disk_block_encode": (ctypes.c_int, [ctypes.POINTER(DiskBlockDescriptor), _P, _SZ, ctypes.POINTER(DiskLayer),
+                                             _SZ, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "llh_disk_block_open": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(_P)]),
+    "llh_disk_block_close": (ctypes.c_int, [_P]),
+    "llh_disk_block_read_descriptor": (ctypes.c_int, [_P, ctypes.POINTER(DiskBlockDescriptor)]),
+    "llh_disk_block_validate": (ctypes.c_int, [_P, ctypes.POINTER(DiskBlockDescriptor),
+                                               ctypes.POINTER(DiskIdentity)]),
+    "llh_disk_block_hidden": (ctypes.c_int, [_P, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "llh_disk_block_layer": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(DiskLayerInfo), _P, _P, _SZ]),
+    "llh_disk_blocks_assemble_check": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(_U64)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -483,6 +533,20 @@ class Context:
         self.check(
             self.lib.llh_kv_append(self.handle, pool.handle, _ptr(slots), _ptr(k), _ptr(v), slots.shape[0],
                                    _stream(stream))
+        )
+
+    def append_f32(self, pool: "KvPool", slots, k, v, stream=None) -> None:
+        """llh_kv_append_f32: f32 token rows (a restored disk block) into pool slots."""
+        self.check(
+            self.lib.llh_kv_append_f32(self.handle, pool.handle, _ptr(slots), _ptr(k), _ptr(v), slots.shape[0],
+                                       _stream(stream))
+        )
+
+    def export_rows_f32(self, pool: "KvPool", slots, k_out, v_out, stream=None) -> None:
+        """llh_kv_export_rows_f32: K/V of pool slots as dequantised f32 rows."""
+        self.check(
+            self.lib.llh_kv_export_rows_f32(self.handle, pool.handle, _ptr(slots), slots.shape[0], _ptr(k_out),
+                                            _ptr(v_out), _stream(stream))
         )
 
     def gather(self, pool: "KvPool", desc: DecodeDesc, seq: int, lo: int, hi: int, tensor: int, out,
@@ -1050,3 +1114,245 @@ class PrefixCache:
             out.append((nsb.raw[: nl.value].decode(), [int(x) for x in toks[: nt.value]]))
             i += 1
         return out
+
+
+# ---------------------------------------------------------------------------
+# On-disk prefix KV blocks (native_text/disk_cache.rs, disk_cache/{io,codec,hashing}.rs)
+# ---------------------------------------------------------------------------
+
+NATIVE_TEXT_DISK_CACHE_ROOT_BLOCK_HASH = "0" * 64
+
+
+class DiskCacheIntegrityError(LlhError):
+    """NativeTextDiskCacheError::Integrity (native_text/disk_cache.rs:262-270)."""
+
+
+def _disk_check(st: int, what: str) -> None:
+    if st == OK:
+        return
+    lib = load_library()
+    if st == ERR_INTEGRITY:
+        raise DiskCacheIntegrityError(st, lib.llh_disk_last_error().decode())
+    raise LlhError(st, what)
+
+
+def _b(s: Optional[str]) -> Optional[bytes]:
+    return None if s is None else s.encode()
+
+
+def disk_hash_components(label: str, components) -> str:
+    """hash_components (hashing.rs:178-190): `components` is a sequence of
+    (name, value-or-None) pairs."""
+    lib = load_library()
+    comps = list(components)
+    names = (ctypes.c_char_p * max(1, len(comps)))(*[_b(n) for n, _ in comps])
+    values = (ctypes.c_char_p * max(1, len(comps)))(*[_b(v) for _, v in comps])
+    out = ctypes.create_string_buffer(65)
+    _disk_check(lib.llh_disk_hash_components(label.encode(), len(comps), names, values, out),
+                "llh_disk_hash_components")
+    return out.value.decode()
+
+
+def native_text_disk_snapshot_hash(snapshot_identity: Optional[str]) -> str:
+    """hashing.rs:32-37"""
+    return disk_hash_components("kir-ai-native-text-disk-snapshot/v1", [("snapshot_identity", snapshot_identity)])
+
+
+def native_text_disk_model_hash(model_id: str, backend: str, snapshot_hash: str, family: Optional[str] = None,
+                                quantization: Optional[str] = None, repo_id: Optional[str] = None,
+                                resolved_commit: Optional[str] = None, profile: Optional[str] = None) -> str:
+    """hashing.rs:50-64"""
+    return disk_hash_components("kir-ai-native-text-disk-model/v1", [
+        ("model_id", model_id), ("backend", backend), ("family", family), ("quantization", quantization),
+        ("repo_id", repo_id), ("resolved_commit", resolved_commit), ("profile", profile),
+        ("snapshot_hash", snapshot_hash)])
+
+
+# NativeTextPrefixCacheNamespace fields in the order the namespace hash takes them (hashing.rs:66-128);
+# a value is a string, an int (the three counters are decimal strings there) or None for an absent option
+DISK_NAMESPACE_FIELDS = (
+    "model_id", "backend", "family", "quantization", "repo_id", "resolved_commit", "profile", "tokenizer_kind",
+    "tokenizer_hash", "tokenizer_normalization", "cache_template_id", "chat_template_kwargs_hash",
+    "adapter_settings", "cache_key", "tool_schema", "request_mode", "cache_layout_version", "cache_tokens",
+    "max_prefill_tokens")
+
+
+def native_text_disk_namespace_hash(namespace: dict) -> str:
+    comps = []
+    for f in DISK_NAMESPACE_FIELDS:
+        v = namespace.get(f)
+        comps.append((f, None if v is None else str(v)))
+    return disk_hash_components("kir-ai-native-text-disk-namespace/v1", comps)
+
+
+def native_text_disk_block_hash(model_hash: str, namespace_hash: str, previous_block_hash: str, block_start: int,
+                                tokens) -> str:
+    """hashing.rs:130-150"""
+    lib = load_library()
+    t = np.ascontiguousarray(tokens, dtype=np.uint64)
+    out = ctypes.create_string_buffer(65)
+    _disk_check(lib.llh_disk_block_hash(model_hash.encode(), namespace_hash.encode(), previous_block_hash.encode(),
+                                        block_start, t.ctypes.data, t.size, out), "llh_disk_block_hash")
+    return out.value.decode()
+
+
+def native_text_disk_previous_block_hash(model_hash: str, namespace_hash: str, block_start: int,
+                                         block_token_count: int, prefix_tokens) -> str:
+    """hashing.rs:152-176"""
+    lib = load_library()
+    t = np.ascontiguousarray(prefix_tokens, dtype=np.uint64)
+    out = ctypes.create_string_buffer(65)
+    _disk_check(lib.llh_disk_previous_block_hash(model_hash.encode(), namespace_hash.encode(), block_start,
+                                                 block_token_count, t.ctypes.data, t.size, out),
+                "llh_disk_previous_block_hash")
+    return out.value.decode()
+
+
+@dataclass
+class DiskIdentityInfo:
+    """NativeTextDiskCacheIdentity (disk_cache.rs:93-147)."""
+    model_hash: str
+    snapshot_hash: str
+    model_family: str
+    allowed_namespace_hash: Optional[str] = None
+
+    def c(self) -> DiskIdentity:
+        return DiskIdentity(_b(self.model_hash), _b(self.snapshot_hash), _b(self.model_family),
+                            _b(self.allowed_namespace_hash))
+
+
+def disk_block_descriptor(identity: DiskIdentityInfo, namespace_hash: str, cache_layout_version: int,
+                          block_start: int, prefix_tokens) -> DiskBlockDescriptor:
+    """NativeTextDiskCacheBlockDescriptor::new (disk_cache.rs:176-217)."""
+    lib = load_library()
+    t = np.ascontiguousarray(prefix_tokens, dtype=np.uint64)
+    d = DiskBlockDescriptor()
+    ident = identity.c()
+    _disk_check(lib.llh_disk_block_descriptor_new(ctypes.byref(ident), namespace_hash.encode(), cache_layout_version,
+                                                  block_start, t.ctypes.data, t.size, ctypes.byref(d)),
+                "llh_disk_block_descriptor_new")
+    return d
+
+
+def disk_block_path(desc: DiskBlockDescriptor) -> str:
+    """path_for_descriptor (disk_cache.rs:527-534), relative to the cache root."""
+    lib = load_library()
+    n = _SZ()
+    _disk_check(lib.llh_disk_block_path(ctypes.byref(desc), None, 0, ctypes.byref(n)), "llh_disk_block_path")
+    buf = ctypes.create_string_buffer(n.value + 1)
+    _disk_check(lib.llh_disk_block_path(ctypes.byref(desc), buf, n.value + 1, ctypes.byref(n)),
+                "llh_disk_block_path")
+    return buf.value.decode()
+
+
+@dataclass
+class DiskLayerRows:
+    """One full-attention layer of a block: keys / values [token_count][kv_heads][head_dim] f32."""
+    kind: int
+    revision: int
+    max_tokens: int
+    key_value_heads: int
+    head_dim: int
+    token_count: int
+    tokens_seen: int
+    keys: np.ndarray
+    values: np.ndarray
+
+
+def encode_disk_block(desc: DiskBlockDescriptor, hidden, layers: Sequence[DiskLayerRows]) -> bytes:
+    """NativeTextDiskCacheBlock::encode (io.rs:40-69)."""
+    lib = load_library()
+    h = np.ascontiguousarray(hidden, dtype=np.float32)
+    keep = []
+    arr = (DiskLayer * max(1, len(layers)))()
+    for i, L in enumerate(layers):
+        k = np.ascontiguousarray(L.keys, dtype=np.float32)
+        v = np.ascontiguousarray(L.values, dtype=np.float32)
+        keep += [k, v]
+        arr[i] = DiskLayer(L.kind, L.revision, L.max_tokens, L.key_value_heads, L.head_dim, L.token_count,
+                           L.tokens_seen, _f32_ptr(k), _f32_ptr(v))
+    n = _SZ()
+    _disk_check(lib.llh_disk_block_encode(ctypes.byref(desc), h.ctypes.data, h.size, arr, len(layers), None, 0,
+                                          ctypes.byref(n)), "llh_disk_block_encode")
+    out = (ctypes.c_uint8 * n.value)()
+    _disk_check(lib.llh_disk_block_encode(ctypes.byref(desc), h.ctypes.data, h.size, arr, len(layers), out, n.value,
+                                          ctypes.byref(n)), "llh_disk_block_encode")
+    return bytes(out)
+
+
+class DiskBlock:
+    """A parsed block file (llh_disk_block): metadata, hidden row and layer tensors."""
+
+    def __init__(self, data: bytes):
+        self._lib = load_library()
+        h = _P()
+        buf = (ctypes.c_uint8 * max(1, len(data))).from_buffer_copy(data if data else b"\0")
+        _disk_check(self._lib.llh_disk_block_open(buf, len(data), ctypes.byref(h)), "llh_disk_block_open")
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.llh_disk_block_close(self._h)
+            self._h = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def descriptor(self) -> DiskBlockDescriptor:
+        """decode_descriptor (io.rs:105-121)."""
+        d = DiskBlockDescriptor()
+        _disk_check(self._lib.llh_disk_block_read_descriptor(self._h, ctypes.byref(d)),
+                    "llh_disk_block_read_descriptor")
+        return d
+
+    def validate(self, expected: DiskBlockDescriptor, identity: DiskIdentityInfo) -> None:
+        """The checks of NativeTextDiskCacheBlock::decode (io.rs:71-103)."""
+        ident = identity.c()
+        _disk_check(self._lib.llh_disk_block_validate(self._h, ctypes.byref(expected), ctypes.byref(ident)),
+                    "llh_disk_block_validate")
+
+    def hidden(self) -> np.ndarray:
+        n = _SZ()
+        _disk_check(self._lib.llh_disk_block_hidden(self._h, None, 0, ctypes.byref(n)), "llh_disk_block_hidden")
+        out = np.zeros(n.value, np.float32)
+        _disk_check(self._lib.llh_disk_block_hidden(self._h, out.ctypes.data, out.size, ctypes.byref(n)),
+                    "llh_disk_block_hidden")
+        return out
+
+    def layer(self, index: int) -> DiskLayerRows:
+        """decode_layer_kv_snapshot (codec.rs:101-130) for one layer."""
+        info = DiskLayerInfo()
+        _disk_check(self._lib.llh_disk_block_layer(self._h, index, ctypes.byref(info), None, None, 0),
+                    "llh_disk_block_layer")
+        k = np.zeros(info.n_values, np.float32)
+        v = np.zeros(info.n_values, np.float32)
+        _disk_check(self._lib.llh_disk_block_layer(self._h, index, ctypes.byref(info), k.ctypes.data, v.ctypes.data,
+                                                   k.size), "llh_disk_block_layer")
+        shape = (int(info.token_count), int(info.key_value_heads), int(info.head_dim))
+        return DiskLayerRows(int(info.kind), int(info.revision), int(info.max_tokens), int(info.key_value_heads),
+                             int(info.head_dim), int(info.token_count), int(info.tokens_seen), k.reshape(shape),
+                             v.reshape(shape))
+
+
+def disk_blocks_assemble_check(blocks: Sequence[DiskBlock]) -> int:
+    """The joins of consecutive blocks of one prefix (codec.rs:252-322); returns the prefix length."""
+    lib = load_library()
+    arr = (_P * max(1, len(blocks)))(*[b._h.value for b in blocks])
+    total = _U64()
+    _disk_check(lib.llh_disk_blocks_assemble_check(arr, len(blocks), ctypes.byref(total)),
+                "llh_disk_blocks_assemble_check")
+    return int(total.value)
+
+
+def decode_disk_block(data: bytes, identity: DiskIdentityInfo, expected: DiskBlockDescriptor):
+    """NativeTextDiskCacheBlock::decode (io.rs:71-103): (hidden, [layers]) or DiskCacheIntegrityError."""
+    blk = DiskBlock(data)
+    try:
+        blk.validate(expected, identity)
+        d = blk.descriptor()
+        return blk.hidden(), [blk.layer(i) for i in range(d.n_layers)]
+    finally:
+        blk.close()

@@ -49,6 +49,12 @@ STRUCTS = {
     "llh_paged_kv_metrics": llm_hip.PagedKvMetrics,
     "llh_cache_block_info": llm_hip.CacheBlockInfo,
     "llh_session_info": llm_hip.SessionInfo,
+    "llh_prefix_hit": llm_hip.PrefixHit,
+    "llh_prefix_cache_counters": llm_hip.PrefixCacheCounters,
+    "llh_disk_block_descriptor": llm_hip.DiskBlockDescriptor,
+    "llh_disk_identity": llm_hip.DiskIdentity,
+    "llh_disk_layer": llm_hip.DiskLayer,
+    "llh_disk_layer_info": llm_hip.DiskLayerInfo,
 }
 
 
