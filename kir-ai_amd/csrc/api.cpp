@@ -448,7 +448,6 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     a.split_blocks = plan.split_blocks;
     a.max_splits = plan.max_splits;
     a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
-    a.wave_splits = env_int("LLH_DECODE_WAVE_SPLITS", 0) ? 1 : 0;
     a.stream_wgs = stream_wgs;
     a.max_seq_len = desc->max_seq_len;
     a.seg_desc = stream_wgs ? reinterpret_cast<int32_t *>(ws + desc_off) : nullptr;
@@ -605,8 +604,8 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   // two query heads of a kv head per workgroup share its K/V tile stream when the group is even
   const int group = desc->num_q_heads / pv.kv_heads;
   const int hpw_env = env_int("LLH_PREFILL_HEADS_PER_WG", 0);
-  const int hpw = (hpw_env == 1 || group % 2 != 0) ? 1 : 2;
-  hipError_t e = launch_prefill(a, hpw, static_cast<hipStream_t>(stream));
+  const int variant = (hpw_env == 1 || group % 2 != 0) ? kPrefillOneHead : kPrefillTwoHeads;
+  hipError_t e = launch_prefill(a, variant, static_cast<hipStream_t>(stream));
   ctx->timing_end(1, ev, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "prefill launch");
   return LLH_OK;

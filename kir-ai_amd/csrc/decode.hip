@@ -137,13 +137,17 @@ struct BlockRegs {
   bool valid;
 };
 
-// Issues the loads of block `phys` (wave-uniform) into r.
+// Issues the loads of block `phys` (wave-uniform) into r.  The loads are
+// unconditional: an entry outside the pool reads pool block 0 instead and is
+// marked invalid, and compute_block consumes (and masks) it like any other
+// block, so no control-flow path leaves loads in flight past the math, which
+// would make the compiler wait for every outstanding load before the next issue.
 template <int FMT>
 __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kvh, int lane, BlockRegs<FMT> &r) {
   const int g = lane >> 4;
   const int c = lane & 15;
   r.valid = phys >= 0 && (int64_t)phys < a.pool.n_blocks;
-  if (!r.valid) return;
+  if (!r.valid) phys = 0;
   constexpr int kBlockBytes = (FMT == kBf16 ? 2 : 1) * BT * D;
   const size_t bh = (size_t)phys * a.pool.kv_heads + kvh;
   const char *kb = reinterpret_cast<const char *>(a.pool.k) + bh * kBlockBytes;
@@ -220,18 +224,15 @@ __device__ __forceinline__ void v_pairs(const BlockRegs<FMT> &r, const uint32_t 
 template <int G, int FMT>
 __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
                                               int lane, const uint32_t (&qw)[G][8], SoftmaxState<G> &st) {
-  if (!r.valid) {
-    if (lane == 0) atomicOr(a.err, kErrBadBlock);
-    return;
-  }
+  if (!r.valid && lane == 0) atomicOr(a.err, kErrBadBlock);  // its tokens are all masked below
   const int g = lane >> 4;
-  const bool partial = (jb * BT < lo) || (jb * BT + BT > len);
+  const bool partial = (jb * BT < lo) || (jb * BT + BT > len) || !r.valid;
   bool ok[4] = {true, true, true, true};
   uint32_t vmask[2] = {0xffffffffu, 0xffffffffu};  // zero V of tokens outside [lo, len) (slots may hold garbage)
   if (partial) {
     const int pos0 = jb * BT + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len);
+    for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len) && r.valid;
     if constexpr (FMT == kBf16) {
       vmask[0] = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
       vmask[1] = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
@@ -370,17 +371,6 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
   }
 }
 
-// Blocks in flight per wavefront (register budget: one bf16 block is 32 VGPRs).
-constexpr int pipeline_stages(int G, int FMT) {
-#ifdef LLH_DECODE_STAGES
-  return LLH_DECODE_STAGES;
-#else
-  // measured on MI355X (C2 bf16, C5 int8/fp8): 2 and 3 stages tie, 4 and more lose
-  // occupancy (2 waves per SIMD) and run 20-40% slower
-  return (void)G, (void)FMT, 2;
-#endif
-}
-
 __device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, int &lo, int &first_blk, int &n_blk,
                                           int &n_splits) {
   len = a.seq_lens[b];
@@ -408,7 +398,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the block loop scalar
   const int g = lane >> 4;
   const int c = lane & 15;
   const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G;
@@ -418,12 +408,19 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     return;
   }
 
-  // ---- this wavefront's blocks and their pool indices (one load, read back per block) ----
+  // ---- this wavefront's blocks: every 4th block of the split ----
   const int blk_begin = first_blk + split * a.split_blocks;
   const int blk_end = min(blk_begin + a.split_blocks, first_blk + n_blk);
-  const int nbw = max(0, (blk_end - blk_begin - wave + 3) / 4);  // <= split_blocks / 4 <= 64
+  const int nbw = max(0, (blk_end - blk_begin - wave + 3) / 4);
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const int my_entry = lane < nbw ? table[(blk_begin + wave + 4 * lane) % a.max_blocks] : -1;
+  // pool index of block k of this wavefront: a scalar load from the block-table
+  // row (no one writes it during the launch), fetched one block ahead, so the
+  // waits before the math cover K/V loads only
+  typedef const __attribute__((address_space(4))) int32_t table_elem_t;
+  const table_elem_t *stable = (const table_elem_t *)table;
+  auto entry = [&](int k) __attribute__((always_inline)) -> int {
+    return stable[(blk_begin + wave + 4 * k) % a.max_blocks];
+  };
 
   // ---- query: packed bf16 pairs (bf16 K: dims 8c..8c+7; int8/fp8 K: dims 16*(lane&7)..+16) ----
   uint32_t qw[G][8];
@@ -459,21 +456,30 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
   }
 
-  // ---- block pipeline: loads run STAGES-1 blocks ahead of the math ----
-  constexpr int STAGES = pipeline_stages(G, FMT);
-  BlockRegs<FMT> r[STAGES];
-#pragma unroll
-  for (int sidx = 0; sidx < STAGES - 1; sidx++)
-    if (sidx < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, sidx), kvh, lane, r[sidx]);
-  for (int k0 = 0; k0 < nbw; k0 += STAGES) {
-#pragma unroll
-    for (int sidx = 0; sidx < STAGES; sidx++) {
-      const int k = k0 + sidx;
-      if (k < nbw) {
-        const int kn = k + STAGES - 1;
-        if (kn < nbw) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, kn), kvh, lane, r[(sidx + STAGES - 1) % STAGES]);
-        compute_block<G, FMT>(a, r[sidx], blk_begin + wave + 4 * k, lo, len, lane, qw, st);
+  // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
+  if (nbw > 0) {
+    BlockRegs<FMT> r[2];
+    load_block<FMT>(a, entry(0), kvh, lane, r[0]);
+    int e_next = nbw > 1 ? entry(1) : -1;
+    // every step inside the loop issues the next block's loads before its math,
+    // so the wait before the math always leaves them in flight
+    auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, bool issue) __attribute__((always_inline)) {
+      if (issue) {
+        load_block<FMT>(a, e_next, kvh, lane, nxt);
+        e_next = k + 2 < nbw ? entry(k + 2) : -1;
       }
+      compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len, lane, qw, st);
+    };
+    int k = 0;
+    for (; k + 2 < nbw; k += 2) {
+      step(k, r[0], r[1], true);
+      step(k + 1, r[1], r[0], true);
+    }
+    if (k + 1 < nbw) {
+      step(k, r[0], r[1], true);
+      step(k + 1, r[1], r[0], false);
+    } else {
+      step(k, r[0], r[1], false);
     }
   }
 
@@ -591,117 +597,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       mm = cm;
     }
     a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
-  }
-}
-
-// Wavefront-granular variant: every wavefront is an independent work item
-// (its own split of `split_blocks` consecutive blocks, its own partial), with
-// no LDS merge and no barrier.  Workgroup (kv head, sequence, z) holds splits
-// 4z .. 4z+3.
-template <int G, int FMT>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_wave_kernel(const DecodeArgs a) {
-  const int kvh = blockIdx.x;
-  const int b = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int split = blockIdx.z * 4 + (tid >> 6);
-  int len, lo, first_blk, n_blk, n_splits;
-  seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
-  if (n_splits > a.max_splits) {
-    if (tid == 0 && blockIdx.z == 0) atomicOr(a.err, kErrTooManySplits);
-    return;
-  }
-  if (split >= max(n_splits, 1)) return;
-  const int g = lane >> 4;
-  const int c = lane & 15;
-  const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G;
-  if (n_blk == 0) {
-    for (int idx = lane; idx < G * D; idx += 64) a.out[qrow0 * D + idx] = 0;
-    return;
-  }
-  const int blk_begin = first_blk + split * a.split_blocks;
-  const int nb = min(a.split_blocks, first_blk + n_blk - blk_begin);  // <= 64
-  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const int my_entry = lane < nb ? table[(blk_begin + lane) % a.max_blocks] : -1;
-
-  uint32_t qw[G][8];
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    if constexpr (FMT == kBf16) {
-      const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c * 8);
-      qw[gi][0] = t.x;
-      qw[gi][1] = t.y;
-      qw[gi][2] = t.z;
-      qw[gi][3] = t.w;
-      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
-    } else {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 7) * 16);
-      const uint4 t0 = src[0], t1 = src[1];
-      qw[gi][0] = t0.x;
-      qw[gi][1] = t0.y;
-      qw[gi][2] = t0.z;
-      qw[gi][3] = t0.w;
-      qw[gi][4] = t1.x;
-      qw[gi][5] = t1.y;
-      qw[gi][6] = t1.z;
-      qw[gi][7] = t1.w;
-    }
-  }
-  SoftmaxState<G> st;
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    st.m[gi] = -INFINITY;
-    st.l[gi] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
-  }
-  constexpr int STAGES = pipeline_stages(G, FMT);
-  BlockRegs<FMT> r[STAGES];
-#pragma unroll
-  for (int sidx = 0; sidx < STAGES - 1; sidx++)
-    if (sidx < nb) load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, sidx), kvh, lane, r[sidx]);
-  for (int k0 = 0; k0 < nb; k0 += STAGES) {
-#pragma unroll
-    for (int sidx = 0; sidx < STAGES; sidx++) {
-      const int k = k0 + sidx;
-      if (k < nb) {
-        const int kn = k + STAGES - 1;
-        if (kn < nb)
-          load_block<FMT>(a, __builtin_amdgcn_readlane(my_entry, kn), kvh, lane, r[(sidx + STAGES - 1) % STAGES]);
-        compute_block<G, FMT>(a, r[sidx], blk_begin + k, lo, len, lane, qw, st);
-      }
-    }
-  }
-  // merge the four token groups; afterwards every group holds the totals, and
-  // group g stores dims 16j + c for j = 2g, 2g + 1
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
-    mm = fmaxf(mm, __shfl_xor(mm, 32));
-    const float mref = (mm == -INFINITY) ? 0.0f : mm;
-    const float f = fast_exp2(st.m[gi] - mref);
-    float ll = st.l[gi] * f;
-    ll += __shfl_xor(ll, 16);
-    ll += __shfl_xor(ll, 32);
-    float o2[2];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      float v = st.o[gi][j] * f;
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (j == 2 * g) o2[0] = v;
-      if (j == 2 * g + 1) o2[1] = v;
-    }
-    if (n_splits == 1) {
-      const float inv = 1.0f / ll;
-      a.out[(qrow0 + gi) * D + 16 * (2 * g) + c] = f32_to_bf16_rne(o2[0] * inv);
-      a.out[(qrow0 + gi) * D + 16 * (2 * g + 1) + c] = f32_to_bf16_rne(o2[1] * inv);
-    } else {
-      const size_t row = (qrow0 + gi) * a.max_splits + split;
-      a.ws_o[row * D + 16 * (2 * g) + c] = o2[0];
-      a.ws_o[row * D + 16 * (2 * g + 1) + c] = o2[1];
-      if (lane == 0) a.ws_ml[row] = make_float2(mm, ll);
-    }
   }
 }
 
@@ -883,7 +778,8 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
 template <int G, int FMT>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
+  const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int W = gridDim.x * 4;
   const int Hkv = a.pool.kv_heads;
   int units;
@@ -901,22 +797,40 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     }
   }
   if (sh.b < 0) return;
-  const int b = sh.b;
-  const int nb = sh.nb;
+  // readfirstlane: these are wave-uniform, so the loop's cursors, branches and
+  // load addresses stay in scalar registers
+  const int b = __builtin_amdgcn_readfirstlane(sh.b);
+  const int nb = __builtin_amdgcn_readfirstlane(sh.nb);
+  const int wb = __builtin_amdgcn_readfirstlane(sh.wb);
+  const int w0 = __builtin_amdgcn_readfirstlane(sh.w0);
   const int ub = Hkv * nb;
-  const int r0 = range_begin(w - sh.w0, ub, sh.wb);
-  const int n = range_begin(w - sh.w0 + 1, ub, sh.wb) - r0;  // >= 1
-  const int len = a.seq_lens[b];
+  const int r0 = __builtin_amdgcn_readfirstlane(range_begin(w - w0, ub, wb));
+  const int n = __builtin_amdgcn_readfirstlane(range_begin(w - w0 + 1, ub, wb)) - r0;  // >= 1
+  const int len = __builtin_amdgcn_readfirstlane(a.seq_lens[b]);
   const int lo = a.window > 0 ? max(0, len - a.window) : 0;
   const int first_blk = lo / BT;
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
 
-  // pool indices of 64 consecutive units, one per lane (an entry depends on the block only)
-  auto window_entries = [&](int k0) __attribute__((always_inline)) -> int {
-    const int k = k0 + lane;
-    if (k >= n) return -1;
-    return table[(first_blk + (r0 + k) % nb) % a.max_blocks];
+  // Pool index of a unit's block (it depends on the block only): a scalar load
+  // from the block-table row, which no one writes during the launch, fetched one
+  // unit ahead.  Scalar loads keep the table out of the vector-memory counter,
+  // so the waits before the math cover K/V loads only.
+  typedef const __attribute__((address_space(4))) int32_t table_elem_t;
+  const table_elem_t *stable = (const table_elem_t *)table;
+  const int tab_first = first_blk % a.max_blocks;
+  int e_j = r0 % nb;                               // entry cursor: block (in segment) of the next entry
+  int e_tab = (first_blk + e_j) % a.max_blocks;    // and its table index
+  auto next_entry = [&]() __attribute__((always_inline)) -> int {
+    const int e = stable[e_tab];
+    if (++e_j == nb) {
+      e_j = 0;
+      e_tab = tab_first;
+    } else if (++e_tab == a.max_blocks) {
+      e_tab = 0;
+    }
+    return e;
   };
+
   int l_j = r0 % nb, l_kvh = r0 / nb;  // load cursor: block and kv head of the next unit to load
   int c_j = l_j;                      // compute cursor: block (within its segment) of the next unit
   int seg_kvh = l_kvh;
@@ -925,11 +839,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   bool need_q = false;
   uint32_t qw[G][8];
   load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
-  int ent = window_entries(0);
-  int ent_next = n > 64 ? window_entries(64) : -1;
 
   BlockRegs<FMT> r[2];
-  load_block<FMT>(a, __builtin_amdgcn_readlane(ent, 0), l_kvh, lane, r[0]);
+  load_block<FMT>(a, next_entry(), l_kvh, lane, r[0]);
+  int e_next = n > 1 ? next_entry() : -1;
   if (++l_j == nb) {
     l_j = 0;
     l_kvh++;
@@ -950,8 +863,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
       // this wavefront holds the segment's first unit: record how to merge it
       int2 d = make_int2(0, 0);
       if (!complete) {
-        const int wf = w - sh.w0;
-        const int wl = wave_of_unit((seg_kvh + 1) * nb - 1, ub, sh.wb);
+        const int wf = w - w0;
+        const int wl = wave_of_unit((seg_kvh + 1) * nb - 1, ub, wb);
         d = make_int2(slot, wl - wf + 1);
       }
       reinterpret_cast<int2 *>(a.seg_desc)[(size_t)b * Hkv + seg_kvh] = d;
@@ -959,22 +872,22 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     first_seg = false;
   };
 
-  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt) __attribute__((always_inline)) {
-    if (k + 1 < n) {
-      const int kk = k + 1;
-      if ((kk & 63) == 0) {
-        ent = ent_next;
-        ent_next = kk + 64 < n ? window_entries(kk + 64) : -1;
-      }
-      load_block<FMT>(a, __builtin_amdgcn_readlane(ent, kk & 63), l_kvh, lane, nxt);
+  // One unit: a new segment's q is loaded first, then unit k+1's loads are
+  // issued, then unit k is computed.  Every step inside the loop issues the
+  // next unit's loads after any q load, so the wait before the math always
+  // leaves the next unit's loads in flight.
+  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, bool issue) __attribute__((always_inline)) {
+    if (need_q) {
+      load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
+      need_q = false;
+    }
+    if (issue) {
+      load_block<FMT>(a, e_next, l_kvh, lane, nxt);
+      e_next = k + 2 < n ? next_entry() : -1;
       if (++l_j == nb) {
         l_j = 0;
         l_kvh++;
       }
-    }
-    if (need_q) {
-      load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
-      need_q = false;
     }
     compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len, lane, qw, st);
     if (++c_j == nb) {  // the segment ends with this unit
@@ -985,9 +898,16 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
       need_q = true;
     }
   };
-  for (int k = 0; k < n; k += 2) {
-    step(k, r[0], r[1]);
-    if (k + 1 < n) step(k + 1, r[1], r[0]);
+  int k = 0;
+  for (; k + 2 < n; k += 2) {
+    step(k, r[0], r[1], true);
+    step(k + 1, r[1], r[0], true);
+  }
+  if (k + 1 < n) {
+    step(k, r[0], r[1], true);
+    step(k + 1, r[1], r[0], false);
+  } else {
+    step(k, r[0], r[1], false);
   }
   if (c_j != 0) end_segment(false);  // the range ends inside a segment
 }
@@ -1275,16 +1195,11 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, 
     hipLaunchKernelGGL((decode_stream_merge_kernel<G>), dim3(a.q_heads, a.num_seqs), dim3(64), 0, s, a);
     return hipGetLastError();
   }
-  if (a.wave_splits) {
-    dim3 grid(a.pool.kv_heads, a.num_seqs, (min(grid_x, a.max_splits) + 3) / 4);
-    hipLaunchKernelGGL((paged_decode_wave_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
-  } else {
-    dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
-    hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
-  }
+  dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
+  hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (hook) hook(hu, 1, s);
-  if (e != hipSuccess || a.max_splits <= 1 || (a.fused_merge && !a.wave_splits)) return e;
+  if (e != hipSuccess || a.max_splits <= 1 || a.fused_merge) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }

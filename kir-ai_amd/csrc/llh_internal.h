@@ -53,7 +53,6 @@ struct DecodeArgs {
   int32_t split_blocks;     // blocks per split
   int32_t max_splits;
   int32_t fused_merge;      // 1: last workgroup merges the splits; 0: second launch merges
-  int32_t wave_splits;      // 1: one split per wavefront (no workgroup merge); 0: one split per workgroup
   int32_t stream_wgs;       // >0: persistent stream kernel over this many workgroups (split fields unused)
   int32_t max_seq_len;      // host bound on seq_lens (stream kernel: longer lengths raise kErrTooManySplits)
   int32_t *seg_desc;        // stream kernel: [B][Hkv][2] (first partial slot, partial count; 0 = written)
@@ -164,7 +163,10 @@ hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStr
                          LaunchHook hook = nullptr);
 hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_f32, hipStream_t s);
 // heads_per_wg: query heads of one kv head that share a workgroup's K/V tiles (1 or 2; 2 needs an even group)
-hipError_t launch_prefill(const PrefillArgs &a, int heads_per_wg, hipStream_t s);
+// prefill kernels: one query head per workgroup, or two heads of a kv head
+// sharing the K/V tiles
+enum { kPrefillOneHead = 1, kPrefillTwoHeads = 2 };
+hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);

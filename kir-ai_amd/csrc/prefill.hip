@@ -368,10 +368,10 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
 
 }  // namespace
 
-hipError_t launch_prefill(const PrefillArgs &a, int heads_per_wg, hipStream_t s) {
-  const int n_items = a.q_tiles * (a.q_heads / heads_per_wg) * a.num_seqs;
+hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s) {
+  const int n_items = a.q_tiles * (a.q_heads / (variant == kPrefillOneHead ? 1 : 2)) * a.num_seqs;
   const int grid = (n_items + 7) / 8 * 8;
-  if (heads_per_wg == 2)
+  if (variant == kPrefillTwoHeads)
     hipLaunchKernelGGL(paged_prefill_kernel<2>, dim3(grid), dim3(2 * kPrefillThreads), 0, s, a);
   else
     hipLaunchKernelGGL(paged_prefill_kernel<1>, dim3(grid), dim3(kPrefillThreads), 0, s, a);
