@@ -43,10 +43,17 @@ int env_int(const char *name, int dflt) {
 
 // Split-K sizing for the tuned decode kernel.  `est_blocks` bounds the blocks
 // any one sequence attends (it sizes the grid and the partial buffer).  The
-// split size is the power of two in [4, 256] that brings the number of
-// non-empty workgroups closest to ~4096 (16 per CU on 256 CUs), measured best
-// on MI355X for both short bf16 and long int8 contexts.  The total work comes
-// from the caller's hint when given, else from the max_seq_len bound.
+// split size is a power of two in [4, 256], measured on MI355X:
+//  * bf16 pools are memory-bound: 8 blocks (two per wavefront, so each
+//    wavefront has a block in flight behind the one it computes) beat larger
+//    splits on ragged and on long contexts (C2 52 us at 8 against 59-65 at
+//    16-64, C4 decode 17 us against 27 at 4); steps too small to give 512
+//    workgroups that way use 4;
+//  * int8 / fp8 pools are bound by their per-block arithmetic: the split that
+//    brings the workgroup count closest to 2048 (C5: 128 blocks, 278 us
+//    against 292 at 64 and 290 at 256).
+// The total work comes from the caller's hint when given, else from the
+// max_seq_len bound.
 constexpr int kMaxDecodeSplits = 1024;  // partials one merge workgroup combines
 
 struct SplitPlan {
@@ -55,7 +62,7 @@ struct SplitPlan {
   int est_blocks;
 };
 
-SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, int total_tokens_hint) {
+SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, int total_tokens_hint, int format) {
   int span = max_seq_len;
   if (window > 0) span = std::min(span, window);
   const int est_blocks = (span + kFastBlockTokens - 1) / kFastBlockTokens + 1;
@@ -63,20 +70,25 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
   if (split <= 0) {
     long long blocks = (long long)num_seqs * est_blocks;
     if (total_tokens_hint > 0) blocks = (long long)total_tokens_hint / kFastBlockTokens + num_seqs;
-    const double target = 4096.0;
-    double best = 1e30;
-    split = 4;
-    for (int s = 4; s <= 256; s *= 2) {
-      const double wgs = (double)kv_heads * (double)(blocks + (long long)num_seqs * (s / 2)) / s;
-      const double cost = wgs > target ? wgs / target : target / wgs;
-      if (cost < best) {
-        best = cost;
-        split = s;
+    auto wgs = [&](int s) { return (double)kv_heads * (double)(blocks + (long long)num_seqs * (s / 2)) / s; };
+    if (format == LLH_KV_BF16) {
+      split = wgs(8) >= 512.0 ? 8 : 4;
+    } else {
+      const double target = 2048.0;
+      double best = 1e30;
+      split = 4;
+      for (int s = 4; s <= 256; s *= 2) {
+        const double w = wgs(s);
+        const double cost = w > target ? w / target : target / w;
+        if (cost < best) {
+          best = cost;
+          split = s;
+        }
       }
     }
   }
-  split = std::min(std::max(split, 4), 64);  // a wavefront reads its table entries from <= 64 lanes
-  while ((est_blocks + split - 1) / split > kMaxDecodeSplits && split < 64) split *= 2;
+  split = std::min(std::max(split, 4), 256);
+  while ((est_blocks + split - 1) / split > kMaxDecodeSplits && split < 256) split *= 2;
   SplitPlan p;
   p.split_blocks = split;
   p.est_blocks = est_blocks;
@@ -414,7 +426,7 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   ctx->decode_calls++;
   if (fast) {
     const SplitPlan plan =
-        plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint);
+        plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint, pv.format);
     const int stream_wgs =
         plan_stream(ctx, pv.format, desc->num_seqs, pv.kv_heads, plan.est_blocks, desc->total_tokens_hint);
     if (!stream_wgs && plan.max_splits > kMaxDecodeSplits)

@@ -969,11 +969,43 @@ __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArg
 
 // Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
 // dim) per (query head, sequence) whose sequence used more than one split.
-// Up to 32 splits, each lane loads every (max, sum) pair and its partial of
-// every split in one round and combines them in registers; beyond that the
-// pairs go through LDS and the partials are loaded 16 splits at a time.
+// The merge is latency-bound, so it is laid out as few dependent memory round
+// trips as possible: up to 64 splits, each lane loads every (max, sum) pair
+// and its partial of every split at once and combines them in registers;
+// beyond that the partials of the first 96 splits are loaded together with
+// the (max, sum) pairs, the pairs are reduced through LDS, and any remaining
+// partials follow 32 at a time.
 constexpr int kMergeMaxSplits = 1024;
-constexpr int kMergeOneRound = 32;  // splits merged from one round of loads
+constexpr int kMergeOneRound = 64;  // splits merged from one round of loads, all in registers
+constexpr int kMergePrefetch = 96;  // partials loaded up front on the LDS path
+
+// Merge of n <= N splits from one round of loads, all in registers.  Loads
+// past the last split re-read the last split (no branch between the loads and
+// their use, so they are all in flight at once) and are weighted 0.
+template <int N>
+__device__ __forceinline__ void merge_in_registers(const DecodeArgs &a, size_t row0, int last, int d, size_t orow) {
+  float o_sp[N];
+  float2 ml[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) o_sp[i] = a.ws_o[(row0 + min(i, last)) * D + d];
+#pragma unroll
+  for (int i = 0; i < N; i++) ml[i] = a.ws_ml[row0 + min(i, last)];
+#pragma unroll
+  for (int i = 0; i < N; i++)
+    if (i > last) ml[i] = make_float2(-INFINITY, 0.0f);
+  float mm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < N; i++) mm = fmaxf(mm, ml[i].x);
+  const float mref = (mm == -INFINITY) ? 0.0f : mm;
+  float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    const float f = fast_exp2(ml[i].x - mref);
+    ll += ml[i].y * f;
+    oo += o_sp[i] * f;
+  }
+  a.out[orow * D + d] = f32_to_bf16_rne(oo / ll);
+}
 
 __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   const int h = blockIdx.x;
@@ -983,37 +1015,24 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMergeMaxSplits) return;
   const int d = threadIdx.x;
   const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
-  if (n_splits <= kMergeOneRound) {
-    // one memory round trip: every (max, sum) pair and this lane's partial of
-    // every split are in flight together, then combined in registers
-    float2 ml[kMergeOneRound];
-    float o_sp[kMergeOneRound];
+  const size_t orow = (size_t)b * a.q_heads + h;
+  const int last = n_splits - 1;
+  if (n_splits <= 8) return merge_in_registers<8>(a, row0, last, d, orow);
+  if (n_splits <= 16) return merge_in_registers<16>(a, row0, last, d, orow);
+  if (n_splits <= 32) return merge_in_registers<32>(a, row0, last, d, orow);
+  if (n_splits <= kMergeOneRound) return merge_in_registers<kMergeOneRound>(a, row0, last, d, orow);
+  // partials of the first splits: in flight while the (max, sum) pairs are reduced
+  float o_pre[kMergePrefetch];
 #pragma unroll
-    for (int i = 0; i < kMergeOneRound; i++) {
-      const bool live = i < n_splits;
-      ml[i] = live ? a.ws_ml[row0 + i] : make_float2(-INFINITY, 0.0f);
-      o_sp[i] = live ? a.ws_o[(row0 + i) * D + d] : 0.0f;
-    }
-    float mm = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kMergeOneRound; i++) mm = fmaxf(mm, ml[i].x);
-    const float mref = (mm == -INFINITY) ? 0.0f : mm;
-    float ll = 0.0f, oo = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kMergeOneRound; i++) {
-      const float f = fast_exp2(ml[i].x - mref);
-      ll += ml[i].y * f;
-      oo += o_sp[i] * f;
-    }
-    a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / ll);
-    return;
-  }
+  for (int i = 0; i < kMergePrefetch; i++) o_pre[i] = a.ws_o[(row0 + min(i, last)) * D + d];
   __shared__ float s_f[kMergeMaxSplits];
+  __shared__ float s_l[kMergeMaxSplits];
   __shared__ float s_red[2];
   float lm = -INFINITY;
   for (int sp = d; sp < n_splits; sp += D) {
     const float2 ml = a.ws_ml[row0 + sp];
     s_f[sp] = ml.x;
+    s_l[sp] = ml.y;
     lm = fmaxf(lm, ml.x);
   }
   // max over the workgroup (two wavefronts)
@@ -1026,7 +1045,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   float ll = 0.0f;
   for (int sp = d; sp < n_splits; sp += D) {
     const float f = fast_exp2(s_f[sp] - mref);
-    ll += a.ws_ml[row0 + sp].y * f;
+    ll += s_l[sp] * f;
     s_f[sp] = f;
   }
 #pragma unroll
@@ -1036,15 +1055,16 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   __syncthreads();
   const float l_tot = s_red[0] + s_red[1];
   float oo = 0.0f;
-  for (int sp0 = 0; sp0 < n_splits; sp0 += 16) {
-    float o_sp[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) o_sp[i] = sp0 + i < n_splits ? a.ws_o[(row0 + sp0 + i) * D + d] : 0.0f;
+  for (int i = 0; i < kMergePrefetch; i++) oo += o_pre[i] * (i <= last ? s_f[min(i, last)] : 0.0f);
+  for (int sp0 = kMergePrefetch; sp0 < n_splits; sp0 += 32) {
+    float o_sp[32];
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-      if (sp0 + i < n_splits) oo += o_sp[i] * s_f[sp0 + i];
+    for (int i = 0; i < 32; i++) o_sp[i] = a.ws_o[(row0 + min(sp0 + i, last)) * D + d];
+#pragma unroll
+    for (int i = 0; i < 32; i++) oo += o_sp[i] * (sp0 + i <= last ? s_f[min(sp0 + i, last)] : 0.0f);
   }
-  a.out[((size_t)b * a.q_heads + h) * D + d] = f32_to_bf16_rne(oo / l_tot);
+  a.out[orow * D + d] = f32_to_bf16_rne(oo / l_tot);
 }
 
 // ---------------------------------------------------------------------------

@@ -130,6 +130,19 @@ def test_decode_split_sizes(ctx, merge_mode, split_blocks, monkeypatch):
     check(ctx, batch, 32, 8, seed=17, what=f"split={split_blocks} merge={merge_mode}")
 
 
+@pytest.mark.parametrize("n_splits", [2, 33, 64, 65, 96, 97, 130])
+def test_decode_merge_split_counts(ctx, n_splits, monkeypatch):
+    """The merge launch's three layouts: every partial in registers (<= 64 splits),
+    LDS-reduced pairs with all partials loaded up front (<= 96) and the chunked tail;
+    one sequence per count at the boundaries, 4-block splits."""
+    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", "4")
+    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
+    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "0")
+    lens = np.array([BT * 4 * n_splits - 5, BT * 4 * (n_splits - 1) + 1], np.int32)  # n_splits each
+    batch = workloads.paged_batch(lens, BT, 0.10, 300 + n_splits)
+    check(ctx, batch, 16, 8, seed=300 + n_splits, what=f"merge of {n_splits} splits")
+
+
 def test_decode_fused_merge_is_deterministic(ctx, monkeypatch):
     """Many splits per sequence and many repeated calls: the last-arriving workgroup
     merges in split order, so every call must give identical bits; a stale partial
