@@ -96,21 +96,25 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
   return p;
 }
 
-// Persistent stream decode (bf16 pools): two workgroups of four wavefronts per
-// compute unit, the best grid measured on MI355X for C2 (one and three per CU
-// run 2-8% slower).  It is chosen when the step has at least
-// kStreamMinUnitsPerWave units (block x kv head) per wavefront and its
-// 32-bit partition arithmetic (units * wavefronts < 2^31) is exact; smaller
-// steps (C1, C4 decode) and quantised pools, whose kernels are bound by their
-// per-block arithmetic rather than by memory, use split-K.  LLH_DECODE_KERNEL
-// = "split" | "stream" overrides the choice, LLH_DECODE_STREAM_WGS the grid.
+// Persistent stream decode: two workgroups of four wavefronts per compute unit
+// for bf16 pools, the best grid measured on MI355X for C2 (one and three per
+// CU run 2-8% slower), and four for int8 / fp8 pools, whose per-block
+// arithmetic keeps two resident per CU: the grid then runs in two rounds of
+// shorter ranges (C5 int8 267 us/step against 280 with two per CU and 294
+// with split-K; fp8 242 against 248 with split-K).  It is chosen when the step
+// has at least kStreamMinUnitsPerWave units (block x kv head) per wavefront
+// and its 32-bit partition arithmetic (units * wavefronts < 2^31) is exact;
+// smaller steps (C1, C4 decode) use split-K.  LLH_DECODE_KERNEL = "split" |
+// "stream" overrides the choice, LLH_DECODE_STREAM_WGS the grid.
 constexpr int kStreamWgsPerCu = 2;
+constexpr int kStreamWgsPerCuQuantized = 4;
 constexpr int kStreamMaxWgs = 1024;
 constexpr int kStreamMinUnitsPerWave = 8;
 
-int stream_grid(const llh_ctx *ctx) {
+int stream_grid(const llh_ctx *ctx, int format) {
   const int wgs = env_int("LLH_DECODE_STREAM_WGS", 0);
-  return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : kStreamWgsPerCu * ctx->cus));
+  const int per_cu = format == LLH_KV_BF16 ? kStreamWgsPerCu : kStreamWgsPerCuQuantized;
+  return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : per_cu * ctx->cus));
 }
 
 // Returns the stream grid (workgroups) for this step, or 0 for split-K.
@@ -119,13 +123,12 @@ int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int 
   const bool want_split = force && std::strcmp(force, "split") == 0;
   const bool want_stream = force && std::strcmp(force, "stream") == 0;
   if (want_split) return 0;
-  const int wgs = stream_grid(ctx);
+  const int wgs = stream_grid(ctx, format);
   const long long waves = 4LL * wgs;
   const long long max_units_seq = (long long)kv_heads * est_blocks;
   const long long max_units = max_units_seq * num_seqs;
   if (2LL * num_seqs >= waves || max_units_seq * waves >= (1LL << 31) || max_units >= (1LL << 31)) return 0;
   if (want_stream) return wgs;
-  if (format != LLH_KV_BF16) return 0;
   const long long units = total_tokens_hint > 0
                               ? (long long)kv_heads * ((long long)total_tokens_hint / kFastBlockTokens + num_seqs)
                               : max_units;

@@ -608,9 +608,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 // non-empty sequence gets one wavefront of the grid plus a share of the
 // remaining wavefronts proportional to its units (at most one per unit), and
 // each of its wavefronts streams an equal, contiguous range of its units,
-// loading one unit ahead of the math across kv-head boundaries.  The whole
-// grid is resident at once, so there are no empty or late workgroups however
-// ragged the lengths are, and no workgroup barrier.
+// loading one unit ahead of the math across kv-head boundaries.  Every
+// workgroup has the same amount of work however ragged the lengths are, and
+// there is no workgroup barrier and no wait on another workgroup, so results
+// do not depend on how many workgroups are resident at once (bf16 grids are
+// all resident; int8 / fp8 grids run in two rounds).
 //
 // A segment that lies wholly inside one wavefront's range is written out
 // directly.  A segment cut between wavefronts leaves one (max, sum, output)
