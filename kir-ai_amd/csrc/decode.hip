@@ -914,9 +914,52 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   if (c_j != 0) end_segment(false);  // the range ends inside a segment
 }
 
+// One round of the stream merge over partials i0 .. i0+cnt-1 (1 <= cnt <= N <=
+// 64) of a cut segment.  Every dim and every (max, sum) pair of the round is
+// loaded before any is used: dims past the last partial re-read the last one
+// and get weight 0, lane j loads pair j, and the weights reach all lanes by
+// readlane.  The merge launch is latency-bound, so this keeps it at two
+// dependent memory round trips (descriptor, then partials).
+template <int G, int N>
+__device__ __forceinline__ void stream_merge_round(const DecodeArgs &a, int first_slot, int wf, int gi, int i0, int cnt,
+                                                   int lane, float &mm, float &ll, float &o0, float &o1) {
+  // partial k of the segment: the first wavefront's slot, then the later wavefronts' first-segment slots
+  auto row_of = [&](int k) { return (size_t)(k == 0 ? first_slot : (wf + k) * 2) * G + gi; };
+  const float2 ml = a.ws_ml[row_of(i0 + min(lane, cnt - 1))];
+  float a0[N], a1[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    const size_t row = row_of(i0 + min(i, cnt - 1));
+    a0[i] = a.ws_o[row * D + lane];
+    a1[i] = a.ws_o[row * D + 64 + lane];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load of the round is issued before the first wait
+  const float m = lane < cnt ? ml.x : -INFINITY;
+  float nm = m;
+#pragma unroll
+  for (int o = N / 2; o > 0; o >>= 1) nm = fmaxf(nm, __shfl_xor(nm, o));
+  nm = fmaxf(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nm))), mm);
+  const float mref = (nm == -INFINITY) ? 0.0f : nm;
+  const float f = fast_exp2(m - mref);  // 0 on lanes past the last partial
+  float ls = ml.y * f;
+#pragma unroll
+  for (int o = N / 2; o > 0; o >>= 1) ls += __shfl_xor(ls, o);
+  const float f0 = fast_exp2(mm - mref);
+  ll = ll * f0 + __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ls)));
+  o0 *= f0;
+  o1 *= f0;
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    const float fi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), i));
+    o0 += a0[i] * fi;
+    o1 += a1[i] * fi;
+  }
+  mm = nm;
+}
+
 // Merges the partials of the stream kernel's cut segments: one wavefront per
-// (query head, sequence), two dims per lane; up to 16 partials are loaded in
-// one round.
+// (query head, sequence), two dims per lane; up to 16 partials in one round,
+// more in rounds of 32.
 template <int G>
 __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArgs a) {
   const int h = blockIdx.x;
@@ -929,39 +972,12 @@ __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArg
   const int wf = d.x >> 1;
   if (d.y < 2 || wf + d.y > W) return;  // written by the stream kernel (or an aborted call)
   float mm = -INFINITY, ll = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  if (d.y <= 16) {
+    stream_merge_round<G, 16>(a, d.x, wf, gi, 0, d.y, lane, mm, ll, o0, o1);
+  } else {
 #pragma unroll 1
-  for (int i0 = 0; i0 < d.y; i0 += 16) {
-    float m_[16], l_[16], a0[16], a1[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      m_[i] = -INFINITY;
-      l_[i] = a0[i] = a1[i] = 0.0f;
-      if (i0 + i < d.y) {
-        const int slot = i0 + i == 0 ? d.x : (wf + i0 + i) * 2;  // later wavefronts: their first segment
-        const size_t row = (size_t)slot * G + gi;
-        const float2 ml = a.ws_ml[row];
-        m_[i] = ml.x;
-        l_[i] = ml.y;
-        a0[i] = a.ws_o[row * D + lane];
-        a1[i] = a.ws_o[row * D + 64 + lane];
-      }
-    }
-    float nm = mm;
-#pragma unroll
-    for (int i = 0; i < 16; i++) nm = fmaxf(nm, m_[i]);
-    const float mref = (nm == -INFINITY) ? 0.0f : nm;
-    const float f0 = fast_exp2(mm - mref);
-    ll *= f0;
-    o0 *= f0;
-    o1 *= f0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float f = fast_exp2(m_[i] - mref);
-      ll += l_[i] * f;
-      o0 += a0[i] * f;
-      o1 += a1[i] * f;
-    }
-    mm = nm;
+    for (int i0 = 0; i0 < d.y; i0 += 32)
+      stream_merge_round<G, 32>(a, d.x, wf, gi, i0, min(32, d.y - i0), lane, mm, ll, o0, o1);
   }
   const float inv = 1.0f / ll;
   const size_t orow = (size_t)b * a.q_heads + h;
