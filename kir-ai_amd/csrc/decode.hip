@@ -109,11 +109,57 @@ __device__ __forceinline__ float row_sum8(float v) {
   return v;
 }
 
+// Value of lane n (0..15) of this lane's 16-lane row (DPP row_newbcast).  n
+// must fold to a constant: callers pass unrolled loop indices.
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  const int x = __float_as_int(v);
+  switch (n) {
+    case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x150, 0xF, 0xF, false));
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x151, 0xF, 0xF, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x152, 0xF, 0xF, false));
+    case 3: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x153, 0xF, 0xF, false));
+    case 4: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x154, 0xF, 0xF, false));
+    case 5: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x155, 0xF, 0xF, false));
+    case 6: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x156, 0xF, 0xF, false));
+    case 7: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x157, 0xF, 0xF, false));
+    case 8: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x158, 0xF, 0xF, false));
+    case 9: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x159, 0xF, 0xF, false));
+    case 10: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15A, 0xF, 0xF, false));
+    case 11: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15B, 0xF, 0xF, false));
+    case 12: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15C, 0xF, 0xF, false));
+    case 13: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15D, 0xF, 0xF, false));
+    case 14: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15E, 0xF, 0xF, false));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x15F, 0xF, 0xF, false));
+  }
+}
+
+// Reduction over the four lanes l, l+4, l+8, l+12 of a 16-lane row (row_ror 4, 8).
+__device__ __forceinline__ float row_max_stride4(float v) {
+  v = fmaxf(v, dpp<0x124>(v));
+  return fmaxf(v, dpp<0x128>(v));
+}
+__device__ __forceinline__ float row_sum_stride4(float v) {
+  v += dpp<0x124>(v);
+  return v + dpp<0x128>(v);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
+
+// int8 / fp8 pools with G <= 4 query heads per kv head use the token-lane
+// layout for q . k: lane 16g + 4tq + c holds token 4g + tq of the block at
+// dims 32c .. 32c+31 and scores that token for head c % G, so every score is
+// computed (and exponentiated) once per wavefront instead of once per lane of
+// a 16-lane row.  Other shapes keep the row layout (16 dims of two tokens per
+// lane).  V is laid out the same way in both.
+template <int G, int FMT>
+constexpr bool kTokenLanes = FMT != kBf16 && G <= 4;
+// q words (packed bf16 pairs) per lane and head
+template <int G, int FMT>
+constexpr int kQWords = kTokenLanes<G, FMT> ? 16 : 8;
 
 // Raw registers of one block for one wavefront.
 template <int FMT>
@@ -142,7 +188,7 @@ struct BlockRegs {
 // marked invalid, and compute_block consumes (and masks) it like any other
 // block, so no control-flow path leaves loads in flight past the math, which
 // would make the compiler wait for every outstanding load before the next issue.
-template <int FMT>
+template <int FMT, bool TL>
 __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kvh, int lane, BlockRegs<FMT> &r) {
   const int g = lane >> 4;
   const int c = lane & 15;
@@ -158,10 +204,16 @@ __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kv
 #pragma unroll
     for (int j = 0; j < 8; j++) r.v[j] = ld_nt8(vb + (16 * j + c) * (BT * 2) + g * 8);
   } else {
-    const int hf = (lane >> 3) & 1;
-    const int c8 = lane & 7;
+    if constexpr (TL) {
+      // token 4g + tq, dims 32c .. 32c+31: the 32 bytes at lane * 32
 #pragma unroll
-    for (int i = 0; i < 2; i++) r.k[i] = ld_nt16(kb + (4 * g + 2 * i + hf) * D + c8 * 16);
+      for (int i = 0; i < 2; i++) r.k[i] = ld_nt16(kb + lane * 32 + i * 16);
+    } else {
+      const int hf = (lane >> 3) & 1;
+      const int c8 = lane & 7;
+#pragma unroll
+      for (int i = 0; i < 2; i++) r.k[i] = ld_nt16(kb + (4 * g + 2 * i + hf) * D + c8 * 16);
+    }
 #pragma unroll
     for (int j = 0; j < 8; j++) r.v[j] = ld_nt4(vb + (16 * j + c) * BT + g * 4);
     if constexpr (FMT == kInt8) {
@@ -180,7 +232,38 @@ struct SoftmaxState {
   float m[G];
   float l[G];
   float o[G][8];
+  // token-lane layout: running max and weight sum of this lane's head (c % G)
+  // in its row; folded into m / l by finalize_state
+  float m_own;
+  float l_own;
 };
+
+template <int G>
+__device__ __forceinline__ void reset_state(SoftmaxState<G> &st) {
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    st.m[gi] = -INFINITY;
+    st.l[gi] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
+  }
+  st.m_own = -INFINITY;
+  st.l_own = 0.0f;
+}
+
+// Token-lane layout: makes m[gi] and l[gi] the row's running max and weight
+// sum of head gi in every lane of the row, as the row layout keeps them.
+template <int G, int FMT>
+__device__ __forceinline__ void finalize_state(SoftmaxState<G> &st) {
+  if constexpr (kTokenLanes<G, FMT>) {
+    const float lr = row_sum_stride4(st.l_own);  // the row's four tokens of this lane's head
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      st.m[gi] = row_bcast(st.m_own, gi);  // row lane gi: token 0 of the row, head gi
+      st.l[gi] = row_bcast(lr, gi);
+    }
+  }
+}
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // round to nearest even
@@ -223,7 +306,8 @@ __device__ __forceinline__ void v_pairs(const BlockRegs<FMT> &r, const uint32_t 
 // p . v products, the softmax denominator sums them in fp32.
 template <int G, int FMT>
 __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
-                                              int lane, const uint32_t (&qw)[G][8], SoftmaxState<G> &st) {
+                                              int lane, const uint32_t (&qw)[G][kQWords<G, FMT>],
+                                              SoftmaxState<G> &st) {
   if (!r.valid && lane == 0) atomicOr(a.err, kErrBadBlock);  // its tokens are all masked below
   const int g = lane >> 4;
   const bool partial = (jb * BT < lo) || (jb * BT + BT > len) || !r.valid;
@@ -241,125 +325,199 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     }
   }
 
-  float s[G][4];
-  float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-
-  if constexpr (FMT == kBf16) {
-#pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float acc = dot2_bf16(r.k[i].x, qw[gi][0], 0.0f);
-        acc = dot2_bf16(r.k[i].y, qw[gi][1], acc);
-        acc = dot2_bf16(r.k[i].z, qw[gi][2], acc);
-        acc = dot2_bf16(r.k[i].w, qw[gi][3], acc);
-        s[gi][i] = row_sum16(acc) * a.scale_log2e;
-      }
-    }
-  } else {
-    // int8 / fp8: K token rows of 128 bytes; lane (g, half hf, c8) holds tokens
-    // 4g + 2i + hf (i = 0, 1) at dims 16*c8 .. +16.  V dim rows of 16 bytes;
-    // lane holds the 4 bytes of tokens 4g..4g+3 for dims 16j + c.
-    const int hf = (lane >> 3) & 1;
-    float kscale_own[2];
-    if constexpr (FMT == kInt8) {
-      const float k4[4] = {f16_bits_to_f32(r.ks.x & 0xffffu), f16_bits_to_f32(r.ks.x >> 16),
-                           f16_bits_to_f32(r.ks.y & 0xffffu), f16_bits_to_f32(r.ks.y >> 16)};
-      vsc[0] = f16_bits_to_f32(r.vs.x & 0xffffu);
-      vsc[1] = f16_bits_to_f32(r.vs.x >> 16);
-      vsc[2] = f16_bits_to_f32(r.vs.y & 0xffffu);
-      vsc[3] = f16_bits_to_f32(r.vs.y >> 16);
-      kscale_own[0] = (hf ? k4[1] : k4[0]) * a.scale_log2e;
-      kscale_own[1] = (hf ? k4[3] : k4[2]) * a.scale_log2e;
-    } else {
-      kscale_own[0] = kscale_own[1] = r.ksb * a.scale_log2e;
-      vsc[0] = vsc[1] = vsc[2] = vsc[3] = r.vsb;
-    }
-    float own[G][2];
+  uint32_t w01[G], w23[G];
+  if constexpr (kTokenLanes<G, FMT>) {
+    // this lane: token 4g + tq of the row, dims 32c4 .. 32c4+31, scores head c4 % G
+    const int tq = (lane >> 2) & 3;
+    const int c4 = lane & 3;
+    const bool ok_own = !partial || ((jb * BT + 4 * g + tq >= lo) && (jb * BT + 4 * g + tq < len) && r.valid);
+    uint32_t kp[16];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
-      uint32_t kp[8];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         if constexpr (FMT == kInt8) {
-          kp[2 * k] = i8x2_to_bf16(w[k], 0);
-          kp[2 * k + 1] = i8x2_to_bf16(w[k], 2);
+          kp[8 * i + 2 * k] = i8x2_to_bf16(w[k], 0);
+          kp[8 * i + 2 * k + 1] = i8x2_to_bf16(w[k], 2);
         } else {
-          kp[2 * k] = fp8x2_to_bf16<false>(w[k]);
-          kp[2 * k + 1] = fp8x2_to_bf16<true>(w[k]);
+          kp[8 * i + 2 * k] = fp8x2_to_bf16<false>(w[k]);
+          kp[8 * i + 2 * k + 1] = fp8x2_to_bf16<true>(w[k]);
+        }
+      }
+    }
+    // q . k of this token for every head over the lane's 32 dims, summed over
+    // the token's four lanes (quad_perm butterflies: all four get the sum)
+    float s_own = 0.0f;
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
+      acc += dpp<0xB1>(acc);  // quad_perm [1,0,3,2]
+      acc += dpp<0x4E>(acc);  // quad_perm [2,3,0,1]
+      if (gi == 0 || (c4 & (G - 1)) == gi) s_own = acc;
+    }
+    float ks_own, vs_own;
+    if constexpr (FMT == kInt8) {
+      const int sh = 16 * (tq & 1);
+      ks_own = f16_bits_to_f32(((tq & 2) ? r.ks.y : r.ks.x) >> sh);
+      vs_own = f16_bits_to_f32(((tq & 2) ? r.vs.y : r.vs.x) >> sh);
+    } else {
+      ks_own = r.ksb;
+      vs_own = r.vsb;
+    }
+    s_own *= ks_own * a.scale_log2e;
+    if (!ok_own) {
+      s_own = -INFINITY;
+      vs_own = 0.0f;  // its scale bits may be garbage: keep 0 * garbage out of the sums
+    }
+    // lazy running max per (row, head), as in the row layout; the lanes of a
+    // row that score one head see the same row max
+    const float tmax = row_max_stride4(s_own);
+    const bool grow = tmax > st.m_own + 8.0f;  // true on the first block with a finite score
+    if (__any(grow)) {
+      const float nm = grow ? tmax : st.m_own;
+      const float alpha = grow ? fast_exp2(st.m_own - nm) : 1.0f;  // 0 when st.m_own = -inf
+      st.m_own = nm;
+      st.l_own *= alpha;
+#pragma unroll
+      for (int gi = 0; gi < G; gi++) {
+        const float al = row_bcast(alpha, gi);  // row lane gi scores head gi
+#pragma unroll
+        for (int j = 0; j < 8; j++) st.o[gi][j] *= al;
+      }
+    }
+    const float mref = (st.m_own == -INFINITY) ? 0.0f : st.m_own;
+    const float p = fast_exp2(s_own - mref);
+    st.l_own += p;
+    const float wv = p * vs_own;
+    // every lane of the row gathers the row's 4 tokens' value weights of each head
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      w01[gi] = pack_bf16(row_bcast(wv, gi), row_bcast(wv, 4 + gi));
+      w23[gi] = pack_bf16(row_bcast(wv, 8 + gi), row_bcast(wv, 12 + gi));
+    }
+  } else {
+    float s[G][4];
+    float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+
+    if constexpr (FMT == kBf16) {
+#pragma unroll
+      for (int gi = 0; gi < G; gi++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float acc = dot2_bf16(r.k[i].x, qw[gi][0], 0.0f);
+          acc = dot2_bf16(r.k[i].y, qw[gi][1], acc);
+          acc = dot2_bf16(r.k[i].z, qw[gi][2], acc);
+          acc = dot2_bf16(r.k[i].w, qw[gi][3], acc);
+          s[gi][i] = row_sum16(acc) * a.scale_log2e;
+        }
+      }
+    } else {
+      // int8 / fp8: K token rows of 128 bytes; lane (g, half hf, c8) holds tokens
+      // 4g + 2i + hf (i = 0, 1) at dims 16*c8 .. +16.  V dim rows of 16 bytes;
+      // lane holds the 4 bytes of tokens 4g..4g+3 for dims 16j + c.
+      const int hf = (lane >> 3) & 1;
+      float kscale_own[2];
+      if constexpr (FMT == kInt8) {
+        const float k4[4] = {f16_bits_to_f32(r.ks.x & 0xffffu), f16_bits_to_f32(r.ks.x >> 16),
+                             f16_bits_to_f32(r.ks.y & 0xffffu), f16_bits_to_f32(r.ks.y >> 16)};
+        vsc[0] = f16_bits_to_f32(r.vs.x & 0xffffu);
+        vsc[1] = f16_bits_to_f32(r.vs.x >> 16);
+        vsc[2] = f16_bits_to_f32(r.vs.y & 0xffffu);
+        vsc[3] = f16_bits_to_f32(r.vs.y >> 16);
+        kscale_own[0] = (hf ? k4[1] : k4[0]) * a.scale_log2e;
+        kscale_own[1] = (hf ? k4[3] : k4[2]) * a.scale_log2e;
+      } else {
+        kscale_own[0] = kscale_own[1] = r.ksb * a.scale_log2e;
+        vsc[0] = vsc[1] = vsc[2] = vsc[3] = r.vsb;
+      }
+      float own[G][2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
+        uint32_t kp[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          if constexpr (FMT == kInt8) {
+            kp[2 * k] = i8x2_to_bf16(w[k], 0);
+            kp[2 * k + 1] = i8x2_to_bf16(w[k], 2);
+          } else {
+            kp[2 * k] = fp8x2_to_bf16<false>(w[k]);
+            kp[2 * k + 1] = fp8x2_to_bf16<true>(w[k]);
+          }
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 8; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
+          own[gi][i] = row_sum8(acc) * kscale_own[i];
         }
       }
 #pragma unroll
       for (int gi = 0; gi < G; gi++) {
-        float acc = 0.0f;
+        const float oth0 = row_mirror(own[gi][0]);  // swaps the two 8-lane halves of a row
+        const float oth1 = row_mirror(own[gi][1]);
+        s[gi][0] = hf ? oth0 : own[gi][0];
+        s[gi][1] = hf ? own[gi][0] : oth0;
+        s[gi][2] = hf ? oth1 : own[gi][1];
+        s[gi][3] = hf ? own[gi][1] : oth1;
+      }
+    }
+
+    if (partial) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
-        own[gi][i] = row_sum8(acc) * kscale_own[i];
+      for (int gi = 0; gi < G; gi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (!ok[i]) s[gi][i] = -INFINITY;
+      // slots outside [lo, len) may hold any scale bits: zero their weights' scale
+      // (their V codes are masked too) so that 0 * garbage cannot reach the sums
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (!ok[i]) vsc[i] = 0.0f;
+    }
+
+    // Online softmax per head with a lazy reference max (log2 units): st.m only
+    // moves when a score exceeds it by more than 8, so the weights stay <= 2^8 and
+    // the accumulators are rescaled on few blocks (a wavefront-uniform branch).
+    // Any reference max gives the same softmax; the partials carry theirs.
+    bool grow[G];
+    bool any_grow = false;
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
+      grow[gi] = tmax > st.m[gi] + 8.0f;  // true on the first block with a finite score
+      any_grow |= grow[gi];
+    }
+    if (__any(any_grow)) {
+#pragma unroll
+      for (int gi = 0; gi < G; gi++) {
+        const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
+        const float nm = grow[gi] ? tmax : st.m[gi];
+        const float alpha = grow[gi] ? fast_exp2(st.m[gi] - nm) : 1.0f;  // 0 when st.m = -inf
+        st.m[gi] = nm;
+        st.l[gi] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; j++) st.o[gi][j] *= alpha;
       }
     }
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-      const float oth0 = row_mirror(own[gi][0]);  // swaps the two 8-lane halves of a row
-      const float oth1 = row_mirror(own[gi][1]);
-      s[gi][0] = hf ? oth0 : own[gi][0];
-      s[gi][1] = hf ? own[gi][0] : oth0;
-      s[gi][2] = hf ? oth1 : own[gi][1];
-      s[gi][3] = hf ? own[gi][1] : oth1;
-    }
-  }
-
-  if (partial) {
+      const float mref = (st.m[gi] == -INFINITY) ? 0.0f : st.m[gi];
+      float p[4];
 #pragma unroll
-    for (int gi = 0; gi < G; gi++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (!ok[i]) s[gi][i] = -INFINITY;
-    // slots outside [lo, len) may hold any scale bits: zero their weights' scale
-    // (their V codes are masked too) so that 0 * garbage cannot reach the sums
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      if (!ok[i]) vsc[i] = 0.0f;
-  }
-
-  // Online softmax per head with a lazy reference max (log2 units): st.m only
-  // moves when a score exceeds it by more than 8, so the weights stay <= 2^8 and
-  // the accumulators are rescaled on few blocks (a wavefront-uniform branch).
-  // Any reference max gives the same softmax; the partials carry theirs.
-  bool grow[G];
-  bool any_grow = false;
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
-    grow[gi] = tmax > st.m[gi] + 8.0f;  // true on the first block with a finite score
-    any_grow |= grow[gi];
-  }
-  if (__any(any_grow)) {
-#pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-      const float tmax = fmaxf(fmaxf(s[gi][0], s[gi][1]), fmaxf(s[gi][2], s[gi][3]));
-      const float nm = grow[gi] ? tmax : st.m[gi];
-      const float alpha = grow[gi] ? fast_exp2(st.m[gi] - nm) : 1.0f;  // 0 when st.m = -inf
-      st.m[gi] = nm;
-      st.l[gi] *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; j++) st.o[gi][j] *= alpha;
-    }
-  }
-  uint32_t w01[G], w23[G];
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    const float mref = (st.m[gi] == -INFINITY) ? 0.0f : st.m[gi];
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
-    st.l[gi] += (p[0] + p[1]) + (p[2] + p[3]);
-    if constexpr (FMT == kBf16) {
-      w01[gi] = pack_bf16(p[0], p[1]);
-      w23[gi] = pack_bf16(p[2], p[3]);
-    } else {
-      w01[gi] = pack_bf16(p[0] * vsc[0], p[1] * vsc[1]);
-      w23[gi] = pack_bf16(p[2] * vsc[2], p[3] * vsc[3]);
+      for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
+      st.l[gi] += (p[0] + p[1]) + (p[2] + p[3]);
+      if constexpr (FMT == kBf16) {
+        w01[gi] = pack_bf16(p[0], p[1]);
+        w23[gi] = pack_bf16(p[2], p[3]);
+      } else {
+        w01[gi] = pack_bf16(p[0] * vsc[0], p[1] * vsc[1]);
+        w23[gi] = pack_bf16(p[2] * vsc[2], p[3] * vsc[3]);
+      }
     }
   }
 #pragma unroll
@@ -378,6 +536,36 @@ __device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, 
   first_blk = lo / BT;
   n_blk = len > lo ? (len - 1) / BT - first_blk + 1 : 0;
   n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
+}
+
+// The query words of this lane: bf16 K rows, dims 8c..8c+7 (c = lane & 15);
+// int8 / fp8 row layout, dims 16 * (lane & 7) .. +16; token-lane layout, dims
+// 32 * (lane & 3) .. +32.
+template <int G, int FMT>
+__device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int lane,
+                                       uint32_t (&qw)[G][kQWords<G, FMT>]) {
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    if constexpr (FMT == kBf16) {
+      const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 15) * 8);
+      qw[gi][0] = t.x;
+      qw[gi][1] = t.y;
+      qw[gi][2] = t.z;
+      qw[gi][3] = t.w;
+      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
+    } else {
+      constexpr int N = kQWords<G, FMT> / 4;  // uint4 per head
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & (16 / N - 1)) * 8 * N);
+#pragma unroll
+      for (int i = 0; i < N; i++) {
+        const uint4 t = src[i];
+        qw[gi][4 * i] = t.x;
+        qw[gi][4 * i + 1] = t.y;
+        qw[gi][4 * i + 2] = t.z;
+        qw[gi][4 * i + 3] = t.w;
+      }
+    }
+  }
 }
 
 template <int G, int FMT>
@@ -422,50 +610,23 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     return stable[(blk_begin + wave + 4 * k) % a.max_blocks];
   };
 
-  // ---- query: packed bf16 pairs (bf16 K: dims 8c..8c+7; int8/fp8 K: dims 16*(lane&7)..+16) ----
-  uint32_t qw[G][8];
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    if constexpr (FMT == kBf16) {
-      const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c * 8);
-      qw[gi][0] = t.x;
-      qw[gi][1] = t.y;
-      qw[gi][2] = t.z;
-      qw[gi][3] = t.w;
-      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
-    } else {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 7) * 16);
-      const uint4 t0 = src[0], t1 = src[1];
-      qw[gi][0] = t0.x;
-      qw[gi][1] = t0.y;
-      qw[gi][2] = t0.z;
-      qw[gi][3] = t0.w;
-      qw[gi][4] = t1.x;
-      qw[gi][5] = t1.y;
-      qw[gi][6] = t1.z;
-      qw[gi][7] = t1.w;
-    }
-  }
+  constexpr bool TL = kTokenLanes<G, FMT>;
+  uint32_t qw[G][kQWords<G, FMT>];
+  load_q<G, FMT>(a, qrow0, lane, qw);
 
   SoftmaxState<G> st;
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    st.m[gi] = -INFINITY;
-    st.l[gi] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
-  }
+  reset_state(st);
 
   // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
   if (nbw > 0) {
     BlockRegs<FMT> r[2];
-    load_block<FMT>(a, entry(0), kvh, lane, r[0]);
+    load_block<FMT, TL>(a, entry(0), kvh, lane, r[0]);
     int e_next = nbw > 1 ? entry(1) : -1;
     // every step inside the loop issues the next block's loads before its math,
     // so the wait before the math always leaves them in flight
     auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, bool issue) __attribute__((always_inline)) {
       if (issue) {
-        load_block<FMT>(a, e_next, kvh, lane, nxt);
+        load_block<FMT, TL>(a, e_next, kvh, lane, nxt);
         e_next = k + 2 < nbw ? entry(k + 2) : -1;
       }
       compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len, lane, qw, st);
@@ -484,6 +645,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   }
 
   // ---- merge the four token groups of the wavefront ----
+  finalize_state<G, FMT>(st);
   __shared__ float s_o[4][G][D];
   __shared__ float s_m[4][G];
   __shared__ float s_l[4][G];
@@ -703,33 +865,6 @@ __device__ __forceinline__ SeqShare stream_share(const DecodeArgs &a, int W, int
   return {-1, 0, 0, 0};
 }
 
-template <int G, int FMT>
-__device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int lane, uint32_t (&qw)[G][8]) {
-  const int c = lane & 15;
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    if constexpr (FMT == kBf16) {
-      const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + c * 8);
-      qw[gi][0] = t.x;
-      qw[gi][1] = t.y;
-      qw[gi][2] = t.z;
-      qw[gi][3] = t.w;
-      qw[gi][4] = qw[gi][5] = qw[gi][6] = qw[gi][7] = 0u;
-    } else {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 7) * 16);
-      const uint4 t0 = src[0], t1 = src[1];
-      qw[gi][0] = t0.x;
-      qw[gi][1] = t0.y;
-      qw[gi][2] = t0.z;
-      qw[gi][3] = t0.w;
-      qw[gi][4] = t1.x;
-      qw[gi][5] = t1.y;
-      qw[gi][6] = t1.z;
-      qw[gi][7] = t1.w;
-    }
-  }
-}
-
 // Ends a segment: merges the wavefront's four token groups, then writes the
 // bf16 output (complete segment) or the partial in `slot`; resets the state.
 template <int G>
@@ -768,13 +903,7 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
       if (lane == 0) a.ws_ml[row] = make_float2(mm, ll);
     }
   }
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    st.m[gi] = -INFINITY;
-    st.l[gi] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
-  }
+  reset_state(st);
 }
 
 template <int G, int FMT>
@@ -839,27 +968,23 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   bool seg_from_start = c_j == 0;
   bool first_seg = true;
   bool need_q = false;
-  uint32_t qw[G][8];
+  constexpr bool TL = kTokenLanes<G, FMT>;
+  uint32_t qw[G][kQWords<G, FMT>];
   load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
 
   BlockRegs<FMT> r[2];
-  load_block<FMT>(a, next_entry(), l_kvh, lane, r[0]);
+  load_block<FMT, TL>(a, next_entry(), l_kvh, lane, r[0]);
   int e_next = n > 1 ? next_entry() : -1;
   if (++l_j == nb) {
     l_j = 0;
     l_kvh++;
   }
   SoftmaxState<G> st;
-#pragma unroll
-  for (int gi = 0; gi < G; gi++) {
-    st.m[gi] = -INFINITY;
-    st.l[gi] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) st.o[gi][j] = 0.0f;
-  }
+  reset_state(st);
 
   auto end_segment = [&](bool complete) __attribute__((always_inline)) {
     const int slot = w * 2 + (first_seg ? 0 : 1);
+    finalize_state<G, FMT>(st);
     stream_flush<G>(a, st, b, seg_kvh, complete, slot, lane);
     if (lane == 0 && (complete || seg_from_start)) {
       // this wavefront holds the segment's first unit: record how to merge it
@@ -884,7 +1009,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
       need_q = false;
     }
     if (issue) {
-      load_block<FMT>(a, e_next, l_kvh, lane, nxt);
+      load_block<FMT, TL>(a, e_next, l_kvh, lane, nxt);
       e_next = k + 2 < n ? next_entry() : -1;
       if (++l_j == nb) {
         l_j = 0;
