@@ -96,25 +96,21 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
   return p;
 }
 
-// Persistent stream decode: two workgroups of four wavefronts per compute unit
-// for bf16 pools, the best grid measured on MI355X for C2 (one and three per
-// CU run 2-8% slower), and four for int8 / fp8 pools, whose per-block
-// arithmetic keeps two resident per CU: the grid then runs in two rounds of
-// shorter ranges (C5 int8 267 us/step against 280 with two per CU and 294
-// with split-K; fp8 242 against 248 with split-K).  It is chosen when the step
-// has at least kStreamMinUnitsPerWave units (block x kv head) per wavefront
-// and its 32-bit partition arithmetic (units * wavefronts < 2^31) is exact;
-// smaller steps (C1, C4 decode) use split-K.  LLH_DECODE_KERNEL = "split" |
-// "stream" overrides the choice, LLH_DECODE_STREAM_WGS the grid.
+// Persistent stream decode: two workgroups of four wavefronts per compute unit,
+// all resident at once, the best grid measured on MI355X for C2 (one and three
+// per CU run 2-8% slower) and for C5 int8 / fp8 (three and four per CU, which
+// run in rounds, 2-4% slower).  It is chosen when the step has at least
+// kStreamMinUnitsPerWave units (block x kv head) per wavefront and its 32-bit
+// partition arithmetic (units * wavefronts < 2^31) is exact; smaller steps
+// (C1, C4 decode) use split-K.  LLH_DECODE_KERNEL = "split" | "stream"
+// overrides the choice, LLH_DECODE_STREAM_WGS the grid.
 constexpr int kStreamWgsPerCu = 2;
-constexpr int kStreamWgsPerCuQuantized = 4;
 constexpr int kStreamMaxWgs = 1024;
 constexpr int kStreamMinUnitsPerWave = 8;
 
-int stream_grid(const llh_ctx *ctx, int format) {
+int stream_grid(const llh_ctx *ctx) {
   const int wgs = env_int("LLH_DECODE_STREAM_WGS", 0);
-  const int per_cu = format == LLH_KV_BF16 ? kStreamWgsPerCu : kStreamWgsPerCuQuantized;
-  return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : per_cu * ctx->cus));
+  return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : kStreamWgsPerCu * ctx->cus));
 }
 
 // Returns the stream grid (workgroups) for this step, or 0 for split-K.
@@ -123,7 +119,7 @@ int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int 
   const bool want_split = force && std::strcmp(force, "split") == 0;
   const bool want_stream = force && std::strcmp(force, "stream") == 0;
   if (want_split) return 0;
-  const int wgs = stream_grid(ctx, format);
+  const int wgs = stream_grid(ctx);
   const long long waves = 4LL * wgs;
   const long long max_units_seq = (long long)kv_heads * est_blocks;
   const long long max_units = max_units_seq * num_seqs;

@@ -773,8 +773,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 // loading one unit ahead of the math across kv-head boundaries.  Every
 // workgroup has the same amount of work however ragged the lengths are, and
 // there is no workgroup barrier and no wait on another workgroup, so results
-// do not depend on how many workgroups are resident at once (bf16 grids are
-// all resident; int8 / fp8 grids run in two rounds).
+// do not depend on how many workgroups are resident at once (the default grid
+// is all resident).
 //
 // A segment that lies wholly inside one wavefront's range is written out
 // directly.  A segment cut between wavefronts leaves one (max, sum, output)

@@ -332,7 +332,7 @@ def test_stream_is_the_default_for_large_bf16_batches(ctx, monkeypatch):
 @pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
 def test_stream_is_the_default_for_large_quantized_batches(ctx, fmt, monkeypatch):
     """A C5-shaped batch (64 sequences, Hq32/Hkv8) of int8 / fp8 blocks takes the stream
-    kernel without an override (its grid runs in two rounds) and meets the bar."""
+    kernel without an override and meets the bar."""
     monkeypatch.delenv("LLH_DECODE_KERNEL", raising=False)
     batch = workloads.paged_batch(np.full(64, 2048, np.int32), BT, 0.10, 61)
     before = ctx.metrics()["stream_decode_calls"]
