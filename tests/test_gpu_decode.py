@@ -206,6 +206,34 @@ def test_decode_quantized_ragged_window(ctx, decode_kernel, fmt):
     check(ctx, batch, 16, 8, fmt, window=333, seed=22, what=f"fmt={fmt} W=333")
 
 
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+def test_decode_quantized_gqa_groups(ctx, decode_kernel, fmt, Hq, Hkv):
+    """Every group size through both lane layouts of the quantized path: G <= 4
+    scores one (token, head) per lane (token-lane layout, q words of 32 dims),
+    G = 8 keeps the row layout; with and without a window cutting blocks."""
+    lens = [300, 700, 1200]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq * 10 + Hkv + fmt)
+    check(ctx, batch, Hq, Hkv, fmt, seed=13, what=f"fmt={fmt} Hq={Hq} Hkv={Hkv}")
+    check(ctx, batch, Hq, Hkv, fmt, window=250, seed=14, what=f"fmt={fmt} Hq={Hq} Hkv={Hkv} W=250")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_bad_block_is_masked_and_flagged(ctx, decode_kernel, fmt):
+    """A table entry outside the pool raises the sticky flag, its tokens are
+    masked (the output stays finite) and the other sequences are unaffected."""
+    batch = workloads.paged_batch([64, 64], BT, 0.10, seed=19)
+    pool, q = build_case(ctx, batch, 16, 8, fmt, 19)
+    bad = workloads.PagedBatch(batch.seq_lens, batch.tables.copy(), batch.n_blocks, BT, batch.first_block)
+    bad.tables[1, 2] = batch.n_blocks + 5
+    out = run_decode(ctx, pool, bad, q, 16, 0, 0.1)
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
+    assert np.all(np.isfinite(oracle.bf16_to_f32(out)))
+    first = workloads.PagedBatch(batch.seq_lens[:1], batch.tables[:1], batch.n_blocks, BT, batch.first_block[:1])
+    ref = oracle_decode(pool, first, fmt, 16, 8, 0, q[: 16 * D], 0.1)
+    assert_parity(out[: 16 * D], ref, what=f"good sequence beside a bad one, fmt={fmt}")
+
+
 def test_decode_empty_sequence_is_zero(ctx, decode_kernel):
     """R = 0 gives a zero output (weighted sum of nothing, primitives.rs:1125-1128)."""
     batch = workloads.paged_batch([0, 20], BT, 0.10, seed=3)
