@@ -12,7 +12,10 @@ the mean step time from HIP events on the launch stream over --steps steps.
 `secondary` adds the other BASELINE configs (C1, C3 prefill MFMA utilisation,
 C4 window decode/prefill, C5 int8/fp8 decode) measured the same way.
 `cpu_baseline` times the CPU oracle (a C restatement of the reference's
-single-threaded per-head loop) on the same pool, on this host.
+single-threaded per-head loop) on the same pool, on this host, on one thread
+(the reference's own setting) and, under `all_threads`, on all of this
+process's host threads (at most 16); each secondary config carries the same
+two timings under `cpu` (C5 and the prefills on a stated, scaled sample).
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
 """
@@ -164,6 +167,91 @@ def cpu_baseline_decode(w: DecodeWorkload, budget_s: float):
         "us_per_step": round(sec_per_step * 1e6, 1),
         "host": host_info(),
     }
+
+
+def host_threads() -> int:
+    """Threads of the all-cores CPU timing: this process's CPU set, at most 16 (one GPU's share of the box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _timed(fn, budget_s: float, max_reps: int = 20) -> tuple[float, int]:
+    """Mean seconds per call of fn over at least one call, until budget_s or max_reps."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= max_reps:
+            return el / reps, reps
+
+
+def cpu_decode_times(w: DecodeWorkload, budget_s: float, sample_seqs: int = 0) -> dict:
+    """The oracle's decode step on w's pool on 1 thread and on all host threads.  With
+    sample_seqs > 0 (workloads whose sequences all have one length) each call decodes the
+    first sample_seqs sequences and the time is scaled by B / sample_seqs."""
+    import numpy as np
+    import oracle
+
+    b = w.batch
+    B = b.seq_lens.size
+    k = B if sample_seqs <= 0 else min(B, sample_seqs)
+    opool = oracle.Pool.from_raw(w.fmt, BT, w.Hkv, D, b.n_blocks, w.pool.raw())
+    q = w.q.view(w.torch.int16).cpu().numpy().view(np.uint16).ravel()[: k * w.Hq * D]
+    lens, tabs = b.seq_lens[:k], b.tables[:k]
+    res = {"threads": host_threads(), "sample": f"{k} of {B} sequences per call" + ("" if k == B else f", scaled x{B / k:g}")}
+    for key, th in (("us_per_step_1_thread", 1), ("us_per_step_all_threads", res["threads"])):
+        def call():
+            st, _ = opool.decode(w.Hq, lens, tabs, w.window, q, w.scale, threads=th)
+            if st != 0:
+                raise RuntimeError(f"oracle decode failed: {st}")
+        sec, reps = _timed(call, budget_s)
+        res[key] = round(sec * B / k * 1e6, 1)
+        res[key.replace("us_per_step", "calls")] = reps
+    res["gbs_all_threads"] = round(w.algorithmic_bytes() / (res["us_per_step_all_threads"] * 1e-6) / 1e9, 3)
+    res["tokens_per_s_all_threads"] = round(B / (res["us_per_step_all_threads"] * 1e-6), 1)
+    return res
+
+
+def cpu_prefill_times(keep, B: int, prefix: int, chunk: int, Hq: int, Hkv: int, window: int, rows: int,
+                      budget_s: float) -> dict:
+    """The oracle's prefill on `rows` query rows of sequence 0 (the middle of its chunk), on 1 thread
+    and on all host threads, scaled to the whole step by the count of unmasked (query, key) pairs
+    (the oracle's work is proportional to it)."""
+    import numpy as np
+    import oracle
+    import llm_hip
+
+    pool, q, out, starts, clens, tab = keep
+    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, int(pool.info.n_blocks), pool.raw())
+    qh = q.view(torch_int16()).cpu().numpy().view(np.uint16).ravel()
+    cs, cl, tb = starts.cpu().numpy(), clens.cpu().numpy(), tab.cpu().numpy()
+    lo_row = (chunk - rows) // 2
+    pairs = lambda i: (prefix + i) - (max(0, prefix + i - window + 1) if window > 0 else 0) + 1
+    scale_up = B * sum(pairs(i) for i in range(chunk)) / sum(pairs(i) for i in range(lo_row, lo_row + rows))
+    buf = np.zeros(int(cs[-1]) * Hq * D, dtype=np.float32)
+    res = {"threads": host_threads(), "sample": f"rows {lo_row}..{lo_row + rows - 1} of sequence 0, all {Hq} heads, "
+                                                f"scaled x{scale_up:.1f} by unmasked (query, key) pairs"}
+    for key, th in (("us_per_step_1_thread", 1), ("us_per_step_all_threads", res["threads"])):
+        def call():
+            st = opool.prefill_rows(0, Hq, cs, cl, tb, window, qh, 1.0 / math.sqrt(D), lo_row, lo_row + rows, buf,
+                                    threads=th)
+            if st != 0:
+                raise RuntimeError(f"oracle prefill failed: {st}")
+        sec, reps = _timed(call, budget_s, max_reps=5)
+        res[key] = round(sec * scale_up * 1e6, 1)
+        res[key.replace("us_per_step", "calls")] = reps
+    res["tokens_per_s_all_threads"] = round(B * chunk / (res["us_per_step_all_threads"] * 1e-6), 1)
+    return res
+
+
+def torch_int16():
+    import torch
+
+    return torch.int16
 
 
 def host_info() -> str:
@@ -337,14 +425,20 @@ def main() -> int:
         log("CPU baseline (oracle, 1 thread) on the C2 pool ...")
         cpu = cpu_baseline_decode(w, args.cpu_seconds)
         log(f"CPU: {cpu['us_per_step']} us/step")
+        mt = cpu_decode_times(w, 3.0)
+        cpu["all_threads"] = {k: mt[k] for k in ("threads", "us_per_step_all_threads", "gbs_all_threads", "calls_all_threads")}
+        log(f"CPU, {mt['threads']} threads: {mt['us_per_step_all_threads']} us/step")
     del w
     torch.cuda.empty_cache()
 
     secondary = []
     if not args.no_secondary:
         sec_steps = max(10, args.steps // 2)
-        _, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, args.warmup,
-                              seed=workloads.SEED_BASE, free=0.0)
+        w1, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, args.warmup,
+                               seed=workloads.SEED_BASE, free=0.0)
+        if not args.no_cpu:
+            r["cpu"] = cpu_decode_times(w1, 1.0)
+        del w1
         secondary.append(r)
         log(f"C1: {r}")
         L, W = 32768, 4096
@@ -355,6 +449,8 @@ def main() -> int:
         for fmt, nm in ((llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
             wq, r = measure_decode(ctx, f"C5 decode {nm} B=64 L=8192 Hq32/Hkv8", [8192] * 64, 32, 8, fmt,
                                    sec_steps, args.warmup, seed=workloads.SEED_BASE + 4, free=0.0)
+            if not args.no_cpu:
+                r["cpu"] = cpu_decode_times(wq, 1.0, sample_seqs=4)
             secondary.append(r)
             log(f"C5 {nm}: {r}")
             del wq
@@ -371,6 +467,8 @@ def main() -> int:
             r = {"config": name, "us_per_step": round(pms * 1e3, 2), "kernel_us": round(pkms * 1e3, 2), "tflops": round(tf, 1),
                  "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
                  "flops_per_step": flops}
+            if not args.no_cpu:
+                r["cpu"] = cpu_prefill_times(keep, B, prefix, chunk, Hq, Hkv, window, 16, 1.0)
             secondary.append(r)
             log(f"{name}: {r}")
             del keep

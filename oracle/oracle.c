@@ -93,6 +93,13 @@ float orc_fp8e4m3_to_f32(uint8_t c) {
   return s ? -v : v;
 }
 
+/* orc_fp8e4m3_to_f32 of every code, filled when the library loads (the pool reads
+   of an fp8 pool go through it: the same values, without a ldexpf per element) */
+static float fp8_table[256];
+__attribute__((constructor)) static void fill_fp8_table(void) {
+  for (int c = 0; c < 256; c++) fp8_table[c] = orc_fp8e4m3_to_f32((uint8_t)c);
+}
+
 uint8_t orc_f32_to_fp8e4m3(float x) {
   uint32_t u = f32_bits(x);
   uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
@@ -445,7 +452,7 @@ float orc_pool_elem(const orc_pool *p, int tensor, int64_t block, int32_t head, 
     }
     case ORC_KV_FP8_E4M3: {
       float s = ((const float *)scales)[(int64_t)block * p->kv_heads + head];
-      return orc_fp8e4m3_to_f32(((const uint8_t *)base)[idx]) * s;
+      return fp8_table[((const uint8_t *)base)[idx]] * s;
     }
     default:
       return NAN;
