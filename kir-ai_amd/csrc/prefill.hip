@@ -160,7 +160,18 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
   const int GW = Hq / Hkv / HPW;  // workgroups per (kv head, query tile)
   const int n_items = a.q_tiles * Hkv * GW * a.num_seqs;
   const int per_xcd = (n_items + 7) / 8;
-  const int w = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  // Within one XCD's items, the longest go first: when its block of items is
+  // whole (sequence, kv head) groups, dispatch i takes tile q_tiles-1-r of
+  // group g (r = i / (groups * GW)), so the first round runs the tiles with
+  // the longest causal reach and the last round the shortest.
+  const int per_group = a.q_tiles * GW;
+  const int di = blockIdx.x / 8;
+  int local = di;
+  if (per_xcd % per_group == 0) {
+    const int groups = per_xcd / per_group;
+    local = ((di / GW) % groups) * per_group + (a.q_tiles - 1 - di / (groups * GW)) * GW + di % GW;
+  }
+  const int w = (blockIdx.x % 8) * per_xcd + local;
   if (w >= n_items) return;
   const int tile = (w / GW) % a.q_tiles;
   const int kvh = (w / (GW * a.q_tiles)) % Hkv;
