@@ -11,8 +11,8 @@
 //  * paged_decode_stream_kernel (large batches): a persistent grid whose
 //    wavefronts each stream an equal, contiguous range of one sequence's
 //    (kv head, block) units; see its own comment.
-//  * paged_decode_kernel (small batches, quantised pools): one
-//    workgroup per (split, kv head, sequence).  A split is `split_blocks`
+//  * paged_decode_kernel (small batches: fewer than 8 units per stream
+//    wavefront): one workgroup per (split, kv head, sequence).  A split is `split_blocks`
 // consecutive blocks of the attended range; the four wavefronts take its blocks
 // round-robin, double-buffering the loads of the next block behind the math of
 // the current one.  Every K/V byte of the kv head is read once and serves all
@@ -34,7 +34,12 @@
 //             four 256-B segments per instruction.  q . k runs on packed bf16
 //             dot2 with fp32 accumulation, then a 16-lane DPP butterfly.
 //   V (bf16): lane loads 8 B = tokens 4g..4g+3 of dim 16j + c (j = 0..7):
-//             512 contiguous bytes per instruction.
+//             512 contiguous bytes per instruction (int8 / fp8: 4 B, 256).
+//   K (int8 / fp8, G <= 4, token-lane layout): lane 4tq + c4 of row g loads
+//             the 32 B of token 4g + tq at dims 32c4 .. 32c4+31 and scores that
+//             token for head c4 % G after a 4-lane butterfly (see kTokenLanes);
+//   K (int8 / fp8, G = 8): lane loads 16 B of tokens 4g + 2i + hf at dims
+//             16 (c % 8) .. +16, then an 8-lane butterfly and a row mirror.
 // Each group keeps its own online-softmax state (running max in log2 units,
 // sum, 8 output dims per lane per head); groups, wavefronts and splits are
 // merged by log-sum-exp.
