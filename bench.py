@@ -308,6 +308,71 @@ def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos
     return step, flops, keep
 
 
+def measure_neighbours(ctx, steps: int, warmup: int) -> list:
+    """The steps either side of decode attention, at C2's shape: the new token's K/V append
+    (32 rows into 16-token blocks; bf16, and int8 quantised on write) and the o_proj of
+    Qwen3-0.6B (W bf16 1024 x 2048, 32 attention outputs), alone and fused behind the decode.
+    W rotates over copies totalling > 2 x 256 MB so each step reads it from HBM."""
+    import torch
+    import llm_hip
+    from llm_hip import workloads
+
+    out = []
+    g = torch.Generator(device="cuda")
+    g.manual_seed(workloads.SEED_BASE + 7)
+    B, Hkv, Hq = 32, 8, 16
+    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8")):
+        pool = ctx.pool(fmt, BT, Hkv, D, 4096)
+        slots = torch.randperm(4096 * BT, generator=g, device="cuda")[:B].to(torch.int64)
+        k = torch.randn((B, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((B, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        ms = time_steps(lambda s: ctx.append(pool, slots, k, v, stream=s), steps, warmup)
+        esz = 2 if fmt == llm_hip.KV_BF16 else 1
+        nbytes = B * Hkv * D * 2 * 2 + B * Hkv * D * esz * 2 + B * 8 + (B * Hkv * 2 * 2 if esz == 1 else 0)
+        out.append({"config": f"KV append C2 batch ({B} tokens, Hkv8, {nm})", "us_per_step": round(ms * 1e3, 2),
+                    "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "kernel": "append_kernel (launch-bound at this size)"})
+        if ctx.device_errors() != 0:
+            raise RuntimeError("append: device error flags set")
+        del pool
+    rows, cols = 1024, Hq * D
+    wbytes = rows * cols * 2
+    ws = [torch.randn((rows, cols), generator=g, device="cuda").to(torch.bfloat16)
+          for _ in range(2 * LLC_BYTES // wbytes + 2)]
+    x = torch.randn((B, cols), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((B, rows), dtype=torch.float32, device="cuda")
+    st = {"i": 0}
+
+    def proj(s):
+        ctx.matvec_bf16(ws[st["i"] % len(ws)], rows, cols, x, B, y, stream=s)
+        st["i"] += 1
+
+    ms = time_steps(proj, steps, warmup)
+    nbytes = wbytes + B * cols * 2 + B * rows * 4
+    out.append({"config": f"o_proj matvec W {rows}x{cols} bf16, {B} rows", "us_per_step": round(ms * 1e3, 2),
+                "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "w_copies": len(ws),
+                "kernel": "matvec_bf16_kernel (MFMA)"})
+    lens = list(workloads.uniform_lengths(B, 256, 4096, workloads.SEED_BASE + 1))
+    w = DecodeWorkload(ctx, lens, Hq, Hkv, llm_hip.KV_BF16, seed=workloads.SEED_BASE + 3)
+    st["i"] = 0
+
+    def fused(s):
+        ctx.paged_decode_output_projection(w.pool, w.desc, w.q, ws[st["i"] % len(ws)], rows, y, w.scale, stream=s)
+        st["i"] += 1
+
+    ms_f = time_steps(fused, steps, warmup)
+    ms_d = time_steps(lambda s: w.step(s), steps, warmup)
+    out.append({"config": "C2 decode + o_proj fused (llh_paged_decode_output_projection)", "us_per_step": round(ms_f * 1e3, 2),
+                "decode_alone_us": round(ms_d * 1e3, 2), "projection_added_us": round((ms_f - ms_d) * 1e3, 2),
+                "note": "one pool copy: the K/V of consecutive steps may be partly cache resident"})
+    if ctx.device_errors() != 0:
+        raise RuntimeError("o_proj: device error flags set")
+    del w, ws
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_copy(mb: int) -> dict:
     """A plain device-to-device copy of `mb` MiB: the measured bandwidth ceiling, and the
     known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -455,6 +520,7 @@ def main() -> int:
             log(f"C5 {nm}: {r}")
             del wq
             torch.cuda.empty_cache()
+        secondary.extend(measure_neighbours(ctx, sec_steps, args.warmup))
         for name, B, prefix, chunk, Hq, Hkv, window, res in (
                 ("C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None),
                 ("C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096)):

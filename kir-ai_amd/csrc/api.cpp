@@ -548,6 +548,12 @@ int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t col
   a.ldx = cols;
   a.ldo = rows;
   a.x_f32 = x_f32 ? 1 : 0;
+  a.ksplit = matvec_ksplit(rows, cols, n, ctx->cus);
+  if (a.ksplit > 1) {  // partial tiles after the decode counters at the front of the workspace
+    st = ctx->ensure_ws(kCounterBytes + (size_t)a.ksplit * n * rows * sizeof(float));
+    if (st != LLH_OK) return st;
+    a.partial = reinterpret_cast<float *>(static_cast<char *>(ctx->ws) + kCounterBytes);
+  }
   hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
   return LLH_OK;
@@ -562,8 +568,10 @@ int llh_paged_decode_output_projection(llh_ctx *ctx, const llh_kv_pool *pool, co
   int st = check_projection(ctx, d_w_o, rows, cols, d_out);
   if (st != LLH_OK) return st;
   const size_t attn_bytes = align_up((size_t)desc->num_seqs * cols * sizeof(uint16_t));
-  void *attn = nullptr;
-  st = paged_decode_impl(ctx, pool, desc, d_q, nullptr, score_scale, stream, attn_bytes, &attn);
+  const int ksplit = matvec_ksplit(rows, cols, desc->num_seqs, ctx->cus);
+  const size_t partial_bytes = ksplit > 1 ? (size_t)ksplit * desc->num_seqs * rows * sizeof(float) : 0;
+  void *attn = nullptr;  // the attention output, then the projection's partial tiles
+  st = paged_decode_impl(ctx, pool, desc, d_q, nullptr, score_scale, stream, attn_bytes + partial_bytes, &attn);
   if (st != LLH_OK) return st;
   MatvecArgs a{};
   a.w = static_cast<const uint16_t *>(d_w_o);
@@ -575,6 +583,8 @@ int llh_paged_decode_output_projection(llh_ctx *ctx, const llh_kv_pool *pool, co
   a.ldx = cols;
   a.ldo = rows;
   a.x_f32 = 0;
+  a.ksplit = ksplit;
+  a.partial = ksplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(attn) + attn_bytes) : nullptr;
   hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
   return LLH_OK;

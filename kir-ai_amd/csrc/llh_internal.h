@@ -153,7 +153,13 @@ struct MatvecArgs {
   int32_t ldx;
   int32_t ldo;
   int32_t x_f32;
+  int32_t ksplit;           // > 1: K split over this many workgroups, partials summed by a second launch
+  float *partial;           // ksplit > 1: [ksplit][n][ldo] f32 workspace
 };
+
+// K split of the projection for a grid of about one workgroup per CU (1 = none);
+// the partial workspace then holds ksplit * n * ldo floats.
+int matvec_ksplit(int rows, int cols, int n, int cus);
 
 // launchers (return hipError_t of the launch)
 // `hook(user, 0, s)` runs just before and `hook(user, 1, s)` just after the main

@@ -12,6 +12,12 @@
 // K inside a wavefront is permuted so that every lane streams one contiguous
 // half of its K slice (A and B use the same permutation, so the contraction is
 // unchanged): step s, lane half h covers k = k0 + h * K/16 + 8s .. +8.
+//
+// A skinny projection has few 32 x 32 output tiles (o_proj of Qwen3-0.6B at
+// B = 32: 32 tiles), too few workgroups to pull W from HBM at full rate.  Such
+// calls also split K over `ksplit` workgroups per tile (grid z), each writing
+// its partial tile to a workspace, and a second launch sums the partials in a
+// fixed order (the result does not depend on scheduling).
 #include "llh_internal.h"
 
 namespace llh {
@@ -49,9 +55,10 @@ __global__ __launch_bounds__(64 * kWaves) void matvec_bf16_kernel(const MatvecAr
   const int h = lane >> 5;
   const int r0 = blockIdx.x * 32;
   const int i0 = blockIdx.y * 32;
-  const int kw = a.cols / kWaves;  // this wavefront's K slice
-  const int kh = kw / 2;           // per lane half
-  const int k0 = wave * kw + h * kh;
+  const int kslice = a.cols / (int)gridDim.z;  // this workgroup's K slice
+  const int kw = kslice / kWaves;               // this wavefront's
+  const int kh = kw / 2;                        // per lane half
+  const int k0 = (int)blockIdx.z * kslice + wave * kw + h * kh;
   const int row = min(r0 + c, a.rows - 1);  // rows / inputs past the end are computed on clamped data, not stored
   const int inp = min(i0 + c, a.n - 1);
   const uint16_t *wp = a.w + (size_t)row * a.cols + k0;
@@ -83,7 +90,8 @@ __global__ __launch_bounds__(64 * kWaves) void matvec_bf16_kernel(const MatvecAr
   // accumulator j of this lane: row 8(j/4) + 4h + (j%4) of the tile, input c
   const int i = i0 + c;
   if (i >= a.n) return;
-  float *orow = a.out + (size_t)i * a.ldo + r0;
+  float *const out = gridDim.z > 1 ? a.partial + (size_t)blockIdx.z * a.n * a.ldo : a.out;
+  float *orow = out + (size_t)i * a.ldo + r0;
 #pragma unroll
   for (int jq = 0; jq < 4; jq++) {
     const int rr = 8 * jq + 4 * h;
@@ -97,15 +105,48 @@ __global__ __launch_bounds__(64 * kWaves) void matvec_bf16_kernel(const MatvecAr
   }
 }
 
+// out[i][r] = sum over k of partial[k][i][r], k = 0 .. ksplit-1 in order.
+__global__ __launch_bounds__(256) void matvec_sum_kernel(const MatvecArgs a) {
+  const int r = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int i = blockIdx.y;
+  if (r >= a.rows) return;
+  const size_t plane = (size_t)a.n * a.ldo;
+  const float *p = a.partial + (size_t)i * a.ldo + r;
+  float *o = a.out + (size_t)i * a.ldo + r;
+  if (r + 3 < a.rows && a.ldo % 4 == 0) {
+    f32x4_t acc = *reinterpret_cast<const f32x4_t *>(p);
+    for (int k = 1; k < a.ksplit; k++) acc += *reinterpret_cast<const f32x4_t *>(p + k * plane);
+    *reinterpret_cast<f32x4_t *>(o) = acc;
+  } else {
+    for (int e = 0; e < 4 && r + e < a.rows; e++) {
+      float acc = p[e];
+      for (int k = 1; k < a.ksplit; k++) acc += p[k * plane + e];
+      o[e] = acc;
+    }
+  }
+}
+
 }  // namespace
+
+int matvec_ksplit(int rows, int cols, int n, int cus) {
+  const int tiles = ((rows + 31) / 32) * ((n + 31) / 32);
+  int ks = 1;
+  while (ks < 16 && tiles * ks * 2 <= cus && cols % (2 * ks * kMatvecColsMultiple) == 0) ks *= 2;
+  return ks;
+}
 
 hipError_t launch_matvec_bf16(const MatvecArgs &a, hipStream_t s) {
   if (a.rows <= 0 || a.n <= 0) return hipSuccess;
-  const dim3 grid((a.rows + 31) / 32, (a.n + 31) / 32);
+  const int ks = a.ksplit > 1 && a.partial ? a.ksplit : 1;
+  const dim3 grid((a.rows + 31) / 32, (a.n + 31) / 32, ks);
   if (a.x_f32)
     hipLaunchKernelGGL(matvec_bf16_kernel<float>, grid, dim3(64 * kWaves), 0, s, a);
   else
     hipLaunchKernelGGL(matvec_bf16_kernel<uint16_t>, grid, dim3(64 * kWaves), 0, s, a);
+  if (ks == 1) return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(matvec_sum_kernel, dim3((a.rows + 1023) / 1024, a.n), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -53,7 +53,7 @@ def test_known_answer_and_unsupported_shape(ctx):
     assert out.cpu().numpy().reshape(2, ka["rows"]).tolist() == ka["expected"]
 
 
-@pytest.mark.parametrize("rows,cols,n", [(1024, 2048, 32), (1000, 2048, 1), (77, 128, 45), (300, 512, 7)])
+@pytest.mark.parametrize("rows,cols,n", [(1024, 2048, 32), (1000, 2048, 1), (77, 128, 45), (300, 512, 7), (99, 512, 5)])
 @pytest.mark.parametrize("x_f32", [False, True])
 def test_matvec_matches_oracle(ctx, rows, cols, n, x_f32):
     import torch
