@@ -321,16 +321,34 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     g = torch.Generator(device="cuda")
     g.manual_seed(workloads.SEED_BASE + 7)
     B, Hkv, Hq = 32, 8, 16
+    # decode: the C2 batch's 32 new tokens (one row per sequence, scattered slots);
+    # prefill: C3's 8 x 512-token chunks, whole 16-token blocks (llh_kv_write_blocks)
     for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8")):
-        pool = ctx.pool(fmt, BT, Hkv, D, 4096)
-        slots = torch.randperm(4096 * BT, generator=g, device="cuda")[:B].to(torch.int64)
-        k = torch.randn((B, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
-        v = torch.randn((B, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        nblk, H = 8 * 512 // BT, 4
+        pool = ctx.pool(fmt, BT, H, D, 8192)
+        ids = torch.randperm(8192, generator=g, device="cuda")[:nblk].to(torch.int32)
+        k = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
+        ms = time_steps(lambda s: ctx.write_blocks(pool, ids, k, v, stream=s), steps, warmup)
+        esz = 2 if fmt == llm_hip.KV_BF16 else 1
+        T = nblk * BT
+        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + (T * H * 2 * 2 if esz == 1 else 0)
+        out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
+                    "us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
+                    "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_kernel"})
+        del pool
+    for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv)):
+        pool = ctx.pool(fmt, BT, H, D, 8192)
+        slots = torch.randperm(8192 * BT, generator=g, device="cuda")[:T].to(torch.int64)
+        k = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.append(pool, slots, k, v, stream=s), steps, warmup)
         esz = 2 if fmt == llm_hip.KV_BF16 else 1
-        nbytes = B * Hkv * D * 2 * 2 + B * Hkv * D * esz * 2 + B * 8 + (B * Hkv * 2 * 2 if esz == 1 else 0)
-        out.append({"config": f"KV append C2 batch ({B} tokens, Hkv8, {nm})", "us_per_step": round(ms * 1e3, 2),
+        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + T * 8 + (T * H * 2 * 2 if esz == 1 else 0)
+        out.append({"config": f"KV append C2 batch ({T} tokens, Hkv{H}, {nm})", "us_per_step": round(ms * 1e3, 2),
                     "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "kernel": "append_kernel (launch-bound at this size)"})
         if ctx.device_errors() != 0:
             raise RuntimeError("append: device error flags set")
