@@ -336,7 +336,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
                     "us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
                     "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_kernel"})
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_d128_kernel"})
         del pool
     for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv)):
         pool = ctx.pool(fmt, BT, H, D, 8192)

@@ -70,6 +70,79 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Whole 16-token blocks of head_dim 128, bf16 or int8 pools: one workgroup of
+// 256 lanes per (block, head).  Lane (t = lane / 16, c = lane % 16) loads the
+// 16 B of token t at dims 8c .. 8c+7 of K and of V (coalesced), writes K rows
+// straight out, and V is transposed through LDS so that every lane then writes
+// 16 B (bf16) or 8 B (int8) of one dim row: every global access is a full,
+// coalesced vector access.  int8: the per-(token, head) scale is the 16 lanes'
+// absmax, then the same f16 rounding and code rule as the generic kernel.
+__global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlocksArgs a) {
+  constexpr int BT = 16, Dh = 128;
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t = tid >> 4, c = tid & 15;
+  const int Hkv = a.pool.kv_heads;
+  const int blk = a.blocks[i];
+  if (blk < 0 || (int64_t)blk >= a.pool.n_blocks) {
+    if (tid == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const size_t src = (((size_t)i * BT + t) * Hkv + h) * Dh + 8 * c;
+  const uint4 kw = *reinterpret_cast<const uint4 *>(a.k + src);
+  const uint4 vw = *reinterpret_cast<const uint4 *>(a.v + src);
+  const int d = tid >> 1, half = tid & 1;  // the dim row and token half this lane writes after the transpose
+  if (a.pool.format == kBf16) {
+    __shared__ uint16_t lv[BT][Dh + 8];
+    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) = kw;
+    *reinterpret_cast<uint4 *>(&lv[t][8 * c]) = vw;
+    __syncthreads();
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      w[j] = (uint32_t)lv[8 * half + 2 * j][d] | ((uint32_t)lv[8 * half + 2 * j + 1][d] << 16);
+    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.v_dst) + (bh * Dh + d) * BT + 8 * half) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  // int8 with per (token, head) fp16 scales
+  __shared__ uint8_t lq[BT][Dh + 16];
+  uint32_t codes[2][2];
+#pragma unroll
+  for (int tensor = 0; tensor < 2; tensor++) {
+    const uint4 wv = tensor ? vw : kw;
+    const uint32_t u[4] = {wv.x, wv.y, wv.z, wv.w};
+    float x[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      x[2 * j] = bf16_to_f32((uint16_t)(u[j] & 0xffffu));
+      x[2 * j + 1] = bf16_to_f32((uint16_t)(u[j] >> 16));
+      mx = fmaxf(mx, fmaxf(fabsf(x[2 * j]), fabsf(x[2 * j + 1])));
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // the token's 16 lanes
+    const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
+    const float sc = (float)s16;
+    uint32_t q[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)(uint8_t)quant_int8(x[j], sc) << (8 * (j & 3));
+    codes[tensor][0] = q[0];
+    codes[tensor][1] = q[1];
+    if (c == 0) reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[bh * BT + t] = __builtin_bit_cast(uint16_t, s16);
+  }
+  *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) =
+      make_uint2(codes[0][0], codes[0][1]);
+  *reinterpret_cast<uint2 *>(&lq[t][8 * c]) = make_uint2(codes[1][0], codes[1][1]);
+  __syncthreads();
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; j++) w[j >> 2] |= (uint32_t)lq[8 * half + j][d] << (8 * (j & 3));
+  *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(a.v_dst) + (bh * Dh + d) * BT + 8 * half) = make_uint2(w[0], w[1]);
+}
+
 // One workgroup per (block i, kv head).  Source rows src[i][t][h][d].
 __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs a) {
   const int i = blockIdx.x;
@@ -297,7 +370,14 @@ hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
 
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(write_blocks_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
+  const bool fast = a.pool.head_dim == 128 && a.pool.block_tokens == 16 &&
+                    (a.pool.format == kBf16 || a.pool.format == kInt8) &&
+                    reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
+  if (fast)
+    hipLaunchKernelGGL(write_blocks_d128_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(write_blocks_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -122,6 +122,60 @@ def test_fp8_quantise_on_write_is_bit_exact(ctx):
 
 
 @pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_block_write_vector_and_generic_kernels_agree(ctx, fmt):
+    """head_dim 128 / 16-token blocks from 16-byte aligned rows take the vector
+    kernel; the same rows 2 bytes off alignment take the generic one.  Pools equal."""
+    import torch
+
+    Hkv = 4
+    batch, pool_fast, ids, sk, sv = write_case(ctx, fmt, [40, 17, 300], Hkv, 500)
+    pool_gen = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
+
+    def misaligned(a):
+        flat = torch.zeros(a.size + 1, dtype=torch.int16, device="cuda")
+        flat[1:] = to_dev(a).reshape(-1)
+        view = flat[1:]
+        assert view.data_ptr() % 16 != 0
+        return view
+
+    ctx.write_blocks(pool_gen, to_dev(ids), misaligned(sk), misaligned(sv))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0
+    rf, rg = pool_fast.raw(), pool_gen.raw()
+    written = np.asarray(ids)  # blocks no write touched hold whatever the allocation held
+    for key in rf:
+        f = rf[key].reshape(batch.n_blocks, -1)[written]
+        g = rg[key].reshape(batch.n_blocks, -1)[written]
+        assert np.array_equal(f, g), key
+
+
+def test_int8_quantise_on_write_generic_head_dim(ctx):
+    """head_dim 64 goes through the generic kernel: same quantiser, bit for bit."""
+    Hkv, hd = 2, 64
+    batch, pool, ids, sk, sv = write_case(ctx, llm_hip.KV_INT8, [33], Hkv, 600, head_dim=hd)
+    raw = pool.raw()
+    k = raw["k"].view(np.int8).reshape(batch.n_blocks, Hkv, BT, hd)
+    v = raw["v"].view(np.int8).reshape(batch.n_blocks, Hkv, hd, BT)
+    for i, blk in enumerate(ids):
+        for h in range(Hkv):
+            for t in range(BT):
+                _, codes, _ = oracle.quantize_int8_head(oracle.bf16_to_f32(sk[i, t, h]))
+                assert np.array_equal(k[blk, h, t], codes)
+                _, codes, _ = oracle.quantize_int8_head(oracle.bf16_to_f32(sv[i, t, h]))
+                assert np.array_equal(v[blk, h, :, t], codes)
+
+
+def test_block_write_flags_bad_block(ctx):
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 2, D, 2)
+    z = torch.zeros(BT * 2 * D, dtype=torch.int16, device="cuda")
+    ctx.write_blocks(pool, torch.tensor([2], dtype=torch.int32, device="cuda"), z, z)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
 def test_append_equals_block_write(ctx, fmt):
     import torch
 
