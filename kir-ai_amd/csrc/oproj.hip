@@ -126,6 +126,27 @@ __global__ __launch_bounds__(256) void matvec_sum_kernel(const MatvecArgs a) {
   }
 }
 
+// The same sum with the slice count fixed at compile time: the KS loads of a
+// lane are unrolled and all issued before the first add (the runtime-count loop
+// above waits for each load in turn), and 64-lane workgroups spread the few
+// rows over more compute units.  Same order of additions, same result.
+template <int KS>
+__global__ __launch_bounds__(64) void matvec_sum_fixed_kernel(const MatvecArgs a) {
+  const int r = (blockIdx.x * 64 + threadIdx.x) * 4;
+  const int i = blockIdx.y;
+  if (r >= a.rows) return;
+  const size_t plane = (size_t)a.n * a.ldo;
+  const float *p = a.partial + (size_t)i * a.ldo + r;
+  float *o = a.out + (size_t)i * a.ldo + r;
+  f32x4_t v[KS];
+#pragma unroll
+  for (int k = 0; k < KS; k++) v[k] = *reinterpret_cast<const f32x4_t *>(p + k * plane);
+  f32x4_t acc = v[0];
+#pragma unroll
+  for (int k = 1; k < KS; k++) acc += v[k];
+  *reinterpret_cast<f32x4_t *>(o) = acc;
+}
+
 }  // namespace
 
 int matvec_ksplit(int rows, int cols, int n, int cus) {
@@ -146,7 +167,17 @@ hipError_t launch_matvec_bf16(const MatvecArgs &a, hipStream_t s) {
   if (ks == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(matvec_sum_kernel, dim3((a.rows + 1023) / 1024, a.n), dim3(256), 0, s, a);
+  if (a.rows % 4 == 0 && a.ldo % 4 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (ks == 2 || ks == 4 || ks == 8 || ks == 16)) {
+    const dim3 g((a.rows / 4 + 63) / 64, a.n);
+    switch (ks) {
+      case 2: hipLaunchKernelGGL(matvec_sum_fixed_kernel<2>, g, dim3(64), 0, s, a); break;
+      case 4: hipLaunchKernelGGL(matvec_sum_fixed_kernel<4>, g, dim3(64), 0, s, a); break;
+      case 8: hipLaunchKernelGGL(matvec_sum_fixed_kernel<8>, g, dim3(64), 0, s, a); break;
+      default: hipLaunchKernelGGL(matvec_sum_fixed_kernel<16>, g, dim3(64), 0, s, a); break;
+    }
+  } else {
+    hipLaunchKernelGGL(matvec_sum_kernel, dim3((a.rows + 1023) / 1024, a.n), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 
