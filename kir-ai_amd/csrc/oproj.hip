@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64 * kWaves) void matvec_bf16_kernel(const MatvecAr
 #pragma unroll
   for (int jq = 0; jq < 4; jq++) {
     const int rr = 8 * jq + 4 * h;
-    if (a.ldo % 4 == 0 && r0 + rr + 3 < a.rows) {
+    if (a.ldo % 4 == 0 && r0 + rr + 3 < a.rows && (reinterpret_cast<uintptr_t>(orow + rr) & 15) == 0) {
       *reinterpret_cast<f32x4_t *>(orow + rr) = f32x4_t{acc[4 * jq], acc[4 * jq + 1], acc[4 * jq + 2], acc[4 * jq + 3]};
     } else {
 #pragma unroll
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void matvec_sum_kernel(const MatvecArgs a) {
   const size_t plane = (size_t)a.n * a.ldo;
   const float *p = a.partial + (size_t)i * a.ldo + r;
   float *o = a.out + (size_t)i * a.ldo + r;
-  if (r + 3 < a.rows && a.ldo % 4 == 0) {
+  if (r + 3 < a.rows && a.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
     f32x4_t acc = *reinterpret_cast<const f32x4_t *>(p);
     for (int k = 1; k < a.ksplit; k++) acc += *reinterpret_cast<const f32x4_t *>(p + k * plane);
     *reinterpret_cast<f32x4_t *>(o) = acc;

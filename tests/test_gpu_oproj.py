@@ -53,7 +53,10 @@ def test_known_answer_and_unsupported_shape(ctx):
     assert out.cpu().numpy().reshape(2, ka["rows"]).tolist() == ka["expected"]
 
 
-@pytest.mark.parametrize("rows,cols,n", [(1024, 2048, 32), (1000, 2048, 1), (77, 128, 45), (300, 512, 7), (99, 512, 5)])
+# On 256 compute units K is split over 8 (1024x2048, 1000x2048), 16 (300x512),
+# 4 (2048x1024) and 2 (4096x512) workgroups; 77 and 99 rows take the generic sum.
+@pytest.mark.parametrize("rows,cols,n", [(1024, 2048, 32), (1000, 2048, 1), (77, 128, 45), (300, 512, 7), (99, 512, 5),
+                                         (2048, 1024, 3), (4096, 512, 2)])
 @pytest.mark.parametrize("x_f32", [False, True])
 def test_matvec_matches_oracle(ctx, rows, cols, n, x_f32):
     import torch
@@ -74,6 +77,25 @@ def test_matvec_matches_oracle(ctx, rows, cols, n, x_f32):
     # f32 inputs are rounded to bf16 for the MFMA (relative 2^-9 per product)
     assert d.max() <= (2e-2 if x_f32 else 1e-4), d.max()
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("rows,cols,n", [(1024, 2048, 32), (4096, 512, 2), (300, 512, 7)])
+def test_matvec_unaligned_output_is_identical(ctx, rows, cols, n):
+    """An output one float off 16-byte alignment takes the element-wise stores
+    of both launches: the same sums in the same order, bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(7 * rows + n)
+    w = oracle.f32_to_bf16((rng.standard_normal((rows, cols)) / math.sqrt(cols)).astype(np.float32))
+    xb = oracle.f32_to_bf16(rng.standard_normal((n, cols)).astype(np.float32))
+    out = torch.zeros(n * rows, dtype=torch.float32, device="cuda")
+    ctx.matvec_bf16(to_dev(w), rows, cols, to_dev(xb), n, out)
+    flat = torch.zeros(n * rows + 1, dtype=torch.float32, device="cuda")
+    shifted = flat[1:]
+    assert shifted.data_ptr() % 16 != 0
+    ctx.matvec_bf16(to_dev(w), rows, cols, to_dev(xb), n, shifted)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), shifted.cpu().numpy().view(np.uint32))
 
 
 def test_fused_decode_projection(ctx):
