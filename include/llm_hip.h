@@ -200,7 +200,8 @@ typedef struct llh_prefill_desc {
   const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] */
 } llh_prefill_desc;
 
-/* d_q, d_out: [total_q_rows][Hq][head_dim] bf16.  bf16 pools only. */
+/* d_q, d_out: [total_q_rows][Hq][head_dim] bf16, 16-byte aligned (else
+ * LLH_ERR_UNSUPPORTED).  bf16 pools only. */
 int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
                       void *d_out, float score_scale, void *stream);
 

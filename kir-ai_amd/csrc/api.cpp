@@ -418,7 +418,11 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   const PoolView &pv = pool->view;
   const int group = desc->num_q_heads / pv.kv_heads;
-  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
+  // The fast kernels move q and output rows in 16-byte vectors; rows that are
+  // not 16-byte aligned go through the element-wise generic kernel.
+  const bool rows_aligned = (reinterpret_cast<uintptr_t>(d_q) & 15) == 0 &&
+                            (reinterpret_cast<uintptr_t>(d_out) & 15) == 0;
+  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens && rows_aligned &&
                     (group == 1 || group == 2 || group == 4 || group == 8) &&
                     (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !env_int("LLH_FORCE_GENERIC", 0);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -605,6 +609,8 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   }
   if (!d_q || !d_out || !desc->d_chunk_starts || !desc->d_context_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in prefill call");
+  if (((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) != 0)
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill q and output rows must be 16-byte aligned");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   PrefillArgs a{};
   a.pool = pv;

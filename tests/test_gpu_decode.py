@@ -73,6 +73,37 @@ def check(ctx, batch, Hq, Hkv, fmt=llm_hip.KV_BF16, window=0, seed=1, head_dim=D
     return assert_parity(out, ref, what=what)
 
 
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_decode_unaligned_rows_take_the_generic_kernel(ctx, fmt):
+    """q and out 2 bytes off 16-byte alignment: the element-wise generic kernel
+    runs (no stream launch) and matches the oracle like the fast path."""
+    import torch
+
+    Hq, Hkv = 8, 2
+    batch = workloads.paged_batch([37, 300, 1], BT, 0.1, 41)
+    scale = 1.0 / math.sqrt(D)
+    pool, q = build_case(ctx, batch, Hq, Hkv, fmt, 41)
+
+    def shifted(n):
+        flat = torch.zeros(n + 1, dtype=torch.int16, device="cuda")
+        view = flat[1:]
+        assert view.data_ptr() % 16 != 0
+        return view
+
+    B = batch.seq_lens.size
+    d_q = shifted(q.size)
+    d_q.copy_(to_dev(q).view(-1))
+    d_out = shifted(B * Hq * D)
+    desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(batch.tables), Hq, int(batch.seq_lens.max()))
+    before = ctx.metrics()["stream_decode_calls"]
+    ctx.paged_decode(pool, desc, d_q, d_out, scale)
+    torch.cuda.synchronize()
+    assert ctx.metrics()["stream_decode_calls"] == before
+    assert ctx.device_errors() == 0, ctx.last_error()
+    ref = oracle_decode(pool, batch, fmt, Hq, Hkv, 0, q, scale)
+    assert_parity(from_dev_bf16(d_out), ref, what="unaligned rows")
+
+
 def identity_batch(lens, block_tokens=BT):
     lens = np.asarray(lens, dtype=np.int32)
     nblk = (lens + block_tokens - 1) // block_tokens

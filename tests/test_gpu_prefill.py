@@ -135,6 +135,20 @@ def test_prefill_rejects_quantized_pool(ctx):
     assert e.value.status == llm_hip.ERR_UNSUPPORTED
 
 
+def test_prefill_rejects_unaligned_rows(ctx):
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 8, D, 4)
+    z = torch.zeros(2, dtype=torch.int32, device="cuda")
+    desc = ctx.prefill_desc(z, z[:1], z.view(1, 2), 16, 1, 0, total_q_rows=1)
+    buf = torch.zeros(16 * D + 1, dtype=torch.int16, device="cuda")
+    good = torch.zeros(16 * D, dtype=torch.int16, device="cuda")
+    for q, out in ((buf[1:], good), (good, buf[1:])):
+        with pytest.raises(llm_hip.LlhError) as e:
+            ctx.paged_prefill(pool, desc, q, out, 0.1)
+        assert e.value.status == llm_hip.ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("W", [0, 300])
 def test_prefill_two_heads_per_workgroup_match_one(ctx, W, monkeypatch):
     """Two query heads sharing a workgroup's K/V tiles give the same bits as one head
