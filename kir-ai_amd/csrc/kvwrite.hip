@@ -70,6 +70,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Max over the 16 lanes of a DPP row (lanes 16g .. 16g+15), in every lane of
+// the row: quad butterflies (quad_perm [1,0,3,2] and [2,3,0,1]), then the row
+// rotated by 4 and by 8 lanes.  No LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float row_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, row_dpp<0xB1>(v));
+  v = fmaxf(v, row_dpp<0x4E>(v));
+  v = fmaxf(v, row_dpp<0x124>(v));
+  v = fmaxf(v, row_dpp<0x128>(v));
+  return v;
+}
+
 // Whole 16-token blocks of head_dim 128, bf16 or int8 pools: one workgroup of
 // 256 lanes per (block, head).  Lane (t = lane / 16, c = lane % 16) loads the
 // 16 B of token t at dims 8c .. 8c+7 of K and of V (coalesced), writes K rows
@@ -122,8 +137,7 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
       x[2 * j + 1] = bf16_to_f32((uint16_t)(u[j] >> 16));
       mx = fmaxf(mx, fmaxf(fabsf(x[2 * j]), fabsf(x[2 * j + 1])));
     }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // the token's 16 lanes
+    mx = row16_max(mx);  // the token's 16 lanes
     const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
     const float sc = (float)s16;
     uint32_t q[2] = {0u, 0u};
