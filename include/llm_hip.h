@@ -12,12 +12,23 @@
  *   - Every function returns an int status (llh_status); none aborts.
  *   - Pointers named `d_*` are device pointers; `h_*` are host pointers.
  *   - Batched entry points are asynchronous on the given stream (hipStream_t
- *     passed as void*, NULL = the null stream) and allocate nothing once the
- *     context's workspace is large enough (llh_ctx_reserve_workspace).
+ *     passed as void*, NULL = the null stream).  Each stream gets its own
+ *     device workspace inside the context (split partials, merge descriptors,
+ *     projection staging), allocated by the stream's first call and grown when
+ *     a call needs more; a stream whose workspace is large enough allocates
+ *     nothing (llh_ctx_reserve_stream_workspace sizes it ahead of time).
  *   - Trait-mirror entry points (llh_layer_cache_*, llh_full_attention_*,
  *     llh_append_kv_cache_*) are synchronous, like the reference's awaited
- *     command buffers (crates/llm-metal/src/device/primitives.rs:1325-1338).
- *   - A context is safe to use from several threads on distinct streams.
+ *     command buffers (crates/llm-metal/src/device/primitives.rs:1325-1338):
+ *     each layer cache owns a stream and waits for that stream only.
+ *   - Threading (the reference shares one backend process-wide and calls its
+ *     &self methods concurrently, crates/llm-native-runtime/src/native_matvec.rs:2787-2819):
+ *     a context may be used from several threads at once.  Batched calls on
+ *     distinct streams never share device scratch memory; calls on one stream
+ *     from several threads are serialised by that stream's workspace lock.
+ *     Layer caches and block pools lock themselves; the caches and clones that
+ *     share device blocks are serialised on those blocks.  Pools and
+ *     descriptors passed to concurrent calls must not be written meanwhile.
  */
 #ifndef LLM_HIP_H
 #define LLM_HIP_H
@@ -29,7 +40,7 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 1
+#define LLH_ABI_VERSION 2
 
 /* Status codes.  Mirrors MathError / KvCacheError
  * (crates/llm-backend/src/core/math.rs:10-15, crates/llm-kv-cache/src/lib.rs). */
@@ -68,11 +79,35 @@ typedef struct llh_layer_cache llh_layer_cache;
  * system_default (crates/llm-native-runtime/src/native_matvec.rs:2823-2832). */
 int llh_ctx_create(int device, llh_ctx **out);
 int llh_ctx_destroy(llh_ctx *ctx);
-/* Message of the last error on this context (like MathError's String); never NULL. */
+/* Message of the last error on this context (like MathError's String); never
+ * NULL.  The returned string is the calling thread's copy: it stays valid
+ * until this thread's next llh_ctx_last_error call. */
 const char *llh_ctx_last_error(const llh_ctx *ctx);
-/* Grows the device workspace used by split-K partials and counters so that
- * later batched calls of at most this size allocate nothing. */
+/* Sets the minimum workspace size of every stream of this context (existing
+ * ones grow now; a new stream's first call allocates at least this much). */
 int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes);
+/* Allocates (or grows) the workspace of one stream now, so that its batched
+ * calls of at most this size allocate nothing. */
+int llh_ctx_reserve_stream_workspace(llh_ctx *ctx, void *stream, size_t bytes);
+/* Frees one stream's workspace (after waiting for the device).  Call it before
+ * destroying a stream that made batched calls on this context. */
+int llh_ctx_release_stream(llh_ctx *ctx, void *stream);
+
+/* Tuning options.  Their initial values come from the environment at
+ * llh_ctx_create (the names in parentheses; unset = 0 = automatic) and are
+ * never read from it again. */
+typedef enum llh_option {
+  LLH_OPT_DECODE_KERNEL = 0,         /* (LLH_DECODE_KERNEL: "split" = 1, "stream" = 2) 0 = by step size */
+  LLH_OPT_DECODE_SPLIT_BLOCKS = 1,   /* (LLH_DECODE_SPLIT_BLOCKS) blocks per split-K split, 0 = planned */
+  LLH_OPT_DECODE_STREAM_WGS = 2,     /* (LLH_DECODE_STREAM_WGS) stream-kernel workgroups, 0 = 2 per CU */
+  LLH_OPT_FORCE_GENERIC = 3,         /* (LLH_FORCE_GENERIC) 1 = reference-order decode for every shape */
+  LLH_OPT_PREFILL_HEADS_PER_WG = 4,  /* (LLH_PREFILL_HEADS_PER_WG) 1 = one query head per prefill workgroup */
+  LLH_OPT_TRAIT_REFERENCE_ORDER = 5, /* (LLH_TRAIT_REFERENCE_ORDER) trait-mirror attention: 0 = the tuned
+                                        kernels where the shape allows, 1 = the reference-order kernel always */
+  LLH_OPT_COUNT = 6
+} llh_option;
+int llh_ctx_set_option(llh_ctx *ctx, int32_t option, int32_t value);
+int llh_ctx_get_option(const llh_ctx *ctx, int32_t option, int32_t *value);
 /* Workspace bytes a llh_paged_decode call with these bounds needs. */
 size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len);
 /* Fallback/attempt counters, as MetalBackendMetrics' attention counters
@@ -85,12 +120,15 @@ typedef struct llh_metrics {
   uint64_t device_errors;
   uint64_t shape_errors;
   uint64_t stream_decode_calls; /* decode calls that ran the persistent stream kernel */
+  uint64_t trait_tuned_calls;   /* trait-mirror attention calls served by the tuned decode kernels */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Waits for the device, then reads (and optionally clears) the sticky error
  * flags the batched kernels raise instead of faulting: 1 = a block table entry
  * outside the pool, 2 = a sequence longer than the call's max_seq_len allows,
- * 4 = a non-finite score. */
+ * 4 = a non-finite score, 8 = a sequence's attended span needs more blocks
+ * than its block-table row holds (the row is read modulo its length, so the
+ * span would alias its own blocks).  The flags are shared by every stream. */
 int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset);
 /* Kernel timing for measurement: while enabled, each llh_paged_decode /
  * llh_paged_prefill call records a pair of HIP events on its stream around its

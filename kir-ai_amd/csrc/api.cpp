@@ -41,6 +41,20 @@ int env_int(const char *name, int dflt) {
   return std::atoi(v);
 }
 
+// Initial option values, read once when a context is created.
+void read_env_options(llh_ctx *ctx) {
+  const char *k = std::getenv("LLH_DECODE_KERNEL");
+  int kernel = 0;
+  if (k && std::strcmp(k, "split") == 0) kernel = 1;
+  if (k && std::strcmp(k, "stream") == 0) kernel = 2;
+  ctx->options[LLH_OPT_DECODE_KERNEL] = kernel;
+  ctx->options[LLH_OPT_DECODE_SPLIT_BLOCKS] = env_int("LLH_DECODE_SPLIT_BLOCKS", 0);
+  ctx->options[LLH_OPT_DECODE_STREAM_WGS] = env_int("LLH_DECODE_STREAM_WGS", 0);
+  ctx->options[LLH_OPT_FORCE_GENERIC] = env_int("LLH_FORCE_GENERIC", 0);
+  ctx->options[LLH_OPT_PREFILL_HEADS_PER_WG] = env_int("LLH_PREFILL_HEADS_PER_WG", 0);
+  ctx->options[LLH_OPT_TRAIT_REFERENCE_ORDER] = env_int("LLH_TRAIT_REFERENCE_ORDER", 0);
+}
+
 // Split-K sizing for the tuned decode kernel.  `est_blocks` bounds the blocks
 // any one sequence attends (it sizes the grid and the partial buffer).  The
 // split size is a power of two in [4, 256], measured on MI355X:
@@ -62,11 +76,12 @@ struct SplitPlan {
   int est_blocks;
 };
 
-SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, int total_tokens_hint, int format) {
+SplitPlan plan_splits(const llh_ctx *ctx, int num_seqs, int kv_heads, int max_seq_len, int window,
+                      int total_tokens_hint, int format) {
   int span = max_seq_len;
   if (window > 0) span = std::min(span, window);
   const int est_blocks = (span + kFastBlockTokens - 1) / kFastBlockTokens + 1;
-  int split = env_int("LLH_DECODE_SPLIT_BLOCKS", 0);
+  int split = ctx->opt(LLH_OPT_DECODE_SPLIT_BLOCKS);
   if (split <= 0) {
     long long blocks = (long long)num_seqs * est_blocks;
     if (total_tokens_hint > 0) blocks = (long long)total_tokens_hint / kFastBlockTokens + num_seqs;
@@ -102,22 +117,22 @@ SplitPlan plan_splits(int num_seqs, int kv_heads, int max_seq_len, int window, i
 // run in rounds, 2-4% slower).  It is chosen when the step has at least
 // kStreamMinUnitsPerWave units (block x kv head) per wavefront and its 32-bit
 // partition arithmetic (units * wavefronts < 2^31) is exact; smaller steps
-// (C1, C4 decode) use split-K.  LLH_DECODE_KERNEL = "split" | "stream"
-// overrides the choice, LLH_DECODE_STREAM_WGS the grid.
+// (C1, C4 decode) use split-K.  LLH_OPT_DECODE_KERNEL overrides the choice,
+// LLH_OPT_DECODE_STREAM_WGS the grid.
 constexpr int kStreamWgsPerCu = 2;
 constexpr int kStreamMaxWgs = 1024;
 constexpr int kStreamMinUnitsPerWave = 8;
 
 int stream_grid(const llh_ctx *ctx) {
-  const int wgs = env_int("LLH_DECODE_STREAM_WGS", 0);
+  const int wgs = ctx->opt(LLH_OPT_DECODE_STREAM_WGS);
   return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : kStreamWgsPerCu * ctx->cus));
 }
 
 // Returns the stream grid (workgroups) for this step, or 0 for split-K.
 int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int est_blocks, int total_tokens_hint) {
-  const char *force = std::getenv("LLH_DECODE_KERNEL");
-  const bool want_split = force && std::strcmp(force, "split") == 0;
-  const bool want_stream = force && std::strcmp(force, "stream") == 0;
+  const int force = ctx->opt(LLH_OPT_DECODE_KERNEL);
+  const bool want_split = force == 1;
+  const bool want_stream = force == 2;
   if (want_split) return 0;
   const int wgs = stream_grid(ctx);
   const long long waves = 4LL * wgs;
@@ -145,13 +160,15 @@ int llh_ctx_create(int device, llh_ctx **out) {
   if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return LLH_ERR_DEVICE;
   auto *ctx = new llh_ctx();
   ctx->device = device;
+  // (hipMemset is asynchronous to the host: wait for it before any stream can use the flags)
   if (hipSetDevice(device) != hipSuccess || hipMalloc(&ctx->d_err, sizeof(int32_t)) != hipSuccess ||
-      hipMemset(ctx->d_err, 0, sizeof(int32_t)) != hipSuccess ||
+      hipMemset(ctx->d_err, 0, sizeof(int32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
       hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
     delete ctx;
     return LLH_ERR_DEVICE;
   }
   ctx->cus = std::max(1, ctx->cus);
+  read_env_options(ctx);
   *out = ctx;
   return LLH_OK;
 }
@@ -166,7 +183,8 @@ int llh_ctx_destroy(llh_ctx *ctx) {
       (void)hipEventDestroy(ev.second);
     }
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
-  if (ctx->ws) (void)hipFree(ctx->ws);
+  for (auto &w : ctx->workspaces)
+    if (w->ptr) (void)hipFree(w->ptr);
   if (ctx->d_err) (void)hipFree(ctx->d_err);
   delete ctx;
   return LLH_OK;
@@ -174,12 +192,72 @@ int llh_ctx_destroy(llh_ctx *ctx) {
 
 const char *llh_ctx_last_error(const llh_ctx *ctx) {
   if (!ctx) return "null context";
-  return ctx->last_error.c_str();
+  // a copy per thread: another thread's failure may replace ctx->last_error at any time
+  static thread_local std::string copy;
+  auto *c = const_cast<llh_ctx *>(ctx);
+  std::lock_guard<std::mutex> g(c->err_mu);
+  copy = c->last_error;
+  return copy.c_str();
 }
 
 int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes) {
   if (!ctx) return LLH_ERR_NULL;
-  return ctx->ensure_ws(kCounterBytes + bytes);
+  std::vector<std::shared_ptr<StreamWorkspace>> slots;
+  {
+    std::lock_guard<std::mutex> g(ctx->ws_mu);
+    ctx->ws_min_bytes = std::max(ctx->ws_min_bytes, kCounterBytes + bytes);
+    slots = ctx->workspaces;
+  }
+  for (auto &w : slots) {
+    std::lock_guard<std::mutex> g(w->mu);
+    const int st = ctx->grow_locked(*w, 0);
+    if (st != LLH_OK) return st;
+  }
+  return LLH_OK;
+}
+
+int llh_ctx_reserve_stream_workspace(llh_ctx *ctx, void *stream, size_t bytes) {
+  if (!ctx) return LLH_ERR_NULL;
+  WsLease lease;
+  return lease.acquire(ctx, static_cast<hipStream_t>(stream), kCounterBytes + bytes);
+}
+
+int llh_ctx_release_stream(llh_ctx *ctx, void *stream) {
+  if (!ctx) return LLH_ERR_NULL;
+  std::shared_ptr<StreamWorkspace> w;
+  {
+    std::lock_guard<std::mutex> g(ctx->ws_mu);
+    auto it = std::find_if(ctx->workspaces.begin(), ctx->workspaces.end(),
+                           [&](const std::shared_ptr<StreamWorkspace> &x) { return x->stream == stream; });
+    if (it == ctx->workspaces.end()) return LLH_OK;
+    w = *it;
+    ctx->workspaces.erase(it);
+  }
+  std::lock_guard<std::mutex> g(w->mu);  // waits for a call still holding it
+  if (w->ptr) {
+    // the stream may already be gone: wait for the whole device before freeing
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return ctx->hip_fail(e, "release stream workspace");
+    (void)hipFree(w->ptr);
+    w->ptr = nullptr;
+    w->bytes = 0;
+  }
+  return LLH_OK;
+}
+
+int llh_ctx_set_option(llh_ctx *ctx, int32_t option, int32_t value) {
+  if (!ctx) return LLH_ERR_NULL;
+  if (option < 0 || option >= LLH_OPT_COUNT) return ctx->fail(LLH_ERR_INVALID_SHAPE, "unknown option");
+  ctx->options[option].store(value);
+  return LLH_OK;
+}
+
+int llh_ctx_get_option(const llh_ctx *ctx, int32_t option, int32_t *value) {
+  if (!ctx || !value) return LLH_ERR_NULL;
+  if (option < 0 || option >= LLH_OPT_COUNT) return LLH_ERR_INVALID_SHAPE;
+  *value = ctx->opt(option);
+  return LLH_OK;
 }
 
 size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len) {
@@ -205,6 +283,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->device_errors = ctx->device_errors.load();
   out->shape_errors = ctx->shape_errors.load();
   out->stream_decode_calls = ctx->stream_decode_calls.load();
+  out->trait_tuned_calls = ctx->trait_tuned_calls.load();
   return LLH_OK;
 }
 
@@ -214,6 +293,7 @@ int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset) {
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e == hipSuccess) e = hipMemcpy(flags, ctx->d_err, sizeof(int32_t), hipMemcpyDeviceToHost);
   if (e == hipSuccess && reset) e = hipMemset(ctx->d_err, 0, sizeof(int32_t));
+  if (e == hipSuccess && reset) e = hipDeviceSynchronize();  // the reset lands before any later kernel
   if (e != hipSuccess) return ctx->hip_fail(e, "device error flags");
   return LLH_OK;
 }
@@ -274,6 +354,9 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
   if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
   if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->ks, 0, pool->s_bytes);
   if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->vs, 0, pool->s_bytes);
+  // null-stream memsets are asynchronous to the host and unordered with non-blocking
+  // streams: the pool is ready for any stream only once they have completed
+  if (e == hipSuccess && pool->s_bytes) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     llh_kv_pool_destroy(pool);
     return ctx->hip_fail(e, "hipMalloc(kv pool)");
@@ -402,17 +485,32 @@ static int check_desc_common(llh_ctx *ctx, const llh_kv_pool *pool, int32_t num_
 
 }  // extern "C"
 
+// The kernels read block-table rows modulo their length (a ring of blocks serves
+// a sliding window), so two attended positions alias one slot when a sequence
+// attends more tokens than its row holds.  Rejects a call whose bound allows it.
+static int check_span(llh_ctx *ctx, const llh_kv_pool *pool, int32_t max_seq_len, int32_t window,
+                      int32_t max_blocks) {
+  const int64_t span = window > 0 ? std::min<int64_t>(window, max_seq_len) : max_seq_len;
+  if (span > (int64_t)max_blocks * pool->view.block_tokens)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE,
+                     "attended span exceeds the block-table row (max_blocks_per_seq * block_tokens)");
+  return LLH_OK;
+}
+
 // One decode step.  With d_out == nullptr the bf16 output goes to a buffer of
-// `extra_bytes` placed after the call's own workspace regions (returned in
-// *extra_ptr), so a following kernel on the stream can consume it without any
-// allocation.
+// `extra_bytes` placed after the call's own regions of the stream's workspace
+// (returned in *extra_ptr), so a following kernel on the stream can consume it
+// without any allocation; the caller keeps `lease` through that launch.
 static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
-                             void *d_out, float score_scale, void *stream, size_t extra_bytes, void **extra_ptr) {
+                             void *d_out, float score_scale, void *stream, size_t extra_bytes, void **extra_ptr,
+                             WsLease &lease) {
   if (!ctx || !pool || !desc) return LLH_ERR_NULL;
   int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
   if (st != LLH_OK) return st;
   if (desc->num_seqs == 0) return LLH_OK;
   if (desc->max_seq_len < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "max_seq_len must be >= 0");
+  st = check_span(ctx, pool, desc->max_seq_len, desc->window, desc->max_blocks_per_seq);
+  if (st != LLH_OK) return st;
   if (!d_q || (!d_out && !extra_ptr) || !desc->d_seq_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
@@ -424,12 +522,12 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
                             (reinterpret_cast<uintptr_t>(d_out) & 15) == 0;
   const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens && rows_aligned &&
                     (group == 1 || group == 2 || group == 4 || group == 8) &&
-                    (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !env_int("LLH_FORCE_GENERIC", 0);
+                    (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ctx->decode_calls++;
   if (fast) {
-    const SplitPlan plan =
-        plan_splits(desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window, desc->total_tokens_hint, pv.format);
+    const SplitPlan plan = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
+                                       desc->total_tokens_hint, pv.format);
     const int stream_wgs =
         plan_stream(ctx, pv.format, desc->num_seqs, pv.kv_heads, plan.est_blocks, desc->total_tokens_hint);
     if (!stream_wgs && plan.max_splits > kMaxDecodeSplits)
@@ -441,9 +539,9 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     const size_t o_off = ml_off + align_up(rows * sizeof(float2));
     const size_t desc_off = align_up(o_off + rows * kFastHeadDim * sizeof(float));
     const size_t need = align_up(desc_off + (stream_wgs ? (size_t)desc->num_seqs * pv.kv_heads * 2 * sizeof(int32_t) : 0));
-    st = ctx->ensure_ws(need + extra_bytes);
+    st = lease.acquire(ctx, s, need + extra_bytes);
     if (st != LLH_OK) return st;
-    char *ws = static_cast<char *>(ctx->ws);
+    char *ws = lease.base();
     if (extra_ptr) *extra_ptr = ws + need;
     if (!d_out) d_out = ws + need;
     DecodeArgs a{};
@@ -454,7 +552,6 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     a.tables = desc->d_block_tables;
     a.ws_o = reinterpret_cast<float *>(ws + o_off);
     a.ws_ml = reinterpret_cast<float2 *>(ws + ml_off);
-    a.counters = reinterpret_cast<int32_t *>(ws);
     a.err = ctx->d_err;
     a.num_seqs = desc->num_seqs;
     a.q_heads = desc->num_q_heads;
@@ -462,7 +559,6 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     a.window = desc->window;
     a.split_blocks = plan.split_blocks;
     a.max_splits = plan.max_splits;
-    a.fused_merge = env_int("LLH_DECODE_FUSED_MERGE", 0) ? 1 : 0;
     a.stream_wgs = stream_wgs;
     a.max_seq_len = desc->max_seq_len;
     a.seg_desc = stream_wgs ? reinterpret_cast<int32_t *>(ws + desc_off) : nullptr;
@@ -487,10 +583,11 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   const int stride = std::max(1, span);
   const size_t off = kCounterBytes;
   const size_t need = align_up(off + (size_t)desc->num_seqs * desc->num_q_heads * stride * sizeof(float));
-  st = ctx->ensure_ws(need + extra_bytes);
+  st = lease.acquire(ctx, s, need + extra_bytes);
   if (st != LLH_OK) return st;
-  if (extra_ptr) *extra_ptr = static_cast<char *>(ctx->ws) + need;
-  if (!d_out) d_out = static_cast<char *>(ctx->ws) + need;
+  char *ws = lease.base();
+  if (extra_ptr) *extra_ptr = ws + need;
+  if (!d_out) d_out = ws + need;
   GenericDecodeArgs g{};
   g.pool = pv;
   g.q = d_q;
@@ -498,7 +595,7 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   g.seq_lens = desc->d_seq_lens;
   g.starts = nullptr;
   g.tables = desc->d_block_tables;
-  g.scores = reinterpret_cast<float *>(static_cast<char *>(ctx->ws) + off);
+  g.scores = reinterpret_cast<float *>(ws + off);
   g.err = ctx->d_err;
   g.num_seqs = desc->num_seqs;
   g.q_heads = desc->num_q_heads;
@@ -524,13 +621,49 @@ static int check_projection(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t
   return LLH_OK;
 }
 
+// One decode step whose bf16 attention output stays in the stream's workspace,
+// then out[b] = W_o attn[b] on the same stream (both launches under one lease).
+static int decode_projection_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
+                                  const void *d_q, const void *d_w_o, int32_t rows, float *d_out, float score_scale,
+                                  void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (desc->num_seqs <= 0) return desc->num_seqs == 0 ? LLH_OK : ctx->fail(LLH_ERR_INVALID_SHAPE, "num_seqs < 0");
+  const int32_t cols = desc->num_q_heads * pool->view.head_dim;
+  int st = check_projection(ctx, d_w_o, rows, cols, d_out);
+  if (st != LLH_OK) return st;
+  const size_t attn_bytes = align_up((size_t)desc->num_seqs * cols * sizeof(uint16_t));
+  const int ksplit = matvec_ksplit(rows, cols, desc->num_seqs, ctx->cus);
+  const size_t partial_bytes = ksplit > 1 ? (size_t)ksplit * desc->num_seqs * rows * sizeof(float) : 0;
+  void *attn = nullptr;  // the attention output, then the projection's partial tiles
+  WsLease lease;         // held through the projection launch
+  st = paged_decode_impl(ctx, pool, desc, d_q, nullptr, score_scale, stream, attn_bytes + partial_bytes, &attn,
+                         lease);
+  if (st != LLH_OK) return st;
+  MatvecArgs a{};
+  a.w = static_cast<const uint16_t *>(d_w_o);
+  a.x = attn;
+  a.out = d_out;
+  a.rows = rows;
+  a.cols = cols;
+  a.n = desc->num_seqs;
+  a.ldx = cols;
+  a.ldo = rows;
+  a.x_f32 = 0;
+  a.ksplit = ksplit;
+  a.partial = ksplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(attn) + attn_bytes) : nullptr;
+  hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
+  return LLH_OK;
+}
+
 extern "C" {
 
 int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q, void *d_out,
                      float score_scale, void *stream) {
   if (!ctx || !pool || !desc) return LLH_ERR_NULL;
   if (!d_out && desc->num_seqs > 0) return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
-  return paged_decode_impl(ctx, pool, desc, d_q, d_out, score_scale, stream, 0, nullptr);
+  WsLease lease;
+  return paged_decode_impl(ctx, pool, desc, d_q, d_out, score_scale, stream, 0, nullptr, lease);
 }
 
 int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, const void *d_x, int32_t x_f32,
@@ -553,10 +686,11 @@ int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t col
   a.ldo = rows;
   a.x_f32 = x_f32 ? 1 : 0;
   a.ksplit = matvec_ksplit(rows, cols, n, ctx->cus);
-  if (a.ksplit > 1) {  // partial tiles after the decode counters at the front of the workspace
-    st = ctx->ensure_ws(kCounterBytes + (size_t)a.ksplit * n * rows * sizeof(float));
+  WsLease lease;
+  if (a.ksplit > 1) {  // partial tiles after the counters at the front of the stream's workspace
+    st = lease.acquire(ctx, static_cast<hipStream_t>(stream), kCounterBytes + (size_t)a.ksplit * n * rows * sizeof(float));
     if (st != LLH_OK) return st;
-    a.partial = reinterpret_cast<float *>(static_cast<char *>(ctx->ws) + kCounterBytes);
+    a.partial = reinterpret_cast<float *>(lease.base() + kCounterBytes);
   }
   hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
@@ -566,32 +700,7 @@ int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t col
 int llh_paged_decode_output_projection(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
                                        const void *d_q, const void *d_w_o, int32_t rows, float *d_out,
                                        float score_scale, void *stream) {
-  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
-  if (desc->num_seqs <= 0) return desc->num_seqs == 0 ? LLH_OK : ctx->fail(LLH_ERR_INVALID_SHAPE, "num_seqs < 0");
-  const int32_t cols = desc->num_q_heads * pool->view.head_dim;
-  int st = check_projection(ctx, d_w_o, rows, cols, d_out);
-  if (st != LLH_OK) return st;
-  const size_t attn_bytes = align_up((size_t)desc->num_seqs * cols * sizeof(uint16_t));
-  const int ksplit = matvec_ksplit(rows, cols, desc->num_seqs, ctx->cus);
-  const size_t partial_bytes = ksplit > 1 ? (size_t)ksplit * desc->num_seqs * rows * sizeof(float) : 0;
-  void *attn = nullptr;  // the attention output, then the projection's partial tiles
-  st = paged_decode_impl(ctx, pool, desc, d_q, nullptr, score_scale, stream, attn_bytes + partial_bytes, &attn);
-  if (st != LLH_OK) return st;
-  MatvecArgs a{};
-  a.w = static_cast<const uint16_t *>(d_w_o);
-  a.x = attn;
-  a.out = d_out;
-  a.rows = rows;
-  a.cols = cols;
-  a.n = desc->num_seqs;
-  a.ldx = cols;
-  a.ldo = rows;
-  a.x_f32 = 0;
-  a.ksplit = ksplit;
-  a.partial = ksplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(attn) + attn_bytes) : nullptr;
-  hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
-  return LLH_OK;
+  return decode_projection_impl(ctx, pool, desc, d_q, d_w_o, rows, d_out, score_scale, stream);
 }
 
 int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
@@ -630,7 +739,7 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   auto ev = ctx->timing_begin(static_cast<hipStream_t>(stream));
   // two query heads of a kv head per workgroup share its K/V tile stream when the group is even
   const int group = desc->num_q_heads / pv.kv_heads;
-  const int hpw_env = env_int("LLH_PREFILL_HEADS_PER_WG", 0);
+  const int hpw_env = ctx->opt(LLH_OPT_PREFILL_HEADS_PER_WG);
   const int variant = (hpw_env == 1 || group % 2 != 0) ? kPrefillOneHead : kPrefillTwoHeads;
   hipError_t e = launch_prefill(a, variant, static_cast<hipStream_t>(stream));
   ctx->timing_end(1, ev, static_cast<hipStream_t>(stream));
@@ -681,6 +790,9 @@ constexpr int kRingBlockTokens = 16;
 
 // Device blocks shared by a cache and its clones, with reference counts
 // (the Arc<CacheBlockStorage> sharing of crates/llm-kv-cache/src/block.rs:124-160).
+// `mu` is held by every trait call on any cache of the store from its first
+// read of the store through its final stream wait, so a growth (which frees
+// the old buffers) or a copy never overlaps another cache's kernels.
 struct BlockStore {
   llh_ctx *ctx = nullptr;
   int32_t format = 0;
@@ -701,6 +813,7 @@ struct BlockStore {
   PoolView view() const {
     return PoolView{format, kRingBlockTokens, kv_heads, head_dim, capacity, k, v, ks, vs};
   }
+  // Grows the store; callers hold `mu` and no kernel on the store is in flight.
   hipError_t allocate(int64_t cap) {
     kblock = (size_t)kv_heads * kRingBlockTokens * head_dim * elem_bytes(format);
     sblock = scale_bytes_per_block(format, kv_heads, kRingBlockTokens);
@@ -719,6 +832,10 @@ struct BlockStore {
       if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, sblock * capacity, hipMemcpyDeviceToDevice);
       if (e == hipSuccess && sblock) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
     }
+    // the memsets and device-to-device copies above run on the null stream,
+    // asynchronously to the host: they must land before the caches' own
+    // (non-blocking) streams touch the new buffers, and before the old ones go
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
       for (void *p : {nk, nv, nks, nvs})
         if (p) (void)hipFree(p);
@@ -749,36 +866,67 @@ struct BlockStore {
   void release(int32_t idx) {
     if (--refs[idx] == 0) free_list.push_back(idx);
   }
-  hipError_t copy_block(int32_t src, int32_t dst) {
-    hipError_t e = hipMemcpy((char *)k + kblock * dst, (char *)k + kblock * src, kblock, hipMemcpyDeviceToDevice);
+  hipError_t copy_block(int32_t src, int32_t dst, hipStream_t s) {
+    hipError_t e = hipMemcpyAsync((char *)k + kblock * dst, (char *)k + kblock * src, kblock,
+                                  hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess)
-      e = hipMemcpy((char *)v + kblock * dst, (char *)v + kblock * src, kblock, hipMemcpyDeviceToDevice);
+      e = hipMemcpyAsync((char *)v + kblock * dst, (char *)v + kblock * src, kblock, hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess && sblock)
-      e = hipMemcpy((char *)ks + sblock * dst, (char *)ks + sblock * src, sblock, hipMemcpyDeviceToDevice);
+      e = hipMemcpyAsync((char *)ks + sblock * dst, (char *)ks + sblock * src, sblock, hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess && sblock)
-      e = hipMemcpy((char *)vs + sblock * dst, (char *)vs + sblock * src, sblock, hipMemcpyDeviceToDevice);
+      e = hipMemcpyAsync((char *)vs + sblock * dst, (char *)vs + sblock * src, sblock, hipMemcpyDeviceToDevice, s);
     return e;
   }
 };
 
-// Scratch for the synchronous trait calls: small device buffers reused per call.
+// Scratch of the synchronous trait calls: a device buffer and a pinned host
+// staging buffer, reused per call (a call waits for its stream before returning).
 struct TraitScratch {
-  void *buf = nullptr;
-  size_t bytes = 0;
-  hipError_t ensure(size_t n) {
-    if (n <= bytes) return hipSuccess;
-    if (buf) (void)hipFree(buf);
-    buf = nullptr;
-    bytes = 0;
-    const size_t nb = align_up(std::max(n, (size_t)4096));
-    hipError_t e = hipMalloc(&buf, nb);
-    if (e == hipSuccess) bytes = nb;
-    return e;
+  void *dev = nullptr;
+  size_t dev_bytes = 0;
+  void *host = nullptr;
+  size_t host_bytes = 0;
+  hipError_t ensure(size_t dev_n, size_t host_n) {
+    if (dev_n > dev_bytes) {
+      if (dev) (void)hipFree(dev);
+      dev = nullptr;
+      dev_bytes = 0;
+      const size_t nb = align_up(std::max(dev_n, (size_t)4096));
+      hipError_t e = hipMalloc(&dev, nb);
+      if (e != hipSuccess) return e;
+      dev_bytes = nb;
+    }
+    if (host_n > host_bytes) {
+      if (host) (void)hipHostFree(host);
+      host = nullptr;
+      host_bytes = 0;
+      const size_t nb = align_up(std::max(host_n, (size_t)4096));
+      hipError_t e = hipHostMalloc(&host, nb, hipHostMallocDefault);
+      if (e != hipSuccess) return e;
+      host_bytes = nb;
+    }
+    return hipSuccess;
   }
   ~TraitScratch() {
-    if (buf) (void)hipFree(buf);
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
   }
 };
+
+uint16_t host_f32_to_bf16(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float host_bf16_to_f32(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float x;
+  std::memcpy(&x, &u, 4);
+  return x;
+}
 
 }  // namespace
 
@@ -790,12 +938,17 @@ struct llh_layer_cache {
   size_t max_tokens = 0, kv_heads = 0, head_dim = 0;
   int32_t format = 0;
   size_t token_count = 0, tokens_seen = 0, window_start = 0;
-  std::vector<int32_t> table;  // pool index per ring block
-  std::vector<uint64_t> ids;   // BlockId per ring block
+  bool non_finite_rows = false;  // a row with a non-finite value was appended (bf16 caches)
+  std::vector<int32_t> table;    // pool index per ring block
+  std::vector<uint64_t> ids;     // BlockId per ring block
+  hipStream_t stream = nullptr;  // this cache's own stream (default priority)
   TraitScratch scratch;
   std::mutex mu;
 
   size_t vector_len() const { return kv_heads * head_dim; }
+  ~llh_layer_cache() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
 };
 
 
@@ -825,6 +978,7 @@ int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, siz
   c->store->kv_heads = (int32_t)kv_heads;
   c->store->head_dim = (int32_t)head_dim;
   hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = c->store->allocate((int64_t)nb * 2 + 2);
   for (size_t i = 0; e == hipSuccess && i < nb; i++) {
     int32_t idx;
@@ -853,6 +1007,7 @@ int llh_layer_cache_destroy(llh_layer_cache *cache) {
 
 int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out) {
   if (!cache || !out) return LLH_ERR_NULL;
+  *out = nullptr;
   auto *src = const_cast<llh_layer_cache *>(cache);
   std::lock_guard<std::mutex> g0(src->mu);
   auto *c = new llh_layer_cache();
@@ -867,8 +1022,16 @@ int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out) {
   c->token_count = src->token_count;
   c->tokens_seen = src->tokens_seen;
   c->window_start = src->window_start;
+  c->non_finite_rows = src->non_finite_rows;
   c->table = src->table;
   c->ids = src->ids;
+  hipError_t e = hipSetDevice(c->ctx->device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    c->table.clear();
+    delete c;
+    return src->ctx->hip_fail(e, "layer cache stream");
+  }
   {
     std::lock_guard<std::mutex> g(c->store->mu);
     for (int32_t idx : c->table) c->store->refs[idx]++;
@@ -883,12 +1046,15 @@ int llh_layer_cache_clear(llh_layer_cache *cache) {
   cache->token_count = 0;
   cache->tokens_seen = 0;
   cache->window_start = 0;
+  cache->non_finite_rows = false;
   cache->revision += 1;
   return LLH_OK;
 }
 
-int llh_layer_cache_get_state(const llh_layer_cache *cache, llh_layer_cache_state *out) {
-  if (!cache || !out) return LLH_ERR_NULL;
+int llh_layer_cache_get_state(const llh_layer_cache *cache_c, llh_layer_cache_state *out) {
+  if (!cache_c || !out) return LLH_ERR_NULL;
+  auto *cache = const_cast<llh_layer_cache *>(cache_c);
+  std::lock_guard<std::mutex> g(cache->mu);
   out->id = cache->id;
   out->revision = cache->revision;
   out->max_tokens = cache->max_tokens;
@@ -903,8 +1069,10 @@ int llh_layer_cache_get_state(const llh_layer_cache *cache, llh_layer_cache_stat
   return LLH_OK;
 }
 
-int llh_layer_cache_block_ids(const llh_layer_cache *cache, uint64_t *h_out, size_t capacity, size_t *count) {
-  if (!cache || !count) return LLH_ERR_NULL;
+int llh_layer_cache_block_ids(const llh_layer_cache *cache_c, uint64_t *h_out, size_t capacity, size_t *count) {
+  if (!cache_c || !count) return LLH_ERR_NULL;
+  auto *cache = const_cast<llh_layer_cache *>(cache_c);
+  std::lock_guard<std::mutex> g(cache->mu);
   *count = cache->ids.size();
   if (h_out) std::memcpy(h_out, cache->ids.data(), std::min(capacity, cache->ids.size()) * sizeof(uint64_t));
   return capacity >= cache->ids.size() || !h_out ? LLH_OK : LLH_ERR_CAPACITY;
@@ -913,9 +1081,11 @@ int llh_layer_cache_block_ids(const llh_layer_cache *cache, uint64_t *h_out, siz
 // Runs of logical tokens contiguous in one device block, in logical order:
 // the closed form of append_active_block_run / remove_oldest_active_block_token
 // (layer.rs:1097-1162) for 16-token blocks.
-int llh_layer_cache_active_blocks(const llh_layer_cache *cache, llh_block_run *h_out, size_t capacity,
+int llh_layer_cache_active_blocks(const llh_layer_cache *cache_c, llh_block_run *h_out, size_t capacity,
                                   size_t *count) {
-  if (!cache || !count) return LLH_ERR_NULL;
+  if (!cache_c || !count) return LLH_ERR_NULL;
+  auto *cache = const_cast<llh_layer_cache *>(cache_c);
+  std::lock_guard<std::mutex> g(cache->mu);
   std::vector<llh_block_run> runs;
   for (size_t i = 0; i < cache->token_count; i++) {
     const size_t phys = (cache->window_start + i) % cache->max_tokens;
@@ -941,11 +1111,10 @@ static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key
   if (!ctx || !cache || !h_key || !h_value) return LLH_ERR_NULL;
   std::lock_guard<std::mutex> g(cache->mu);
   if (len != cache->vector_len()) return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV row length does not match the cache");
-  if (cache->format == LLH_KV_INT8) {
-    for (size_t i = 0; i < len; i++)
-      if (!std::isfinite(h_key[i]) || !std::isfinite(h_value[i]))
-        return ctx->fail(LLH_ERR_NON_FINITE, "int8 KV cache rows must be finite");
-  }
+  bool finite = true;
+  for (size_t i = 0; i < len && finite; i++) finite = std::isfinite(h_key[i]) && std::isfinite(h_value[i]);
+  if (!finite && cache->format == LLH_KV_INT8)
+    return ctx->fail(LLH_ERR_NON_FINITE, "int8 KV cache rows must be finite");
   const bool full = cache->token_count == cache->max_tokens;
   if (full && !sliding) return ctx->fail(LLH_ERR_CAPACITY, "KV cache capacity exceeded");
   const size_t phys = full ? cache->window_start : cache->token_count;
@@ -953,49 +1122,49 @@ static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key
   const size_t off = phys % kRingBlockTokens;
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
-  {
-    // copy-on-write: a block shared with a clone gets a fresh device block and id
-    BlockStore &bs = *cache->store;
-    std::lock_guard<std::mutex> gs(bs.mu);
-    const int32_t idx = cache->table[bi];
-    if (bs.refs[idx] > 1) {
-      int32_t fresh;
-      e = bs.take(fresh);
-      if (e == hipSuccess) e = bs.copy_block(idx, fresh);
-      if (e != hipSuccess) return ctx->hip_fail(e, "copy-on-write block");
-      bs.release(idx);
-      cache->table[bi] = fresh;
-      cache->ids[bi] = next_block_id();
-    }
-  }
+  BlockStore &bs = *cache->store;
+  std::lock_guard<std::mutex> gs(bs.mu);  // through the stream wait below
   const size_t row_bytes = len * sizeof(float);
-  e = cache->scratch.ensure(2 * row_bytes + 2 * sizeof(int64_t) + kAlign);
+  const size_t k_off = kAlign, v_off = kAlign + align_up(row_bytes);
+  const size_t bytes = v_off + row_bytes;
+  e = cache->scratch.ensure(bytes, bytes);
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
-  char *sb = static_cast<char *>(cache->scratch.buf);
-  int64_t *d_slot = reinterpret_cast<int64_t *>(sb);
-  float *d_k = reinterpret_cast<float *>(sb + kAlign);
-  float *d_v = reinterpret_cast<float *>(sb + kAlign + row_bytes);
+  // copy-on-write: a block shared with a clone gets a fresh device block and id
+  const int32_t idx = cache->table[bi];
+  if (bs.refs[idx] > 1) {
+    int32_t fresh;
+    e = bs.take(fresh);
+    if (e == hipSuccess) e = bs.copy_block(idx, fresh, cache->stream);
+    if (e != hipSuccess) return ctx->hip_fail(e, "copy-on-write block");
+    bs.release(idx);
+    cache->table[bi] = fresh;
+    cache->ids[bi] = next_block_id();
+  }
+  char *hb = static_cast<char *>(cache->scratch.host);
+  char *sb = static_cast<char *>(cache->scratch.dev);
   const int64_t slot = (int64_t)cache->table[bi] * kRingBlockTokens + (int64_t)off;
-  e = hipMemcpy(d_slot, &slot, sizeof(slot), hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(d_k, h_key, row_bytes, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(d_v, h_value, row_bytes, hipMemcpyHostToDevice);
+  std::memcpy(hb, &slot, sizeof(slot));
+  std::memcpy(hb + k_off, h_key, row_bytes);
+  std::memcpy(hb + v_off, h_value, row_bytes);
+  e = hipMemcpyAsync(sb, hb, bytes, hipMemcpyHostToDevice, cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "row upload");
   AppendArgs a{};
-  a.pool = cache->store->view();
-  a.k_dst = cache->store->k;
-  a.v_dst = cache->store->v;
-  a.ks_dst = cache->store->ks;
-  a.vs_dst = cache->store->vs;
-  a.slots = d_slot;
-  a.k = d_k;
-  a.v = d_v;
+  a.pool = bs.view();
+  a.k_dst = bs.k;
+  a.v_dst = bs.v;
+  a.ks_dst = bs.ks;
+  a.vs_dst = bs.vs;
+  a.slots = reinterpret_cast<const int64_t *>(sb);
+  a.k = sb + k_off;
+  a.v = sb + v_off;
   a.n = 1;
   a.src_f32 = 1;
   a.err = ctx->d_err;
-  e = launch_append(a, nullptr);
-  if (e == hipSuccess) e = hipDeviceSynchronize();
+  e = launch_append(a, cache->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "append");
   ctx->append_calls++;
+  if (!finite) cache->non_finite_rows = true;
   if (full) {
     cache->window_start = (cache->window_start + 1) % cache->max_tokens;
   } else {
@@ -1017,6 +1186,87 @@ int llh_append_kv_cache_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h
 }
 
 }  // extern "C"
+
+// The tuned decode kernels serve a trait call when the cache has the tuned
+// shape (head_dim 128, a GQA group of 1, 2, 4 or 8) and its ring is whole
+// blocks (then ring slot p % max_tokens is table[(p / 16) % blocks] at offset
+// p % 16, the batched kernels' own mapping), and nothing non-finite can reach
+// the scores: the reference's softmax_f32 errors on non-finite scores
+// (math.rs:485-489), which only the reference-order kernel reports, so finite
+// q and rows are checked here and a non-finite result is recomputed there.
+static bool trait_tuned_ok(const llh_ctx *ctx, const llh_layer_cache *cache, const float *h_query, size_t qdim,
+                           size_t heads, size_t kv_heads) {
+  if (ctx->opt(LLH_OPT_TRAIT_REFERENCE_ORDER)) return false;
+  const size_t group = heads / kv_heads;
+  if (cache->head_dim != (size_t)kFastHeadDim || cache->max_tokens % kRingBlockTokens != 0 || cache->non_finite_rows)
+    return false;
+  if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+  for (size_t i = 0; i < qdim; i++)
+    if (!std::isfinite(h_query[i])) return false;
+  return true;
+}
+
+// Attention over the first row_count logical rows on the tuned kernels: one
+// decode step of a batch of one (q rounded to bf16, bf16 output widened to f32),
+// through the cache's stream and its stream workspace.  With d_w the attention
+// output is projected on the device (llh_paged_decode_output_projection).
+// Sets *finite = false when the output holds a non-finite value.
+static int cache_mix_tuned(llh_ctx *ctx, llh_layer_cache *cache, const float *h_query, size_t qdim, size_t row_count,
+                           size_t heads, float score_scale, const void *d_w, int32_t w_rows, float *h_output,
+                           size_t out_len, bool *finite) {
+  BlockStore &bs = *cache->store;
+  const size_t nb = cache->table.size();
+  const size_t off_table = kAlign;  // int32 [nb]; header: seq_len
+  const size_t off_q = off_table + align_up(nb * sizeof(int32_t));
+  const size_t off_out = off_q + align_up(qdim * sizeof(uint16_t));
+  const size_t out_bytes = d_w ? out_len * sizeof(float) : qdim * sizeof(uint16_t);
+  const size_t bytes = off_out + out_bytes;
+  hipError_t e = cache->scratch.ensure(bytes, bytes);
+  if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
+  char *hb = static_cast<char *>(cache->scratch.host);
+  char *sb = static_cast<char *>(cache->scratch.dev);
+  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
+  const int32_t len = (int32_t)(abs_start + (int64_t)row_count);
+  std::memcpy(hb, &len, sizeof(len));
+  std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
+  auto *qh = reinterpret_cast<uint16_t *>(hb + off_q);
+  for (size_t i = 0; i < qdim; i++) qh[i] = host_f32_to_bf16(h_query[i]);
+  e = hipMemcpyAsync(sb, hb, off_out, hipMemcpyHostToDevice, cache->stream);
+  if (e != hipSuccess) return ctx->hip_fail(e, "attention upload");
+  llh_kv_pool pool{};
+  pool.ctx = ctx;
+  pool.view = bs.view();
+  llh_decode_desc desc{};
+  desc.num_seqs = 1;
+  desc.num_q_heads = (int32_t)heads;
+  desc.max_blocks_per_seq = (int32_t)nb;
+  desc.max_seq_len = len;
+  desc.window = (int32_t)row_count;  // attends [len - row_count, len): the first row_count logical rows
+  desc.total_tokens_hint = (int32_t)row_count;
+  desc.d_seq_lens = reinterpret_cast<const int32_t *>(sb);
+  desc.d_block_tables = reinterpret_cast<const int32_t *>(sb + off_table);
+  int st;
+  if (d_w) {
+    st = decode_projection_impl(ctx, &pool, &desc, sb + off_q, d_w, w_rows, reinterpret_cast<float *>(sb + off_out),
+                                score_scale, cache->stream);
+  } else {
+    WsLease lease;
+    st = paged_decode_impl(ctx, &pool, &desc, sb + off_q, sb + off_out, score_scale, cache->stream, 0, nullptr, lease);
+  }
+  if (st != LLH_OK) return st;
+  e = hipMemcpyAsync(hb + off_out, sb + off_out, out_bytes, hipMemcpyDeviceToHost, cache->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(cache->stream);
+  if (e != hipSuccess) return ctx->hip_fail(e, "attention");
+  *finite = true;
+  if (d_w) {
+    std::memcpy(h_output, hb + off_out, out_len * sizeof(float));
+  } else {
+    const auto *oh = reinterpret_cast<const uint16_t *>(hb + off_out);
+    for (size_t i = 0; i < qdim; i++) h_output[i] = host_bf16_to_f32(oh[i]);
+  }
+  for (size_t i = 0; i < out_len; i++) *finite = *finite && std::isfinite(h_output[i]);
+  return LLH_OK;
+}
 
 // Attention over the first row_count logical rows of a layer cache, f32 in and
 // out.  With d_w != nullptr the f32 attention output is projected on the
@@ -1046,6 +1296,18 @@ static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const fl
   }
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
+  BlockStore &bs = *cache->store;
+  std::lock_guard<std::mutex> gs(bs.mu);  // through the stream wait
+  if (trait_tuned_ok(ctx, cache, h_query, qdim, num_attention_heads, num_key_value_heads)) {
+    bool finite = false;
+    const int st = cache_mix_tuned(ctx, cache, h_query, qdim, row_count, num_attention_heads, score_scale, d_w, w_rows,
+                                   h_output, out_len, &finite);
+    if (st != LLH_OK || finite) {
+      if (st == LLH_OK) ctx->trait_tuned_calls++;
+      return st;
+    }
+    // a non-finite output: the reference-order kernel reports the reference's error
+  }
   const size_t nb = cache->table.size();
   const size_t off_table = kAlign;                               // int32 [nb]
   const size_t off_q = off_table + align_up(nb * sizeof(int32_t));
@@ -1053,18 +1315,20 @@ static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const fl
   const size_t off_scores = off_out + align_up(qdim * sizeof(float));
   const size_t off_proj = off_scores + align_up(num_attention_heads * row_count * sizeof(float));
   const size_t need = off_proj + (d_w ? (size_t)w_rows * sizeof(float) : 0);
-  e = cache->scratch.ensure(need);
+  e = cache->scratch.ensure(need, need);
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
-  char *sb = static_cast<char *>(cache->scratch.buf);
+  char *hb = static_cast<char *>(cache->scratch.host);
+  char *sb = static_cast<char *>(cache->scratch.dev);
   // header: err flag, start, end
   const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
   const int32_t hdr[4] = {0, (int32_t)abs_start, (int32_t)(abs_start + (int64_t)row_count), 0};
-  e = hipMemcpy(sb, hdr, sizeof(hdr), hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(sb + off_table, cache->table.data(), nb * sizeof(int32_t), hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(sb + off_q, h_query, qdim * sizeof(float), hipMemcpyHostToDevice);
+  std::memcpy(hb, hdr, sizeof(hdr));
+  std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
+  std::memcpy(hb + off_q, h_query, qdim * sizeof(float));
+  e = hipMemcpyAsync(sb, hb, off_out, hipMemcpyHostToDevice, cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "attention upload");
   GenericDecodeArgs a{};
-  a.pool = cache->store->view();
+  a.pool = bs.view();
   a.q = sb + off_q;
   a.out = sb + off_out;
   a.err = reinterpret_cast<int32_t *>(sb);
@@ -1079,7 +1343,7 @@ static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const fl
   a.ring_tokens = (int32_t)cache->max_tokens;
   a.score_stride = (int32_t)row_count;
   a.scale = score_scale;
-  e = launch_decode_generic(a, 1, 1, nullptr);
+  e = launch_decode_generic(a, 1, 1, cache->stream);
   if (e == hipSuccess && d_w) {
     MatvecArgs m{};
     m.w = static_cast<const uint16_t *>(d_w);
@@ -1091,14 +1355,17 @@ static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const fl
     m.ldx = (int32_t)qdim;
     m.ldo = w_rows;
     m.x_f32 = 1;
-    e = launch_matvec_bf16(m, nullptr);
+    e = launch_matvec_bf16(m, cache->stream);
   }
-  if (e == hipSuccess) e = hipDeviceSynchronize();
-  int32_t flags = 0;
-  if (e == hipSuccess) e = hipMemcpy(&flags, sb, sizeof(flags), hipMemcpyDeviceToHost);
+  const size_t res_off = d_w ? off_proj : off_out;
+  if (e == hipSuccess) e = hipMemcpyAsync(hb, sb, sizeof(int32_t), hipMemcpyDeviceToHost, cache->stream);
   if (e == hipSuccess)
-    e = hipMemcpy(h_output, sb + (d_w ? off_proj : off_out), out_len * sizeof(float), hipMemcpyDeviceToHost);
+    e = hipMemcpyAsync(hb + res_off, sb + res_off, out_len * sizeof(float), hipMemcpyDeviceToHost, cache->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "attention");
+  int32_t flags = 0;
+  std::memcpy(&flags, hb, sizeof(flags));
+  std::memcpy(h_output, hb + res_off, out_len * sizeof(float));
   ctx->decode_calls++;
   if (flags & kErrNonFinite) return ctx->fail(LLH_ERR_NON_FINITE, "softmax scores must be finite");
   if (flags & kErrBadBlock) return ctx->fail(LLH_ERR_STALE, "KV cache block table is stale");
@@ -1150,19 +1417,24 @@ int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cac
   if (row_count == 0 || head_len == 0) return LLH_OK;
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return ctx->hip_fail(e, "hipSetDevice");
+  BlockStore &bs = *cache->store;
+  std::lock_guard<std::mutex> gs(bs.mu);  // through the stream wait
   const size_t nb = cache->table.size();
   const size_t off_table = kAlign;
   const size_t off_out = off_table + align_up(nb * sizeof(int32_t));
-  e = cache->scratch.ensure(off_out + row_count * vl * sizeof(float));
+  const size_t out_bytes = row_count * vl * sizeof(float);
+  e = cache->scratch.ensure(off_out + out_bytes, off_out + out_bytes);
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
-  char *sb = static_cast<char *>(cache->scratch.buf);
+  char *hb = static_cast<char *>(cache->scratch.host);
+  char *sb = static_cast<char *>(cache->scratch.dev);
   const int32_t zero = 0;
-  e = hipMemcpy(sb, &zero, sizeof(zero), hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(sb + off_table, cache->table.data(), nb * sizeof(int32_t), hipMemcpyHostToDevice);
+  std::memcpy(hb, &zero, sizeof(zero));
+  std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
+  e = hipMemcpyAsync(sb, hb, off_out, hipMemcpyHostToDevice, cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "upload");
   const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
   GatherArgs a{};
-  a.pool = cache->store->view();
+  a.pool = bs.view();
   a.table = reinterpret_cast<const int32_t *>(sb + off_table);
   a.max_blocks = (int32_t)nb;
   a.lo = (int32_t)abs_start;
@@ -1172,13 +1444,14 @@ int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cac
   a.out = sb + off_out;
   a.out_f32 = 1;
   a.err = reinterpret_cast<int32_t *>(sb);
-  e = launch_gather(a, nullptr);
-  if (e == hipSuccess) e = hipDeviceSynchronize();
-  std::vector<float> rows(row_count * vl);
-  if (e == hipSuccess) e = hipMemcpy(rows.data(), sb + off_out, rows.size() * sizeof(float), hipMemcpyDeviceToHost);
+  e = launch_gather(a, cache->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(hb + off_out, sb + off_out, out_bytes, hipMemcpyDeviceToHost, cache->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "select head rows");
+  const float *rows = reinterpret_cast<const float *>(hb + off_out);
   for (size_t r = 0; r < row_count; r++)
-    std::memcpy(h_output + r * head_len, rows.data() + r * vl + head_start, head_len * sizeof(float));
+    std::memcpy(h_output + r * head_len, rows + r * vl + head_start, head_len * sizeof(float));
   return LLH_OK;
 }
 

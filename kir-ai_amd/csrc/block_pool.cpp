@@ -266,7 +266,10 @@ struct llh_block_pool {
     return e;
   }
 
-  // Device copy of block src's payload (K, V and their scales) into block dst.
+  // Device copy of block src's payload (K, V and their scales) into block dst,
+  // complete on return: null-stream copies are asynchronous to the host and
+  // unordered with non-blocking streams, so the device is drained (which also
+  // orders the copy after any earlier writes of src).
   hipError_t copy_payload(int64_t src, int64_t dst) {
     const PoolView &v = pool->view;
     const size_t kb = (size_t)v.kv_heads * v.block_tokens * v.head_dim * elem_bytes(v.format);
@@ -280,6 +283,7 @@ struct llh_block_pool {
       e = hipMemcpy((char *)pool->ks + sb * dst, (char *)pool->ks + sb * src, sb, hipMemcpyDeviceToDevice);
     if (e == hipSuccess && sb)
       e = hipMemcpy((char *)pool->vs + sb * dst, (char *)pool->vs + sb * src, sb, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     return e;
   }
 };

@@ -18,14 +18,7 @@
 // the current one.  Every K/V byte of the kv head is read once and serves all
 // G = Hq/Hkv query heads.  A single-split sequence writes its output directly;
 // otherwise each split writes (max, sum, unnormalised output) partials that a
-// second launch (decode_merge_kernel) merges by log-sum-exp.  With fused_merge
-// set, the last workgroup of the (sequence, kv head) to arrive merges instead:
-// partials then cross XCDs (each has its own L2) through agent-scope atomic
-// stores and loads, which the compiler makes coherent per access, with no
-// device-scope fence (on gfx950 such a fence writes back and invalidates the
-// whole L2 of the XCD, and those serialise across workgroups).  Measured on
-// MI355X the second launch is faster: the fused variant makes every
-// workgroup wait for its write-through stores before it can retire.
+// second launch (decode_merge_kernel) merges by log-sum-exp.
 // The path is HBM-bound and uses no MFMA.
 //
 // Lane roles inside a wavefront, per 16-token block (K: token rows, V: dim rows):
@@ -274,6 +267,15 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});  // round to nearest even
 }
 
+// x rounded to bf16 (nearest even), as f32: the value pack_bf16 stores for x
+__device__ __forceinline__ float bf16_round(float x) { return bf16_lo(pack_bf16(x, 0.0f)); }
+
+// acc + lo + hi of a packed bf16 pair, exactly (dot product with (1, 1) in f32)
+__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+
 // Two signed int8 codes (bytes b, b+1 of w) as a packed bf16 pair (exact).
 __device__ __forceinline__ uint32_t i8x2_to_bf16(uint32_t w, int b) {
   return pack_bf16((float)(int8_t)(w >> (8 * b)), (float)(int8_t)(w >> (8 * b + 8)));
@@ -308,7 +310,9 @@ __device__ __forceinline__ void v_pairs(const BlockRegs<FMT> &r, const uint32_t 
 // q . k and p . v both run on packed bf16 dot2 with fp32 accumulation: K, V and
 // q are exact in bf16 (int8 and e4m3 codes convert exactly); the softmax
 // weights p (times the value scale for int8/fp8) are rounded to bf16 for the
-// p . v products, the softmax denominator sums them in fp32.
+// p . v products, and the softmax denominator sums exactly those rounded
+// weights (divided by the value scale for int8/fp8), so the output is a
+// weighted mean of the attended values whose weights sum to one.
 template <int G, int FMT>
 __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
                                               int lane, const uint32_t (&qw)[G][kQWords<G, FMT>],
@@ -395,8 +399,10 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     }
     const float mref = (st.m_own == -INFINITY) ? 0.0f : st.m_own;
     const float p = fast_exp2(s_own - mref);
-    st.l_own += p;
     const float wv = p * vs_own;
+    // the normaliser sums the weights p . v really applies to the dequantised value
+    // (code * scale): bf16(p * scale) / scale, the same bf16 rounding as the packs below
+    st.l_own += vs_own != 0.0f ? bf16_round(wv) * __builtin_amdgcn_rcpf(vs_own) : p;
     // every lane of the row gathers the row's 4 tokens' value weights of each head
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
@@ -509,19 +515,34 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
         for (int j = 0; j < 8; j++) st.o[gi][j] *= alpha;
       }
     }
+    // quantized: the normaliser counts weight bf16(p * s) / s per token (see below)
+    float vinv[4];
+    if constexpr (FMT != kBf16) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) vinv[i] = vsc[i] != 0.0f ? __builtin_amdgcn_rcpf(vsc[i]) : 0.0f;
+    }
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
       const float mref = (st.m[gi] == -INFINITY) ? 0.0f : st.m[gi];
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
-      st.l[gi] += (p[0] + p[1]) + (p[2] + p[3]);
       if constexpr (FMT == kBf16) {
         w01[gi] = pack_bf16(p[0], p[1]);
         w23[gi] = pack_bf16(p[2], p[3]);
+        // the normaliser sums exactly the bf16 weights that enter p . v
+        st.l[gi] = dot2_ones(w23[gi], dot2_ones(w01[gi], st.l[gi]));
       } else {
         w01[gi] = pack_bf16(p[0] * vsc[0], p[1] * vsc[1]);
         w23[gi] = pack_bf16(p[2] * vsc[2], p[3] * vsc[3]);
+        // p . v multiplies the codes by bf16(p * s): on the dequantised value
+        // (code * s) that is the weight bf16(p * s) / s, which the normaliser sums
+        // (a token whose scale is 0 has a zero value and keeps its weight p)
+        const float r[4] = {bf16_lo(w01[gi]), bf16_hi(w01[gi]), bf16_lo(w23[gi]), bf16_hi(w23[gi])};
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) lsum += vsc[i] != 0.0f ? r[i] * vinv[i] : p[i];
+        st.l[gi] += lsum;
       }
     }
   }
@@ -585,6 +606,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
   if (n_splits > a.max_splits) {
     if (threadIdx.x == 0 && split == 0) atomicOr(a.err, kErrTooManySplits);
+    return;
+  }
+  if (len - lo > a.max_blocks * BT) {  // the span would alias its own table entries
+    if (threadIdx.x == 0 && split == 0) atomicOr(a.err, kErrSpan);
     return;
   }
   if (split >= max(n_splits, 1)) return;
@@ -682,7 +707,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   __syncthreads();
 
   // ---- merge the four wavefronts; write the output or this split's partial ----
-  const bool fused = a.fused_merge != 0;
   for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
     const int gi = idx / D;
     const int d = idx % D;
@@ -699,71 +723,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
     } else {
       const size_t row = (qrow0 + gi) * a.max_splits + split;
-      if (fused) {
-        // agent-scope atomic stores: coherent across XCDs without any L2 writeback
-        __hip_atomic_store(&a.ws_o[row * D + d], oo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d == 0) {
-          const uint64_t ml = (uint64_t)__float_as_uint(mm) | ((uint64_t)__float_as_uint(ll) << 32);
-          __hip_atomic_store(reinterpret_cast<uint64_t *>(&a.ws_ml[row]), ml, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-        a.ws_o[row * D + d] = oo;
-        if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
-      }
+      a.ws_o[row * D + d] = oo;
+      if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
     }
-  }
-  if (n_splits == 1 || !fused) return;
-
-  // ---- the last workgroup of this (sequence, kv head) to arrive merges the splits ----
-  // Every wave waits until its partial stores have completed, the barrier
-  // collects the waves, then one lane counts the arrival (agent-scope atomic).
-  __builtin_amdgcn_s_waitcnt(0);
-  __shared__ int s_last;
-  __syncthreads();
-  int32_t *counter = &a.counters[(size_t)b * a.pool.kv_heads + kvh];
-  if (tid == 0) s_last = atomicAdd(counter, 1) == n_splits - 1;
-  __syncthreads();
-  if (!s_last) return;
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-    const int gi = idx / D;
-    const int d = idx % D;
-    const size_t row0 = (qrow0 + gi) * a.max_splits;
-    float m_sp[8], l_sp[8], o_sp[8];
-    float mm = -INFINITY, ll = 0.0f, oo = 0.0f;
-    for (int sp0 = 0; sp0 < n_splits; sp0 += 8) {
-      const int cnt = min(8, n_splits - sp0);
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if (i < cnt) {
-          const uint64_t ml = __hip_atomic_load(reinterpret_cast<const uint64_t *>(&a.ws_ml[row0 + sp0 + i]),
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          m_sp[i] = __uint_as_float((uint32_t)ml);
-          l_sp[i] = __uint_as_float((uint32_t)(ml >> 32));
-          o_sp[i] = __hip_atomic_load(&a.ws_o[(row0 + sp0 + i) * D + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          m_sp[i] = -INFINITY;
-          l_sp[i] = 0.0f;
-          o_sp[i] = 0.0f;
-        }
-      }
-      float cm = mm;
-#pragma unroll
-      for (int i = 0; i < 8; i++) cm = fmaxf(cm, m_sp[i]);
-      const float mref = (cm == -INFINITY) ? 0.0f : cm;
-      const float f0 = fast_exp2(mm - mref);
-      ll *= f0;
-      oo *= f0;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float f = fast_exp2(m_sp[i] - mref);
-        ll += l_sp[i] * f;
-        oo += o_sp[i] * f;
-      }
-      mm = cm;
-    }
-    a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
   }
 }
 
@@ -833,25 +795,34 @@ __device__ __forceinline__ int wave_of_unit(int r, int ub, int wb) {
 
 // The sequence whose wavefronts include wavefront w (W in the grid).  Lane l
 // of the first chunk reads sequence l, so batches up to 64 need one load.
+// Attended tokens of a sequence of length len.
+__device__ __forceinline__ int attended_tokens(const DecodeArgs &a, int len) {
+  return a.window > 0 ? min(len, a.window) : len;
+}
+
 // Returns b = -1 when w is spare; sets *units = 0 when nothing is attended and
-// *too_long when a length exceeds the host's max_seq_len bound.
+// *bad_flags to kErrTooManySplits when a length exceeds the host's max_seq_len
+// bound, kErrSpan when a sequence attends more tokens than its table row holds.
 __device__ __forceinline__ SeqShare stream_share(const DecodeArgs &a, int W, int w, int lane, int *units,
-                                                 bool *too_long) {
+                                                 int *bad_flags) {
   const int B = a.num_seqs;
+  const int row_tokens = a.max_blocks * BT;
   int len0 = lane < B ? a.seq_lens[lane] : 0;
   int nb0 = attended_blocks(a, len0);
   int u = wave_sum(nb0), nz = __popcll(__ballot(nb0 > 0));
-  bool bad = __ballot(len0 > a.max_seq_len) != 0;
+  bool too_long = __ballot(len0 > a.max_seq_len) != 0;
+  bool span = __ballot(attended_tokens(a, len0) > row_tokens) != 0;
   for (int cb = 64; cb < B; cb += 64) {
     const int len = cb + lane < B ? a.seq_lens[cb + lane] : 0;
     const int nb = attended_blocks(a, len);
     u += wave_sum(nb);
     nz += __popcll(__ballot(nb > 0));
-    bad |= __ballot(len > a.max_seq_len) != 0;
+    too_long |= __ballot(len > a.max_seq_len) != 0;
+    span |= __ballot(attended_tokens(a, len) > row_tokens) != 0;
   }
-  *too_long = bad;
+  *bad_flags = (too_long ? kErrTooManySplits : 0) | (span ? kErrSpan : 0);
   *units = u * a.pool.kv_heads;
-  if (bad || u == 0) return {-1, 0, 0, 0};
+  if (*bad_flags || u == 0) return {-1, 0, 0, 0};
   const int spare = W - 2 * nz;  // the host sizes W above 2B, so spare > 0
   int cw = 0;
   for (int cb = 0; cb < B; cb += 64) {
@@ -919,10 +890,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   const int W = gridDim.x * 4;
   const int Hkv = a.pool.kv_heads;
   int units;
-  bool too_long;
-  const SeqShare sh = stream_share(a, W, w, lane, &units, &too_long);
-  if (too_long) {
-    if (w == 0 && lane == 0) atomicOr(a.err, kErrTooManySplits);
+  int bad_flags;
+  const SeqShare sh = stream_share(a, W, w, lane, &units, &bad_flags);
+  if (bad_flags) {
+    if (w == 0 && lane == 0) atomicOr(a.err, bad_flags);
     return;
   }
   // empty sequences: zero output (weighted sum of nothing), nothing to merge
@@ -1160,7 +1131,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   const int b = blockIdx.y;
   int len, lo, first_blk, n_blk, n_splits;
   seq_range(a, b, len, lo, first_blk, n_blk, n_splits);
-  if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMergeMaxSplits) return;
+  if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMergeMaxSplits || len - lo > a.max_blocks * BT) return;
   const int d = threadIdx.x;
   const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
   const size_t orow = (size_t)b * a.q_heads + h;
@@ -1278,6 +1249,10 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(const GenericDecode
     if (threadIdx.x == 0) atomicOr(a.err, kErrTooManySplits);
     return;
   }
+  if (a.ring_tokens == 0 && (int64_t)rows > (int64_t)a.max_blocks * a.pool.block_tokens) {
+    if (threadIdx.x == 0) atomicOr(a.err, kErrSpan);  // the span would alias its own table entries
+    return;
+  }
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
   const size_t qoff = ((size_t)b * a.q_heads + h) * D_;
   float *sc = a.scores + ((size_t)b * a.q_heads + h) * a.score_stride;
@@ -1367,7 +1342,7 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, 
   hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (hook) hook(hu, 1, s);
-  if (e != hipSuccess || a.max_splits <= 1 || a.fused_merge) return e;
+  if (e != hipSuccess || a.max_splits <= 1) return e;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(a.q_heads, a.num_seqs), dim3(D), 0, s, a);
   return hipGetLastError();
 }

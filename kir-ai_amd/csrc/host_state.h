@@ -1,5 +1,6 @@
 // Host-side state shared by the C-ABI translation units (api.cpp, block_pool.cpp):
-// the context, the device KV pool, and small helpers.  Not part of the ABI.
+// the context, its per-stream device workspaces, the device KV pool, and small
+// helpers.  Not part of the ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -7,6 +8,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -17,7 +19,7 @@
 
 namespace llh {
 
-constexpr size_t kCounterSlots = 65536;  // (sequence, kv head) arrival counters
+constexpr size_t kCounterSlots = 65536;  // (sequence, kv head) arrival counters at the front of a workspace
 constexpr size_t kCounterBytes = kCounterSlots * sizeof(int32_t);
 constexpr size_t kAlign = 256;
 
@@ -27,18 +29,35 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // crates/llm-kv-cache/src/block_id.rs:11-41).
 uint64_t next_block_id();
 
+// Device scratch of one stream: split partials, merge descriptors, counters and
+// the fused projection's staging.  A call holds `mu` from planning through its
+// last launch, so two threads on one stream never interleave their use of it,
+// and a growth (which frees the old buffer) never happens under another call.
+struct StreamWorkspace {
+  hipStream_t stream = nullptr;
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  std::mutex mu;
+};
+
 }  // namespace llh
 
 struct llh_ctx {
   int device = 0;
   int cus = 256;  // compute units of the device (sizes the persistent decode grid)
-  std::mutex mu;
-  std::string last_error;
-  void *ws = nullptr;
-  size_t ws_bytes = 0;
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
-      shape_errors{0}, stream_decode_calls{0};
+      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0};
+  std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
+
+  // per-stream workspaces; ws_mu guards the list and ws_min_bytes
+  std::mutex ws_mu;
+  std::vector<std::shared_ptr<llh::StreamWorkspace>> workspaces;
+  size_t ws_min_bytes = 0;
+
+  std::mutex err_mu;
+  std::string last_error;
+
   // kernel timing (measurement only)
   std::atomic<int> timing{0};
   std::mutex timing_mu;
@@ -46,6 +65,8 @@ struct llh_ctx {
   std::vector<hipEvent_t> event_pool;
   double timed_ms[2] = {0.0, 0.0};
   int64_t timed_n[2] = {0, 0};
+
+  int32_t opt(int o) const { return options[o].load(std::memory_order_relaxed); }
 
   hipEvent_t take_event() {
     if (!event_pool.empty()) {
@@ -57,7 +78,7 @@ struct llh_ctx {
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
   }
-  // records the start event of `kind` on stream s; returns the pair index or -1
+  // records the start event on stream s; returns the pair (or nulls when timing is off)
   std::pair<hipEvent_t, hipEvent_t> timing_begin(hipStream_t s) {
     if (!timing.load()) return {nullptr, nullptr};
     std::lock_guard<std::mutex> g(timing_mu);
@@ -83,28 +104,62 @@ struct llh_ctx {
   int hip_fail(hipError_t e, const char *what) {
     return fail(LLH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
   }
-  // Ensures the workspace holds `bytes`; the counter region is zeroed on growth.
-  int ensure_ws(size_t bytes) {
-    std::lock_guard<std::mutex> g(mu);
-    if (bytes <= ws_bytes) return LLH_OK;
+
+  // The workspace slot of stream s (created on first use).
+  std::shared_ptr<llh::StreamWorkspace> slot(hipStream_t s) {
+    std::lock_guard<std::mutex> g(ws_mu);
+    for (auto &w : workspaces)
+      if (w->stream == s) return w;
+    workspaces.push_back(std::make_shared<llh::StreamWorkspace>());
+    workspaces.back()->stream = s;
+    return workspaces.back();
+  }
+  size_t min_ws() {
+    std::lock_guard<std::mutex> g(ws_mu);
+    return ws_min_bytes;
+  }
+  // Grows a locked slot to at least `bytes` (plus the counter region, zeroed on
+  // every allocation).  The old buffer is freed once the slot's stream has
+  // drained, so no kernel still reads it.
+  int grow_locked(llh::StreamWorkspace &w, size_t bytes) {
+    bytes = std::max(bytes, min_ws());
+    if (w.ptr && bytes <= w.bytes) return LLH_OK;
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
-    if (ws) {
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-      (void)hipFree(ws);
-      ws = nullptr;
-      ws_bytes = 0;
+    if (w.ptr) {
+      e = hipStreamSynchronize(w.stream);
+      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize(workspace)");
+      (void)hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
     }
-    size_t nb = llh::align_up(std::max(bytes, llh::kCounterBytes + llh::kAlign));
-    e = hipMalloc(&ws, nb);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-    e = hipMemset(ws, 0, nb);
-    if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace)");
-    ws_bytes = nb;
+    const size_t nb = llh::align_up(std::max(bytes, llh::kCounterBytes + llh::kAlign));
+    e = hipMalloc(&w.ptr, nb);
+    if (e != hipSuccess) {
+      w.ptr = nullptr;
+      return hip_fail(e, "hipMalloc(workspace)");
+    }
+    // zeroed on the slot's own stream: a null-stream memset is asynchronous to the
+    // host and unordered with non-blocking streams, so it could land after this
+    // stream's next kernel
+    e = hipMemsetAsync(w.ptr, 0, nb, w.stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync(workspace)");
+    w.bytes = nb;
     return LLH_OK;
   }
-  std::mutex err_mu;
+};
+
+// A batched call's hold on its stream's workspace: locks the slot for the
+// lifetime of the lease (through the call's last launch).
+struct WsLease {
+  std::shared_ptr<llh::StreamWorkspace> w;
+  std::unique_lock<std::mutex> lock;
+  int acquire(llh_ctx *ctx, hipStream_t s, size_t bytes) {
+    w = ctx->slot(s);
+    lock = std::unique_lock<std::mutex>(w->mu);
+    return ctx->grow_locked(*w, bytes);
+  }
+  char *base() const { return static_cast<char *>(w->ptr); }
 };
 
 struct llh_kv_pool {
@@ -121,4 +176,3 @@ inline size_t scale_bytes_per_block(int32_t format, int32_t kv_heads, int32_t bl
   if (format == LLH_KV_FP8_E4M3) return (size_t)kv_heads * 4;
   return 0;
 }
-

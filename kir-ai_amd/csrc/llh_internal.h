@@ -21,6 +21,7 @@ enum ErrFlag : int32_t {
   kErrBadBlock = 1,      // block table entry outside the pool
   kErrTooManySplits = 2, // a sequence needed more split-K partials than the grid was sized for
   kErrNonFinite = 4,     // non-finite score (softmax_f32 contract)
+  kErrSpan = 8,          // a sequence attends more tokens than its block-table row holds
 };
 
 struct PoolView {
@@ -44,7 +45,6 @@ struct DecodeArgs {
   const int32_t *tables;    // [B][max_blocks]
   float *ws_o;              // [B][Hq][max_splits][128]
   float2 *ws_ml;            // [B][Hq][max_splits]  (running max in log2 units, sum)
-  int32_t *counters;        // [B][Hkv] split arrival counters, zero between calls
   int32_t *err;             // error flags
   int32_t num_seqs;
   int32_t q_heads;
@@ -52,7 +52,6 @@ struct DecodeArgs {
   int32_t window;
   int32_t split_blocks;     // blocks per split
   int32_t max_splits;
-  int32_t fused_merge;      // 1: last workgroup merges the splits; 0: second launch merges
   int32_t stream_wgs;       // >0: persistent stream kernel over this many workgroups (split fields unused)
   int32_t max_seq_len;      // host bound on seq_lens (stream kernel: longer lengths raise kErrTooManySplits)
   int32_t *seg_desc;        // stream kernel: [B][Hkv][2] (first partial slot, partial count; 0 = written)

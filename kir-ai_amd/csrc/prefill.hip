@@ -183,6 +183,15 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
   const int ctx = a.context_lens[b];
   const int i0 = tile * BM;
   if (i0 >= chunk || chunk <= 0 || ctx < chunk) return;
+  {
+    // every key of the chunk's first row through the last must be resident at once:
+    // a longer span would alias its own table entries (rows are read modulo max_blocks)
+    const int first_lo = a.window > 0 ? max(0, ctx - chunk - a.window + 1) : 0;
+    if (ctx - first_lo > a.max_blocks * BT) {
+      if (threadIdx.x == 0 && tile == 0) atomicOr(a.err, kErrSpan);
+      return;
+    }
+  }
 
   const int tid = threadIdx.x;
   const int ltid = tid & (kPrefillThreads - 1);  // thread index within the head's 4 wavefronts

@@ -43,6 +43,16 @@ KV_FP8_E4M3 = 2
 ERR_FLAG_BAD_BLOCK = 1
 ERR_FLAG_TOO_MANY_SPLITS = 2
 ERR_FLAG_NON_FINITE = 4
+ERR_FLAG_SPAN = 8
+
+# llh_option
+OPT_DECODE_KERNEL = 0           # 0 = by step size, 1 = split-K, 2 = stream
+OPT_DECODE_SPLIT_BLOCKS = 1
+OPT_DECODE_STREAM_WGS = 2
+OPT_FORCE_GENERIC = 3
+OPT_PREFILL_HEADS_PER_WG = 4
+OPT_TRAIT_REFERENCE_ORDER = 5
+DECODE_KERNELS = {"auto": 0, "split": 1, "stream": 2}
 
 _STATUS_NAMES = {
     NOT_HANDLED: "not handled",
@@ -118,6 +128,7 @@ class Metrics(ctypes.Structure):
         ("device_errors", ctypes.c_uint64),
         ("shape_errors", ctypes.c_uint64),
         ("stream_decode_calls", ctypes.c_uint64),
+        ("trait_tuned_calls", ctypes.c_uint64),
     ]
 
 
@@ -258,6 +269,10 @@ SIGNATURES = {
     "llh_ctx_destroy": (ctypes.c_int, [_P]),
     "llh_ctx_last_error": (ctypes.c_char_p, [_P]),
     "llh_ctx_reserve_workspace": (ctypes.c_int, [_P, _SZ]),
+    "llh_ctx_reserve_stream_workspace": (ctypes.c_int, [_P, _P, _SZ]),
+    "llh_ctx_release_stream": (ctypes.c_int, [_P, _P]),
+    "llh_ctx_set_option": (ctypes.c_int, [_P, _I32, _I32]),
+    "llh_ctx_get_option": (ctypes.c_int, [_P, _I32, ctypes.POINTER(_I32)]),
     "llh_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "llh_ctx_metrics": (ctypes.c_int, [_P, ctypes.POINTER(Metrics)]),
     "llh_ctx_device_errors": (ctypes.c_int, [_P, ctypes.POINTER(_I32), _I32]),
@@ -451,6 +466,20 @@ class Context:
 
     def reserve_workspace(self, nbytes: int) -> None:
         self.check(self.lib.llh_ctx_reserve_workspace(self.handle, nbytes))
+
+    def reserve_stream_workspace(self, nbytes: int, stream=None) -> None:
+        self.check(self.lib.llh_ctx_reserve_stream_workspace(self.handle, _stream(stream), nbytes))
+
+    def release_stream(self, stream) -> None:
+        self.check(self.lib.llh_ctx_release_stream(self.handle, _stream(stream)))
+
+    def set_option(self, option: int, value: int) -> None:
+        self.check(self.lib.llh_ctx_set_option(self.handle, option, int(value)))
+
+    def get_option(self, option: int) -> int:
+        v = _I32()
+        self.check(self.lib.llh_ctx_get_option(self.handle, option, ctypes.byref(v)))
+        return v.value
 
     def pool(self, fmt: int, block_tokens: int, kv_heads: int, head_dim: int, n_blocks: int) -> "KvPool":
         return KvPool(self, fmt, block_tokens, kv_heads, head_dim, n_blocks)

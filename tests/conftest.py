@@ -31,3 +31,23 @@ def ctx():
     c = llm_hip.Context(0)
     yield c
     c.close()
+
+
+@pytest.fixture
+def opts(ctx):
+    """set(option, value) for one test: context tuning options (llh_ctx_set_option),
+    restored to their previous values afterwards."""
+    import llm_hip
+
+    saved = {}
+
+    def set_(option, value):
+        if option not in saved:
+            saved[option] = ctx.get_option(option)
+        if option == llm_hip.OPT_DECODE_KERNEL and isinstance(value, str):
+            value = llm_hip.DECODE_KERNELS[value]
+        ctx.set_option(option, value)
+
+    yield set_
+    for o, v in saved.items():
+        ctx.set_option(o, v)

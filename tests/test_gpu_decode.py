@@ -49,11 +49,11 @@ def run_decode(ctx, pool, batch, q, Hq, window, scale, head_dim=D, max_seq_len=N
     ctx.paged_decode(pool, desc, d_q, d_out, scale)
     torch.cuda.synchronize()
     streamed = ctx.metrics()["stream_decode_calls"] - before
-    forced = os.environ.get("LLH_DECODE_KERNEL")
-    if forced == "stream" and head_dim == D and batch.block_tokens == BT:
+    forced = ctx.get_option(llm_hip.OPT_DECODE_KERNEL)
+    if forced == llm_hip.DECODE_KERNELS["stream"] and head_dim == D and batch.block_tokens == BT:
         assert streamed == 1, "the stream kernel did not run"
-    if forced == "split":
-        assert streamed == 0, "the stream kernel ran under LLH_DECODE_KERNEL=split"
+    if forced == llm_hip.DECODE_KERNELS["split"]:
+        assert streamed == 0, "the stream kernel ran under the split-K option"
     return from_dev_bf16(d_out)
 
 
@@ -122,20 +122,11 @@ def test_decode_c1_identity_table(ctx, fmt):
     check(ctx, identity_batch([512]), 16, 8, fmt, seed=workloads.SEED_BASE + 0, what="C1")
 
 
-@pytest.fixture(params=["fused", "kernel"])
-def merge_mode(request, monkeypatch):
-    """Split-K partials merged by the last-arriving workgroup (LLH_DECODE_FUSED_MERGE=1) or by a
-    second launch (the default)."""
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
-    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1" if request.param == "fused" else "0")
-    return request.param
-
-
 @pytest.fixture(params=["split", "stream"])
-def decode_kernel(request, monkeypatch):
+def decode_kernel(request, opts):
     """Both tuned decode kernels: split-K (one workgroup per split) and the persistent stream
-    kernel (LLH_DECODE_KERNEL forces the choice the library otherwise makes by batch size)."""
-    monkeypatch.setenv("LLH_DECODE_KERNEL", request.param)
+    kernel (LLH_OPT_DECODE_KERNEL forces the choice the library otherwise makes by batch size)."""
+    opts(llm_hip.OPT_DECODE_KERNEL, request.param)
     return request.param
 
 
@@ -147,39 +138,32 @@ def test_decode_c2_full_size(ctx, decode_kernel):
     check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 kernel={decode_kernel}")
 
 
-def test_decode_c2_fused_merge(ctx, merge_mode):
-    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
-    batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
-    check(ctx, batch, 16, 8, seed=workloads.SEED_BASE + 1, what=f"C2 split-K merge={merge_mode}")
-
-
 @pytest.mark.parametrize("split_blocks", [4, 8, 64])
-def test_decode_split_sizes(ctx, merge_mode, split_blocks, monkeypatch):
-    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", str(split_blocks))
+def test_decode_split_sizes(ctx, opts, split_blocks):
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
+    opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, split_blocks)
     lens = workloads.uniform_lengths(12, 1, 5000, 17)
     batch = workloads.paged_batch(lens, BT, 0.10, 17)
-    check(ctx, batch, 32, 8, seed=17, what=f"split={split_blocks} merge={merge_mode}")
+    check(ctx, batch, 32, 8, seed=17, what=f"split={split_blocks}")
 
 
 @pytest.mark.parametrize("n_splits", [2, 33, 64, 65, 96, 97, 130])
-def test_decode_merge_split_counts(ctx, n_splits, monkeypatch):
+def test_decode_merge_split_counts(ctx, opts, n_splits):
     """The merge launch's three layouts: every partial in registers (<= 64 splits),
     LDS-reduced pairs with all partials loaded up front (<= 96) and the chunked tail;
     one sequence per count at the boundaries, 4-block splits."""
-    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", "4")
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
-    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "0")
+    opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, 4)
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
     lens = np.array([BT * 4 * n_splits - 5, BT * 4 * (n_splits - 1) + 1], np.int32)  # n_splits each
     batch = workloads.paged_batch(lens, BT, 0.10, 300 + n_splits)
     check(ctx, batch, 16, 8, seed=300 + n_splits, what=f"merge of {n_splits} splits")
 
 
-def test_decode_fused_merge_is_deterministic(ctx, monkeypatch):
-    """Many splits per sequence and many repeated calls: the last-arriving workgroup
-    merges in split order, so every call must give identical bits; a stale partial
-    read across XCDs would show up as a difference."""
-    monkeypatch.setenv("LLH_DECODE_FUSED_MERGE", "1")
-    monkeypatch.setenv("LLH_DECODE_SPLIT_BLOCKS", "4")
+def test_decode_split_k_is_deterministic(ctx, opts):
+    """Many splits per sequence and many repeated calls: the merge combines partials in
+    split order, so every call must give identical bits."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
+    opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, 4)
     lens = workloads.uniform_lengths(32, 256, 4096, 23)
     batch = workloads.paged_batch(lens, BT, 0.10, 23)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 23)
@@ -188,7 +172,7 @@ def test_decode_fused_merge_is_deterministic(ctx, monkeypatch):
         assert np.array_equal(run_decode(ctx, pool, batch, q, 16, 0, 0.088), first)
     assert ctx.device_errors() == 0
     ref = oracle_decode(pool, batch, llm_hip.KV_BF16, 16, 8, 0, q, 0.088)
-    assert_parity(first, ref, what="fused merge, split 4")
+    assert_parity(first, ref, what="split-K, split 4")
 
 
 @pytest.mark.parametrize("lens", [[1], [15, 16, 17], [31, 33, 255, 256, 257], [1000, 4095, 4096, 4097]])
@@ -332,21 +316,21 @@ def test_decode_shape_errors(ctx):
 # ---- the persistent stream kernel's partition -------------------------------------------------
 
 @pytest.mark.parametrize("wgs", [1, 2, 3, 7, 16, 64])
-def test_stream_small_grids_cut_segments_everywhere(ctx, wgs, monkeypatch):
+def test_stream_small_grids_cut_segments_everywhere(ctx, wgs, opts):
     """Small grids put wavefront boundaries at every possible place relative to the
     (kv head, block) segments: ranges that start on a segment's last block, span several
     kv heads, or hold one unit; each cut segment is merged from its partials."""
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
-    monkeypatch.setenv("LLH_DECODE_STREAM_WGS", str(wgs))
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
+    opts(llm_hip.OPT_DECODE_STREAM_WGS, wgs)
     lens = [1, 16, 17, 250, 4096, 33, 1000][: max(1, min(7, 2 * wgs - 1))]
     batch = workloads.paged_batch(lens, BT, 0.10, seed=40 + wgs)
     check(ctx, batch, 16, 8, seed=41 + wgs, what=f"stream wgs={wgs}")
 
 
-def test_stream_many_partials_per_segment(ctx, monkeypatch):
+def test_stream_many_partials_per_segment(ctx, opts):
     """Few long sequences on a large grid: ~64 partials per segment, merged in rounds of 16."""
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
-    monkeypatch.setenv("LLH_DECODE_STREAM_WGS", "512")
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
+    opts(llm_hip.OPT_DECODE_STREAM_WGS, 512)
     batch = workloads.paged_batch([4096] * 4, BT, 0.10, seed=44)
     check(ctx, batch, 16, 8, seed=45, what="stream 4 x 4096")
 
@@ -359,17 +343,17 @@ def test_stream_batch_over_64(ctx, decode_kernel):
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (64, 8), (32, 4)])
-def test_stream_group_sizes(ctx, Hq, Hkv, monkeypatch):
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+def test_stream_group_sizes(ctx, Hq, Hkv, opts):
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
     lens = workloads.uniform_lengths(24, 1, 3000, Hq)
     batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq + Hkv)
     check(ctx, batch, Hq, Hkv, seed=48, what=f"stream Hq={Hq} Hkv={Hkv}")
 
 
-def test_stream_is_the_default_for_large_bf16_batches(ctx, monkeypatch):
+def test_stream_is_the_default_for_large_bf16_batches(ctx, opts):
     """Without an override the library picks the stream kernel for C2 and split-K for C1:
     both give the same result as the forced choice, bit for bit."""
-    monkeypatch.delenv("LLH_DECODE_KERNEL", raising=False)
+    opts(llm_hip.OPT_DECODE_KERNEL, "auto")
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     batch = workloads.paged_batch(lens, BT, 0.10, workloads.SEED_BASE + 1)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 50)
@@ -380,20 +364,147 @@ def test_stream_is_the_default_for_large_bf16_batches(ctx, monkeypatch):
     c1pool, c1q = build_case(ctx, c1, 16, 8, llm_hip.KV_BF16, 51)
     run_decode(ctx, c1pool, c1, c1q, 16, 0, 0.088)
     assert ctx.metrics()["stream_decode_calls"] == before + 1  # C1 stays on split-K
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "stream")
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
     assert np.array_equal(run_decode(ctx, pool, batch, q, 16, 0, 0.088), auto)
-    monkeypatch.setenv("LLH_DECODE_KERNEL", "split")
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
     split = run_decode(ctx, pool, batch, q, 16, 0, 0.088)
     assert not np.array_equal(split, auto)  # different summation order: proves the choice
     assert ctx.device_errors() == 0
 
 
 @pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
-def test_stream_is_the_default_for_large_quantized_batches(ctx, fmt, monkeypatch):
+def test_stream_is_the_default_for_large_quantized_batches(ctx, fmt, opts):
     """A C5-shaped batch (64 sequences, Hq32/Hkv8) of int8 / fp8 blocks takes the stream
     kernel without an override and meets the bar."""
-    monkeypatch.delenv("LLH_DECODE_KERNEL", raising=False)
+    opts(llm_hip.OPT_DECODE_KERNEL, "auto")
     batch = workloads.paged_batch(np.full(64, 2048, np.int32), BT, 0.10, 61)
     before = ctx.metrics()["stream_decode_calls"]
     check(ctx, batch, 32, 8, fmt=fmt, seed=61, what=f"default kernel fmt={fmt}")
     assert ctx.metrics()["stream_decode_calls"] == before + 1
+
+
+# ---- block-table span: rows are read modulo their length ---------------------------------------
+
+def test_decode_ring_of_exactly_window_blocks(ctx, decode_kernel):
+    """A sliding window served by a ring of W/16 blocks (positions p and p + W share a slot):
+    the W attended positions fill the ring exactly, so a misaligned window touches the same
+    ring block at both ends with disjoint offsets.  Only in-window rows are written."""
+    import torch
+
+    W, nb, Hq, Hkv = 64, 4, 16, 8
+    lens = np.array([1000, 77, 64, 65, 7], np.int32)
+    B = lens.size
+    tables = (np.arange(B * nb, dtype=np.int32).reshape(B, nb) * 3 + 1) % (B * nb + 3)
+    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, B * nb + 3)
+    slots, ks, vs = [], [], []
+    for b in range(B):
+        lo = max(0, int(lens[b]) - W)
+        for p in range(lo, int(lens[b])):
+            slots.append(int(tables[b, (p // BT) % nb]) * BT + p % BT)
+            ks.append(rows_bf16(71, b, p, p + 1, Hkv, D)[0])
+            vs.append(rows_bf16(72, b, p, p + 1, Hkv, D)[0])
+    ctx.append(pool, to_dev(np.array(slots, np.int64)), to_dev(np.stack(ks)), to_dev(np.stack(vs)))
+    torch.cuda.synchronize()
+    batch = workloads.PagedBatch(lens, tables, B * nb + 3, BT, np.zeros(B, np.int32))
+    q = oracle.normal_bf16(73, B * Hq * D)
+    out = run_decode(ctx, pool, batch, q, Hq, W, 0.09)
+    assert ctx.device_errors() == 0, ctx.last_error()
+    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, Hq, Hkv, W, q, 0.09)
+    assert_parity(out, ref, what=f"ring of {nb} blocks, W={W} {decode_kernel}")
+
+
+def test_decode_span_beyond_table_row_is_rejected(ctx):
+    """A bound that lets a sequence attend more tokens than its table row holds is a shape
+    error on the host (two attended positions would share a slot)."""
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 8, D, 8)
+    lens = torch.tensor([60], dtype=torch.int32, device="cuda")
+    tab = torch.zeros((1, 4), dtype=torch.int32, device="cuda")  # 4 blocks = 64 tokens
+    q = torch.zeros(16 * D, dtype=torch.int16, device="cuda")
+    out = torch.zeros_like(q)
+    for msl, window in ((65, 0), (100, 65), (1000, 65)):
+        with pytest.raises(llm_hip.LlhError) as e:
+            ctx.paged_decode(pool, ctx.decode_desc(lens, tab, 16, msl, window), q, out, 0.1)
+        assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+    for msl, window in ((64, 0), (1000, 64), (64, 100)):  # these fit
+        ctx.paged_decode(pool, ctx.decode_desc(lens, tab, 16, msl, window), q, out, 0.1)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0
+
+
+def test_decode_span_flag_when_lengths_exceed_the_bound(ctx, decode_kernel):
+    """Lengths past the host bound reach the kernel: a sequence attending more tokens than its
+    table row holds raises the span flag and is not attended (no aliased blocks read)."""
+    batch = workloads.paged_batch([70], BT, 0.10, seed=12)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 12)
+    short = workloads.PagedBatch(batch.seq_lens, batch.tables[:, :4].copy(), batch.n_blocks, BT, batch.first_block)
+    run_decode(ctx, pool, short, q, 16, 0, 0.1, max_seq_len=64)
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_SPAN
+
+
+def test_decode_weights_sum_to_one_exactly(ctx, decode_kernel):
+    """The softmax normaliser sums exactly the bf16 weights that multiply V: with V = 1 in
+    every row, the output is 1.0 exactly.  Every fourth token scores 0 (the max of each
+    4-token group the kernels keep a running max for) and the others score -0.9945 in log2
+    units, whose weight 2^-0.9945 = 0.50188 rounds to 0.5 in bf16; a normaliser over the
+    unrounded weights would give (1 + 3 * 0.5) / (1 + 3 * 0.50188) = 0.99775 -> bf16 0.99609375."""
+    Hq, Hkv = 16, 8
+    lens = np.array([256, 1000, 33, 4096], np.int32)
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=77)
+    neg = oracle.f32_to_bf16(np.array([-0.99609375], np.float32))[0]
+    one = oracle.f32_to_bf16(np.array([1.0], np.float32))[0]
+
+    def krows(b, lo, hi):
+        r = np.zeros((hi - lo, Hkv, D), np.uint16)
+        for i, p in enumerate(range(lo, hi)):
+            if p % 4 != 0:
+                r[i, :, 0] = neg
+        return r
+
+    ids, src_k = workloads.block_sources(batch, krows, Hkv, D)
+    _, src_v = workloads.block_sources(batch, lambda b, lo, hi: np.full((hi - lo, Hkv, D), one, np.uint16), Hkv, D)
+    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks)
+    ctx.write_blocks(pool, to_dev(ids), to_dev(src_k), to_dev(src_v))
+    q = np.zeros((lens.size, Hq, D), np.uint16)
+    q[:, :, 0] = one
+    scale = 0.6921  # score * scale * log2(e) = -0.99609375 * 0.99849 = -0.99459
+    for window in (0, 100):
+        out = run_decode(ctx, pool, batch, q.ravel(), Hq, window, scale)
+        assert ctx.device_errors() == 0, ctx.last_error()
+        assert np.all(out == one), np.unique(oracle.bf16_to_f32(out))
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_c5_full_launch_sampled(ctx, opts, fmt):
+    """configs[4] exactly as bench.py times it: all 64 sequences of 8192 tokens (Hq32/Hkv8)
+    in one launch, so the stream kernel's B=64 partition, cut segments and merges are the
+    benchmarked ones; 8 sequences (first and last included) are checked against the oracle."""
+    import torch
+
+    opts(llm_hip.OPT_DECODE_KERNEL, "auto")
+    B, L, Hq, Hkv = 64, 8192, 32, 8
+    batch = workloads.paged_batch([L] * B, BT, 0.0, workloads.SEED_BASE + 4)
+    pool = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(workloads.SEED_BASE + 4 + fmt)
+    ids = torch.from_numpy(batch.tables.ravel().copy()).cuda()
+    for s in range(0, ids.numel(), 4096):
+        idx = ids[s:s + 4096]
+        k = torch.randn((idx.numel(), BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((idx.numel(), BT, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        ctx.write_blocks(pool, idx, k, v)
+    del k, v
+    q = oracle.normal_bf16(workloads.SEED_BASE + 40 + fmt, B * Hq * D)
+    scale = 1.0 / math.sqrt(D)
+    before = ctx.metrics()["stream_decode_calls"]
+    out = run_decode(ctx, pool, batch, q, Hq, 0, scale)
+    assert ctx.metrics()["stream_decode_calls"] == before + 1, "C5 did not take the stream kernel"
+    assert ctx.device_errors() == 0, ctx.last_error()
+    sub = [0, 9, 17, 31, 32, 47, 55, 63]
+    opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, batch.n_blocks, pool.raw())
+    st, ref = opool.decode(Hq, batch.seq_lens[sub], batch.tables[sub], 0, q.reshape(B, -1)[sub].ravel(), scale,
+                           threads=16)
+    assert st == oracle.OK
+    assert_parity(out.reshape(B, -1)[sub], ref, what=f"C5 full launch fmt={fmt}")
+    pool.close()

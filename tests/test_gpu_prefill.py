@@ -150,12 +150,33 @@ def test_prefill_rejects_unaligned_rows(ctx):
 
 
 @pytest.mark.parametrize("W", [0, 300])
-def test_prefill_two_heads_per_workgroup_match_one(ctx, W, monkeypatch):
+def test_prefill_two_heads_per_workgroup_match_one(ctx, W, opts):
     """Two query heads sharing a workgroup's K/V tiles give the same bits as one head
     per workgroup: the per-wavefront arithmetic is identical, only the tile loads are shared."""
     prefix, chunk = [0, 300, 1500], [77, 256, 512]
-    monkeypatch.setenv("LLH_PREFILL_HEADS_PER_WG", "1")
+    opts(llm_hip.OPT_PREFILL_HEADS_PER_WG, 1)
     one = build(ctx, prefix, chunk, 16, 4, W, 60 + W)[4]
-    monkeypatch.delenv("LLH_PREFILL_HEADS_PER_WG")
+    opts(llm_hip.OPT_PREFILL_HEADS_PER_WG, 0)
     two = build(ctx, prefix, chunk, 16, 4, W, 60 + W)[4]
     assert np.array_equal(one, two)
+
+
+def test_prefill_span_beyond_table_row_raises_flag(ctx):
+    """Every key from the chunk's first row to its last must be resident at once; a table
+    row shorter than that span (rows are read modulo their length) raises the span flag
+    instead of attending aliased blocks."""
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 4, D, 16)
+    starts = torch.tensor([0, 20], dtype=torch.int32, device="cuda")
+    clens = torch.tensor([100], dtype=torch.int32, device="cuda")
+    tab = torch.arange(4, dtype=torch.int32, device="cuda").view(1, 4)  # 64 tokens
+    q = torch.zeros(20 * 8 * D, dtype=torch.int16, device="cuda")
+    out = torch.zeros_like(q)
+    ctx.paged_prefill(pool, ctx.prefill_desc(starts, clens, tab, 8, 20, 0, total_q_rows=20), q, out, 0.1)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_SPAN
+    # a window whose span (first row's window start .. context end) fits the ring is accepted
+    ctx.paged_prefill(pool, ctx.prefill_desc(starts, clens, tab, 8, 20, 40, total_q_rows=20), q, out, 0.1)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0

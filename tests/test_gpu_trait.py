@@ -232,3 +232,89 @@ def test_select_head_rows_and_revision(ctx):
     assert list(sel) == [-5.0, -6.0, -9.0, -10.0]
     cache.clear()
     assert cache.token_count() == 0 and cache.next_position() == 0 and cache.revision() == 5
+
+
+# ---- the trait hooks on the tuned decode kernels (head_dim 128, whole-block rings) ----------------
+
+def _filled_cache(ctx, fmt, max_tokens, n_append, seed, hkv=8):
+    """A Qwen3-0.6B-shaped layer cache (8 kv heads x 128) after n_append sliding appends of
+    N(0,1) rows (bf16-exact, so the bf16 store holds them exactly)."""
+    rng = np.random.default_rng(seed)
+    cache = LayerKvCache.new_with_config(ctx, max_tokens, hkv, 128, fmt)
+    backend = HipNativeMatvecBackend(ctx)
+    for _ in range(n_append):
+        k = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal(hkv * 128).astype(np.float32)))
+        v = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal(hkv * 128).astype(np.float32)))
+        backend.append_kv_cache_sliding_f32(cache, k, v)
+    return cache, rng
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+@pytest.mark.parametrize("max_tokens,n_append,hq", [(512, 512, 16), (64, 200, 16), (512, 300, 32), (128, 128, 8)])
+def test_trait_mix_on_tuned_kernels_matches_reference_loop(ctx, opts, fmt, max_tokens, n_append, hq):
+    """full_attention_cache_mix_f32_in_place at head_dim 128 runs the tuned decode kernel
+    (a batch of one; q rounded to bf16) over the ring, wrapped or not, for every row count
+    asked: the result meets the BASELINE bar against the reference's per-head loop on the
+    cache's own rows (dequantised for int8), and the reference-order kernel agrees."""
+    opts(llm_hip.OPT_TRAIT_REFERENCE_ORDER, 0)
+    cache, rng = _filled_cache(ctx, fmt, max_tokens, n_append, max_tokens + n_append + hq + fmt)
+    backend = HipNativeMatvecBackend(ctx)
+    q = rng.standard_normal(hq * 128).astype(np.float32)  # not bf16-exact: the tuned path rounds it
+    keys, vals = cache.keys(), cache.values()
+    n = cache.token_count()
+    for rows in sorted({n, max(1, n // 2), 1, 17}):
+        if rows > n:
+            continue
+        out = np.zeros(hq * 128, np.float32)
+        before = ctx.metrics()["trait_tuned_calls"]
+        assert backend.full_attention_cache_mix_f32_in_place(cache, q, rows, hq, 8, 128, 0.0883883, out)
+        assert ctx.metrics()["trait_tuned_calls"] == before + 1
+        st, ref = oracle.attention_mix(q, keys, vals, rows, hq, 8, 128, 0.0883883)
+        assert st == oracle.OK
+        d = np.abs(out - ref)
+        assert d.max() <= 2e-2 and d.mean() <= 2e-3, (rows, d.max(), d.mean())
+        opts(llm_hip.OPT_TRAIT_REFERENCE_ORDER, 1)
+        exact = np.zeros_like(out)
+        assert backend.full_attention_cache_mix_f32_in_place(cache, q, rows, hq, 8, 128, 0.0883883, exact)
+        assert ctx.metrics()["trait_tuned_calls"] == before + 1
+        opts(llm_hip.OPT_TRAIT_REFERENCE_ORDER, 0)
+        assert np.max(np.abs(exact - ref)) < 1e-4
+    cache.close()
+
+
+def test_trait_mix_projection_on_tuned_kernels(ctx, opts):
+    """The fused o_proj hook on the tuned path: the bf16 attention output stays on the device
+    and is projected there; it agrees with the reference-order path within the bar."""
+    import torch
+
+    opts(llm_hip.OPT_TRAIT_REFERENCE_ORDER, 0)
+    cache, rng = _filled_cache(ctx, llm_hip.KV_BF16, 512, 400, 91)
+    backend = HipNativeMatvecBackend(ctx)
+    q = rng.standard_normal(16 * 128).astype(np.float32)
+    w = torch.from_numpy(oracle.normal_bf16(92, 1024 * 2048).view(np.int16)).cuda().view(1024, 2048)
+    tuned = np.zeros(1024, np.float32)
+    before = ctx.metrics()["trait_tuned_calls"]
+    assert backend.full_attention_cache_mix_bf16_output_projection_f32_in_place(cache, q, 400, 16, 8, 128, 0.088, w,
+                                                                               tuned)
+    assert ctx.metrics()["trait_tuned_calls"] == before + 1
+    st, attn = oracle.attention_mix(q, cache.keys(), cache.values(), 400, 16, 8, 128, 0.088)
+    ref = oracle.matvec_bf16_f32(oracle.normal_bf16(92, 1024 * 2048).reshape(1024, 2048), attn)
+    d = np.abs(tuned - ref)
+    # |W| rows of 2048 N(0,1) weights times an output within 2e-2: the projected bar scales by sqrt(2048)
+    assert d.mean() <= 2e-3 * math.sqrt(2048) and d.max() <= 2e-2 * math.sqrt(2048), (d.max(), d.mean())
+    cache.close()
+
+
+def test_trait_mix_non_finite_scores_still_error_on_the_tuned_shape(ctx, opts):
+    """A finite but huge key row makes the scores overflow: the tuned kernel's non-finite
+    output sends the call to the reference-order kernel, which reports softmax_f32's error."""
+    opts(llm_hip.OPT_TRAIT_REFERENCE_ORDER, 0)
+    cache, rng = _filled_cache(ctx, llm_hip.KV_BF16, 64, 10, 93)
+    HipNativeMatvecBackend(ctx).append_kv_cache_sliding_f32(cache, np.full(8 * 128, 1e30, np.float32),
+                                                            np.ones(8 * 128, np.float32))
+    out = np.zeros(16 * 128, np.float32)
+    with pytest.raises(llm_hip.LlhError) as e:
+        HipNativeMatvecBackend(ctx).full_attention_cache_mix_f32_in_place(cache, np.full(16 * 128, 1e30, np.float32),
+                                                                          11, 16, 8, 128, 1.0, out)
+    assert e.value.status == llm_hip.ERR_NON_FINITE
+    cache.close()

@@ -361,6 +361,45 @@ def test_int8_head_quantisation_bounds():
     assert st == oracle.ERR_NON_FINITE
 
 
+def test_int8_head_codes_are_nearest_codes_of_the_stored_scale():
+    """Brute force over every code: the stored scale is numpy's fp16 rounding of absmax/127
+    (computed in f32), and each code is the c in [-127, 127] nearest to the f32 quotient
+    x / scale (the reference's `(value / scale).round()`, format.rs:711-735), ties going
+    away from zero.  Exact .5 ties are planted.  A code from the unrounded scale, ties to
+    even, truncation or a clamp error each fails here."""
+    rng = np.random.default_rng(41)
+    cands = np.arange(-127, 128, dtype=np.float64)
+    planted = 0
+    for trial in range(300):
+        n = 128
+        x = (rng.standard_normal(n) * rng.uniform(1e-3, 50)).astype(np.float32)
+        amax = np.float32(np.abs(x).max())
+        s = np.float32(np.float16(np.float32(amax / np.float32(127.0))))
+        # plant exact ties (k + 0.5) * s, below the absmax so the scale is unchanged
+        others = np.setdiff1d(np.arange(n), [int(np.argmax(np.abs(x)))])
+        for i in rng.choice(others, 8, replace=False):
+            k = int(rng.integers(-126, 126))
+            t = np.float32((k + 0.5) * s)
+            if abs(t) < amax:
+                x[i] = t
+                planted += 1
+        assert np.float32(np.abs(x).max()) == amax
+        st, codes, s16 = oracle.quantize_int8_head(x)
+        assert st == oracle.OK
+        assert s16 == int(np.float16(np.float32(amax / np.float32(127.0))).view(np.uint16))
+        quot = (x / s).astype(np.float32).astype(np.float64)
+        dist = np.abs(quot[:, None] - cands[None, :])
+        best = dist.min(axis=1, keepdims=True)
+        # nearest codes; among equals the one farthest from zero
+        score = np.where(dist == best, np.abs(cands)[None, :], -1.0)
+        expect = cands[np.argmax(score, axis=1)]
+        assert np.array_equal(codes.astype(np.float64), expect), trial
+    assert planted > 1000
+    # all-zero rows: scale 0, codes 0 (format.rs: scale 0 -> code 0)
+    st, codes, s16 = oracle.quantize_int8_head(np.zeros(8, np.float32))
+    assert st == oracle.OK and s16 == 0 and not codes.any()
+
+
 def test_fp8_block_quantisation_bounds():
     rng = np.random.default_rng(6)
     table = oracle.fp8_decode_table()
