@@ -221,6 +221,21 @@ typedef struct llh_decode_desc {
 int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
                      void *d_out, float score_scale, void *stream);
 
+/* llh_paged_decode without any allocation.  No counterpart in the reference:
+ * this entry point is for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The step's
+ * split partials and merge descriptors live in a static device array of the
+ * library (LLH_NOALLOC_SCRATCH_BYTES per GPU, held by every GPU the library
+ * runs on until the process ends) instead of the stream's workspace; it calls
+ * no hipMalloc/hipFree and creates no events (kernel timing does not see it).
+ * Same arguments, kernels and results as llh_paged_decode.  A step whose plan
+ * needs more scratch than the array holds returns LLH_ERR_CAPACITY (use
+ * llh_paged_decode).  All calls on one GPU share the array: calls that overlap
+ * on one GPU (other streams, other threads) race on it. */
+#define LLH_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int llh_paged_decode_noalloc(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                             void *d_out, float score_scale, void *stream);
+
 /* Chunked prefill over cached prefix blocks.  Sequence b owns query rows
  * [d_chunk_starts[b], d_chunk_starts[b+1]); its context holds d_context_lens[b]
  * tokens (prefix + the chunk, whose K/V are already in the pool).  Row i sits

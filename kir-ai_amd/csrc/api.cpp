@@ -168,6 +168,11 @@ int llh_ctx_create(int device, llh_ctx **out) {
     return LLH_ERR_DEVICE;
   }
   ctx->cus = std::max(1, ctx->cus);
+  if (noalloc_init(device) != LLH_OK) {  // this device's copy of the no-allocation scratch
+    (void)hipFree(ctx->d_err);
+    delete ctx;
+    return LLH_ERR_DEVICE;
+  }
   read_env_options(ctx);
   *out = ctx;
   return LLH_OK;
@@ -497,21 +502,22 @@ static int check_span(llh_ctx *ctx, const llh_kv_pool *pool, int32_t max_seq_len
   return LLH_OK;
 }
 
-// One decode step.  With d_out == nullptr the bf16 output goes to a buffer of
-// `extra_bytes` placed after the call's own regions of the stream's workspace
-// (returned in *extra_ptr), so a following kernel on the stream can consume it
-// without any allocation; the caller keeps `lease` through that launch.
-static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
-                             void *d_out, float score_scale, void *stream, size_t extra_bytes, void **extra_ptr,
-                             WsLease &lease) {
-  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+// Plans one decode step: validates the call, chooses the kernel and lays out
+// its workspace (offsets from the workspace base; plan->bytes in all).
+int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                     const void *d_out, float score_scale, DecodePlan *plan) {
+  if (!ctx || !pool || !desc || !plan) return LLH_ERR_NULL;
+  *plan = DecodePlan{};
   int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
   if (st != LLH_OK) return st;
-  if (desc->num_seqs == 0) return LLH_OK;
+  if (desc->num_seqs == 0) {
+    plan->empty = true;
+    return LLH_OK;
+  }
   if (desc->max_seq_len < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "max_seq_len must be >= 0");
   st = check_span(ctx, pool, desc->max_seq_len, desc->window, desc->max_blocks_per_seq);
   if (st != LLH_OK) return st;
-  if (!d_q || (!d_out && !extra_ptr) || !desc->d_seq_lens || !desc->d_block_tables)
+  if (!d_q || !desc->d_seq_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   const PoolView &pv = pool->view;
@@ -520,38 +526,53 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   // not 16-byte aligned go through the element-wise generic kernel.
   const bool rows_aligned = (reinterpret_cast<uintptr_t>(d_q) & 15) == 0 &&
                             (reinterpret_cast<uintptr_t>(d_out) & 15) == 0;
-  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens && rows_aligned &&
-                    (group == 1 || group == 2 || group == 4 || group == 8) &&
-                    (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !ctx->opt(LLH_OPT_FORCE_GENERIC);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  ctx->decode_calls++;
-  if (fast) {
-    const SplitPlan plan = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
-                                       desc->total_tokens_hint, pv.format);
-    const int stream_wgs =
-        plan_stream(ctx, pv.format, desc->num_seqs, pv.kv_heads, plan.est_blocks, desc->total_tokens_hint);
-    if (!stream_wgs && plan.max_splits > kMaxDecodeSplits)
+  plan->group = group;
+  plan->fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens && rows_aligned &&
+               (group == 1 || group == 2 || group == 4 || group == 8) &&
+               (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !ctx->opt(LLH_OPT_FORCE_GENERIC);
+  if (plan->fast) {
+    const SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
+                                     desc->total_tokens_hint, pv.format);
+    plan->stream_wgs =
+        plan_stream(ctx, pv.format, desc->num_seqs, pv.kv_heads, sp.est_blocks, desc->total_tokens_hint);
+    if (!plan->stream_wgs && sp.max_splits > kMaxDecodeSplits)
       return ctx->fail(LLH_ERR_INVALID_SHAPE, "context too long for one decode call (over 4M attended tokens)");
+    plan->split_blocks = sp.split_blocks;
+    plan->max_splits = sp.max_splits;
     // partial rows: split-K [B][Hq][max_splits]; stream [2 * waves][G]
-    const size_t rows = stream_wgs ? (size_t)2 * 4 * stream_wgs * group
-                                   : (size_t)desc->num_seqs * desc->num_q_heads * plan.max_splits;
-    const size_t ml_off = kCounterBytes;
-    const size_t o_off = ml_off + align_up(rows * sizeof(float2));
-    const size_t desc_off = align_up(o_off + rows * kFastHeadDim * sizeof(float));
-    const size_t need = align_up(desc_off + (stream_wgs ? (size_t)desc->num_seqs * pv.kv_heads * 2 * sizeof(int32_t) : 0));
-    st = lease.acquire(ctx, s, need + extra_bytes);
-    if (st != LLH_OK) return st;
-    char *ws = lease.base();
-    if (extra_ptr) *extra_ptr = ws + need;
-    if (!d_out) d_out = ws + need;
+    const size_t rows = plan->stream_wgs ? (size_t)2 * 4 * plan->stream_wgs * group
+                                         : (size_t)desc->num_seqs * desc->num_q_heads * sp.max_splits;
+    plan->ml_off = kCounterBytes;
+    plan->o_off = plan->ml_off + align_up(rows * sizeof(float2));
+    plan->desc_off = align_up(plan->o_off + rows * kFastHeadDim * sizeof(float));
+    plan->bytes = align_up(plan->desc_off +
+                           (plan->stream_wgs ? (size_t)desc->num_seqs * pv.kv_heads * 2 * sizeof(int32_t) : 0));
+    return LLH_OK;
+  }
+  // any other shape: the reference-order kernel, with a score row per (sequence, head)
+  const int span = desc->window > 0 ? std::min(desc->window, desc->max_seq_len) : desc->max_seq_len;
+  plan->score_stride = std::max(1, span);
+  plan->scores_off = kCounterBytes;
+  plan->bytes = align_up(plan->scores_off + (size_t)desc->num_seqs * desc->num_q_heads * plan->score_stride *
+                                                 sizeof(float));
+  return LLH_OK;
+}
+
+// Launches a planned decode step with its workspace at `ws` (plan.bytes long).
+int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
+                               const DecodePlan &plan, const void *d_q, void *d_out, float score_scale,
+                               hipStream_t s, char *ws, bool timed) {
+  const PoolView &pv = pool->view;
+  ctx->decode_calls++;
+  if (plan.fast) {
     DecodeArgs a{};
     a.pool = pv;
     a.q = static_cast<const uint16_t *>(d_q);
     a.out = static_cast<uint16_t *>(d_out);
     a.seq_lens = desc->d_seq_lens;
     a.tables = desc->d_block_tables;
-    a.ws_o = reinterpret_cast<float *>(ws + o_off);
-    a.ws_ml = reinterpret_cast<float2 *>(ws + ml_off);
+    a.ws_o = reinterpret_cast<float *>(ws + plan.o_off);
+    a.ws_ml = reinterpret_cast<float2 *>(ws + plan.ml_off);
     a.err = ctx->d_err;
     a.num_seqs = desc->num_seqs;
     a.q_heads = desc->num_q_heads;
@@ -559,35 +580,26 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
     a.window = desc->window;
     a.split_blocks = plan.split_blocks;
     a.max_splits = plan.max_splits;
-    a.stream_wgs = stream_wgs;
+    a.stream_wgs = plan.stream_wgs;
     a.max_seq_len = desc->max_seq_len;
-    a.seg_desc = stream_wgs ? reinterpret_cast<int32_t *>(ws + desc_off) : nullptr;
-    if (stream_wgs) ctx->stream_decode_calls++;
+    a.seg_desc = plan.stream_wgs ? reinterpret_cast<int32_t *>(ws + plan.desc_off) : nullptr;
+    if (plan.stream_wgs) ctx->stream_decode_calls++;
     a.scale_log2e = score_scale * 1.4426950408889634f;
     struct TimingHook {
       llh_ctx *ctx;
       std::pair<hipEvent_t, hipEvent_t> ev;
     } th{ctx, {nullptr, nullptr}};
-    hipError_t e = launch_decode(a, group, desc->max_seq_len, s, &th, [](void *u, int phase, hipStream_t st) {
+    const LaunchHook hook = [](void *u, int phase, hipStream_t st) {
       auto *t = static_cast<TimingHook *>(u);
       if (phase == 0)
         t->ev = t->ctx->timing_begin(st);
       else
         t->ctx->timing_end(0, t->ev, st);
-    });
+    };
+    hipError_t e = launch_decode(a, plan.group, desc->max_seq_len, s, timed ? &th : nullptr, timed ? hook : nullptr);
     if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");
     return LLH_OK;
   }
-  // any other shape: reference-order kernel
-  const int span = desc->window > 0 ? std::min(desc->window, desc->max_seq_len) : desc->max_seq_len;
-  const int stride = std::max(1, span);
-  const size_t off = kCounterBytes;
-  const size_t need = align_up(off + (size_t)desc->num_seqs * desc->num_q_heads * stride * sizeof(float));
-  st = lease.acquire(ctx, s, need + extra_bytes);
-  if (st != LLH_OK) return st;
-  char *ws = lease.base();
-  if (extra_ptr) *extra_ptr = ws + need;
-  if (!d_out) d_out = ws + need;
   GenericDecodeArgs g{};
   g.pool = pv;
   g.q = d_q;
@@ -595,18 +607,39 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   g.seq_lens = desc->d_seq_lens;
   g.starts = nullptr;
   g.tables = desc->d_block_tables;
-  g.scores = reinterpret_cast<float *>(ws + off);
+  g.scores = reinterpret_cast<float *>(ws + plan.scores_off);
   g.err = ctx->d_err;
   g.num_seqs = desc->num_seqs;
   g.q_heads = desc->num_q_heads;
   g.max_blocks = desc->max_blocks_per_seq;
   g.window = desc->window;
   g.ring_tokens = 0;
-  g.score_stride = stride;
+  g.score_stride = plan.score_stride;
   g.scale = score_scale;
   hipError_t e = launch_decode_generic(g, 0, 0, s);
   if (e != hipSuccess) return ctx->hip_fail(e, "generic decode launch");
   return LLH_OK;
+}
+
+// One decode step on the stream's workspace.  With d_out == nullptr the bf16
+// output goes to a buffer of `extra_bytes` placed after the step's own regions
+// (returned in *extra_ptr), so a following kernel on the stream can consume it
+// without any allocation; the caller keeps `lease` through that launch.
+static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                             void *d_out, float score_scale, void *stream, size_t extra_bytes, void **extra_ptr,
+                             WsLease &lease) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (!d_out && !extra_ptr && desc->num_seqs > 0) return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
+  DecodePlan plan;
+  int st = plan_decode(ctx, pool, desc, d_q, d_out, score_scale, &plan);
+  if (st != LLH_OK || plan.empty) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = lease.acquire(ctx, s, plan.bytes + extra_bytes);
+  if (st != LLH_OK) return st;
+  char *ws = lease.base();
+  if (extra_ptr) *extra_ptr = ws + plan.bytes;
+  if (!d_out) d_out = ws + plan.bytes;
+  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

@@ -162,6 +162,33 @@ struct WsLease {
   char *base() const { return static_cast<char *>(w->ptr); }
 };
 
+namespace llh {
+
+// A decode step planned on the host: the kernel choice and the byte layout of
+// its workspace (offsets from the workspace base, `bytes` in all).  Shared by
+// llh_paged_decode (per-stream workspace) and llh_paged_decode_noalloc (the
+// library's static scratch).
+struct DecodePlan {
+  bool empty = false;  // nothing to launch (no sequences)
+  bool fast = false;   // tuned kernels (else the reference-order kernel)
+  int group = 0;
+  int split_blocks = 0, max_splits = 0, stream_wgs = 0;
+  size_t ml_off = 0, o_off = 0, desc_off = 0;  // tuned: partial (max, sum), partial outputs, segment descriptors
+  int score_stride = 0;
+  size_t scores_off = 0;  // reference order: score rows
+  size_t bytes = 0;
+};
+int plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
+                const void *d_out, float score_scale, DecodePlan *plan);
+// timed = false leaves out the kernel-timing events (no event is created or recorded)
+int launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const DecodePlan &plan,
+                          const void *d_q, void *d_out, float score_scale, hipStream_t s, char *ws,
+                          bool timed = true);
+// Resolves this device's address of the no-allocation scratch (device current).
+int noalloc_init(int device);
+
+}  // namespace llh
+
 struct llh_kv_pool {
   llh_ctx *ctx = nullptr;
   llh::PoolView view{};

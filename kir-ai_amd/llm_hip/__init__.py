@@ -287,6 +287,7 @@ SIGNATURES = {
     "llh_kv_append_f32": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P]),
     "llh_kv_export_rows_f32": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, _P, _P]),
     "llh_paged_decode": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
+    "llh_paged_decode_noalloc": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
     "llh_paged_prefill": (ctypes.c_int, [_P, _P, ctypes.POINTER(PrefillDesc), _P, _P, ctypes.c_float, _P]),
     "llh_debug_gather": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _I32, _I32, _I32, _I32, _P, _P]),
     "llh_debug_decode_fp8": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
@@ -529,6 +530,12 @@ class Context:
                 self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out), score_scale, _stream(stream)
             )
         )
+
+    def paged_decode_noalloc(self, pool: "KvPool", desc: DecodeDesc, q, out, score_scale: float,
+                             stream=None) -> None:
+        """llh_paged_decode_noalloc: the same step on the library's static scratch (allocates nothing)."""
+        self.check(self.lib.llh_paged_decode_noalloc(self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out),
+                                                     ctypes.c_float(score_scale), _stream(stream)))
 
     def matvec_bf16(self, w, rows: int, cols: int, x, n: int, out, stream=None) -> None:
         """out[n][rows] f32 = x[n][cols] (bf16 or f32 tensor) times W[rows][cols]^T (bf16)."""
