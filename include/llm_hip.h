@@ -187,7 +187,14 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
  * (native_matvec.rs:643-653) and the Metal direct f16/int8 append
  * (crates/llm-native-runtime/src/native_matvec.rs:575-943).
  *   d_slots [n] int64; d_k, d_v [n][kv_heads][head_dim] bf16.
- * fp8 pools return LLH_ERR_UNSUPPORTED (their scale is per block: use llh_kv_write_blocks). */
+ * fp8 pools (one scale per (block, head) and tensor) re-quantise the block as
+ * each token arrives, as the reference re-quantises a block on every int8 append
+ * (crates/llm-kv-cache/src/layer.rs:1396-1408): the scale becomes
+ * max(old, absmax(row) / 448) and, when it grows, the block's tokens before the
+ * new one are re-encoded from their dequantised values; a token at offset 0
+ * starts the block afresh.  Tokens of one block in one call are appended in
+ * call order.  (So a window ring of fp8 blocks needs window/block_tokens + 1
+ * blocks: the offset-0 token must not share its block with live tokens.) */
 int llh_kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k,
                   const void *d_v, int32_t n, void *stream);
 /* llh_kv_append from f32 rows (d_k, d_v [n][kv_heads][head_dim] f32): the
@@ -254,7 +261,9 @@ typedef struct llh_prefill_desc {
 } llh_prefill_desc;
 
 /* d_q, d_out: [total_q_rows][Hq][head_dim] bf16, 16-byte aligned (else
- * LLH_ERR_UNSUPPORTED).  bf16 pools only. */
+ * LLH_ERR_UNSUPPORTED).  Every pool format: int8 / fp8 blocks are dequantised
+ * (code * scale, rounded to bf16) as the key/value tiles are staged, so the
+ * result is attention over the dequantised cache (layer.rs:650-656). */
 int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
                       void *d_out, float score_scale, void *stream);
 

@@ -423,8 +423,6 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
 static int kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
                      int32_t n, int32_t src_f32, void *stream) {
   if (!ctx || !pool) return LLH_ERR_NULL;
-  if (pool->view.format == LLH_KV_FP8_E4M3)
-    return ctx->fail(LLH_ERR_UNSUPPORTED, "fp8 pools carry per-block scales: write whole blocks");
   if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "negative token count");
   if (n == 0) return LLH_OK;
   if (!d_slots || !d_k || !d_v) return ctx->fail(LLH_ERR_NULL, "null device pointer");
@@ -745,9 +743,9 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   if (desc->total_q_rows < 0 || desc->max_chunk_len < 0)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "row counts must be >= 0");
   const PoolView &pv = pool->view;
-  if (pv.format != LLH_KV_BF16 || pv.head_dim != kFastHeadDim || pv.block_tokens != kFastBlockTokens) {
+  if (pv.head_dim != kFastHeadDim || pv.block_tokens != kFastBlockTokens) {
     ctx->not_handled++;
-    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill takes bf16 pools with head_dim 128 and 16-token blocks");
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill takes pools with head_dim 128 and 16-token blocks");
   }
   if (!d_q || !d_out || !desc->d_chunk_starts || !desc->d_context_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in prefill call");

@@ -5,7 +5,9 @@
 //   (crates/llm-kv-cache/src/format.rs:262-276) and the f32->f16 block upload
 //   of the Metal mirror (crates/llm-native-runtime/src/native_matvec.rs:384-465).
 // append: single token rows at absolute slots (the device half of
-//   append_kv_cache_sliding_f32, crates/llm-backend/src/core/native_matvec.rs:643-653).
+//   append_kv_cache_sliding_f32, crates/llm-backend/src/core/native_matvec.rs:643-653);
+//   fp8 blocks are re-quantised as tokens arrive, as the reference re-quantises
+//   a block on every int8 append (crates/llm-kv-cache/src/layer.rs:1396-1408).
 // gather: raw elements of a sequence's positions through its block table
 //   (select_head_rows_*, crates/llm-metal/src/device/shaders/generic.metal:310-360).
 //
@@ -238,6 +240,39 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
   }
 }
 
+// fp8 e4m3 code as f32 (exact).
+__device__ __forceinline__ float decode_e4m3(uint32_t code) { return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0]; }
+
+// Appends one token row (this wavefront's kv head) into an fp8 block whose
+// scale is per (block, head) and tensor: the block's scale becomes
+// max(old scale, absmax(row) / 448); when it grows, the block's earlier tokens
+// (offsets below `off`) are re-encoded from their dequantised values,
+// encode(decode(code) * old / new); a token at offset 0 starts the block
+// afresh (old scale 0).  `scale` is the block's current scale (kept in a
+// register across the tokens of one block in one call); returns the new one.
+template <typename ST, typename LD>
+__device__ __forceinline__ float append_fp8_row(uint8_t *dst, bool dim_major, size_t bh, int BT, int Dh, int off,
+                                                const ST *src, LD ld, float scale, int lane) {
+  const float s_old = off == 0 ? 0.0f : scale;
+  float mx = 0.0f;
+  for (int d = lane; d < Dh; d += 64) mx = fmaxf(mx, fabsf(ld(src, d)));
+  mx = wave_max(mx);
+  const float cand = mx == 0.0f ? 0.0f : __fdiv_rn(mx, 448.0f);
+  const float s_new = fmaxf(s_old, cand);
+  auto at = [&](int u, int d) -> uint8_t & {
+    return dim_major ? dst[(bh * Dh + d) * BT + u] : dst[(bh * BT + u) * Dh + d];
+  };
+  if (s_new != s_old) {
+    for (int u = 0; u < off; u++)
+      for (int d = lane; d < Dh; d += 64) {
+        const float x = s_old == 0.0f ? 0.0f : decode_e4m3(at(u, d)) * s_old;
+        at(u, d) = encode_e4m3(__fdiv_rn(x, s_new));
+      }
+  }
+  for (int d = lane; d < Dh; d += 64) at(off, d) = s_new == 0.0f ? 0 : encode_e4m3(__fdiv_rn(ld(src, d), s_new));
+  return s_new;
+}
+
 // One wavefront per (token row i, kv head).
 template <typename ST>
 __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
@@ -269,6 +304,38 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     for (int d = lane; d < Dh; d += 64) {
       kd[(bh * BT + off) * Dh + d] = f32_to_bf16_rne(ld(ks, d));
       vd[(bh * Dh + d) * BT + off] = f32_to_bf16_rne(ld(vs, d));
+    }
+    return;
+  }
+  if (a.pool.format == kFp8) {
+    // Tokens of one block in one call: the wavefront of the block's first token
+    // in call order appends them all, in that order (each may rescale the block).
+    for (int j0 = 0; j0 < i; j0 += 64) {
+      const int j = j0 + lane;
+      const bool same = j < i && a.slots[j] >= 0 && a.slots[j] / BT == blk;
+      if (__any(same)) return;
+    }
+    float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[bh], reinterpret_cast<const float *>(a.vs_dst)[bh]};
+    for (int j = i; j < a.n; j++) {
+      const int64_t sj = a.slots[j];
+      if (sj < 0 || sj / BT != blk) continue;
+      const int offj = (int)(sj % BT);
+      const ST *kj = reinterpret_cast<const ST *>(a.k) + ((size_t)j * Hkv + h) * Dh;
+      const ST *vj = reinterpret_cast<const ST *>(a.v) + ((size_t)j * Hkv + h) * Dh;
+      bool finite = true;
+      for (int d = lane; d < Dh; d += 64) finite = finite && isfinite(ld(kj, d)) && isfinite(ld(vj, d));
+      if (__any(!finite)) {
+        if (lane == 0) atomicOr(a.err, kErrNonFinite);
+        continue;
+      }
+      // this wavefront's earlier stores to the block are complete before it reads the block again
+      if (j > i) __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      scale[0] = append_fp8_row(reinterpret_cast<uint8_t *>(a.k_dst), false, bh, BT, Dh, offj, kj, ld, scale[0], lane);
+      scale[1] = append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
+    }
+    if (lane == 0) {
+      reinterpret_cast<float *>(a.ks_dst)[bh] = scale[0];
+      reinterpret_cast<float *>(a.vs_dst)[bh] = scale[1];
     }
     return;
   }

@@ -23,6 +23,11 @@
 // query tile, query head in group) with the head fastest, so each XCD works on
 // few (sequence, kv head) pairs at a time and their K/V tiles stay in its L2.
 //
+// int8 / fp8 pools are dequantised while a tile is stored to LDS (code * scale in
+// f32, rounded to bf16), so the MFMA path is the same for every format: the
+// result is attention over the dequantised cache, as the reference attends its
+// int8 cache after dequantising it (crates/llm-kv-cache/src/layer.rs:650-656).
+//
 // Per wavefront, with v_mfma_f32_32x32x16_bf16:
 //   S^T[key][query] = K Q^T       A = K rows (token-major pool layout)
 //                                 B = Q^T    (held in registers)
@@ -79,13 +84,27 @@ __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
                                          __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
 }
 
-// One lane's share of a key tile: for each of the 4 blocks, 16 B of K (token
-// tid/16, dims 8*(tid%16)..) and 16 B of V^T (dim tid/2, tokens 8*(tid&1)..),
-// plus a (wavefront-uniform) bit per block: 1 = the block is needed and valid.
+// One lane's share of a key tile: for each of the 4 blocks, the K elements of
+// token tid/16 at dims 8*(tid%16).. and the V^T elements of dim tid/2 at tokens
+// 8*(tid&1)..: 16 B each for bf16 pools; for int8 / fp8 pools 8 B of codes
+// each plus the scales they need (int8: the fp16 scale of the K token and the
+// eight of the V tokens; fp8: the block's f32 K and V scales), dequantised to
+// bf16 when the tile is stored to LDS.
+template <int FMT, int NB>
+struct TileRegs;
+
 template <int NB>
-struct TileRegs {
+struct TileRegs<kBf16, NB> {
   u32x4_t k[NB];
   u32x4_t v[NB];
+};
+
+template <int FMT, int NB>
+struct TileRegs {
+  uint2 k[NB];
+  uint2 v[NB];
+  uint32_t ks[NB];  // int8: fp16 bits of the K token's scale; fp8: f32 bits of the block's K scale
+  uint4 vs[NB];     // int8: eight fp16 V scales (tokens 8*(tid&1)..); fp8: .x = f32 bits of the V scale
 };
 
 // Block-table entries of the tile starting at kt: lane kb of every wavefront
@@ -101,9 +120,9 @@ __device__ __forceinline__ int fetch_entries(const PrefillArgs &a, const int32_t
 // stored to LDS), so no branch or conditional memory operation sits between
 // the prefetch and the math that overlaps it.  `bad` collects needed blocks
 // with an out-of-pool entry (flagged once, at the end of the kernel).
-template <int NB>
+template <int FMT, int NB>
 __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries, int kvh, int kt, int ctx, int klo,
-                                              int tid, int kb0, TileRegs<NB> &r, bool &bad) {
+                                              int tid, int kb0, TileRegs<FMT, NB> &r, bool &bad) {
   const int Hkv = a.pool.kv_heads;
   uint32_t use_mask = 0;
 #pragma unroll
@@ -116,28 +135,90 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
     bad |= needed && !ok;
     const bool use = needed && ok;
     use_mask |= use ? (1u << i) : 0u;
-    const size_t base = ((size_t)(use ? phys : 0) * Hkv + kvh) * (BT * D);
-    r.k[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
-                                              (tid >> 4) * D + (tid & 15) * 8);
-    r.v[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
-                                              (tid >> 1) * BT + (tid & 1) * 8);
+    const size_t bh = (size_t)(use ? phys : 0) * Hkv + kvh;
+    const size_t base = bh * (BT * D);  // elements of this block-head
+    if constexpr (FMT == kBf16) {
+      r.k[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
+                                                (tid >> 4) * D + (tid & 15) * 8);
+      r.v[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
+                                                (tid >> 1) * BT + (tid & 1) * 8);
+    } else {
+      r.k[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(a.pool.k) + base + (tid >> 4) * D +
+                                                (tid & 15) * 8);
+      r.v[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(a.pool.v) + base +
+                                                (tid >> 1) * BT + (tid & 1) * 8);
+      if constexpr (FMT == kInt8) {
+        r.ks[i] = reinterpret_cast<const uint16_t *>(a.pool.k_scales)[bh * BT + (tid >> 4)];
+        r.vs[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) + bh * BT +
+                                                   (tid & 1) * 8);
+      } else {
+        r.ks[i] = reinterpret_cast<const uint32_t *>(a.pool.k_scales)[bh];
+        r.vs[i].x = reinterpret_cast<const uint32_t *>(a.pool.v_scales)[bh];
+      }
+    }
   }
   return use_mask;
+}
+
+__device__ __forceinline__ float half_bits_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Element e (0..7) of eight int8 / e4m3 codes as f32 (exact).
+template <int FMT>
+__device__ __forceinline__ float code_f32(const uint2 &w, int e) {
+  const uint32_t word = e < 4 ? w.x : w.y;
+  if constexpr (FMT == kInt8) {
+    return (float)(int8_t)(word >> (8 * (e & 3)));
+  } else {
+    const auto f = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(word, true) : __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+    return f[e & 1];
+  }
+}
+
+// The tile's K and V^T elements of this lane as bf16 (the dequantised value,
+// code * scale in f32, rounded to nearest even).
+template <int FMT, int NB>
+__device__ __forceinline__ void tile_bf16(const TileRegs<FMT, NB> &r, int i, u32x4_t &k, u32x4_t &v) {
+  if constexpr (FMT == kBf16) {
+    k = r.k[i];
+    v = r.v[i];
+  } else {
+    float kf[8], vf[8];
+    const float ks = FMT == kInt8 ? half_bits_f32(r.ks[i]) : __uint_as_float(r.ks[i]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) kf[e] = code_f32<FMT>(r.k[i], e) * ks;
+    if constexpr (FMT == kInt8) {
+      const uint32_t sw[4] = {r.vs[i].x, r.vs[i].y, r.vs[i].z, r.vs[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) vf[e] = code_f32<FMT>(r.v[i], e) * half_bits_f32(sw[e >> 1] >> (16 * (e & 1)));
+    } else {
+      const float vs = __uint_as_float(r.vs[i].x);
+#pragma unroll
+      for (int e = 0; e < 8; e++) vf[e] = code_f32<FMT>(r.v[i], e) * vs;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      k[q] = pack_bf16(kf[2 * q], kf[2 * q + 1]);
+      v[q] = pack_bf16(vf[2 * q], vf[2 * q + 1]);
+    }
+  }
 }
 
 // Stores a tile to LDS.  K rows are stored as loaded (keys that are not
 // attended are masked to -inf in the scores, whatever K holds); V^T is zeroed
 // for unused blocks and for tokens at or past the context end, because
 // P = 0 times a non-finite V would still poison the accumulators.
-template <int NB>
-__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, int kb0, const TileRegs<NB> &r,
-                                           uint32_t use_mask, int kt, int ctx) {
+template <int FMT, int NB>
+__device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, int kb0,
+                                           const TileRegs<FMT, NB> &r, uint32_t use_mask, int kt, int ctx) {
   const bool tail = kt + BN > ctx;  // the tile reaches the end of the context (uniform)
 #pragma unroll
   for (int i = 0; i < NB; i++) {
     const int kb = kb0 + i;
-    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = r.k[i];
-    u32x4_t v = r.v[i];
+    u32x4_t kk, v;
+    tile_bf16<FMT, NB>(r, i, kk, v);
+    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = kk;
     if (!(use_mask & (1u << i))) v = u32x4_t{0u, 0u, 0u, 0u};
     if (tail) {
       const int valid = ctx - (kt + kb * BT + (tid & 1) * 8);  // tokens of this 8-run inside the context
@@ -152,7 +233,7 @@ __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int
   }
 }
 
-template <int HPW>
+template <int HPW, int FMT>
 __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_kernel(const PrefillArgs a) {
   // ---- XCD-aware logical work item ----
   const int Hq = a.q_heads;
@@ -247,7 +328,7 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
   const int wlo_last = a.window > 0 ? max(0, wpos_last - a.window + 1) : 0;
   const bool wave_live = wrow0 < chunk;
 
-  TileRegs<KBLK / HPW> next;
+  TileRegs<FMT, KBLK / HPW> next;
   bool bad = false;
   uint32_t use_next =
       load_tile(a, fetch_entries(a, table, t_begin, lane), kvh, t_begin, ctx, klo, ltid, kb0, next, bad);
@@ -386,15 +467,32 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
   }
 }
 
+template <int FMT>
+void launch_prefill_fmt(const PrefillArgs &a, int variant, int grid, hipStream_t s) {
+  if (variant == kPrefillTwoHeads)
+    hipLaunchKernelGGL((paged_prefill_kernel<2, FMT>), dim3(grid), dim3(2 * kPrefillThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((paged_prefill_kernel<1, FMT>), dim3(grid), dim3(kPrefillThreads), 0, s, a);
+}
+
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s) {
   const int n_items = a.q_tiles * (a.q_heads / (variant == kPrefillOneHead ? 1 : 2)) * a.num_seqs;
   const int grid = (n_items + 7) / 8 * 8;
-  if (variant == kPrefillTwoHeads)
-    hipLaunchKernelGGL(paged_prefill_kernel<2>, dim3(grid), dim3(2 * kPrefillThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(paged_prefill_kernel<1>, dim3(grid), dim3(kPrefillThreads), 0, s, a);
+  switch (a.pool.format) {
+    case kBf16:
+      launch_prefill_fmt<kBf16>(a, variant, grid, s);
+      break;
+    case kInt8:
+      launch_prefill_fmt<kInt8>(a, variant, grid, s);
+      break;
+    case kFp8:
+      launch_prefill_fmt<kFp8>(a, variant, grid, s);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -119,6 +119,7 @@ _SIGS = {
     "orc_dequantize_int8_rows": (None, [_P, _P, _SZ, _SZ, _P]),
     "orc_quantize_int8_head": (ctypes.c_int, [_P, _I32, _P, _P]),
     "orc_quantize_fp8_block": (ctypes.c_int, [_P, _I32, _P, _P]),
+    "orc_append_fp8_token": (ctypes.c_int, [_P, _I32, _P, _I32, _P]),
 }
 
 
@@ -406,6 +407,15 @@ def quantize_fp8_block(x: np.ndarray) -> tuple[int, np.ndarray, float]:
     s = ctypes.c_float()
     st = lib().orc_quantize_fp8_block(_p(a), a.size, _p(codes), ctypes.addressof(s))
     return st, codes, s.value
+
+
+def append_fp8_token(codes: np.ndarray, scale: float, off: int, x: np.ndarray) -> tuple[int, float]:
+    """orc_append_fp8_token on codes [block_tokens][dim] uint8 (updated in place); returns (status, scale)."""
+    assert codes.dtype == np.uint8 and codes.flags["C_CONTIGUOUS"]
+    xx = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    s = ctypes.c_float(scale)
+    st = lib().orc_append_fp8_token(codes.ctypes.data_as(ctypes.c_void_p), xx.size, ctypes.addressof(s), off, _p(xx))
+    return st, s.value
 
 
 def chain_hash(model_id: str, cache_context: str, previous_hash: bytes, token_ids) -> bytes:

@@ -702,3 +702,23 @@ int orc_quantize_fp8_block(const float *x, int32_t n, uint8_t *codes, float *sca
   *scale = s;
   return ORC_OK;
 }
+
+int orc_append_fp8_token(uint8_t *codes, int32_t dim, float *scale, int32_t off, const float *x) {
+  float max_abs = 0.0f;
+  for (int32_t d = 0; d < dim; d++) {
+    if (!isfinite(x[d])) return ORC_ERR_NON_FINITE;
+    max_abs = fmaxf(max_abs, fabsf(x[d]));
+  }
+  const float s_old = off == 0 ? 0.0f : *scale;
+  const float cand = max_abs == 0.0f ? 0.0f : max_abs / 448.0f;
+  const float s_new = fmaxf(s_old, cand);
+  if (s_new != s_old)
+    for (int32_t u = 0; u < off; u++)
+      for (int32_t d = 0; d < dim; d++) {
+        const float v = s_old == 0.0f ? 0.0f : orc_fp8e4m3_to_f32(codes[u * dim + d]) * s_old;
+        codes[u * dim + d] = orc_f32_to_fp8e4m3(v / s_new);
+      }
+  for (int32_t d = 0; d < dim; d++) codes[off * dim + d] = s_new == 0.0f ? 0 : orc_f32_to_fp8e4m3(x[d] / s_new);
+  *scale = s_new;
+  return ORC_OK;
+}

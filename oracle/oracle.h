@@ -188,6 +188,14 @@ void orc_dequantize_int8_rows(const int8_t *codes, const float *scales, size_t r
 int orc_quantize_int8_head(const float *x, int32_t n, int8_t *codes, uint16_t *scale_f16);
 /* per (block, head) fp8: scale = absmax/448 over n values (0 -> 0, codes 0), code = e4m3(x/scale) */
 int orc_quantize_fp8_block(const float *x, int32_t n, uint8_t *codes, float *scale);
+/* Per-token append into one fp8 (block, head) tensor, re-quantising the block as
+ * the reference re-quantises a block on every int8 append (layer.rs:1396-1408;
+ * fp8 itself has no counterpart there): codes [block_tokens][dim] token-major,
+ * *scale the block's scale.  Token `off` = row x [dim]: old = off == 0 ? 0 :
+ * *scale; new = max(old, absmax(x) / 448); when new != old the codes of tokens
+ * 0 .. off-1 become e4m3((old == 0 ? 0 : e4m3_to_f32(code) * old) / new); the
+ * row's codes are new == 0 ? 0 : e4m3(x / new).  Non-finite x -> error. */
+int orc_append_fp8_token(uint8_t *codes, int32_t dim, float *scale, int32_t off, const float *x);
 
 #ifdef __cplusplus
 }

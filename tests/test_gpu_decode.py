@@ -508,3 +508,36 @@ def test_decode_c5_full_launch_sampled(ctx, opts, fmt):
     assert st == oracle.OK
     assert_parity(out.reshape(B, -1)[sub], ref, what=f"C5 full launch fmt={fmt}")
     pool.close()
+
+
+def test_stream_and_split_k_steps_alternate_on_one_stream(ctx, opts):
+    """Stream steps (per-wavefront partial slots and segment descriptors) and split-K steps
+    (per-split partials) alternate on one stream's workspace; each keeps giving the bits it
+    gave first, and both meet the oracle bar."""
+    import torch
+
+    lens = workloads.uniform_lengths(32, 256, 4096, 61)
+    batch = workloads.paged_batch(lens, BT, 0.10, 61)
+    pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 61)
+    small = workloads.paged_batch([3000, 17, 900], BT, 0.10, 62)
+    spool, sq = build_case(ctx, small, 16, 8, llm_hip.KV_BF16, 62)
+    first = {}
+    for it in range(6):
+        for kern, (bt, pl, qq) in (("stream", (batch, pool, q)), ("split", (small, spool, sq))):
+            opts(llm_hip.OPT_DECODE_KERNEL, kern)
+            out = run_decode(ctx, pl, bt, qq, 16, 0, 0.09)
+            if it == 0:
+                first[kern] = out
+            assert np.array_equal(out, first[kern]), (kern, it)
+    assert ctx.device_errors() == 0
+    assert_parity(first["stream"], oracle_decode(pool, batch, llm_hip.KV_BF16, 16, 8, 0, q, 0.09), what="stream")
+    assert_parity(first["split"], oracle_decode(spool, small, llm_hip.KV_BF16, 16, 8, 0, sq, 0.09), what="split")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_stream_segment_cut_into_hundreds_of_pieces(ctx, opts, fmt):
+    """One 32768-token sequence on the full stream grid: each kv head's segment is cut into
+    ~256 pieces, which the merge launch combines in rounds of 32."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
+    batch = workloads.paged_batch([32768], BT, 0.0, 63)
+    check(ctx, batch, 16, 8, fmt, seed=63, what=f"1 x 32768 stream fmt={fmt}")

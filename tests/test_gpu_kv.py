@@ -12,7 +12,7 @@ import pytest
 
 import llm_hip
 import oracle
-from helpers import rows_bf16, to_dev
+from helpers import assert_parity, rows_bf16, to_dev
 from llm_hip import workloads
 
 pytestmark = pytest.mark.gpu
@@ -199,17 +199,67 @@ def test_append_equals_block_write(ctx, fmt):
         assert np.array_equal(ra[key], rw[key]), key
 
 
-def test_append_rejects_fp8_and_flags_bad_slots(ctx):
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_FP8_E4M3])
+def test_append_flags_bad_slots(ctx, fmt):
     import torch
 
-    pool = ctx.pool(llm_hip.KV_FP8_E4M3, BT, 2, D, 2)
+    pool = ctx.pool(fmt, BT, 2, D, 2)
     z = torch.zeros(2 * D, dtype=torch.int16, device="cuda")
-    with pytest.raises(llm_hip.LlhError) as e:
-        ctx.append(pool, torch.zeros(1, dtype=torch.int64, device="cuda"), z, z)
-    assert e.value.status == llm_hip.ERR_UNSUPPORTED
-    pool = ctx.pool(llm_hip.KV_BF16, BT, 2, D, 2)
     ctx.append(pool, torch.tensor([2 * BT + 1], dtype=torch.int64, device="cuda"), z, z)
     assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
+
+
+def test_fp8_append_matches_oracle_token_by_token(ctx):
+    """Per-token appends into fp8 blocks (scale per (block, head) and tensor) re-quantise the
+    block as the absmax grows: the pool's codes and scales equal the oracle's restatement of
+    the rule bit for bit, for calls of one token, calls of several tokens of one block (call
+    order), calls spanning two blocks, and a block reused from a stale scale."""
+    import torch
+
+    Hkv, n_tok = 2, 44
+    table = [3, 5, 1]  # position p lives in block table[p // 16]
+    pool = ctx.pool(llm_hip.KV_FP8_E4M3, BT, Hkv, D, 8)
+    # stale content in the blocks: a whole-block write with a large scale first
+    big = torch.full((8, BT, Hkv, D), 100.0, device="cuda").to(torch.bfloat16)
+    ctx.write_blocks(pool, torch.arange(8, dtype=torch.int32, device="cuda"), big, big)
+    rng = np.random.default_rng(5)
+    mag = np.exp(rng.uniform(-3, 2, n_tok)).astype(np.float32)
+    k = oracle.f32_to_bf16(rng.standard_normal((n_tok, Hkv, D)).astype(np.float32) * mag[:, None, None])
+    v = oracle.f32_to_bf16(rng.standard_normal((n_tok, Hkv, D)).astype(np.float32) * mag[:, None, None][::-1])
+    slots = np.array([table[p // BT] * BT + p % BT for p in range(n_tok)], np.int64)
+    calls = [[p] for p in range(0, 20)] + [list(range(20, 28)), list(range(28, 36)), list(range(36, 44))]
+    for c in calls:
+        ctx.append(pool, to_dev(slots[c]), to_dev(k[c]), to_dev(v[c]))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    raw = pool.raw()
+    kc = raw["k"].reshape(8, Hkv, BT, D)
+    vc = raw["v"].reshape(8, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.float32).reshape(8, Hkv)
+    vs = raw["v_scales"].view(np.float32).reshape(8, Hkv)
+    kf, vf = oracle.bf16_to_f32(k), oracle.bf16_to_f32(v)
+    for bi, blk in enumerate(table):
+        n_in = min(BT, n_tok - bi * BT)
+        for h in range(Hkv):
+            for tensor, src, got, gs in ((0, kf, kc[blk, h], ks[blk, h]), (1, vf, vc[blk, h].T, vs[blk, h])):
+                codes = np.zeros((BT, D), np.uint8)
+                s = 999.0
+                for t in range(n_in):
+                    st, s = oracle.append_fp8_token(codes, s, t, src[bi * BT + t, h])
+                    assert st == oracle.OK
+                assert gs == np.float32(s), (blk, h, tensor)
+                assert np.array_equal(got[:n_in], codes[:n_in]), (blk, h, tensor)
+    # attention over the appended cache meets the bar against the dequantise-then-attend oracle
+    lens = np.array([n_tok], np.int32)
+    tab = np.array([table], np.int32)
+    q = oracle.normal_bf16(7, 8 * D)
+    out = torch.zeros(8 * D, dtype=torch.int16, device="cuda")
+    ctx.paged_decode(pool, ctx.decode_desc(to_dev(lens), to_dev(tab), 8, n_tok), to_dev(q), out, 0.09)
+    torch.cuda.synchronize()
+    opool = oracle.Pool.from_raw(llm_hip.KV_FP8_E4M3, BT, Hkv, D, 8, pool.raw())
+    st, ref = opool.decode(8, lens, tab, 0, q, 0.09)
+    assert st == oracle.OK
+    assert_parity(out.cpu().numpy().view(np.uint16), ref, what="decode over appended fp8 blocks")
 
 
 def test_fp8_decode_table(ctx):

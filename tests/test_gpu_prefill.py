@@ -23,7 +23,7 @@ D = 128
 BT = 16
 
 
-def build(ctx, prefix, chunk, Hq, Hkv, window, seed, resident_from=None):
+def build(ctx, prefix, chunk, Hq, Hkv, window, seed, resident_from=None, fmt=llm_hip.KV_BF16):
     import torch
 
     ctxlen = [p + c for p, c in zip(prefix, chunk)]
@@ -31,7 +31,7 @@ def build(ctx, prefix, chunk, Hq, Hkv, window, seed, resident_from=None):
     batch = workloads.paged_batch(ctxlen, BT, 0.10, seed, first)
     ids, sk = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 1, b, lo, hi, Hkv, D), Hkv, D)
     _, sv = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, Hkv, D), Hkv, D)
-    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks)
+    pool = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
     ctx.write_blocks(pool, to_dev(ids), to_dev(sk), to_dev(sv))
     starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
     q = oracle.normal_bf16(seed + 3, int(starts[-1]) * Hq * D)
@@ -66,8 +66,8 @@ def decode_every_row(ctx, batch, pool, starts, prefix, chunk, q, Hq, window, sca
     return from_dev_bf16(d_out)
 
 
-def oracle_rows(pool, batch, starts, Hq, Hkv, window, q, scale, rows_per_seq):
-    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks, pool.raw())
+def oracle_rows(pool, batch, starts, Hq, Hkv, window, q, scale, rows_per_seq, fmt=llm_hip.KV_BF16):
+    opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, batch.n_blocks, pool.raw())
     out = np.zeros(int(starts[-1]) * Hq * D, np.float32)
     picked = []
     for b in range(batch.seq_lens.size):
@@ -123,16 +123,32 @@ def test_prefill_gqa_groups(ctx, Hq, Hkv):
     assert_parity(out, ref, what=f"Hq={Hq} Hkv={Hkv}")
 
 
-def test_prefill_rejects_quantized_pool(ctx):
-    import torch
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_prefill_quantized_c3_shape(ctx, fmt):
+    """configs[2]'s shape over int8 (fp16 scale per (token, head)) and fp8 e4m3 (f32 scale per
+    (block, head)) blocks, dequantised in the tile load: sampled rows against the oracle's
+    dequantise-then-attend loop, every row against the decode kernel on the same pool."""
+    prefix, chunk, Hq, Hkv = [1536] * 8, [512] * 8, 32, 4
+    batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, 0, workloads.SEED_BASE + 2 + fmt,
+                                               fmt=fmt)
+    ref, picked = oracle_rows(pool, batch, starts, Hq, Hkv, 0, q, scale, [sample_rows(c) for c in chunk], fmt)
+    got = out.reshape(-1, Hq * D)
+    assert_parity(got[picked], ref[picked], what=f"C3 fmt={fmt} sampled rows vs oracle")
+    dec = decode_every_row(ctx, batch, pool, starts, prefix, chunk, q, Hq, 0, scale)
+    assert_parity(out, oracle.bf16_to_f32(dec), what=f"C3 fmt={fmt} all rows vs decode kernel")
 
-    pool = ctx.pool(llm_hip.KV_INT8, BT, 8, D, 4)
-    z = torch.zeros(2, dtype=torch.int32, device="cuda")
-    desc = ctx.prefill_desc(z, z[:1], z.view(1, 2), 16, 1, 0, total_q_rows=1)
-    with pytest.raises(llm_hip.LlhError) as e:
-        ctx.paged_prefill(pool, desc, torch.zeros(16 * D, dtype=torch.int16, device="cuda"),
-                          torch.zeros(16 * D, dtype=torch.int16, device="cuda"), 0.1)
-    assert e.value.status == llm_hip.ERR_UNSUPPORTED
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("W", [0, 37])
+def test_prefill_quantized_ragged_full_oracle(ctx, fmt, W):
+    prefix = [0, 17, 1000, 3, 64]
+    chunk = [1, 5, 130, 300, 64]
+    Hq, Hkv = 16, 8
+    batch, pool, starts, q, out, scale = build(ctx, prefix, chunk, Hq, Hkv, W, 70 + W + fmt, fmt=fmt)
+    opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, batch.n_blocks, pool.raw())
+    st, ref = opool.prefill(Hq, starts, batch.seq_lens, batch.tables, W, q, scale, threads=16)
+    assert st == oracle.OK
+    assert_parity(out, ref, what=f"ragged fmt={fmt} W={W}")
 
 
 def test_prefill_rejects_unaligned_rows(ctx):

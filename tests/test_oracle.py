@@ -413,6 +413,54 @@ def test_fp8_block_quantisation_bounds():
         assert np.all(np.abs(deq - x)[~big] <= 2.0 ** -10 * s + 1e-12)
 
 
+def test_fp8_append_equals_block_quantiser_when_the_first_row_holds_the_max():
+    """Appending a block's rows one by one (the per-token rule) gives exactly the whole-block
+    quantiser's codes and scale when no later row raises the block's absmax: the scale is
+    fixed by row 0 and every row is encoded x / scale."""
+    rng = np.random.default_rng(12)
+    for trial in range(40):
+        D, n = 128, int(rng.integers(1, 17))
+        x = (rng.standard_normal((n, D)) * rng.uniform(0.01, 5)).astype(np.float32)
+        x[0, int(rng.integers(D))] = np.float32(np.abs(x).max() * 1.5)  # row 0 holds the block max
+        codes = np.zeros((16, D), np.uint8)
+        s = 123.0  # stale scale of a reused block: offset 0 ignores it
+        for t in range(n):
+            st, s = oracle.append_fp8_token(codes, s, t, x[t])
+            assert st == oracle.OK
+        st, ref_codes, ref_s = oracle.quantize_fp8_block(x)
+        assert st == oracle.OK and s == ref_s
+        assert np.array_equal(codes[:n].ravel(), ref_codes), trial
+
+
+def test_fp8_append_rescales_earlier_tokens_within_the_double_rounding_bound():
+    """Rows whose absmax grows: the scale follows the running absmax / 448 and every stored
+    value stays within the error of one e4m3 rounding per rescale it went through (a 3-bit
+    mantissa: half an ulp = 2^-4 relative, plus the subnormal step 2^-10 * scale)."""
+    rng = np.random.default_rng(13)
+    table = oracle.fp8_decode_table()
+    for trial in range(40):
+        D, n = 64, 16
+        x = (rng.standard_normal((n, D)) * np.geomspace(0.01, 10, n)[:, None]).astype(np.float32)
+        codes = np.zeros((16, D), np.uint8)
+        s, rescales = 0.0, np.zeros(n, int)
+        for t in range(n):
+            prev = s
+            st, s = oracle.append_fp8_token(codes, s, t, x[t])
+            assert st == oracle.OK
+            if t > 0 and s != prev:
+                rescales[:t] += 1
+            assert s == max(prev if t else 0.0, float(np.float32(np.abs(x[t]).max()) / np.float32(448.0)))
+        deq = table[codes[:n]] * np.float32(s)
+        for t in range(n):
+            k = rescales[t] + 1
+            bound = np.abs(x[t]) * ((1 + 2.0 ** -4) ** k - 1) + k * 2.0 ** -10 * s + 1e-12
+            assert np.all(np.abs(deq[t] - x[t]) <= bound), (trial, t)
+    # all-zero rows keep a zero scale and zero codes; non-finite rows are refused
+    codes = np.full((16, 8), 7, np.uint8)
+    assert oracle.append_fp8_token(codes, 0.0, 0, np.zeros(8)) == (oracle.OK, 0.0) and not codes[0].any()
+    assert oracle.append_fp8_token(codes, 0.0, 1, np.array([np.nan] * 8))[0] == oracle.ERR_NON_FINITE
+
+
 def test_prng_moments():
     x = oracle.normal_f32(123, 200000)
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
