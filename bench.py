@@ -90,24 +90,36 @@ class DecodeWorkload:
         return lens - lo, lo
 
     def algorithmic_bytes(self) -> int:
-        import numpy as np
-
-        rows, lo = self.attended_rows()
-        elem = 2 if self.fmt == self.llm_hip.KV_BF16 else 1
-        kv = int(rows.sum()) * self.Hkv * D * elem * 2
-        blocks = ((self.batch.seq_lens.astype(np.int64) + BT - 1) // BT) - lo // BT
-        scales = 0
-        if self.fmt == self.llm_hip.KV_INT8:
-            scales = int(rows.sum()) * self.Hkv * 2 * 2
-        elif self.fmt == self.llm_hip.KV_FP8_E4M3:
-            scales = int(blocks.sum()) * self.Hkv * 4 * 2
-        B = self.batch.seq_lens.size
-        qo = 2 * B * self.Hq * D * 2
-        tables = int(blocks.sum()) * 4 + B * 4
-        return kv + scales + qo + tables
+        return decode_bytes(self.batch.seq_lens, self.Hq, self.Hkv, self.fmt, self.window)
 
     def step(self, stream):
         self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
+
+    def prepare_append(self):
+        """The new token of every sequence (position len-1): its pool slot and N(0,1) K/V rows."""
+        import numpy as np
+
+        b = self.batch
+        lens = b.seq_lens.astype(np.int64)
+        pos = lens - 1
+        blocks = b.tables[np.arange(lens.size), (pos // BT) % b.max_blocks].astype(np.int64)
+        self.d_slots = self.torch.from_numpy(blocks * BT + pos % BT).cuda()
+        g = self.torch.Generator(device="cuda")
+        g.manual_seed(int(lens.sum()))
+        self.k_new = self.torch.randn((lens.size, self.Hkv, D), generator=g, device="cuda").to(self.torch.bfloat16)
+        self.v_new = self.torch.randn((lens.size, self.Hkv, D), generator=g, device="cuda").to(self.torch.bfloat16)
+
+    def append_step(self, stream):
+        """kir-ai's decode step order (native_attention.rs:307-329): append the new token, then attend."""
+        self.ctx.append(self.pool, self.d_slots, self.k_new, self.v_new, stream=stream)
+        self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
+
+    def append_bytes(self) -> int:
+        """Algorithmic bytes of the append: the new rows read (bf16) and written (pool format), slots."""
+        B = self.batch.seq_lens.size
+        elem = 2 if self.fmt == self.llm_hip.KV_BF16 else 1
+        scales = B * self.Hkv * 2 * 2 if self.fmt == self.llm_hip.KV_INT8 else 0
+        return B * self.Hkv * D * 2 * 2 + B * self.Hkv * D * elem * 2 + scales + B * 8
 
 
 def time_steps(fn, steps: int, warmup: int, kernel_timing=None):
@@ -267,17 +279,19 @@ def host_info() -> str:
     return f"{model} (nproc={os.cpu_count()})"
 
 
-def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos=None):
-    """Prefill workload: B sequences of prefix + chunk tokens, all K/V resident."""
+def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos=None, fmt=None):
+    """Prefill workload: B sequences of prefix + chunk tokens, all K/V resident (bf16 pool
+    unless fmt names a quantised one)."""
     import torch
     import llm_hip
     from llm_hip import workloads
 
+    fmt = llm_hip.KV_BF16 if fmt is None else fmt
     ctxlen = prefix + chunk
     lens = [ctxlen] * B
     first = None if resident_from_pos is None else [resident_from_pos // BT] * B
     batch = workloads.paged_batch(lens, BT, 0.10, seed, first)
-    pool = ctx.pool(llm_hip.KV_BF16, BT, Hkv, D, batch.n_blocks)
+    pool = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
     ids = [int(batch.tables[i, j]) for i in range(B) for j in range(int(batch.first_block[i]), (ctxlen + BT - 1) // BT)]
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -391,6 +405,47 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     return out
 
 
+def measure_trait_c1(ctx, calls: int, cpu_seconds: float, with_cpu: bool) -> dict:
+    """Per-call latency of the trait hook full_attention_cache_mix_f32_in_place
+    (native_matvec.rs:656-668) on a C1-shaped layer cache (512 tokens, 8 kv heads x 128,
+    16 query heads): the synchronous call kir-ai makes once per layer per token, host
+    timed end to end (f32 q in, f32 out), on the tuned kernels and on the reference-order
+    kernel, with the reference's CPU loop (the oracle) on the same rows beside it."""
+    import numpy as np
+    import llm_hip
+    import oracle
+
+    rng = np.random.default_rng(0x6B69722D00)
+    cache = llm_hip.LayerKvCache.new(ctx, 512, 8, D)
+    backend = llm_hip.HipNativeMatvecBackend(ctx)
+    for _ in range(512):
+        k = rng.standard_normal(8 * D).astype(np.float32)
+        v = rng.standard_normal(8 * D).astype(np.float32)
+        backend.append_kv_cache_sliding_f32(cache, k, v)
+    q = rng.standard_normal(16 * D).astype(np.float32)
+    out = np.zeros(16 * D, np.float32)
+    res = {"config": "trait hook full_attention_cache_mix_f32_in_place, C1 cache (512 x Hkv8 x 128, Hq16), per call",
+           "calls": calls}
+    saved = ctx.get_option(llm_hip.OPT_TRAIT_REFERENCE_ORDER)
+    for key, ref_order in (("tuned_us_per_call", 0), ("reference_order_us_per_call", 1)):
+        ctx.set_option(llm_hip.OPT_TRAIT_REFERENCE_ORDER, ref_order)
+        for _ in range(10):
+            backend.full_attention_cache_mix_f32_in_place(cache, q, 512, 16, 8, D, 0.0883883, out)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            backend.full_attention_cache_mix_f32_in_place(cache, q, 512, 16, 8, D, 0.0883883, out)
+        res[key] = round((time.perf_counter() - t0) / calls * 1e6, 2)
+    ctx.set_option(llm_hip.OPT_TRAIT_REFERENCE_ORDER, saved)
+    res["tuned_calls_counted"] = ctx.metrics()["trait_tuned_calls"] >= calls
+    if with_cpu:
+        keys, vals = cache.keys(), cache.values()
+        sec, reps = _timed(lambda: oracle.attention_mix(q, keys, vals, 512, 16, 8, D, 0.0883883), cpu_seconds, 200)
+        res["cpu_oracle_us_per_call"] = round(sec * 1e6, 1)
+        res["cpu_threads"] = 1
+    cache.close()
+    return res
+
+
 def measure_copy(mb: int) -> dict:
     """A plain device-to-device copy of `mb` MiB: the measured bandwidth ceiling, and the
     known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -410,20 +465,26 @@ def measure_copy(mb: int) -> dict:
 LLC_BYTES = 256 << 20  # MI355X Infinity Cache (memory-side last-level cache)
 
 
-def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10):
+def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10,
+                   append=False):
     """Mean step time over `steps` decode steps.  Steps rotate over enough independent
     copies of the workload (same lengths, own pool, own block permutation and data) that
     the bytes read between two visits of one copy exceed the 256 MB Infinity Cache: every
-    step reads its K/V from HBM, not from cache."""
+    step reads its K/V from HBM, not from cache.  append=True times kir-ai's whole decode
+    step instead: the new token's K/V append, then attention over the cache holding it."""
     first = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free)
-    nbytes = first.algorithmic_bytes()
+    nbytes = first.algorithmic_bytes() + (first.append_bytes() if append else 0)
     copies = [first]
     while (len(copies) - 1) * nbytes < 2 * LLC_BYTES:
         copies.append(DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed + 1000 * len(copies), free))
+    if append:
+        for c in copies:
+            c.prepare_append()
     state = {"i": 0}
 
     def step(stream):
-        copies[state["i"] % len(copies)].step(stream)
+        c = copies[state["i"] % len(copies)]
+        c.append_step(stream) if append else c.step(stream)
         state["i"] += 1
 
     # step time over all timed steps, then the decode kernel alone (library-recorded events)
@@ -434,11 +495,14 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     if ctx.device_errors() != 0:
         raise RuntimeError(f"{name}: device error flags set during timing")
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the event pair around the main kernel also spans its dispatch; a figure above the step
+    # time is not a kernel duration and is not reported (rocprof's trace gives the duration)
+    kernel_ok = kms <= ms
     return first, {
         "config": name,
         "us_per_step": round(ms * 1e3, 2),
-        "kernel_us": round(kms * 1e3, 2),
-        "kernel_gbs": round(nbytes / (kms * 1e-3) / 1e9, 1),
+        "kernel_us": round(kms * 1e3, 2) if kernel_ok else None,
+        "kernel_gbs": round(first.algorithmic_bytes() / (kms * 1e-3) / 1e9, 1) if kernel_ok else None,
         "hbm_gbs": round(gbs, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
@@ -448,18 +512,246 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     }
 
 
+def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0) -> int:
+    """Algorithmic bytes of one decode step: K and V of every attended position (+ int8 /
+    fp8 scales), q and out, the block-table entries read and the lengths."""
+    import numpy as np
+
+    lens = np.asarray(lens, np.int64)
+    lo = np.maximum(0, lens - window) if window > 0 else np.zeros_like(lens)
+    rows = lens - lo
+    elem = 2 if fmt == 0 else 1
+    kv = int(rows.sum()) * Hkv * D * elem * 2
+    blocks = ((lens + BT - 1) // BT) - lo // BT
+    scales = int(rows.sum()) * Hkv * 4 if fmt == 1 else (int(blocks.sum()) * Hkv * 8 if fmt == 2 else 0)
+    return kv + scales + 2 * lens.size * Hq * D * 2 + int(blocks.sum()) * 4 + lens.size * 4
+
+
+def prefill_flops(B: int, prefix: int, chunk: int, Hq: int, window: int) -> int:
+    """4 * D FLOPs per unmasked (query, key) pair per head."""
+    pairs = 0
+    for i in range(chunk):
+        pos = prefix + i
+        lo = max(0, pos - window + 1) if window > 0 else 0
+        pairs += pos - lo + 1
+    return 4 * D * pairs * Hq * B
+
+
+def summarize(root: str) -> int:
+    """Writes profiles/*.md from rocprofv3 csv output: ROOT/<section>/kt (--kernel-trace --stats),
+    ROOT/<section>/fetch and /write (--pmc FETCH_SIZE, --pmc WRITE_SIZE) and, for prefill
+    sections, ROOT/<section>/mfma, each made by `bench.py --only <section>` (the c2 section by
+    the default run).  Counters are scaled by what they read for the run's own 512 MiB copy."""
+    import csv
+    import glob
+    import statistics
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "kir-ai_amd"))
+    from llm_hip import workloads
+
+    def short(n):
+        n = n.replace("void ", "").replace("llh::(anonymous namespace)::", "").replace("llh::", "")
+        return n.split("(")[0].strip()
+
+    def rows_of(sec, sub, suffix):
+        out = []
+        for f in glob.glob(os.path.join(root, sec, sub, "**", "*" + suffix), recursive=True):
+            out.extend(csv.DictReader(open(f)))
+        return out
+
+    c2lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    c2b = decode_bytes(c2lens, 16, 8, 0)
+    append_b = 32 * 8 * D * 2 * 2 * 2 + 32 * 8  # bf16 rows read and written, K and V, slots
+    alg = {  # section -> {kernel prefix: (unit, amount)}
+        "c2": {"paged_decode_stream_kernel": ("B", c2b)},
+        "c2append": {"paged_decode_stream_kernel": ("B", c2b), "append_kernel": ("B", append_b)},
+        "c1": {"paged_decode_kernel": ("B", decode_bytes([512], 16, 8, 0))},
+        "c4": {"paged_decode_kernel": ("B", decode_bytes([32768] * 4, 16, 8, 0, 4096))},
+        "c5int8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 1))},
+        "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
+        "c3": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
+        "c3int8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
+        "c3fp8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
+        "c4prefill": {"paged_prefill_kernel": ("F", prefill_flops(4, 31744, 1024, 16, 4096))},
+        "neighbours": {"matvec_bf16_kernel": ("B", 1024 * 2048 * 2 + 32 * 2048 * 2 + 32 * 1024 * 4)},
+    }
+    groups = (
+        ("decode_c2_bf16.md", "Paged GQA decode, C2 (B=32, L~U[256,4096], Hq16/Hkv8, bf16 KV), and kir-ai's step "
+                              "order (append the new token, then attend)", ("c2", "c2append")),
+        ("decode_c1_c4_bf16.md", "Paged GQA decode, C1 (B=1, L=512) and C4 (4 x 32768, window 4096), bf16 KV",
+         ("c1", "c4")),
+        ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
+                                  "scales) and fp8 e4m3 (per (block, head) scales)", ("c5int8", "c5fp8")),
+        ("prefill_mfma.md", "Chunked causal prefill (MFMA): C3 (8 x (1536 + 512), Hq32/Hkv4) over bf16, int8 and fp8 "
+                            "blocks, C4 (4 x (31744 + 1024), window 4096)", ("c3", "c3int8", "c3fp8", "c4prefill")),
+        ("kv_write_oproj.md", "KV writes (whole blocks, per-token append) and the output projection",
+         ("neighbours",)),
+    )
+    med = statistics.median
+    wrote = 0
+    for fname, title, secs in groups:
+        body, cmds, cal_notes = "", [], []
+        for sec in secs:
+            if not os.path.isdir(os.path.join(root, sec)):
+                continue
+            run = f"python3 /root/repo/bench.py --only {sec} --no-cpu"
+            cmds.append(f"    cd /tmp && rocprofv3 --kernel-trace --stats --output-format csv -d <dir>/{sec}/kt -o run -- {run}")
+            tr = {}
+            for r in rows_of(sec, "kt", "kernel_trace.csv"):
+                k = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+                tr.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+            ctr = {}
+            for sub in ("fetch", "write", "mfma"):
+                got = rows_of(sec, sub, "counter_collection.csv")
+                if got and sub != "mfma":
+                    cmds.append(f"    cd /tmp && rocprofv3 --pmc {sub.upper()}_SIZE --output-format csv "
+                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2")
+                elif got:
+                    names = sorted({r["Counter_Name"] for r in got})
+                    cmds.append(f"    cd /tmp && rocprofv3 --pmc {' '.join(names)} --output-format csv "
+                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2")
+                for r in got:
+                    k = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
+                    ctr.setdefault((k, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+            copies = [k for (k, c) in ctr if k[0].startswith("__amd_rocclr_copyBuffer") and c == "FETCH_SIZE"]
+            fcal = wcal = None
+            if copies:
+                ck = max(copies, key=lambda k: med(ctr[(k, "FETCH_SIZE")]))
+                fcal = 512 * 1024 / med(ctr[(ck, "FETCH_SIZE")])
+                wcal = 512 * 1024 / med(ctr[(ck, "WRITE_SIZE")]) if (ck, "WRITE_SIZE") in ctr else None
+                cal_notes.append(f"{sec}: FETCH_SIZE x{fcal:.4f}" + (f", WRITE_SIZE x{wcal:.4f}" if wcal else ""))
+            for k in sorted(tr, key=lambda k: -med(tr[k])):
+                if not k[0] or k[0].startswith("__amd") or "::" in k[0] or "elementwise" in k[0] or k[0].startswith(
+                        "_ZN") or k[0].startswith("Cijk"):
+                    continue  # the copy, torch's and rocprim's kernels of the set-up
+                d = tr[k]
+                unit = next((v for pfx, v in alg.get(sec, {}).items() if k[0].startswith(pfx)), None)
+                rate = "-"
+                if unit and unit[0] == "B":
+                    rate = f"{unit[1] / (med(d) * 1e-6) / 1e9:.0f} GB/s"
+                elif unit:
+                    tf = unit[1] / (med(d) * 1e-6) / 1e12
+                    rate = f"{tf:.1f} TFLOP/s = {100 * tf / BF16_PEAK_TFLOPS:.1f}% of 2.5 PF"
+                f = ctr.get((k, "FETCH_SIZE"))
+                w = ctr.get((k, "WRITE_SIZE"))
+                traffic = (med(f) * fcal + (med(w) * wcal if w and wcal else 0)) * 1024 if f and fcal else None
+                ratio = f"{traffic / unit[1]:.3f}" if traffic and unit and unit[0] == "B" else "-"
+                body += (f"| {sec.upper() if sec != 'c2' else 'C2'} | `{k[0]}` | {k[1]} | {len(d)} | {med(d):.2f} | "
+                         f"{statistics.mean(d):.2f} | {unit[1] if unit else '-'} | {rate} | "
+                         f"{med(f) if f else float('nan'):.0f} | {med(w) if w else float('nan'):.0f} | "
+                         f"{traffic if traffic else float('nan'):.0f} | {ratio} |\n")
+            mf = [(k, c) for (k, c) in ctr if not c.endswith("_SIZE") and not k[0].startswith("__amd")]
+            for k, c in sorted(mf):
+                body += f"| {sec.upper()} | `{k[0]}` | {k[1]} | counter `{c}` | {med(ctr[(k, c)]):.4g} per dispatch |  |  |  |  |  |  |  |\n"
+        if not body:
+            continue
+        text = (f"# {title}\n\nMI355X (gfx950), rocprofv3 from ROCm 7.2.  Made by `python bench.py --summarize <dir>` "
+                f"from the csv output of these commands (run on the GPU box; <dir> is the output root):\n\n"
+                + "\n".join(cmds) + "\n\nCounter scale factors from each run's own 512 MiB device copy "
+                "(`__amd_rocclr_copyBuffer`, 512 MiB read and written): " + "; ".join(cal_notes) + ".\n\n"
+                "| section | kernel | grid (work-items) | dispatches | median us | mean us | algorithmic bytes or FLOPs "
+                "per dispatch | rate at the median | FETCH KiB/dispatch (raw) | WRITE KiB/dispatch (raw) | "
+                "HBM bytes/dispatch (scaled) | HBM traffic / algorithmic bytes |\n"
+                "|---|---|---|---|---|---|---|---|---|---|---|---|\n" + body)
+        with open(os.path.join(ROOT, "profiles", fname), "w") as fh:
+            fh.write(text)
+        wrote += 1
+        log(f"wrote profiles/{fname}")
+    return 0 if wrote else 1
+
+
 def traffic_from_profile(kernel: str):
     """HBM bytes per launch of the C2 decode kernel from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel calibration; written by
+    `bench.py --summarize`), or None."""
     path = os.path.join(ROOT, "profiles", "decode_c2_bf16.md")
     try:
         for line in open(path):
             cells = [c.strip() for c in line.split("|")]
-            if len(cells) > 11 and cells[1] == "C2" and cells[2].strip("`").startswith(kernel):
-                return int(float(cells[10]))
+            if len(cells) > 12 and cells[1] == "C2" and cells[2].strip("`").startswith(kernel):
+                return int(float(cells[11]))
     except (OSError, ValueError):
         pass
     return None
+
+
+# sections of the secondary measurements (--only runs one, for a profiler run)
+SECTIONS = ("c1", "c2", "c2append", "c4", "c5int8", "c5fp8", "neighbours", "trait", "c3", "c4prefill", "c3int8",
+            "c3fp8")
+
+
+def run_sections(ctx, args, lens, sel) -> list:
+    """The secondary measurements: all of them, or the one --only names."""
+    import torch
+    import llm_hip
+    from llm_hip import workloads
+
+    secondary = []
+    # secondaries time at least 100 steps whatever --steps is (the driver passes few)
+    sec_steps, sec_warm = max(100, args.steps), max(10, args.warmup)
+    if sel("c1"):
+        w1, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, sec_warm,
+                               seed=workloads.SEED_BASE, free=0.0)
+        if not args.no_cpu:
+            r["cpu"] = cpu_decode_times(w1, 1.0)
+        del w1
+        secondary.append(r)
+        log(f"C1: {r}")
+    if sel("c2append"):
+        _, r = measure_decode(ctx, "C2 append + attend (kir-ai's step order: llh_kv_append then llh_paged_decode)",
+                              lens, 16, 8, llm_hip.KV_BF16, sec_steps, sec_warm, seed=workloads.SEED_BASE + 1,
+                              append=True)
+        secondary.append(r)
+        log(f"C2 append+attend: {r}")
+        torch.cuda.empty_cache()
+    if sel("c4"):
+        L, W = 32768, 4096
+        _, r = measure_decode(ctx, "C4 decode 4x32768 W=4096", [L] * 4, 16, 8, llm_hip.KV_BF16, sec_steps,
+                              sec_warm, window=W, resident_from=[(L - W) // BT] * 4, seed=workloads.SEED_BASE + 3)
+        secondary.append(r)
+        log(f"C4 decode: {r}")
+    for fmt, nm in ((llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
+        if not sel("c5" + nm):
+            continue
+        wq, r = measure_decode(ctx, f"C5 decode {nm} B=64 L=8192 Hq32/Hkv8", [8192] * 64, 32, 8, fmt,
+                               sec_steps, sec_warm, seed=workloads.SEED_BASE + 4, free=0.0)
+        if not args.no_cpu:
+            r["cpu"] = cpu_decode_times(wq, 1.0, sample_seqs=4)
+        secondary.append(r)
+        log(f"C5 {nm}: {r}")
+        del wq
+        torch.cuda.empty_cache()
+    if sel("neighbours"):
+        secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))
+    if sel("trait"):
+        r = measure_trait_c1(ctx, 200, 2.0, not args.no_cpu)
+        secondary.append(r)
+        log(f"trait C1: {r}")
+    for key, name, B, prefix, chunk, Hq, Hkv, window, res, fmt in (
+            ("c3", "C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_BF16),
+            ("c4prefill", "C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096,
+             llm_hip.KV_BF16),
+            ("c3int8", "C3 prefill over int8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_INT8),
+            ("c3fp8", "C3 prefill over fp8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_FP8_E4M3)):
+        if not sel(key):
+            continue
+        step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res, fmt)
+        pms = time_steps(step, sec_steps, sec_warm)
+        _, pkms = time_steps(step, sec_steps, 0, kernel_timing=(ctx, "prefill"))
+        if ctx.device_errors() != 0:
+            raise RuntimeError(f"{name}: device error flags set")
+        tf = flops / (pms * 1e-3) / 1e12
+        r = {"config": name, "us_per_step": round(pms * 1e3, 2),
+             "kernel_us": round(pkms * 1e3, 2) if pkms <= pms else None, "tflops": round(tf, 1),
+             "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
+             "flops_per_step": flops}
+        if not args.no_cpu and fmt == llm_hip.KV_BF16:
+            r["cpu"] = cpu_prefill_times(keep, B, prefix, chunk, Hq, Hkv, window, 16, 1.0)
+        secondary.append(r)
+        log(f"{name}: {r}")
+        del keep
+        torch.cuda.empty_cache()
+    return secondary
 
 
 def main() -> int:
@@ -472,7 +764,14 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-mb", type=int, default=512,
                     help="size of the plain device copy that measures the copy-bandwidth ceiling (0 = skip)")
+    ap.add_argument("--only", choices=sorted(SECTIONS),
+                    help="run one measurement (and the copy that calibrates the counters) for a profiler run; "
+                         "prints its record instead of the headline line")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="write profiles/*.md from rocprofv3 csv output under DIR/<section>/{kt,fetch,write,mfma}")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize(args.summarize)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (the batch shards by sequence with "
               "no communication). Run with --gpus 1.", file=sys.stderr)
@@ -487,9 +786,21 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     ctx = llm_hip.Context(0)
+    only = args.only
+
+    def sel(name):
+        return only is None or only == name
+
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    if only is not None and only != "c2":
+        records = run_sections(ctx, args, lens, sel)
+        if args.copy_mb > 0:
+            records.append({"copy": measure_copy(args.copy_mb)})
+        print(json.dumps({"only": only, "records": records}), flush=True)
+        ctx.close()
+        return 0
 
     # ---- headline: C2 batched paged decode ----
-    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     log(f"C2 decode: B=32 sum(L)={int(lens.sum())}")
     w, c2 = measure_decode(ctx, "C2", lens, 16, 8, llm_hip.KV_BF16, args.steps, args.warmup,
                            seed=workloads.SEED_BASE + 1)
@@ -514,49 +825,7 @@ def main() -> int:
     del w
     torch.cuda.empty_cache()
 
-    secondary = []
-    if not args.no_secondary:
-        sec_steps = max(10, args.steps // 2)
-        w1, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, args.warmup,
-                               seed=workloads.SEED_BASE, free=0.0)
-        if not args.no_cpu:
-            r["cpu"] = cpu_decode_times(w1, 1.0)
-        del w1
-        secondary.append(r)
-        log(f"C1: {r}")
-        L, W = 32768, 4096
-        _, r = measure_decode(ctx, "C4 decode 4x32768 W=4096", [L] * 4, 16, 8, llm_hip.KV_BF16, sec_steps,
-                              args.warmup, window=W, resident_from=[(L - W) // BT] * 4, seed=workloads.SEED_BASE + 3)
-        secondary.append(r)
-        log(f"C4 decode: {r}")
-        for fmt, nm in ((llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
-            wq, r = measure_decode(ctx, f"C5 decode {nm} B=64 L=8192 Hq32/Hkv8", [8192] * 64, 32, 8, fmt,
-                                   sec_steps, args.warmup, seed=workloads.SEED_BASE + 4, free=0.0)
-            if not args.no_cpu:
-                r["cpu"] = cpu_decode_times(wq, 1.0, sample_seqs=4)
-            secondary.append(r)
-            log(f"C5 {nm}: {r}")
-            del wq
-            torch.cuda.empty_cache()
-        secondary.extend(measure_neighbours(ctx, sec_steps, args.warmup))
-        for name, B, prefix, chunk, Hq, Hkv, window, res in (
-                ("C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None),
-                ("C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096)):
-            step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res)
-            pms = time_steps(step, sec_steps, args.warmup)
-            _, pkms = time_steps(step, sec_steps, 0, kernel_timing=(ctx, "prefill"))
-            if ctx.device_errors() != 0:
-                raise RuntimeError(f"{name}: device error flags set")
-            tf = flops / (pms * 1e-3) / 1e12
-            r = {"config": name, "us_per_step": round(pms * 1e3, 2), "kernel_us": round(pkms * 1e3, 2), "tflops": round(tf, 1),
-                 "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
-                 "flops_per_step": flops}
-            if not args.no_cpu:
-                r["cpu"] = cpu_prefill_times(keep, B, prefix, chunk, Hq, Hkv, window, 16, 1.0)
-            secondary.append(r)
-            log(f"{name}: {r}")
-            del keep
-            torch.cuda.empty_cache()
+    secondary = [] if args.no_secondary or only == "c2" else run_sections(ctx, args, lens, sel)
 
     line = {
         "metric": METRIC,
@@ -585,12 +854,13 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{c2['kernel']}, G=2, bf16 (the merge launch is excluded)",
-            "achieved": c2["kernel_gbs"],
+            "kernel": f"{c2['kernel']}, G=2, bf16 (the merge launch is excluded)"
+                      if c2["kernel_gbs"] else "the whole step (kernel events exceeded the step time)",
+            "achieved": c2["kernel_gbs"] or c2["hbm_gbs"],
             "kernel_us": c2["kernel_us"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "frac": round((c2["kernel_gbs"] or c2["hbm_gbs"]) / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(c2["kernel"].split(" ")[0]),
         },
         "cpu_baseline": cpu,
