@@ -130,6 +130,22 @@ def decode_kernel(request, opts):
     return request.param
 
 
+def test_decode_c1_matches_golden_fixture(ctx, decode_kernel):
+    """configs[0] against the committed fixture tests/golden/c1_decode.json (written by
+    tests/golden/make_golden.py): the same seeded rows go into a 32-block pool and the
+    device output is held to the parity bar against the fixture's f32 output."""
+    import json
+
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "c1_decode.json")))
+    L, Hq, Hkv = g["row_count"], g["q_heads"], g["kv_heads"]
+    assert (L, Hq, Hkv, g["head_dim"]) == (512, 16, 8, D) and g["seed"] == workloads.SEED_BASE
+    pool, q = build_case(ctx, identity_batch([L]), Hq, Hkv, llm_hip.KV_BF16, g["seed"])
+    assert np.array_equal(q, oracle.normal_bf16(g["seed"] + 3, Hq * D))  # the fixture's q
+    out = run_decode(ctx, pool, identity_batch([L]), q, Hq, 0, g["scale"])
+    assert ctx.device_errors() == 0, ctx.last_error()
+    assert_parity(out, np.array(g["output_f32"], np.float32), what=f"C1 golden kernel={decode_kernel}")
+
+
 def test_decode_c2_full_size(ctx, decode_kernel):
     """B=32, L~U[256,4096], permuted pool +10% free blocks."""
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
