@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 2
+#define LLH_ABI_VERSION 3
 
 /* Status codes.  Mirrors MathError / KvCacheError
  * (crates/llm-backend/src/core/math.rs:10-15, crates/llm-kv-cache/src/lib.rs). */
@@ -100,7 +100,8 @@ typedef enum llh_option {
   LLH_OPT_DECODE_KERNEL = 0,         /* (LLH_DECODE_KERNEL: "split" = 1, "stream" = 2) 0 = by step size */
   LLH_OPT_DECODE_SPLIT_BLOCKS = 1,   /* (LLH_DECODE_SPLIT_BLOCKS) blocks per split-K split, 0 = planned */
   LLH_OPT_DECODE_STREAM_WGS = 2,     /* (LLH_DECODE_STREAM_WGS) stream-kernel workgroups, 0 = 2 per CU */
-  LLH_OPT_FORCE_GENERIC = 3,         /* (LLH_FORCE_GENERIC) 1 = reference-order decode for every shape */
+  LLH_OPT_FORCE_GENERIC = 3,         /* (LLH_FORCE_GENERIC) 1 = the element-wise decode and prefill
+                                        kernels for every shape */
   LLH_OPT_PREFILL_HEADS_PER_WG = 4,  /* (LLH_PREFILL_HEADS_PER_WG) 1 = one query head per prefill workgroup */
   LLH_OPT_TRAIT_REFERENCE_ORDER = 5, /* (LLH_TRAIT_REFERENCE_ORDER) trait-mirror attention: 0 = the tuned
                                         kernels where the shape allows, 1 = the reference-order kernel always */
@@ -121,6 +122,7 @@ typedef struct llh_metrics {
   uint64_t shape_errors;
   uint64_t stream_decode_calls; /* decode calls that ran the persistent stream kernel */
   uint64_t trait_tuned_calls;   /* trait-mirror attention calls served by the tuned decode kernels */
+  uint64_t generic_prefill_calls; /* prefill calls that ran the element-wise kernel */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Waits for the device, then reads (and optionally clears) the sticky error
@@ -260,10 +262,13 @@ typedef struct llh_prefill_desc {
   const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] */
 } llh_prefill_desc;
 
-/* d_q, d_out: [total_q_rows][Hq][head_dim] bf16, 16-byte aligned (else
- * LLH_ERR_UNSUPPORTED).  Every pool format: int8 / fp8 blocks are dequantised
- * (code * scale, rounded to bf16) as the key/value tiles are staged, so the
- * result is attention over the dequantised cache (layer.rs:650-656). */
+/* d_q, d_out: [total_q_rows][Hq][head_dim] bf16 (2-byte aligned).  Every pool
+ * format: int8 / fp8 blocks are dequantised, so the result is attention over
+ * the dequantised cache (layer.rs:650-656).  head_dim 128 with 16-token blocks
+ * and 16-byte aligned rows runs the MFMA kernel (codes * scale rounded to bf16
+ * as the key/value tiles are staged); every other shape with head_dim <= 512
+ * runs an element-wise kernel (sequential f32 dot products, online softmax in
+ * f32); head_dim > 512 returns LLH_ERR_UNSUPPORTED. */
 int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_desc *desc, const void *d_q,
                       void *d_out, float score_scale, void *stream);
 

@@ -289,6 +289,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->shape_errors = ctx->shape_errors.load();
   out->stream_decode_calls = ctx->stream_decode_calls.load();
   out->trait_tuned_calls = ctx->trait_tuned_calls.load();
+  out->generic_prefill_calls = ctx->generic_prefill_calls.load();
   return LLH_OK;
 }
 
@@ -743,15 +744,20 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   if (desc->total_q_rows < 0 || desc->max_chunk_len < 0)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "row counts must be >= 0");
   const PoolView &pv = pool->view;
-  if (pv.head_dim != kFastHeadDim || pv.block_tokens != kFastBlockTokens) {
+  if (pv.head_dim > kGenericPrefillMaxDim) {
     ctx->not_handled++;
-    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill takes pools with head_dim 128 and 16-token blocks");
+    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill takes head_dim <= " + std::to_string(kGenericPrefillMaxDim));
   }
   if (!d_q || !d_out || !desc->d_chunk_starts || !desc->d_context_lens || !desc->d_block_tables)
     return ctx->fail(LLH_ERR_NULL, "null device pointer in prefill call");
-  if (((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) != 0)
-    return ctx->fail(LLH_ERR_UNSUPPORTED, "prefill q and output rows must be 16-byte aligned");
+  if (((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 1) != 0)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "prefill q and output must be bf16-aligned (2 bytes)");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
+  // the tuned MFMA kernel takes head_dim 128, 16-token blocks and 16-byte aligned
+  // rows; every other call runs the element-wise kernel
+  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
+                    ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) == 0 &&
+                    ctx->opt(LLH_OPT_FORCE_GENERIC) == 0;
   PrefillArgs a{};
   a.pool = pv;
   a.q = static_cast<const uint16_t *>(d_q);
@@ -766,13 +772,20 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   a.window = desc->window;
   a.q_tiles = std::max(1, (desc->max_chunk_len + 127) / 128);
   a.scale_log2e = score_scale * 1.4426950408889634f;
+  a.scale = score_scale;
   ctx->prefill_calls++;
   auto ev = ctx->timing_begin(static_cast<hipStream_t>(stream));
-  // two query heads of a kv head per workgroup share its K/V tile stream when the group is even
-  const int group = desc->num_q_heads / pv.kv_heads;
-  const int hpw_env = ctx->opt(LLH_OPT_PREFILL_HEADS_PER_WG);
-  const int variant = (hpw_env == 1 || group % 2 != 0) ? kPrefillOneHead : kPrefillTwoHeads;
-  hipError_t e = launch_prefill(a, variant, static_cast<hipStream_t>(stream));
+  hipError_t e;
+  if (fast) {
+    // two query heads of a kv head per workgroup share its K/V tile stream when the group is even
+    const int group = desc->num_q_heads / pv.kv_heads;
+    const int hpw_env = ctx->opt(LLH_OPT_PREFILL_HEADS_PER_WG);
+    const int variant = (hpw_env == 1 || group % 2 != 0) ? kPrefillOneHead : kPrefillTwoHeads;
+    e = launch_prefill(a, variant, static_cast<hipStream_t>(stream));
+  } else {
+    ctx->generic_prefill_calls++;
+    e = launch_prefill_generic(a, desc->total_q_rows, static_cast<hipStream_t>(stream));
+  }
   ctx->timing_end(1, ev, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "prefill launch");
   return LLH_OK;

@@ -36,7 +36,7 @@
 // Each group keeps its own online-softmax state (running max in log2 units,
 // sum, 8 output dims per lane per head); groups, wavefronts and splits are
 // merged by log-sum-exp.
-#include "llh_internal.h"
+#include "device_common.h"
 
 namespace llh {
 
@@ -66,13 +66,6 @@ __device__ __forceinline__ uint32_t ld_nt4(const char *p) {
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
@@ -1202,20 +1195,6 @@ __device__ __forceinline__ float load_as_f32<float>(const void *p, size_t i) {
 template <>
 __device__ __forceinline__ float load_as_f32<uint16_t>(const void *p, size_t i) {
   return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(p)[i] << 16);
-}
-
-__device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_t blk, int h, int t, int d) {
-  const int64_t bh = blk * p.kv_heads + h;
-  const int64_t idx = tensor ? (bh * p.head_dim + d) * p.block_tokens + t : (bh * p.block_tokens + t) * p.head_dim + d;
-  const void *base = tensor ? p.v : p.k;
-  const void *sc = tensor ? p.v_scales : p.k_scales;
-  if (p.format == kBf16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(base)[idx] << 16);
-  if (p.format == kInt8) {
-    const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + t]);
-    return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
-  }
-  const uint32_t code = reinterpret_cast<const uint8_t *>(base)[idx];
-  return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * reinterpret_cast<const float *>(sc)[bh];
 }
 
 __device__ __forceinline__ bool slot_of(const GenericDecodeArgs &a, const int32_t *table, int pos, int64_t &blk,

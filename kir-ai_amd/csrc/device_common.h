@@ -1,0 +1,33 @@
+// Device helpers shared by the HIP kernels of libllm_hip (decode, prefill, KV writes).
+#pragma once
+
+#include "llh_internal.h"
+
+namespace llh {
+
+// f32 -> bf16 bits, round to nearest even; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// One dequantised K (tensor 0) or V (tensor 1) element of any pool format and
+// shape: token t of block blk, kv head h, dim d (K rows token-major, V rows
+// dim-major).
+__device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_t blk, int h, int t, int d) {
+  const int64_t bh = blk * p.kv_heads + h;
+  const int64_t idx = tensor ? (bh * p.head_dim + d) * p.block_tokens + t : (bh * p.block_tokens + t) * p.head_dim + d;
+  const void *base = tensor ? p.v : p.k;
+  const void *sc = tensor ? p.v_scales : p.k_scales;
+  if (p.format == kBf16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(base)[idx] << 16);
+  if (p.format == kInt8) {
+    const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + t]);
+    return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
+  }
+  const uint32_t code = reinterpret_cast<const uint8_t *>(base)[idx];
+  return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * reinterpret_cast<const float *>(sc)[bh];
+}
+
+}  // namespace llh

@@ -47,7 +47,7 @@ struct llh_ctx {
   int cus = 256;  // compute units of the device (sizes the persistent decode grid)
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
-      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0};
+      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0};
   std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
 
   // per-stream workspaces; ws_mu guards the list and ws_min_bytes

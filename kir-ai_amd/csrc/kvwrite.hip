@@ -16,20 +16,13 @@
 // with the rounded scale (the symmetric rule of format.rs:702-737 at per
 // (token, head) granularity); fp8 scale = absmax / 448 per (block, head) and
 // codes are OCP e4m3fn, round to nearest even, saturating.
-#include "llh_internal.h"
+#include "device_common.h"
 
 namespace llh {
 
 namespace {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
 
 __device__ __forceinline__ int8_t quant_int8(float x, float s) {
   if (s == 0.0f) return 0;

@@ -91,6 +91,7 @@ struct PrefillArgs {
   int32_t window;
   int32_t q_tiles;          // tiles of 128 rows per sequence in the grid
   float scale_log2e;
+  float scale;              // score_scale (generic kernel)
 };
 
 struct WriteBlocksArgs {
@@ -172,6 +173,10 @@ hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_
 // sharing the K/V tiles
 enum { kPrefillOneHead = 1, kPrefillTwoHeads = 2 };
 hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s);
+constexpr int kGenericPrefillMaxDim = 512;  // head_dim bound of the generic prefill kernel
+// Element-wise prefill for every other shape (any head_dim <= 512, block size,
+// row alignment); total_rows = chunk_starts[num_seqs].
+hipError_t launch_prefill_generic(const PrefillArgs &a, int total_rows, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);

@@ -38,7 +38,7 @@
 // 16-key step is {4h..4h+3, 8+4h..8+4h+3} for lane half h; the V^T operand is
 // read from LDS with the same key order, so no transpose is ever done.
 // Softmax statistics are kept per query column in log2 units (online softmax).
-#include "llh_internal.h"
+#include "device_common.h"
 
 namespace llh {
 
@@ -475,6 +475,113 @@ void launch_prefill_fmt(const PrefillArgs &a, int variant, int grid, hipStream_t
     hipLaunchKernelGGL((paged_prefill_kernel<1, FMT>), dim3(grid), dim3(kPrefillThreads), 0, s, a);
 }
 
+// Prefill for every shape the tuned kernel does not take (head_dim != 128,
+// block size != 16, q / output rows not 16-byte aligned), and for the
+// force-generic option.  One workgroup per (chunk row, query head) attends
+// [lo(pos), pos] in chunks of 256 keys: scores are sequential f32 dot
+// products (the reference's order), softmax is online in f32 with expf, and
+// the pool is read element-wise in any format, dequantised.
+__global__ __launch_bounds__(256) void prefill_generic_kernel(const PrefillArgs a) {
+  const int r = blockIdx.x;  // global chunk row
+  const int h = blockIdx.y;  // query head
+  const int tid = threadIdx.x;
+  // the sequence of row r: the last b with chunk_starts[b] <= r
+  int lo_b = 0, hi_b = a.num_seqs;
+  while (hi_b - lo_b > 1) {
+    const int mid = (lo_b + hi_b) / 2;
+    if (a.chunk_starts[mid] <= r) lo_b = mid;
+    else hi_b = mid;
+  }
+  const int b = lo_b;
+  const int c0 = a.chunk_starts[b];
+  const int chunk = a.chunk_starts[b + 1] - c0;
+  const int ctx = a.context_lens[b];
+  const int i = r - c0;
+  if (i < 0 || i >= chunk || ctx < chunk) return;
+  const int bt = a.pool.block_tokens;
+  const int Dh = a.pool.head_dim;
+  const int Hq = a.q_heads;
+  {
+    const int first_lo = a.window > 0 ? max(0, ctx - chunk - a.window + 1) : 0;
+    if ((int64_t)(ctx - first_lo) > (int64_t)a.max_blocks * bt) {  // would alias its own table entries
+      if (tid == 0 && i == 0 && h == 0) atomicOr(a.err, kErrSpan);
+      return;
+    }
+  }
+  const int pos = ctx - chunk + i;
+  const int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
+  const int kvh = h / (Hq / a.pool.kv_heads);
+  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
+  const size_t row = ((size_t)r * Hq + h) * Dh;
+
+  __shared__ float qs[kGenericPrefillMaxDim];
+  __shared__ float w[256];
+  __shared__ float red[256];
+  __shared__ int64_t kblk[256];
+  __shared__ int koff[256];
+  __shared__ int s_bad;
+  for (int d = tid; d < Dh; d += 256) qs[d] = __uint_as_float((uint32_t)a.q[row + d] << 16);
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+
+  float m = -INFINITY, l = 0.0f;
+  float acc[kGenericPrefillMaxDim / 256] = {};
+  for (int k0 = lo; k0 <= pos; k0 += 256) {
+    const int n = min(256, pos - k0 + 1);
+    float s = -INFINITY;
+    if (tid < n) {
+      const int kp = k0 + tid;
+      const int64_t blk = table[(kp / bt) % a.max_blocks];
+      const int off = kp % bt;
+      kblk[tid] = blk;
+      koff[tid] = off;
+      if (blk >= 0 && blk < a.pool.n_blocks) {
+        float dot = 0.0f;
+        for (int d = 0; d < Dh; d++) dot = __fadd_rn(dot, __fmul_rn(pool_elem(a.pool, 0, blk, kvh, off, d), qs[d]));
+        s = __fmul_rn(dot, a.scale);
+      } else {
+        atomicOr(&s_bad, 1);
+      }
+    }
+    red[tid] = s;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+      if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
+      __syncthreads();
+    }
+    const float m_new = fmaxf(m, red[0]);
+    __syncthreads();
+    const float alpha = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, m_new));
+    const float e = s == -INFINITY ? 0.0f : expf(__fsub_rn(s, m_new));
+    w[tid] = e;
+    red[tid] = e;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+      if (tid < st) red[tid] += red[tid + st];
+      __syncthreads();
+    }
+    l = l * alpha + red[0];
+    m = m_new;
+#pragma unroll
+    for (int j = 0; j < kGenericPrefillMaxDim / 256; j++) {
+      const int d = tid + 256 * j;
+      if (d >= Dh) break;
+      float o = acc[j] * alpha;
+      for (int t = 0; t < n; t++)
+        if (w[t] != 0.0f) o = __fadd_rn(o, __fmul_rn(w[t], pool_elem(a.pool, 1, kblk[t], kvh, koff[t], d)));
+      acc[j] = o;
+    }
+    __syncthreads();  // w, kblk, koff and red are rewritten by the next chunk
+  }
+  if (tid == 0 && s_bad) atomicOr(a.err, kErrBadBlock);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int j = 0; j < kGenericPrefillMaxDim / 256; j++) {
+    const int d = tid + 256 * j;
+    if (d < Dh) a.out[row + d] = f32_to_bf16_rne(acc[j] * inv);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s) {
@@ -493,6 +600,12 @@ hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s) {
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_generic(const PrefillArgs &a, int total_rows, hipStream_t s) {
+  if (total_rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(prefill_generic_kernel, dim3(total_rows, a.q_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -129,6 +129,7 @@ class Metrics(ctypes.Structure):
         ("shape_errors", ctypes.c_uint64),
         ("stream_decode_calls", ctypes.c_uint64),
         ("trait_tuned_calls", ctypes.c_uint64),
+        ("generic_prefill_calls", ctypes.c_uint64),
     ]
 
 

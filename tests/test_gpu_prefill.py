@@ -151,18 +151,91 @@ def test_prefill_quantized_ragged_full_oracle(ctx, fmt, W):
     assert_parity(out, ref, what=f"ragged fmt={fmt} W={W}")
 
 
-def test_prefill_rejects_unaligned_rows(ctx):
+def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm_hip.KV_BF16, misalign=False):
+    """Any pool shape: the rows go in through llh_kv_write_blocks, prefill runs on q / out
+    that are 2 bytes off 16-byte alignment when misalign is set.  Returns what the oracle
+    check needs and the output."""
     import torch
 
-    pool = ctx.pool(llm_hip.KV_BF16, BT, 8, D, 4)
+    ctxlen = [p + c for p, c in zip(prefix, chunk)]
+    batch = workloads.paged_batch(ctxlen, bt, 0.10, seed)
+    ids, sk = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 1, b, lo, hi, Hkv, head_dim), Hkv,
+                                      head_dim)
+    _, sv = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, Hkv, head_dim), Hkv,
+                                    head_dim)
+    pool = ctx.pool(fmt, bt, Hkv, head_dim, batch.n_blocks)
+    ctx.write_blocks(pool, to_dev(ids), to_dev(sk), to_dev(sv))
+    starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
+    n = int(starts[-1]) * Hq * head_dim
+    q = oracle.normal_bf16(seed + 3, n)
+    off = 1 if misalign else 0
+    qbuf = torch.zeros(n + 8, dtype=torch.int16, device="cuda")
+    qbuf[off:off + n] = to_dev(q)
+    obuf = torch.full((n + 8,), 0x7FC0, dtype=torch.int16, device="cuda")
+    d_starts, d_lens, d_tab = to_dev(starts), to_dev(batch.seq_lens), to_dev(batch.tables)
+    desc = ctx.prefill_desc(d_starts, d_lens, d_tab, Hq, max(chunk), window, total_q_rows=int(starts[-1]))
+    scale = 1.0 / math.sqrt(head_dim)
+    ctx.paged_prefill(pool, desc, qbuf[off:off + n], obuf[off:off + n], scale)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    opool = oracle.Pool.from_raw(fmt, bt, Hkv, head_dim, batch.n_blocks, pool.raw())
+    st, ref = opool.prefill(Hq, starts, batch.seq_lens, batch.tables, window, q, scale, threads=16)
+    assert st == oracle.OK
+    return from_dev_bf16(obuf[off:off + n]), ref
+
+
+@pytest.mark.parametrize("head_dim,bt,Hq,Hkv,W,fmt", [
+    (256, 16, 8, 4, 0, llm_hip.KV_BF16),       # Gemma-like head_dim
+    (256, 16, 8, 4, 200, llm_hip.KV_INT8),
+    (64, 32, 12, 4, 48, llm_hip.KV_BF16),      # odd group (3), 32-token blocks, window
+    (96, 8, 4, 1, 0, llm_hip.KV_FP8_E4M3),     # MQA, 8-token blocks
+    (128, 32, 16, 8, 0, llm_hip.KV_INT8),      # tuned head_dim, other block size
+])
+def test_prefill_generic_shapes_full_oracle(ctx, head_dim, bt, Hq, Hkv, W, fmt):
+    """Shapes the MFMA kernel does not take run the element-wise prefill kernel: ragged
+    chunks (an empty one included) over cached prefixes, every row against the oracle."""
+    before = ctx.metrics()["generic_prefill_calls"]
+    out, ref = build_shape(ctx, [100, 0, 37, 5], [37, 70, 0, 130], Hq, Hkv, W, 900 + head_dim + bt, head_dim, bt, fmt)
+    assert ctx.metrics()["generic_prefill_calls"] == before + 1
+    assert_parity(out, ref, what=f"generic D={head_dim} bt={bt} fmt={fmt} W={W}")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_prefill_unaligned_rows_take_the_generic_kernel(ctx, fmt):
+    """q and out 2 bytes off 16-byte alignment on the tuned shape: the element-wise kernel
+    runs and matches the oracle like the MFMA kernel."""
+    before = ctx.metrics()["generic_prefill_calls"]
+    out, ref = build_shape(ctx, [300, 0], [129, 64], 16, 8, 0, 77, D, BT, fmt, misalign=True)
+    assert ctx.metrics()["generic_prefill_calls"] == before + 1
+    assert_parity(out, ref, what=f"unaligned fmt={fmt}")
+
+
+@pytest.mark.parametrize("W", [0, 300])
+def test_prefill_force_generic_matches_mfma_kernel(ctx, opts, W):
+    """The same call on the tuned shape through both kernels (the force-generic option):
+    each within the bar of the oracle, and of each other."""
+    prefix, chunk = [0, 700], [200, 333]
+    fast, ref = build_shape(ctx, prefix, chunk, 16, 4, W, 41 + W, D, BT)
+    opts(llm_hip.OPT_FORCE_GENERIC, 1)
+    before = ctx.metrics()["generic_prefill_calls"]
+    gen, ref2 = build_shape(ctx, prefix, chunk, 16, 4, W, 41 + W, D, BT)
+    assert ctx.metrics()["generic_prefill_calls"] == before + 1
+    assert np.array_equal(ref, ref2)
+    assert_parity(fast, ref, what="mfma")
+    assert_parity(gen, ref, what="generic")
+    assert_parity(gen, oracle.bf16_to_f32(fast), what="generic vs mfma")
+
+
+def test_prefill_rejects_head_dim_beyond_generic_bound(ctx):
+    import torch
+
+    pool = ctx.pool(llm_hip.KV_BF16, BT, 1, 520, 2)
     z = torch.zeros(2, dtype=torch.int32, device="cuda")
-    desc = ctx.prefill_desc(z, z[:1], z.view(1, 2), 16, 1, 0, total_q_rows=1)
-    buf = torch.zeros(16 * D + 1, dtype=torch.int16, device="cuda")
-    good = torch.zeros(16 * D, dtype=torch.int16, device="cuda")
-    for q, out in ((buf[1:], good), (good, buf[1:])):
-        with pytest.raises(llm_hip.LlhError) as e:
-            ctx.paged_prefill(pool, desc, q, out, 0.1)
-        assert e.value.status == llm_hip.ERR_UNSUPPORTED
+    desc = ctx.prefill_desc(z, z[:1], z.view(1, 2), 1, 1, 0, total_q_rows=1)
+    buf = torch.zeros(520, dtype=torch.int16, device="cuda")
+    with pytest.raises(llm_hip.LlhError) as e:
+        ctx.paged_prefill(pool, desc, buf, buf, 0.1)
+    assert e.value.status == llm_hip.ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("W", [0, 300])
@@ -177,11 +250,14 @@ def test_prefill_two_heads_per_workgroup_match_one(ctx, W, opts):
     assert np.array_equal(one, two)
 
 
-def test_prefill_span_beyond_table_row_raises_flag(ctx):
+@pytest.mark.parametrize("generic", [0, 1])
+def test_prefill_span_beyond_table_row_raises_flag(ctx, opts, generic):
     """Every key from the chunk's first row to its last must be resident at once; a table
     row shorter than that span (rows are read modulo their length) raises the span flag
-    instead of attending aliased blocks."""
+    instead of attending aliased blocks (both prefill kernels)."""
     import torch
+
+    opts(llm_hip.OPT_FORCE_GENERIC, generic)
 
     pool = ctx.pool(llm_hip.KV_BF16, BT, 4, D, 16)
     starts = torch.tensor([0, 20], dtype=torch.int32, device="cuda")
