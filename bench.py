@@ -337,7 +337,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     B, Hkv, Hq = 32, 8, 16
     # decode: the C2 batch's 32 new tokens (one row per sequence, scattered slots);
     # prefill: C3's 8 x 512-token chunks, whole 16-token blocks (llh_kv_write_blocks)
-    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8")):
+    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
         nblk, H = 8 * 512 // BT, 4
         pool = ctx.pool(fmt, BT, H, D, 8192)
         ids = torch.randperm(8192, generator=g, device="cuda")[:nblk].to(torch.int32)
@@ -346,20 +346,24 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         ms = time_steps(lambda s: ctx.write_blocks(pool, ids, k, v, stream=s), steps, warmup)
         esz = 2 if fmt == llm_hip.KV_BF16 else 1
         T = nblk * BT
-        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + (T * H * 2 * 2 if esz == 1 else 0)
+        scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: nblk * H * 4 * 2}.get(fmt, 0)
+        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + scales
         out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
                     "us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
                     "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_d128_kernel"})
         del pool
-    for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv)):
+    for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv),
+                          (llm_hip.KV_FP8_E4M3, "fp8", B, Hkv)):
         pool = ctx.pool(fmt, BT, H, D, 8192)
         slots = torch.randperm(8192 * BT, generator=g, device="cuda")[:T].to(torch.int64)
         k = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
         v = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.append(pool, slots, k, v, stream=s), steps, warmup)
         esz = 2 if fmt == llm_hip.KV_BF16 else 1
-        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + T * 8 + (T * H * 2 * 2 if esz == 1 else 0)
+        # fp8: the block's scale is read and written per token (an earlier row re-encode is not counted)
+        scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: T * H * 4 * 2 * 2}.get(fmt, 0)
+        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + T * 8 + scales
         out.append({"config": f"KV append C2 batch ({T} tokens, Hkv{H}, {nm})", "us_per_step": round(ms * 1e3, 2),
                     "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

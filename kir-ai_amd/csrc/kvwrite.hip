@@ -80,13 +80,15 @@ __device__ __forceinline__ float row16_max(float v) {
   return v;
 }
 
-// Whole 16-token blocks of head_dim 128, bf16 or int8 pools: one workgroup of
+// Whole 16-token blocks of head_dim 128, any pool format: one workgroup of
 // 256 lanes per (block, head).  Lane (t = lane / 16, c = lane % 16) loads the
 // 16 B of token t at dims 8c .. 8c+7 of K and of V (coalesced), writes K rows
 // straight out, and V is transposed through LDS so that every lane then writes
 // 16 B (bf16) or 8 B (int8) of one dim row: every global access is a full,
 // coalesced vector access.  int8: the per-(token, head) scale is the 16 lanes'
-// absmax, then the same f16 rounding and code rule as the generic kernel.
+// absmax, then the same f16 rounding and code rule as the generic kernel; fp8:
+// the per-(block, head) scale is the workgroup's absmax / 448, then the generic
+// kernel's encode, so both kernels write identical bytes.
 __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlocksArgs a) {
   constexpr int BT = 16, Dh = 128;
   const int i = blockIdx.x;
@@ -117,9 +119,44 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
         make_uint4(w[0], w[1], w[2], w[3]);
     return;
   }
-  // int8 with per (token, head) fp16 scales
   __shared__ uint8_t lq[BT][Dh + 16];
   uint32_t codes[2][2];
+  if (a.pool.format == kFp8) {
+    // one f32 scale per (block, head) and tensor: absmax over the block / 448,
+    // codes as the generic kernel computes them (RNE e4m3 of x / scale)
+    __shared__ float red[2][4];
+    float x[2][8];
+    float mx[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int tensor = 0; tensor < 2; tensor++) {
+      const uint4 wv = tensor ? vw : kw;
+      const uint32_t u[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        x[tensor][2 * j] = bf16_to_f32((uint16_t)(u[j] & 0xffffu));
+        x[tensor][2 * j + 1] = bf16_to_f32((uint16_t)(u[j] >> 16));
+        mx[tensor] = fmaxf(mx[tensor], fmaxf(fabsf(x[tensor][2 * j]), fabsf(x[tensor][2 * j + 1])));
+      }
+      mx[tensor] = wave_max(mx[tensor]);
+      if ((tid & 63) == 0) red[tensor][tid >> 6] = mx[tensor];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tensor = 0; tensor < 2; tensor++) {
+      const float m = fmaxf(fmaxf(red[tensor][0], red[tensor][1]), fmaxf(red[tensor][2], red[tensor][3]));
+      const float sc = m == 0.0f ? 0.0f : __fdiv_rn(m, 448.0f);
+      uint32_t q[2] = {0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t code = sc == 0.0f ? 0u : encode_e4m3(__fdiv_rn(x[tensor][j], sc));
+        q[j >> 2] |= code << (8 * (j & 3));
+      }
+      codes[tensor][0] = q[0];
+      codes[tensor][1] = q[1];
+      if (tid == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[bh] = sc;
+    }
+  } else {
+  // int8 with per (token, head) fp16 scales
 #pragma unroll
   for (int tensor = 0; tensor < 2; tensor++) {
     const uint4 wv = tensor ? vw : kw;
@@ -142,6 +179,8 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     codes[tensor][1] = q[1];
     if (c == 0) reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[bh * BT + t] = __builtin_bit_cast(uint16_t, s16);
   }
+  }
+  // one-byte codes (int8 / fp8): K rows straight out, V transposed through LDS
   *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) =
       make_uint2(codes[0][0], codes[0][1]);
   *reinterpret_cast<uint2 *>(&lq[t][8 * c]) = make_uint2(codes[1][0], codes[1][1]);
@@ -445,7 +484,7 @@ hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const bool fast = a.pool.head_dim == 128 && a.pool.block_tokens == 16 &&
-                    (a.pool.format == kBf16 || a.pool.format == kInt8) &&
+                    (a.pool.format == kBf16 || a.pool.format == kInt8 || a.pool.format == kFp8) &&
                     reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
   if (fast)

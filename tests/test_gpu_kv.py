@@ -121,7 +121,7 @@ def test_fp8_quantise_on_write_is_bit_exact(ctx):
             assert np.array_equal(v[blk, h], codes.reshape(BT, D).T) and vs[blk, h] == np.float32(s)
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
 def test_block_write_vector_and_generic_kernels_agree(ctx, fmt):
     """head_dim 128 / 16-token blocks from 16-byte aligned rows take the vector
     kernel; the same rows 2 bytes off alignment take the generic one.  Pools equal."""
