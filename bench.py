@@ -114,6 +114,11 @@ class DecodeWorkload:
         self.ctx.append(self.pool, self.d_slots, self.k_new, self.v_new, stream=stream)
         self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
 
+    def fused_step(self, stream):
+        """The same step as append_step in one call (llh_paged_decode_append)."""
+        self.ctx.paged_decode_append(self.pool, self.desc, self.k_new, self.v_new, self.q, self.out, self.scale,
+                                     stream=stream)
+
     def append_bytes(self) -> int:
         """Algorithmic bytes of the append: the new rows read (bf16) and written (pool format), slots."""
         B = self.batch.seq_lens.size
@@ -470,25 +475,31 @@ LLC_BYTES = 256 << 20  # MI355X Infinity Cache (memory-side last-level cache)
 
 
 def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10,
-                   append=False):
+                   append=False, fused=False):
     """Mean step time over `steps` decode steps.  Steps rotate over enough independent
     copies of the workload (same lengths, own pool, own block permutation and data) that
     the bytes read between two visits of one copy exceed the 256 MB Infinity Cache: every
     step reads its K/V from HBM, not from cache.  append=True times kir-ai's whole decode
-    step instead: the new token's K/V append, then attention over the cache holding it."""
+    step instead: the new token's K/V append, then attention over the cache holding it.  fused=True
+    times the same step through llh_paged_decode_append (one call)."""
     first = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free)
-    nbytes = first.algorithmic_bytes() + (first.append_bytes() if append else 0)
+    nbytes = first.algorithmic_bytes() + (first.append_bytes() if append or fused else 0)
     copies = [first]
     while (len(copies) - 1) * nbytes < 2 * LLC_BYTES:
         copies.append(DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed + 1000 * len(copies), free))
-    if append:
+    if append or fused:
         for c in copies:
             c.prepare_append()
     state = {"i": 0}
 
     def step(stream):
         c = copies[state["i"] % len(copies)]
-        c.append_step(stream) if append else c.step(stream)
+        if fused:
+            c.fused_step(stream)
+        elif append:
+            c.append_step(stream)
+        else:
+            c.step(stream)
         state["i"] += 1
 
     # step time over all timed steps, then the decode kernel alone (library-recorded events)
@@ -569,6 +580,7 @@ def summarize(root: str) -> int:
     alg = {  # section -> {kernel prefix: (unit, amount)}
         "c2": {"paged_decode_stream_kernel": ("B", c2b)},
         "c2append": {"paged_decode_stream_kernel": ("B", c2b), "append_kernel": ("B", append_b)},
+        "c2fused": {"paged_decode_stream_kernel": ("B", c2b + append_b)},
         "c1": {"paged_decode_kernel": ("B", decode_bytes([512], 16, 8, 0))},
         "c4": {"paged_decode_kernel": ("B", decode_bytes([32768] * 4, 16, 8, 0, 4096))},
         "c5int8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 1))},
@@ -581,7 +593,7 @@ def summarize(root: str) -> int:
     }
     groups = (
         ("decode_c2_bf16.md", "Paged GQA decode, C2 (B=32, L~U[256,4096], Hq16/Hkv8, bf16 KV), and kir-ai's step "
-                              "order (append the new token, then attend)", ("c2", "c2append")),
+                              "order (append the new token, then attend: two calls, and one call)", ("c2", "c2append", "c2fused")),
         ("decode_c1_c4_bf16.md", "Paged GQA decode, C1 (B=1, L=512) and C4 (4 x 32768, window 4096), bf16 KV",
          ("c1", "c4")),
         ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
@@ -680,7 +692,7 @@ def traffic_from_profile(kernel: str):
 
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
-SECTIONS = ("c1", "c2", "c2append", "c4", "c5int8", "c5fp8", "neighbours", "trait", "c3", "c4prefill", "c3int8",
+SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "neighbours", "trait", "c3", "c4prefill", "c3int8",
             "c3fp8")
 
 
@@ -707,6 +719,12 @@ def run_sections(ctx, args, lens, sel) -> list:
                               append=True)
         secondary.append(r)
         log(f"C2 append+attend: {r}")
+        torch.cuda.empty_cache()
+    if sel("c2fused"):
+        _, r = measure_decode(ctx, "C2 append + attend in one call (llh_paged_decode_append)", lens, 16, 8,
+                              llm_hip.KV_BF16, sec_steps, sec_warm, seed=workloads.SEED_BASE + 1, fused=True)
+        secondary.append(r)
+        log(f"C2 fused append+attend: {r}")
         torch.cuda.empty_cache()
     if sel("c4"):
         L, W = 32768, 4096

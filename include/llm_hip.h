@@ -123,6 +123,7 @@ typedef struct llh_metrics {
   uint64_t stream_decode_calls; /* decode calls that ran the persistent stream kernel */
   uint64_t trait_tuned_calls;   /* trait-mirror attention calls served by the tuned decode kernels */
   uint64_t generic_prefill_calls; /* prefill calls that ran the element-wise kernel */
+  uint64_t fused_append_calls;    /* llh_paged_decode_append calls served by one launch */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Waits for the device, then reads (and optionally clears) the sticky error
@@ -229,6 +230,19 @@ typedef struct llh_decode_desc {
  * (native_attention.rs:707-773).  d_q, d_out: [num_seqs][Hq][head_dim] bf16. */
 int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
                      void *d_out, float score_scale, void *stream);
+
+/* kir-ai's decode step, append then attend (native_attention.rs:307-329), in one
+ * call: the same result as llh_kv_append of each sequence's new token, at position
+ * d_seq_lens[b] - 1 through its block-table row, followed by llh_paged_decode.
+ * d_k_new, d_v_new: [num_seqs][kv_heads][head_dim] bf16 (sequences with
+ * d_seq_lens[b] == 0 have none).  bf16 pools on the tuned kernels run it as one
+ * launch: the new token is attended from d_k_new / d_v_new and written to its slot
+ * by the wavefront that computes the sequence's last block; other pools (the
+ * quantised token must be attended as stored) and shapes run the append kernel,
+ * then the decode.  The pool is written: unlike llh_paged_decode, concurrent calls
+ * must not share the sequences' last blocks. */
+int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_k_new,
+                            const void *d_v_new, const void *d_q, void *d_out, float score_scale, void *stream);
 
 /* llh_paged_decode without any allocation.  No counterpart in the reference:
  * this entry point is for callers that cannot allocate -- code under HIP graph

@@ -290,6 +290,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->stream_decode_calls = ctx->stream_decode_calls.load();
   out->trait_tuned_calls = ctx->trait_tuned_calls.load();
   out->generic_prefill_calls = ctx->generic_prefill_calls.load();
+  out->fused_append_calls = ctx->fused_append_calls.load();
   return LLH_OK;
 }
 
@@ -560,7 +561,7 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
 // Launches a planned decode step with its workspace at `ws` (plan.bytes long).
 int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
                                const DecodePlan &plan, const void *d_q, void *d_out, float score_scale,
-                               hipStream_t s, char *ws, bool timed) {
+                               hipStream_t s, char *ws, bool timed, const uint16_t *k_new, const uint16_t *v_new) {
   const PoolView &pv = pool->view;
   ctx->decode_calls++;
   if (plan.fast) {
@@ -584,6 +585,8 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
     a.seg_desc = plan.stream_wgs ? reinterpret_cast<int32_t *>(ws + plan.desc_off) : nullptr;
     if (plan.stream_wgs) ctx->stream_decode_calls++;
     a.scale_log2e = score_scale * 1.4426950408889634f;
+    a.k_new = k_new;
+    a.v_new = v_new;
     struct TimingHook {
       llh_ctx *ctx;
       std::pair<hipEvent_t, hipEvent_t> ev;
@@ -696,6 +699,38 @@ int llh_paged_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   if (!d_out && desc->num_seqs > 0) return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
   WsLease lease;
   return paged_decode_impl(ctx, pool, desc, d_q, d_out, score_scale, stream, 0, nullptr, lease);
+}
+
+int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_k_new,
+                            const void *d_v_new, const void *d_q, void *d_out, float score_scale, void *stream) {
+  if (!ctx || !pool || !desc) return LLH_ERR_NULL;
+  if (desc->num_seqs > 0 && (!d_out || !d_k_new || !d_v_new))
+    return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
+  DecodePlan plan;
+  int st = plan_decode(ctx, pool, desc, d_q, d_out, score_scale, &plan);
+  if (st != LLH_OK || plan.empty) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const PoolView &pv = pool->view;
+  // one launch for bf16 pools on the tuned kernels (new-token rows 16-byte aligned);
+  // any other case appends through the append kernel first, then decodes
+  const bool fused = plan.fast && pv.format == LLH_KV_BF16 && aligned16(d_k_new) && aligned16(d_v_new);
+  const size_t slot_bytes = fused ? 0 : align_up((size_t)desc->num_seqs * sizeof(int64_t));
+  WsLease lease;
+  st = lease.acquire(ctx, s, plan.bytes + slot_bytes);
+  if (st != LLH_OK) return st;
+  char *ws = lease.base();
+  if (fused) {
+    ctx->fused_append_calls++;
+    return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, true,
+                                 static_cast<const uint16_t *>(d_k_new), static_cast<const uint16_t *>(d_v_new));
+  }
+  int64_t *slots = reinterpret_cast<int64_t *>(ws + plan.bytes);
+  hipError_t e = launch_new_token_slots(desc->d_seq_lens, desc->d_block_tables, desc->max_blocks_per_seq,
+                                        pv.block_tokens, desc->num_seqs, slots, s);
+  if (e != hipSuccess) return ctx->hip_fail(e, "new-token slot launch");
+  st = kv_append(ctx, pool, slots, d_k_new, d_v_new, desc->num_seqs, 0, stream);
+  if (st != LLH_OK) return st;
+  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws);
 }
 
 int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, const void *d_x, int32_t x_f32,

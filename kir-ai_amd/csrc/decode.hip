@@ -587,8 +587,76 @@ __device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int la
   }
 }
 
-template <int G, int FMT>
+// Fused append, bf16 pools (row layout): adds sequence b's new token (position
+// len - 1, which the pool part of the step masks out) from a.k_new / a.v_new to
+// this wavefront's state, in row 0 (lanes 0..15) as one more token of that row,
+// with the same bf16 weight and normaliser rule as compute_block; then writes
+// the token to its pool slot (nothing reads that slot during the launch: the
+// block holding it is computed by this wavefront only, which already has it).
+// This lane's share of a sequence's new K / V rows: K dims 8c .. 8c+7, V dims
+// 16j + c (low halves), as the row layout holds a block's tokens.
+struct NewToken {
+  uint4 k;
+  uint32_t v[8];
+};
+
+__device__ __forceinline__ void load_new_token(const DecodeArgs &a, int b, int kvh, int lane, NewToken &nt) {
+  const int c = lane & 15;
+  const size_t row = (size_t)b * a.pool.kv_heads + kvh;
+  nt.k = *reinterpret_cast<const uint4 *>(a.k_new + row * D + 8 * c);
+#pragma unroll
+  for (int j = 0; j < 8; j++) nt.v[j] = a.v_new[row * D + 16 * j + c];
+}
+
+template <int G>
+__device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<G> &st, int b, int kvh, int len,
+                                              int lane, const uint32_t (&qw)[G][kQWords<G, kBf16>],
+                                              const NewToken &nt) {
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const uint4 kn = nt.k;
+  const uint32_t(&vn)[8] = nt.v;
+  float s[G];
+#pragma unroll
+  for (int gi = 0; gi < G; gi++) {
+    float acc = dot2_bf16(kn.x, qw[gi][0], 0.0f);
+    acc = dot2_bf16(kn.y, qw[gi][1], acc);
+    acc = dot2_bf16(kn.z, qw[gi][2], acc);
+    acc = dot2_bf16(kn.w, qw[gi][3], acc);
+    s[gi] = row_sum16(acc) * a.scale_log2e;
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      if (s[gi] > st.m[gi] + 8.0f) {  // the lazy reference max of compute_block
+        const float alpha = fast_exp2(st.m[gi] - s[gi]);  // 0 when st.m = -inf
+        st.m[gi] = s[gi];
+        st.l[gi] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; j++) st.o[gi][j] *= alpha;
+      }
+      const float mref = (st.m[gi] == -INFINITY) ? 0.0f : st.m[gi];
+      const uint32_t w = pack_bf16(fast_exp2(s[gi] - mref), 0.0f);
+      st.l[gi] = dot2_ones(w, st.l[gi]);
+#pragma unroll
+      for (int j = 0; j < 8; j++) st.o[gi][j] = dot2_bf16(vn[j], w, st.o[gi][j]);
+    }
+  }
+  const int pos = len - 1;
+  const int e = a.tables[(size_t)b * a.max_blocks + (pos / BT) % a.max_blocks];
+  if (g == 0 && e >= 0 && (int64_t)e < a.pool.n_blocks) {
+    const size_t bh = (size_t)e * a.pool.kv_heads + kvh;
+    uint16_t *kd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.k));
+    uint16_t *vd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.v));
+    *reinterpret_cast<uint4 *>(kd + (bh * BT + pos % BT) * D + 8 * c) = kn;
+#pragma unroll
+    for (int j = 0; j < 8; j++) vd[(bh * D + 16 * j + c) * BT + pos % BT] = (uint16_t)vn[j];
+  }
+}
+
+template <int G, int FMT, bool FUSED = false>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeArgs a) {
+  static_assert(!FUSED || FMT == kBf16, "fused append: bf16 pools");
   // consecutive workgroups are consecutive splits of one (kv head, sequence):
   // they share its query rows and block-table row in L2 (measured faster on
   // MI355X than dispatching all first splits first)
@@ -639,6 +707,15 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 
   SoftmaxState<G> st;
   reset_state(st);
+  // fused append: the pool part attends [lo, len - 1); the new token comes from a.k_new
+  constexpr bool fused = FUSED;
+  const int len_kv = fused ? len - 1 : len;
+  // the wavefront that walks the sequence's last block takes the new token: its rows
+  // are loaded now, ahead of the block loop
+  const int last_blk = first_blk + n_blk - 1;
+  const bool takes_new = fused && last_blk >= blk_begin && last_blk < blk_end && (last_blk - blk_begin) % 4 == wave;
+  NewToken nt;
+  if (takes_new) load_new_token(a, b, kvh, lane, nt);
 
   // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
   if (nbw > 0) {
@@ -652,7 +729,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
         load_block<FMT, TL>(a, e_next, kvh, lane, nxt);
         e_next = k + 2 < nbw ? entry(k + 2) : -1;
       }
-      compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len, lane, qw, st);
+      compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len_kv, lane, qw, st);
     };
     int k = 0;
     for (; k + 2 < nbw; k += 2) {
@@ -666,6 +743,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       step(k, r[0], r[1], false);
     }
   }
+
+  if constexpr (FMT == kBf16)
+    if (takes_new) add_new_token<G>(a, st, b, kvh, len, lane, qw, nt);
 
   // ---- merge the four token groups of the wavefront ----
   finalize_state<G, FMT>(st);
@@ -875,8 +955,9 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
   reset_state(st);
 }
 
-template <int G, int FMT>
+template <int G, int FMT, bool FUSED = false>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(const DecodeArgs a) {
+  static_assert(!FUSED || FMT == kBf16, "fused append: bf16 pools");
   const int lane = threadIdx.x & 63;
   // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
   const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
@@ -907,6 +988,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   const int r0 = __builtin_amdgcn_readfirstlane(range_begin(w - w0, ub, wb));
   const int n = __builtin_amdgcn_readfirstlane(range_begin(w - w0 + 1, ub, wb)) - r0;  // >= 1
   const int len = __builtin_amdgcn_readfirstlane(a.seq_lens[b]);
+  // fused append: the pool part attends [lo, len - 1); the new token comes from a.k_new
+  constexpr bool fused = FUSED;
+  const int len_kv = fused ? len - 1 : len;
   const int lo = a.window > 0 ? max(0, len - a.window) : 0;
   const int first_blk = lo / BT;
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
@@ -943,6 +1027,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
 
   BlockRegs<FMT> r[2];
   load_block<FMT, TL>(a, next_entry(), l_kvh, lane, r[0]);
+  // fused append: a segment's new-token rows are loaded with its last unit, into
+  // the buffer that travels with that unit's registers (r[0] / r[1])
+  NewToken nt[2];
+  if constexpr (FMT == kBf16)
+    if (fused && l_j == nb - 1) load_new_token(a, b, l_kvh, lane, nt[0]);
   int e_next = n > 1 ? next_entry() : -1;
   if (++l_j == nb) {
     l_j = 0;
@@ -972,21 +1061,26 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   // issued, then unit k is computed.  Every step inside the loop issues the
   // next unit's loads after any q load, so the wait before the math always
   // leaves the next unit's loads in flight.
-  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, bool issue) __attribute__((always_inline)) {
+  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, NewToken &cur_nt, NewToken &nxt_nt, bool issue)
+                  __attribute__((always_inline)) {
     if (need_q) {
       load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
       need_q = false;
     }
     if (issue) {
       load_block<FMT, TL>(a, e_next, l_kvh, lane, nxt);
+      if constexpr (FMT == kBf16)
+        if (fused && l_j == nb - 1) load_new_token(a, b, l_kvh, lane, nxt_nt);
       e_next = k + 2 < n ? next_entry() : -1;
       if (++l_j == nb) {
         l_j = 0;
         l_kvh++;
       }
     }
-    compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len, lane, qw, st);
+    compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len_kv, lane, qw, st);
     if (++c_j == nb) {  // the segment ends with this unit
+      if constexpr (FMT == kBf16)
+        if (fused) add_new_token<G>(a, st, b, seg_kvh, len, lane, qw, cur_nt);
       end_segment(seg_from_start);
       c_j = 0;
       seg_kvh++;
@@ -996,14 +1090,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   };
   int k = 0;
   for (; k + 2 < n; k += 2) {
-    step(k, r[0], r[1], true);
-    step(k + 1, r[1], r[0], true);
+    step(k, r[0], r[1], nt[0], nt[1], true);
+    step(k + 1, r[1], r[0], nt[1], nt[0], true);
   }
   if (k + 1 < n) {
-    step(k, r[0], r[1], true);
-    step(k + 1, r[1], r[0], false);
+    step(k, r[0], r[1], nt[0], nt[1], true);
+    step(k + 1, r[1], r[0], nt[1], nt[0], false);
   } else {
-    step(k, r[0], r[1], false);
+    step(k, r[0], r[1], nt[0], nt[1], false);
   }
   if (c_j != 0) end_segment(false);  // the range ends inside a segment
 }
@@ -1304,13 +1398,14 @@ __global__ void decode_fp8_kernel(const uint8_t *codes, float *out, int32_t n) {
   if (i < n) out[i] = bf16_lo(fp8x2_to_bf16<false>((uint32_t)codes[i]));
 }
 
-template <int G, int FMT>
+template <int G, int FMT, bool FUSED>
 hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   const int max_blk = (max_seq_len + BT - 1) / BT + 1;
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
   if (hook) hook(hu, 0, s);
   if (a.stream_wgs > 0) {
-    hipLaunchKernelGGL((paged_decode_stream_kernel<G, FMT>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_stream_kernel<G, FMT, FUSED>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s,
+                       a);
     hipError_t e = hipGetLastError();
     if (hook) hook(hu, 1, s);
     if (e != hipSuccess) return e;
@@ -1318,7 +1413,7 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, 
     return hipGetLastError();
   }
   dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<G, FMT>), grid, dim3(kDecodeThreads), 0, s, a);
+  hipLaunchKernelGGL((paged_decode_kernel<G, FMT, FUSED>), grid, dim3(kDecodeThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (hook) hook(hu, 1, s);
   if (e != hipSuccess || a.max_splits <= 1) return e;
@@ -1329,12 +1424,13 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, 
 template <int G>
 hipError_t launch_decode_fmt(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   switch (a.pool.format) {
-    case kBf16:
-      return launch_decode_t<G, kBf16>(a, max_seq_len, s, hu, hook);
+    case kBf16:  // a.k_new: fused append of each sequence's new token
+      return a.k_new ? launch_decode_t<G, kBf16, true>(a, max_seq_len, s, hu, hook)
+                     : launch_decode_t<G, kBf16, false>(a, max_seq_len, s, hu, hook);
     case kInt8:
-      return launch_decode_t<G, kInt8>(a, max_seq_len, s, hu, hook);
+      return a.k_new ? hipErrorInvalidValue : launch_decode_t<G, kInt8, false>(a, max_seq_len, s, hu, hook);
     case kFp8:
-      return launch_decode_t<G, kFp8>(a, max_seq_len, s, hu, hook);
+      return a.k_new ? hipErrorInvalidValue : launch_decode_t<G, kFp8, false>(a, max_seq_len, s, hu, hook);
   }
   return hipErrorInvalidValue;
 }

@@ -47,7 +47,7 @@ struct llh_ctx {
   int cus = 256;  // compute units of the device (sizes the persistent decode grid)
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
-      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0};
+      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0}, fused_append_calls{0};
   std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
 
   // per-stream workspaces; ws_mu guards the list and ws_min_bytes
@@ -180,10 +180,11 @@ struct DecodePlan {
 };
 int plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
                 const void *d_out, float score_scale, DecodePlan *plan);
-// timed = false leaves out the kernel-timing events (no event is created or recorded)
+// timed = false leaves out the kernel-timing events (no event is created or recorded);
+// k_new / v_new (bf16 pools, tuned kernels): fused append of each sequence's new token
 int launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const DecodePlan &plan,
                           const void *d_q, void *d_out, float score_scale, hipStream_t s, char *ws,
-                          bool timed = true);
+                          bool timed = true, const uint16_t *k_new = nullptr, const uint16_t *v_new = nullptr);
 // Resolves this device's address of the no-allocation scratch (device current).
 int noalloc_init(int device);
 

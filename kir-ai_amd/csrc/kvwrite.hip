@@ -315,6 +315,7 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
   const int Hkv = a.pool.kv_heads;
   const int Dh = a.pool.head_dim;
   const int64_t slot = a.slots[i];
+  if (slot == kNoSlot) return;  // a sequence with no new token (fused-append fallback)
   const int64_t blk = slot / BT;
   const int off = (int)(slot % BT);
   if (slot < 0 || blk >= a.pool.n_blocks) {
@@ -478,6 +479,23 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   hipLaunchKernelGGL(export_rows_kernel, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(64) void new_token_slots_kernel(const int32_t *seq_lens, const int32_t *tables,
+                                                             int32_t max_blocks, int32_t bt, int32_t n,
+                                                             int64_t *slots) {
+  const int b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= n) return;
+  const int pos = seq_lens[b] - 1;
+  slots[b] = pos < 0 ? kNoSlot : (int64_t)tables[(size_t)b * max_blocks + (pos / bt) % max_blocks] * bt + pos % bt;
+}
+
+hipError_t launch_new_token_slots(const int32_t *seq_lens, const int32_t *tables, int32_t max_blocks,
+                                  int32_t block_tokens, int32_t n, int64_t *slots, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(new_token_slots_kernel, dim3((n + 63) / 64), dim3(64), 0, s, seq_lens, tables, max_blocks,
+                     block_tokens, n, slots);
   return hipGetLastError();
 }
 

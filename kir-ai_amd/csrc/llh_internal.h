@@ -56,6 +56,11 @@ struct DecodeArgs {
   int32_t max_seq_len;      // host bound on seq_lens (stream kernel: longer lengths raise kErrTooManySplits)
   int32_t *seg_desc;        // stream kernel: [B][Hkv][2] (first partial slot, partial count; 0 = written)
   float scale_log2e;        // score_scale * log2(e)
+  // fused append (bf16 pools): each sequence's new token (position len - 1), [B][Hkv][128]
+  // bf16, is attended from here and written to its pool slot by the wavefront that
+  // computes the sequence's last block; null: plain decode
+  const uint16_t *k_new;
+  const uint16_t *v_new;
 };
 
 // Reference-order decode for any head_dim / block size / group size.
@@ -179,6 +184,12 @@ constexpr int kGenericPrefillMaxDim = 512;  // head_dim bound of the generic pre
 hipError_t launch_prefill_generic(const PrefillArgs &a, int total_rows, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
+// slots[b] = the pool slot of position seq_lens[b] - 1 through table row b (kNoSlot
+// when seq_lens[b] <= 0: the append kernel skips it), for an append of each
+// sequence's new token
+constexpr int64_t kNoSlot = INT64_MIN;
+hipError_t launch_new_token_slots(const int32_t *seq_lens, const int32_t *tables, int32_t max_blocks,
+                                  int32_t block_tokens, int32_t n, int64_t *slots, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s);
 hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);

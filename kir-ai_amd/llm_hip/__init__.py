@@ -130,6 +130,7 @@ class Metrics(ctypes.Structure):
         ("stream_decode_calls", ctypes.c_uint64),
         ("trait_tuned_calls", ctypes.c_uint64),
         ("generic_prefill_calls", ctypes.c_uint64),
+        ("fused_append_calls", ctypes.c_uint64),
     ]
 
 
@@ -289,6 +290,8 @@ SIGNATURES = {
     "llh_kv_export_rows_f32": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, _P, _P]),
     "llh_paged_decode": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
     "llh_paged_decode_noalloc": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, ctypes.c_float, _P]),
+    "llh_paged_decode_append": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _P, _P, _P, _P, ctypes.c_float,
+                                               _P]),
     "llh_paged_prefill": (ctypes.c_int, [_P, _P, ctypes.POINTER(PrefillDesc), _P, _P, ctypes.c_float, _P]),
     "llh_debug_gather": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _I32, _I32, _I32, _I32, _P, _P]),
     "llh_debug_decode_fp8": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
@@ -531,6 +534,13 @@ class Context:
                 self.handle, pool.handle, ctypes.byref(desc), _ptr(q), _ptr(out), score_scale, _stream(stream)
             )
         )
+
+    def paged_decode_append(self, pool: "KvPool", desc: DecodeDesc, k_new, v_new, q, out, score_scale: float,
+                            stream=None) -> None:
+        """llh_paged_decode_append: append each sequence's new token (position len - 1), then attend."""
+        self.check(self.lib.llh_paged_decode_append(self.handle, pool.handle, ctypes.byref(desc), _ptr(k_new),
+                                                    _ptr(v_new), _ptr(q), _ptr(out), ctypes.c_float(score_scale),
+                                                    _stream(stream)))
 
     def paged_decode_noalloc(self, pool: "KvPool", desc: DecodeDesc, q, out, score_scale: float,
                              stream=None) -> None:
