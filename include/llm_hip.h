@@ -64,7 +64,10 @@ typedef enum llh_status {
 typedef enum llh_kv_format {
   LLH_KV_BF16 = 0,    /* bf16 K and V */
   LLH_KV_INT8 = 1,    /* int8 codes, fp16 scale per (token, kv head): absmax/127 */
-  LLH_KV_FP8_E4M3 = 2 /* OCP e4m3fn codes, f32 scale per (block, kv head) for K and for V: absmax/448 */
+  LLH_KV_FP8_E4M3 = 2, /* OCP e4m3fn codes, f32 scale per (block, kv head) for K and for V: absmax/448 */
+  LLH_KV_INT8_ROW = 3  /* int8 codes, f32 scale per token row over all kv heads: absmax/127 -- the
+                          reference's own int8 layout (crates/llm-kv-cache/src/format.rs:702-759);
+                          served by the element-wise kernels */
 } llh_kv_format;
 
 typedef struct llh_ctx llh_ctx;
@@ -322,9 +325,12 @@ int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int
 
 /* LayerKvCache::new_with_config (crates/llm-kv-cache/src/layer.rs:345-400):
  * a ring of `max_tokens` token slots whose storage is paged device blocks.
- * format: LLH_KV_BF16 (the reference's f32 rows are stored as bf16) or
- * LLH_KV_INT8 (per (token, head) fp16 scales).  Errors as the reference:
- * zero sizes -> INVALID_SHAPE, fp8 -> UNSUPPORTED. */
+ * format: LLH_KV_BF16 (the reference's f32 rows are stored as bf16),
+ * LLH_KV_INT8 (per (token, head) fp16 scales; the tuned kernels) or
+ * LLH_KV_INT8_ROW (the reference's KvCacheFormat::Int8 bit for bit: one f32
+ * scale per token row, quantised from the f32 rows; the reference-order
+ * kernel).  Errors as the reference: zero sizes -> INVALID_SHAPE, fp8 ->
+ * UNSUPPORTED. */
 int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, size_t head_dim, int32_t format,
                            llh_layer_cache **out);
 int llh_layer_cache_destroy(llh_layer_cache *cache);

@@ -343,7 +343,7 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
                        int64_t n_blocks, llh_kv_pool **out) {
   if (!ctx || !out) return LLH_ERR_NULL;
   *out = nullptr;
-  if (format < LLH_KV_BF16 || format > LLH_KV_FP8_E4M3)
+  if (format < LLH_KV_BF16 || format > LLH_KV_INT8_ROW)
     return ctx->fail(LLH_ERR_UNSUPPORTED, "unsupported KV format");
   if (block_tokens <= 0 || kv_heads <= 0 || head_dim <= 0 || n_blocks <= 0)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "kv pool sizes must be positive");
@@ -527,7 +527,8 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   const bool rows_aligned = (reinterpret_cast<uintptr_t>(d_q) & 15) == 0 &&
                             (reinterpret_cast<uintptr_t>(d_out) & 15) == 0;
   plan->group = group;
-  plan->fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens && rows_aligned &&
+  plan->fast = pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
+               rows_aligned &&
                (group == 1 || group == 2 || group == 4 || group == 8) &&
                (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   if (plan->fast) {
@@ -790,7 +791,8 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   // the tuned MFMA kernel takes head_dim 128, 16-token blocks and 16-byte aligned
   // rows; every other call runs the element-wise kernel
-  const bool fast = pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
+  const bool fast = pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim &&
+                    pv.block_tokens == kFastBlockTokens &&
                     ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) == 0 &&
                     ctx->opt(LLH_OPT_FORCE_GENERIC) == 0;
   PrefillArgs a{};
@@ -1039,7 +1041,7 @@ int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, siz
   *out = nullptr;
   if (max_tokens == 0 || kv_heads == 0 || head_dim == 0)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "invalid KV cache shape");
-  if (format != LLH_KV_BF16 && format != LLH_KV_INT8)
+  if (format != LLH_KV_BF16 && format != LLH_KV_INT8 && format != LLH_KV_INT8_ROW)
     return ctx->fail(LLH_ERR_UNSUPPORTED, "unsupported KV cache format for the layer cache");
   if (max_tokens > (size_t)INT32_MAX / 2 || kv_heads * head_dim > (1u << 20))
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV cache shape too large");
@@ -1192,7 +1194,7 @@ static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key
   if (len != cache->vector_len()) return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV row length does not match the cache");
   bool finite = true;
   for (size_t i = 0; i < len && finite; i++) finite = std::isfinite(h_key[i]) && std::isfinite(h_value[i]);
-  if (!finite && cache->format == LLH_KV_INT8)
+  if (!finite && (cache->format == LLH_KV_INT8 || cache->format == LLH_KV_INT8_ROW))
     return ctx->fail(LLH_ERR_NON_FINITE, "int8 KV cache rows must be finite");
   const bool full = cache->token_count == cache->max_tokens;
   if (full && !sliding) return ctx->fail(LLH_ERR_CAPACITY, "KV cache capacity exceeded");
@@ -1275,7 +1277,7 @@ int llh_append_kv_cache_f32(llh_ctx *ctx, llh_layer_cache *cache, const float *h
 // q and rows are checked here and a non-finite result is recomputed there.
 static bool trait_tuned_ok(const llh_ctx *ctx, const llh_layer_cache *cache, const float *h_query, size_t qdim,
                            size_t heads, size_t kv_heads) {
-  if (ctx->opt(LLH_OPT_TRAIT_REFERENCE_ORDER)) return false;
+  if (ctx->opt(LLH_OPT_TRAIT_REFERENCE_ORDER) || cache->format == LLH_KV_INT8_ROW) return false;
   const size_t group = heads / kv_heads;
   if (cache->head_dim != (size_t)kFastHeadDim || cache->max_tokens % kRingBlockTokens != 0 || cache->non_finite_rows)
     return false;

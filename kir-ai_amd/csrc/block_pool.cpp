@@ -736,7 +736,7 @@ int llh_block_pool_append_f32(llh_block_pool *bp, uint64_t block_id, const float
     return bp->fail(LLH_ERR_INVALID_SHAPE, "block is not exclusively owned (copy it on write first)");
   if (len != bp->vector_len) return bp->fail(LLH_ERR_INVALID_SHAPE, "KV row length does not match the block");
   if (b->token_count == bp->capacity_tokens) return bp->fail(LLH_ERR_CAPACITY, "KV block is full");
-  if (bp->pool->view.format == LLH_KV_INT8)
+  if (bp->pool->view.format == LLH_KV_INT8 || bp->pool->view.format == LLH_KV_INT8_ROW)
     for (size_t i = 0; i < len; i++)
       if (!std::isfinite(h_key[i]) || !std::isfinite(h_value[i]))
         return bp->fail(LLH_ERR_NON_FINITE, "int8 KV rows must be finite");

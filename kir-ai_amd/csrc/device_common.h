@@ -26,6 +26,8 @@ __device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_
     const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + t]);
     return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
   }
+  if (p.format == kInt8Row)  // one f32 scale per token row of the block (all heads)
+    return (float)reinterpret_cast<const int8_t *>(base)[idx] * reinterpret_cast<const float *>(sc)[blk * p.block_tokens + t];
   const uint32_t code = reinterpret_cast<const uint8_t *>(base)[idx];
   return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * reinterpret_cast<const float *>(sc)[bh];
 }

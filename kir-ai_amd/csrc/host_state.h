@@ -201,6 +201,7 @@ inline size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 ? 2 : 1;
 
 inline size_t scale_bytes_per_block(int32_t format, int32_t kv_heads, int32_t block_tokens) {
   if (format == LLH_KV_INT8) return (size_t)kv_heads * block_tokens * 2;
+  if (format == LLH_KV_INT8_ROW) return (size_t)block_tokens * 4;  // f32 per token row, shared by the heads
   if (format == LLH_KV_FP8_E4M3) return (size_t)kv_heads * 4;
   return 0;
 }

@@ -272,6 +272,45 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
   }
 }
 
+// The reference's own int8 layout (format.rs:702-737): one f32 scale per token
+// row over all kv heads, absmax / 127, codes round(x / scale) half away from zero,
+// clamped to +-127.  One workgroup per block: wavefront w quantises tokens w,
+// w + 4, ... of K, then of V (a row spans every head, so no per-head split).
+__global__ __launch_bounds__(256) void write_blocks_row_kernel(const WriteBlocksArgs a) {
+  const int i = blockIdx.x;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int blk = a.blocks[i];
+  if (blk < 0 || (int64_t)blk >= a.pool.n_blocks) {
+    if (threadIdx.x == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const int vl = Hkv * Dh;
+  for (int t = wave; t < BT; t += 4) {
+    for (int tensor = 0; tensor < 2; tensor++) {
+      const uint16_t *src = (tensor ? a.v : a.k) + ((size_t)i * BT + t) * vl;  // [h][d] of token t
+      float mx = 0.0f;
+      for (int e = lane; e < vl; e += 64) mx = fmaxf(mx, fabsf(bf16_to_f32(src[e])));
+      mx = wave_max(mx);
+      const float s = mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f);
+      int8_t *dst = reinterpret_cast<int8_t *>(tensor ? a.v_dst : a.k_dst);
+      for (int e = lane; e < vl; e += 64) {
+        const int h = e / Dh, d = e % Dh;
+        const size_t bh = (size_t)blk * Hkv + h;
+        const int8_t code = quant_int8(bf16_to_f32(src[e]), s);
+        if (tensor)
+          dst[(bh * Dh + d) * BT + t] = code;
+        else
+          dst[(bh * BT + t) * Dh + d] = code;
+      }
+      if (lane == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[(size_t)blk * BT + t] = s;
+    }
+  }
+}
+
 // fp8 e4m3 code as f32 (exact).
 __device__ __forceinline__ float decode_e4m3(uint32_t code) { return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0]; }
 
@@ -303,6 +342,50 @@ __device__ __forceinline__ float append_fp8_row(uint8_t *dst, bool dim_major, si
   }
   for (int d = lane; d < Dh; d += 64) at(off, d) = s_new == 0.0f ? 0 : encode_e4m3(__fdiv_rn(ld(src, d), s_new));
   return s_new;
+}
+
+// One wavefront per token row i: the reference's int8 row layout (one f32
+// scale over all kv heads of the row; write_blocks_row_kernel's rule).
+template <typename ST>
+__global__ __launch_bounds__(64) void append_row_kernel(const AppendArgs a) {
+  const int i = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  const int64_t slot = a.slots[i];
+  if (slot == kNoSlot) return;
+  const int64_t blk = slot / BT;
+  const int off = (int)(slot % BT);
+  if (slot < 0 || blk >= a.pool.n_blocks) {
+    if (lane == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const int vl = Hkv * Dh;
+  for (int tensor = 0; tensor < 2; tensor++) {
+    const ST *src = reinterpret_cast<const ST *>(tensor ? a.v : a.k) + (size_t)i * vl;
+    auto ld = [&](int e) -> float {
+      if constexpr (sizeof(ST) == 4)
+        return src[e];
+      else
+        return bf16_to_f32(src[e]);
+    };
+    float mx = 0.0f;
+    for (int e = lane; e < vl; e += 64) mx = fmaxf(mx, fabsf(ld(e)));
+    mx = wave_max(mx);
+    const float s = mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f);
+    int8_t *dst = reinterpret_cast<int8_t *>(tensor ? a.v_dst : a.k_dst);
+    for (int e = lane; e < vl; e += 64) {
+      const int h = e / Dh, d = e % Dh;
+      const size_t bh = (size_t)blk * Hkv + h;
+      const int8_t code = quant_int8(ld(e), s);
+      if (tensor)
+        dst[(bh * Dh + d) * BT + off] = code;
+      else
+        dst[(bh * BT + off) * Dh + d] = code;
+    }
+    if (lane == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[blk * BT + off] = s;
+  }
 }
 
 // One wavefront per (token row i, kv head).
@@ -410,6 +493,9 @@ __device__ __forceinline__ float load_f32(const PoolView &p, const void *base, c
     const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + off]);
     return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
   }
+  if (p.format == kInt8Row)
+    return (float)reinterpret_cast<const int8_t *>(base)[idx] *
+           reinterpret_cast<const float *>(sc)[(bh / p.kv_heads) * p.block_tokens + off];
   return __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)reinterpret_cast<const uint8_t *>(base)[idx], false)[0] *
          reinterpret_cast<const float *>(sc)[bh];
 }
@@ -505,7 +591,9 @@ hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
                     (a.pool.format == kBf16 || a.pool.format == kInt8 || a.pool.format == kFp8) &&
                     reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
-  if (fast)
+  if (a.pool.format == kInt8Row)
+    hipLaunchKernelGGL(write_blocks_row_kernel, dim3(a.n), dim3(256), 0, s, a);
+  else if (fast)
     hipLaunchKernelGGL(write_blocks_d128_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(write_blocks_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
@@ -514,7 +602,11 @@ hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
 
 hipError_t launch_append(const AppendArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  if (a.src_f32)
+  if (a.pool.format == kInt8Row && a.src_f32)
+    hipLaunchKernelGGL(append_row_kernel<float>, dim3(a.n), dim3(64), 0, s, a);
+  else if (a.pool.format == kInt8Row)
+    hipLaunchKernelGGL(append_row_kernel<uint16_t>, dim3(a.n), dim3(64), 0, s, a);
+  else if (a.src_f32)
     hipLaunchKernelGGL(append_kernel<float>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
   else
     hipLaunchKernelGGL(append_kernel<uint16_t>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);

@@ -14,7 +14,7 @@ constexpr int kPrefillThreads = 256;  // 4 wavefronts, 32 query rows each
 constexpr int kMatvecWaves = 8;       // wavefronts (K slices) per output-projection workgroup
 constexpr int kMatvecColsMultiple = kMatvecWaves * 16;  // cols the projection kernel takes
 
-enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2 };
+enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2, kInt8Row = 3 };
 
 // Device error flags (bit set by kernels, read back by the host).
 enum ErrFlag : int32_t {

@@ -39,6 +39,7 @@ ERR_INTEGRITY = -8
 KV_BF16 = 0
 KV_INT8 = 1
 KV_FP8_E4M3 = 2
+KV_INT8_ROW = 3  # the reference's int8 layout: f32 scale per token row over all kv heads
 
 ERR_FLAG_BAD_BLOCK = 1
 ERR_FLAG_TOO_MANY_SPLITS = 2

@@ -24,6 +24,7 @@ ERR_NON_FINITE = -3
 KV_BF16 = 0
 KV_INT8 = 1
 KV_FP8_E4M3 = 2
+KV_INT8_ROW = 3
 
 _lib = None
 
@@ -307,6 +308,9 @@ class Pool:
         elif fmt == KV_INT8:
             k, v = raw["k"].view(np.int8), raw["v"].view(np.int8)
             ks, vs = raw["k_scales"].view(np.uint16), raw["v_scales"].view(np.uint16)
+        elif fmt == KV_INT8_ROW:
+            k, v = raw["k"].view(np.int8), raw["v"].view(np.int8)
+            ks, vs = raw["k_scales"].view(np.float32), raw["v_scales"].view(np.float32)
         else:
             k, v = raw["k"].view(np.uint8), raw["v"].view(np.uint8)
             ks, vs = raw["k_scales"].view(np.float32), raw["v_scales"].view(np.float32)

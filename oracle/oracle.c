@@ -454,6 +454,8 @@ float orc_pool_elem(const orc_pool *p, int tensor, int64_t block, int32_t head, 
       float s = ((const float *)scales)[(int64_t)block * p->kv_heads + head];
       return fp8_table[((const uint8_t *)base)[idx]] * s;
     }
+    case ORC_KV_INT8_ROW: /* dequantize_int8_rows (format.rs:739-759): code * row scale */
+      return (float)((const int8_t *)base)[idx] * ((const float *)scales)[(int64_t)block * p->block_tokens + t];
     default:
       return NAN;
   }

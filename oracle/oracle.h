@@ -47,6 +47,7 @@ extern "C" {
 #define ORC_KV_BF16 0
 #define ORC_KV_INT8 1
 #define ORC_KV_FP8_E4M3 2
+#define ORC_KV_INT8_ROW 3 /* the reference's own int8 layout: f32 scale per token row over all heads */
 
 /* ---------------- scalar conversions ---------------- */
 uint16_t orc_f32_to_bf16(float x);   /* round to nearest even, NaN kept quiet */
@@ -133,6 +134,7 @@ void orc_ring_logical_rows(const orc_ring *r, int tensor, float *out);
  * V  : [n_blocks][kv_heads][head_dim][block_tokens]   (dim rows, i.e. transposed)
  * int8 scales: [n_blocks][kv_heads][block_tokens] fp16 for K and for V
  * fp8 scales : [n_blocks][kv_heads] f32 for K and for V
+ * int8 row scales: [n_blocks][block_tokens] f32 for K and for V (format.rs:702-759)
  * Position p of a sequence lives in block table[(p / block_tokens) % n_table],
  * at offset p % block_tokens. */
 typedef struct orc_pool {

@@ -283,6 +283,14 @@ def test_decode_generic_shapes(ctx, head_dim, bt, Hq, Hkv):
     check(ctx, batch, Hq, Hkv, seed=31, head_dim=head_dim, what=f"D={head_dim} BT={bt}")
 
 
+@pytest.mark.parametrize("window", [0, 100])
+def test_decode_int8_row_pool(ctx, window):
+    """The reference's own int8 layout (LLH_KV_INT8_ROW: f32 scale per token row over all
+    kv heads) runs the reference-order kernel, on the tuned shape too."""
+    batch = workloads.paged_batch([5, 77, 300, 1024], BT, 0.10, seed=44)
+    check(ctx, batch, 16, 8, llm_hip.KV_INT8_ROW, window=window, seed=45, what=f"int8 row W={window}")
+
+
 def test_decode_bad_block_raises_flag(ctx, decode_kernel):
     batch = workloads.paged_batch([64, 64], BT, 0.10, seed=9)
     pool, q = build_case(ctx, batch, 16, 8, llm_hip.KV_BF16, 9)

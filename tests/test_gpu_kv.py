@@ -32,7 +32,7 @@ def write_case(ctx, fmt, lens, Hkv, seed, head_dim=D, free=0.1):
     return batch, pool, ids, sk, sv
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_INT8_ROW])
 def test_gather_is_bit_exact(ctx, fmt):
     import torch
 
@@ -84,6 +84,68 @@ def test_gather_ring_table(ctx):
     ctx.gather(pool, desc, 0, 50, 90, 0, out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint16), rows[50:90].ravel())
+
+
+def test_int8_row_quantise_on_write_is_the_reference_rule(ctx):
+    """LLH_KV_INT8_ROW, the reference's own int8 layout (format.rs:702-737): one f32 scale
+    per token row over every kv head.  Whole-block writes store exactly the oracle's
+    quantize_int8_rows codes and scales of each token row."""
+    Hkv = 4
+    batch, pool, ids, sk, sv = write_case(ctx, llm_hip.KV_INT8_ROW, [40, 17], Hkv, 210)
+    raw = pool.raw()
+    n = batch.n_blocks
+    k = raw["k"].view(np.int8).reshape(n, Hkv, BT, D)
+    v = raw["v"].view(np.int8).reshape(n, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.float32).reshape(n, BT)
+    vs = raw["v_scales"].view(np.float32).reshape(n, BT)
+    for i, blk in enumerate(ids):
+        for src, codes_dev, scales_dev in ((sk, k[blk].transpose(1, 0, 2), ks[blk]),
+                                           (sv, v[blk].transpose(2, 0, 1), vs[blk])):
+            st, codes, scales = oracle.quantize_int8_rows(oracle.bf16_to_f32(src[i]).reshape(BT, Hkv * D), Hkv * D)
+            assert st == oracle.OK
+            assert np.array_equal(codes_dev, codes.reshape(BT, Hkv, D)) and np.array_equal(scales_dev, scales)
+    assert ctx.device_errors() == 0
+
+
+@pytest.mark.parametrize("src_f32", [False, True])
+def test_int8_row_append_is_the_reference_rule(ctx, src_f32):
+    """Per-token appends into an LLH_KV_INT8_ROW pool, from bf16 or f32 rows (the trait
+    mirror's f32 rows are quantised as they are, like the reference's), store the oracle's
+    quantize_int8_rows codes and scale; the f32 export returns code * scale."""
+    import torch
+
+    Hkv, n_tok, n_blocks = 3, 40, 8
+    pool = ctx.pool(llm_hip.KV_INT8_ROW, BT, Hkv, D, n_blocks)
+    rng = np.random.default_rng(17)
+    mag = np.exp(rng.uniform(-4, 3, n_tok)).astype(np.float32)[:, None, None]
+    xk = (rng.standard_normal((n_tok, Hkv, D)) * mag).astype(np.float32)
+    xv = (rng.standard_normal((n_tok, Hkv, D)) * mag[::-1]).astype(np.float32)
+    xk[3] = 0.0  # an all-zero row: scale 0, codes 0
+    slots = rng.permutation(n_blocks * BT)[:n_tok].astype(np.int64)
+    if src_f32:
+        ctx.append_f32(pool, to_dev(slots), to_dev(xk), to_dev(xv))
+    else:
+        xk, xv = (oracle.bf16_to_f32(oracle.f32_to_bf16(x)).reshape(x.shape) for x in (xk, xv))
+        ctx.append(pool, to_dev(slots), to_dev(oracle.f32_to_bf16(xk)), to_dev(oracle.f32_to_bf16(xv)))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    raw = pool.raw()
+    k = raw["k"].view(np.int8).reshape(n_blocks, Hkv, BT, D)
+    v = raw["v"].view(np.int8).reshape(n_blocks, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.float32).reshape(n_blocks, BT)
+    vs = raw["v_scales"].view(np.float32).reshape(n_blocks, BT)
+    ko = torch.zeros((n_tok, Hkv, D), dtype=torch.float32, device="cuda")
+    vo = torch.zeros_like(ko)
+    ctx.export_rows_f32(pool, to_dev(slots), ko, vo)
+    ko, vo = ko.cpu().numpy(), vo.cpu().numpy()
+    for i, sl in enumerate(slots):
+        blk, t = divmod(int(sl), BT)
+        for x, codes_dev, scale_dev, exported in ((xk, k[blk, :, t, :], ks[blk, t], ko[i]),
+                                                  (xv, v[blk, :, :, t], vs[blk, t], vo[i])):
+            st, codes, scales = oracle.quantize_int8_rows(x[i].ravel(), Hkv * D)
+            assert st == oracle.OK
+            assert np.array_equal(codes_dev.ravel(), codes) and scale_dev == scales[0]
+            assert np.array_equal(exported.ravel(), oracle.dequantize_int8_rows(codes, scales, Hkv * D))
 
 
 def test_int8_quantise_on_write_is_bit_exact(ctx):

@@ -190,6 +190,7 @@ def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm
     (64, 32, 12, 4, 48, llm_hip.KV_BF16),      # odd group (3), 32-token blocks, window
     (96, 8, 4, 1, 0, llm_hip.KV_FP8_E4M3),     # MQA, 8-token blocks
     (128, 32, 16, 8, 0, llm_hip.KV_INT8),      # tuned head_dim, other block size
+    (128, 16, 16, 8, 300, llm_hip.KV_INT8_ROW),  # the reference's int8 layout
 ])
 def test_prefill_generic_shapes_full_oracle(ctx, head_dim, bt, Hq, Hkv, W, fmt):
     """Shapes the MFMA kernel does not take run the element-wise prefill kernel: ragged

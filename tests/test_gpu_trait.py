@@ -56,6 +56,24 @@ def test_full_attention_cache_mix_int8_matches_reference_values(ctx):
     assert np.max(np.abs(out - np.array(c["expected"]))) < 1e-2
 
 
+def test_int8_row_cache_stores_the_reference_codes_and_scales(ctx):
+    """primitives/tests.rs:413-466 on LLH_KV_INT8_ROW, the reference's own int8 layout: the
+    cache holds exactly the test's key/value codes and f32 scales (keys() / values() return
+    code * scale), and the output meets the test's own tolerance."""
+    c = KA["int8_closed_form"]
+    cache = LayerKvCache.new_with_config(ctx, 8, 1, 2, llm_hip.KV_INT8_ROW)
+    cache.append_sliding([1.0, 0.0], [10.0, 0.0])
+    cache.append_sliding([0.0, 1.0], [0.0, 10.0])
+    kc = np.array(c["key_codes"], np.float32).reshape(2, 2)
+    vc = np.array(c["value_codes"], np.float32).reshape(2, 2)
+    ks = np.array(c["key_scales"], np.float32)[:, None]
+    vs = np.array(c["value_scales"], np.float32)[:, None]
+    assert np.array_equal(cache.keys(), (kc * ks).ravel())
+    assert np.array_equal(cache.values(), (vc * vs).ravel())
+    out = mix(ctx, cache, c["query"], 2, 2, 1, 2, 1.0)
+    assert np.max(np.abs(out - np.array(c["expected"]))) < c["tolerance"]
+
+
 def test_sequence_is_causal(ctx):
     c = KA["causal_sequence"]
     cache = LayerKvCache.new(ctx, 8, 1, 1)
@@ -101,7 +119,8 @@ def test_small_cache_uses_sliding_window(ctx):
     assert np.max(np.abs(out * 0.5 - np.array(c["expected_after_gate"]))) < 1e-6
 
 
-@pytest.mark.parametrize("fmt,tol", [(llm_hip.KV_BF16, "tolerance_f16_mirror"), (llm_hip.KV_INT8, "tolerance_int8")])
+@pytest.mark.parametrize("fmt,tol", [(llm_hip.KV_BF16, "tolerance_f16_mirror"), (llm_hip.KV_INT8, "tolerance_int8"),
+                                     (llm_hip.KV_INT8_ROW, "tolerance_int8")])
 def test_block_mirror_attention_matches_cpu_reference_across_blocks(ctx, fmt, tol):
     """native_matvec.rs:2065-2184: 257 rows span two device blocks."""
     c = KA["cross_block_257_rows"]
