@@ -554,9 +554,10 @@ def prefill_flops(B: int, prefix: int, chunk: int, Hq: int, window: int) -> int:
 
 def summarize(root: str) -> int:
     """Writes profiles/*.md from rocprofv3 csv output: ROOT/<section>/kt (--kernel-trace --stats),
-    ROOT/<section>/fetch and /write (--pmc FETCH_SIZE, --pmc WRITE_SIZE) and, for prefill
-    sections, ROOT/<section>/mfma, each made by `bench.py --only <section>` (the c2 section by
-    the default run).  Counters are scaled by what they read for the run's own 512 MiB copy."""
+    ROOT/<section>/fetch and /write (--pmc FETCH_SIZE, --pmc WRITE_SIZE) and, where present,
+    ROOT/<section>/ctr (one --pmc pass of other counters: MFMA for prefill, issue and wait
+    cycles for decode), each made by `bench.py --only <section>`.  FETCH_SIZE and WRITE_SIZE
+    are scaled by what they read for the run's own 512 MiB copy."""
     import csv
     import glob
     import statistics
@@ -617,9 +618,9 @@ def summarize(root: str) -> int:
                 k = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
                 tr.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
             ctr = {}
-            for sub in ("fetch", "write", "mfma"):
+            for sub in ("fetch", "write", "ctr"):
                 got = rows_of(sec, sub, "counter_collection.csv")
-                if got and sub != "mfma":
+                if got and sub != "ctr":
                     cmds.append(f"    cd /tmp && rocprofv3 --pmc {sub.upper()}_SIZE --output-format csv "
                                 f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2")
                 elif got:
@@ -659,6 +660,17 @@ def summarize(root: str) -> int:
             mf = [(k, c) for (k, c) in ctr if not c.endswith("_SIZE") and not k[0].startswith("__amd")]
             for k, c in sorted(mf):
                 body += f"| {sec.upper()} | `{k[0]}` | {k[1]} | counter `{c}` | {med(ctr[(k, c)]):.4g} per dispatch |  |  |  |  |  |  |  |\n"
+            for k in sorted({k for (k, c) in mf}):
+                g = {c: med(ctr[(k, c)]) for (kk, c) in mf if kk == k}
+                if "SQ_WAVE_CYCLES" in g and "SQ_ACTIVE_INST_ANY" in g:
+                    wc = g["SQ_WAVE_CYCLES"]
+                    body += (f"| {sec.upper()} | `{k[0]}` | {k[1]} | derived | of wave cycles: issuing "
+                             f"{100 * g['SQ_ACTIVE_INST_ANY'] / wc:.0f} %, waiting on counters / barrier "
+                             f"{100 * g.get('SQ_WAIT_ANY', 0) / wc:.0f} %, waiting to issue "
+                             f"{100 * g.get('SQ_WAIT_INST_ANY', 0) / wc:.0f} %, VALU active "
+                             f"{100 * g.get('SQ_ACTIVE_INST_VALU', 0) / wc:.0f} %; VALU instructions per vector "
+                             f"load {g.get('SQ_INSTS_VALU', 0) / max(g.get('SQ_INSTS_VMEM_RD', 1), 1):.1f} "
+                             f"|  |  |  |  |  |  |  |\n")
         if not body:
             continue
         text = (f"# {title}\n\nMI355X (gfx950), rocprofv3 from ROCm 7.2.  Made by `python bench.py --summarize <dir>` "
@@ -790,7 +802,7 @@ def main() -> int:
                     help="run one measurement (and the copy that calibrates the counters) for a profiler run; "
                          "prints its record instead of the headline line")
     ap.add_argument("--summarize", metavar="DIR",
-                    help="write profiles/*.md from rocprofv3 csv output under DIR/<section>/{kt,fetch,write,mfma}")
+                    help="write profiles/*.md from rocprofv3 csv output under DIR/<section>/{kt,fetch,write,ctr}")
     args = ap.parse_args()
     if args.summarize:
         return summarize(args.summarize)

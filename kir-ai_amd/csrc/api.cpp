@@ -351,16 +351,23 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "quantised pools need block_tokens and head_dim divisible by 4");
   if (n_blocks > INT32_MAX) return ctx->fail(LLH_ERR_INVALID_SHAPE, "block indices are int32");
   auto *pool = new llh_kv_pool();
+  pool->view.format = format;  // destroy() reads it on the error path below
   pool->ctx = ctx;
   pool->k_bytes = (size_t)n_blocks * kv_heads * block_tokens * head_dim * elem_bytes(format);
   pool->s_bytes = (size_t)n_blocks * scale_bytes_per_block(format, kv_heads, block_tokens);
   hipError_t e = hipSetDevice(ctx->device);
   if (e == hipSuccess) e = hipMalloc(&pool->k, pool->k_bytes);
   if (e == hipSuccess) e = hipMalloc(&pool->v, pool->k_bytes);
-  if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->ks, pool->s_bytes);
-  if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
-  if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->ks, 0, pool->s_bytes);
-  if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->vs, 0, pool->s_bytes);
+  if (scales_interleaved(format)) {
+    if (e == hipSuccess) e = hipMalloc(&pool->ks, 2 * pool->s_bytes);
+    if (e == hipSuccess) e = hipMemset(pool->ks, 0, 2 * pool->s_bytes);
+    if (e == hipSuccess) pool->vs = static_cast<char *>(pool->ks) + (size_t)block_tokens * 2;
+  } else {
+    if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->ks, pool->s_bytes);
+    if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
+    if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->ks, 0, pool->s_bytes);
+    if (e == hipSuccess && pool->s_bytes) e = hipMemset(pool->vs, 0, pool->s_bytes);
+  }
   // null-stream memsets are asynchronous to the host and unordered with non-blocking
   // streams: the pool is ready for any stream only once they have completed
   if (e == hipSuccess && pool->s_bytes) e = hipDeviceSynchronize();
@@ -379,7 +386,7 @@ int llh_kv_pool_destroy(llh_kv_pool *pool) {
   if (pool->k) (void)hipFree(pool->k);
   if (pool->v) (void)hipFree(pool->v);
   if (pool->ks) (void)hipFree(pool->ks);
-  if (pool->vs) (void)hipFree(pool->vs);
+  if (pool->vs && !scales_interleaved(pool->view.format)) (void)hipFree(pool->vs);
   delete pool;
   return LLH_OK;
 }
@@ -888,9 +895,11 @@ struct BlockStore {
 
   ~BlockStore() {
     if (ctx) (void)hipSetDevice(ctx->device);
-    for (void *p : {k, v, ks, vs})
+    for (void *p : {k, v, ks, vs_alloc()})
       if (p) (void)hipFree(p);
   }
+  // the V scales' own allocation (none for int8: they sit inside the K scales' one)
+  void *vs_alloc() const { return scales_interleaved(format) ? nullptr : vs; }
   PoolView view() const {
     return PoolView{format, kRingBlockTokens, kv_heads, head_dim, capacity, k, v, ks, vs};
   }
@@ -898,31 +907,35 @@ struct BlockStore {
   hipError_t allocate(int64_t cap) {
     kblock = (size_t)kv_heads * kRingBlockTokens * head_dim * elem_bytes(format);
     sblock = scale_bytes_per_block(format, kv_heads, kRingBlockTokens);
+    // scale bytes per block in the K scales' allocation (int8: K and V interleaved)
+    const bool il = scales_interleaved(format);
+    const size_t kscale = il ? 2 * sblock : sblock;
     void *nk = nullptr, *nv = nullptr, *nks = nullptr, *nvs = nullptr;
     hipError_t e = hipMalloc(&nk, kblock * cap);
     if (e == hipSuccess) e = hipMalloc(&nv, kblock * cap);
-    if (e == hipSuccess && sblock) e = hipMalloc(&nks, sblock * cap);
-    if (e == hipSuccess && sblock) e = hipMalloc(&nvs, sblock * cap);
+    if (e == hipSuccess && sblock) e = hipMalloc(&nks, kscale * cap);
+    if (e == hipSuccess && sblock && !il) e = hipMalloc(&nvs, sblock * cap);
     if (e == hipSuccess) e = hipMemset(nk, 0, kblock * cap);
     if (e == hipSuccess) e = hipMemset(nv, 0, kblock * cap);
-    if (e == hipSuccess && sblock) e = hipMemset(nks, 0, sblock * cap);
-    if (e == hipSuccess && sblock) e = hipMemset(nvs, 0, sblock * cap);
+    if (e == hipSuccess && sblock) e = hipMemset(nks, 0, kscale * cap);
+    if (e == hipSuccess && sblock && !il) e = hipMemset(nvs, 0, sblock * cap);
     if (e == hipSuccess && capacity > 0) {
       e = hipMemcpy(nk, k, kblock * capacity, hipMemcpyDeviceToDevice);
       if (e == hipSuccess) e = hipMemcpy(nv, v, kblock * capacity, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, sblock * capacity, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess && sblock) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
+      if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, kscale * capacity, hipMemcpyDeviceToDevice);
+      if (e == hipSuccess && sblock && !il) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
     }
+    if (il && nks) nvs = static_cast<char *>(nks) + (size_t)kRingBlockTokens * 2;
     // the memsets and device-to-device copies above run on the null stream,
     // asynchronously to the host: they must land before the caches' own
     // (non-blocking) streams touch the new buffers, and before the old ones go
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
-      for (void *p : {nk, nv, nks, nvs})
+      for (void *p : {nk, nv, nks, il ? nullptr : nvs})
         if (p) (void)hipFree(p);
       return e;
     }
-    for (void *p : {k, v, ks, vs})
+    for (void *p : {k, v, ks, vs_alloc()})
       if (p) (void)hipFree(p);
     k = nk;
     v = nv;
@@ -952,9 +965,10 @@ struct BlockStore {
                                   hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess)
       e = hipMemcpyAsync((char *)v + kblock * dst, (char *)v + kblock * src, kblock, hipMemcpyDeviceToDevice, s);
+    const size_t kscale = scales_interleaved(format) ? 2 * sblock : sblock;
     if (e == hipSuccess && sblock)
-      e = hipMemcpyAsync((char *)ks + sblock * dst, (char *)ks + sblock * src, sblock, hipMemcpyDeviceToDevice, s);
-    if (e == hipSuccess && sblock)
+      e = hipMemcpyAsync((char *)ks + kscale * dst, (char *)ks + kscale * src, kscale, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && sblock && !scales_interleaved(format))
       e = hipMemcpyAsync((char *)vs + sblock * dst, (char *)vs + sblock * src, sblock, hipMemcpyDeviceToDevice, s);
     return e;
   }

@@ -279,9 +279,10 @@ struct llh_block_pool {
       e = hipMemcpy((char *)pool->k + kb * dst, (char *)pool->k + kb * src, kb, hipMemcpyDeviceToDevice);
     if (e == hipSuccess)
       e = hipMemcpy((char *)pool->v + kb * dst, (char *)pool->v + kb * src, kb, hipMemcpyDeviceToDevice);
+    const size_t ksb = scales_interleaved(v.format) ? 2 * sb : sb;  // int8: K and V scales in one run
     if (e == hipSuccess && sb)
-      e = hipMemcpy((char *)pool->ks + sb * dst, (char *)pool->ks + sb * src, sb, hipMemcpyDeviceToDevice);
-    if (e == hipSuccess && sb)
+      e = hipMemcpy((char *)pool->ks + ksb * dst, (char *)pool->ks + ksb * src, ksb, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess && sb && !scales_interleaved(v.format))
       e = hipMemcpy((char *)pool->vs + sb * dst, (char *)pool->vs + sb * src, sb, hipMemcpyDeviceToDevice);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     return e;

@@ -208,8 +208,10 @@ __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kv
 #pragma unroll
     for (int j = 0; j < 8; j++) r.v[j] = ld_nt4(vb + (16 * j + c) * BT + g * 4);
     if constexpr (FMT == kInt8) {
-      r.ks = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales) + bh * BT + 4 * g);
-      r.vs = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) + bh * BT + 4 * g);
+      r.ks = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales) +
+                                              int8_scale_index(bh, 4 * g, BT));
+      r.vs = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) +
+                                              int8_scale_index(bh, 4 * g, BT));
     } else {
       r.ksb = reinterpret_cast<const float *>(a.pool.k_scales)[bh];
       r.vsb = reinterpret_cast<const float *>(a.pool.v_scales)[bh];

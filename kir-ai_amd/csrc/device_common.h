@@ -23,7 +23,8 @@ __device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_
   const void *sc = tensor ? p.v_scales : p.k_scales;
   if (p.format == kBf16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(base)[idx] << 16);
   if (p.format == kInt8) {
-    const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + t]);
+    const float s =
+        (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[int8_scale_index(bh, t, p.block_tokens)]);
     return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
   }
   if (p.format == kInt8Row)  // one f32 scale per token row of the block (all heads)

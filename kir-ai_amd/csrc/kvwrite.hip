@@ -177,7 +177,9 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)(uint8_t)quant_int8(x[j], sc) << (8 * (j & 3));
     codes[tensor][0] = q[0];
     codes[tensor][1] = q[1];
-    if (c == 0) reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[bh * BT + t] = __builtin_bit_cast(uint16_t, s16);
+    if (c == 0)
+      reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[int8_scale_index(bh, t, BT)] =
+          __builtin_bit_cast(uint16_t, s16);
   }
   }
   // one-byte codes (int8 / fp8): K rows straight out, V transposed through LDS
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
           else
             kd[(bh * BT + t) * Dh + d] = code;
         }
-        if (lane == 0) (tensor ? vsd : ksd)[bh * BT + t] = __builtin_bit_cast(uint16_t, s16);
+        if (lane == 0) (tensor ? vsd : ksd)[int8_scale_index(bh, t, BT)] = __builtin_bit_cast(uint16_t, s16);
       }
     }
     return;
@@ -482,7 +484,8 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
         kd[(bh * BT + off) * Dh + d] = code;
     }
     if (lane == 0)
-      reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[bh * BT + off] = __builtin_bit_cast(uint16_t, s16);
+      reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[int8_scale_index(bh, off, BT)] =
+          __builtin_bit_cast(uint16_t, s16);
   }
 }
 
@@ -490,7 +493,8 @@ __device__ __forceinline__ float load_f32(const PoolView &p, const void *base, c
                                           int off) {
   if (p.format == kBf16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
   if (p.format == kInt8) {
-    const float s = (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[bh * p.block_tokens + off]);
+    const float s = (float)__builtin_bit_cast(
+        _Float16, reinterpret_cast<const uint16_t *>(sc)[int8_scale_index(bh, off, p.block_tokens)]);
     return (float)reinterpret_cast<const int8_t *>(base)[idx] * s;
   }
   if (p.format == kInt8Row)

@@ -148,8 +148,9 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
       r.v[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(a.pool.v) + base +
                                                 (tid >> 1) * BT + (tid & 1) * 8);
       if constexpr (FMT == kInt8) {
-        r.ks[i] = reinterpret_cast<const uint16_t *>(a.pool.k_scales)[bh * BT + (tid >> 4)];
-        r.vs[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) + bh * BT +
+        r.ks[i] = reinterpret_cast<const uint16_t *>(a.pool.k_scales)[int8_scale_index(bh, tid >> 4, BT)];
+        r.vs[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) +
+                                                   int8_scale_index(bh, 0, BT) +
                                                    (tid & 1) * 8);
       } else {
         r.ks[i] = reinterpret_cast<const uint32_t *>(a.pool.k_scales)[bh];

@@ -648,7 +648,12 @@ class KvPool:
             return buf.cpu().numpy()
 
         out = {"k": dl(i.d_k, i.k_bytes), "v": dl(i.d_v, i.k_bytes)}
-        if i.scale_bytes:
+        if i.scale_bytes and i.format == KV_INT8:
+            # one allocation, per (block, head) the K scales then the V scales
+            both = dl(i.d_k_scales, 2 * i.scale_bytes).reshape(-1, 2, i.block_tokens * 2)
+            out["k_scales"] = np.ascontiguousarray(both[:, 0]).ravel()
+            out["v_scales"] = np.ascontiguousarray(both[:, 1]).ravel()
+        elif i.scale_bytes:
             out["k_scales"] = dl(i.d_k_scales, i.scale_bytes)
             out["v_scales"] = dl(i.d_v_scales, i.scale_bytes)
         return out
