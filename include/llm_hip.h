@@ -154,10 +154,11 @@ int llh_ctx_kernel_time(llh_ctx *ctx, int32_t kind, double *total_ms, int64_t *c
  * parameter).  Device layout, block b, kv head h:
  *   K  [n_blocks][kv_heads][block_tokens][head_dim]   token rows
  *   V  [n_blocks][kv_heads][head_dim][block_tokens]   dim rows (transposed)
- *   int8 scales: fp16 [n_blocks][kv_heads][2][block_tokens] in one allocation:
- *                the K scales of (block, head), then its V scales, so one
- *                decode unit reads its scales from one 2 * block_tokens * 2-byte
- *                run (d_v_scales = d_k_scales + block_tokens * 2 bytes)
+ *   int8 scales: fp16 [n_blocks][kv_heads][block_tokens][2] in one allocation:
+ *                per token the pair (K scale, V scale), so a decode lane reads
+ *                its token's two scales with one 4-byte load
+ *                (d_v_scales = d_k_scales + 2 bytes; both have a stride of
+ *                4 bytes per token)
  *   fp8 scales : f32  [n_blocks][kv_heads]               for K and for V
  *   int8 row scales (LLH_KV_INT8_ROW): f32 [n_blocks][block_tokens] for K and for V
  * Position p of a sequence lives in block_table[(p / block_tokens) % max_blocks]
@@ -176,7 +177,7 @@ typedef struct llh_kv_pool_info {
   void *d_v_scales; /* NULL for bf16; int8: inside d_k_scales' allocation (see above) */
   size_t k_bytes;   /* bytes of d_k (and of d_v) */
   size_t scale_bytes; /* bytes of the K (and of the V) scales; int8: the allocation at d_k_scales
-                         holds both, 2 * scale_bytes, interleaved per (block, head) */
+                         holds both, 2 * scale_bytes, interleaved per token */
 } llh_kv_pool_info;
 
 int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32_t kv_heads,

@@ -361,7 +361,7 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
   if (scales_interleaved(format)) {
     if (e == hipSuccess) e = hipMalloc(&pool->ks, 2 * pool->s_bytes);
     if (e == hipSuccess) e = hipMemset(pool->ks, 0, 2 * pool->s_bytes);
-    if (e == hipSuccess) pool->vs = static_cast<char *>(pool->ks) + (size_t)block_tokens * 2;
+    if (e == hipSuccess) pool->vs = static_cast<char *>(pool->ks) + kInt8VScaleOffsetBytes;
   } else {
     if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->ks, pool->s_bytes);
     if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
@@ -925,7 +925,7 @@ struct BlockStore {
       if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, kscale * capacity, hipMemcpyDeviceToDevice);
       if (e == hipSuccess && sblock && !il) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
     }
-    if (il && nks) nvs = static_cast<char *>(nks) + (size_t)kRingBlockTokens * 2;
+    if (il && nks) nvs = static_cast<char *>(nks) + kInt8VScaleOffsetBytes;
     // the memsets and device-to-device copies above run on the null stream,
     // asynchronously to the host: they must land before the caches' own
     // (non-blocking) streams touch the new buffers, and before the old ones go

@@ -76,6 +76,10 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
 
 // Value of lane (l ^ 15) within its 16-lane row: every lane is written, so no
 // old value is needed (mov_dpp leaves the destination's prior bits unused).
@@ -167,8 +171,9 @@ template <int FMT>
 struct BlockRegs {
   uint4 k[2];
   uint32_t v[8];
-  uint2 ks;   // int8: fp16 scales of tokens 4g..4g+3
-  uint2 vs;
+  // int8: fp16 (K scale, V scale) pairs, one per word: the lane's own token in
+  // the token-lane layout (x only), tokens 4g..4g+3 in the row layout
+  uint4 sc;
   float ksb;  // fp8: per (block, head) scales
   float vsb;
   bool valid;
@@ -208,10 +213,12 @@ __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kv
 #pragma unroll
     for (int j = 0; j < 8; j++) r.v[j] = ld_nt4(vb + (16 * j + c) * BT + g * 4);
     if constexpr (FMT == kInt8) {
-      r.ks = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales) +
-                                              int8_scale_index(bh, 4 * g, BT));
-      r.vs = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) +
-                                              int8_scale_index(bh, 4 * g, BT));
+      const uint16_t *sp = reinterpret_cast<const uint16_t *>(a.pool.k_scales);
+      if constexpr (TL) {
+        r.sc.x = *reinterpret_cast<const uint32_t *>(sp + int8_scale_index(bh, 4 * g + ((lane >> 2) & 3), BT));
+      } else {
+        r.sc = *reinterpret_cast<const uint4 *>(sp + int8_scale_index(bh, 4 * g, BT));
+      }
     } else {
       r.ksb = reinterpret_cast<const float *>(a.pool.k_scales)[bh];
       r.vsb = reinterpret_cast<const float *>(a.pool.v_scales)[bh];
@@ -282,35 +289,32 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
 }
 
-// The V elements of dim 16j + c for tokens 4g..4g+3 as two packed bf16 pairs:
-// (token 0, token 1) and (token 2, token 3); masked tokens are zero.
+// One V word of a quantized pool (dim 16j + c, tokens 4g..4g+3) as two packed
+// bf16 pairs: (token 0, token 1) and (token 2, token 3).
 template <int FMT>
-__device__ __forceinline__ void v_pairs(const BlockRegs<FMT> &r, const uint32_t (&vmask)[2], int j, uint32_t &p01,
-                                        uint32_t &p23) {
-  if constexpr (FMT == kBf16) {
-    p01 = r.v[j].x & vmask[0];
-    p23 = r.v[j].y & vmask[1];
-  } else if constexpr (FMT == kInt8) {
-    const uint32_t w = r.v[j] & vmask[0];
+__device__ __forceinline__ void v_code_pairs(uint32_t w, uint32_t &p01, uint32_t &p23) {
+  if constexpr (FMT == kInt8) {
     p01 = i8x2_to_bf16(w, 0);
     p23 = i8x2_to_bf16(w, 2);
   } else {
-    const uint32_t w = r.v[j] & vmask[0];
     p01 = fp8x2_to_bf16<false>(w);
     p23 = fp8x2_to_bf16<true>(w);
   }
 }
 
 // One 16-token block for the G query heads of this wavefront's kv head.
-// q . k and p . v both run on packed bf16 dot2 with fp32 accumulation: K, V and
-// q are exact in bf16 (int8 and e4m3 codes convert exactly); the softmax
-// weights p (times the value scale for int8/fp8) are rounded to bf16 for the
-// p . v products, and the softmax denominator sums exactly those rounded
-// weights (divided by the value scale for int8/fp8), so the output is a
-// weighted mean of the attended values whose weights sum to one.
+// q . k and p . v run on packed bf16 dot2 with fp32 accumulation: K, V and q
+// are exact in bf16 (int8 and e4m3 codes convert exactly).  The exception is
+// q . k on int8 pools in the token-lane layout, which runs on v_dot4_i32_i8
+// against q in 16-bit fixed point (prep_q; qstep is the fixed-point step of
+// this lane's head).  The softmax weights p (times the value scale for
+// int8/fp8) are rounded to bf16 for the p . v products, and the softmax
+// denominator sums exactly those rounded weights (divided by the value scale
+// for int8/fp8), so the output is a weighted mean of the attended values whose
+// weights sum to one.
 template <int G, int FMT>
 __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRegs<FMT> &r, int jb, int lo, int len,
-                                              int lane, const uint32_t (&qw)[G][kQWords<G, FMT>],
+                                              int lane, const uint32_t (&qw)[G][kQWords<G, FMT>], float qstep,
                                               SoftmaxState<G> &st) {
   if (!r.valid && lane == 0) atomicOr(a.err, kErrBadBlock);  // its tokens are all masked below
   const int g = lane >> 4;
@@ -335,38 +339,52 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     const int tq = (lane >> 2) & 3;
     const int c4 = lane & 3;
     const bool ok_own = !partial || ((jb * BT + 4 * g + tq >= lo) && (jb * BT + 4 * g + tq < len) && r.valid);
-    uint32_t kp[16];
+    // q . k of this token for every head over the lane's 32 dims, summed over
+    // the token's four lanes (quad_perm butterflies: all four get the sum)
+    float s_own = 0.0f;
+    if constexpr (FMT == kInt8) {
+      // the codes against q's fixed-point words (prep_q): 256 (hi . k) + lo . k,
+      // exact in int32 (|sum| < 2^29), times the head's step 2^e
+      const uint32_t kw[8] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w, r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+      int s_int = 0;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
+      for (int gi = 0; gi < G; gi++) {
+        int acc = 0;
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        if constexpr (FMT == kInt8) {
-          kp[8 * i + 2 * k] = i8x2_to_bf16(w[k], 0);
-          kp[8 * i + 2 * k + 1] = i8x2_to_bf16(w[k], 2);
-        } else {
+        for (int k = 0; k < 8; k++) acc = __builtin_amdgcn_sdot4((int)kw[k], (int)qw[gi][k], acc, false);
+        acc *= 256;
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc = __builtin_amdgcn_sdot4((int)kw[k], (int)qw[gi][8 + k], acc, false);
+        acc += dpp_i32<0xB1>(acc);
+        acc += dpp_i32<0x4E>(acc);
+        if (gi == 0 || (c4 & (G - 1)) == gi) s_int = acc;
+      }
+      s_own = (float)s_int * qstep;
+    } else {
+      uint32_t kp[16];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t w[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
           kp[8 * i + 2 * k] = fp8x2_to_bf16<false>(w[k]);
           kp[8 * i + 2 * k + 1] = fp8x2_to_bf16<true>(w[k]);
         }
       }
-    }
-    // q . k of this token for every head over the lane's 32 dims, summed over
-    // the token's four lanes (quad_perm butterflies: all four get the sum)
-    float s_own = 0.0f;
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-      float acc = 0.0f;
+      for (int gi = 0; gi < G; gi++) {
+        float acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 16; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
-      acc += dpp<0xB1>(acc);  // quad_perm [1,0,3,2]
-      acc += dpp<0x4E>(acc);  // quad_perm [2,3,0,1]
-      if (gi == 0 || (c4 & (G - 1)) == gi) s_own = acc;
+        for (int k = 0; k < 16; k++) acc = dot2_bf16(kp[k], qw[gi][k], acc);
+        acc += dpp<0xB1>(acc);  // quad_perm [1,0,3,2]
+        acc += dpp<0x4E>(acc);  // quad_perm [2,3,0,1]
+        if (gi == 0 || (c4 & (G - 1)) == gi) s_own = acc;
+      }
     }
     float ks_own, vs_own;
     if constexpr (FMT == kInt8) {
-      const int sh = 16 * (tq & 1);
-      ks_own = f16_bits_to_f32(((tq & 2) ? r.ks.y : r.ks.x) >> sh);
-      vs_own = f16_bits_to_f32(((tq & 2) ? r.vs.y : r.vs.x) >> sh);
+      ks_own = f16_bits_to_f32(r.sc.x & 0xffffu);
+      vs_own = f16_bits_to_f32(r.sc.x >> 16);
     } else {
       ks_own = r.ksb;
       vs_own = r.vsb;
@@ -427,12 +445,13 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
       const int hf = (lane >> 3) & 1;
       float kscale_own[2];
       if constexpr (FMT == kInt8) {
-        const float k4[4] = {f16_bits_to_f32(r.ks.x & 0xffffu), f16_bits_to_f32(r.ks.x >> 16),
-                             f16_bits_to_f32(r.ks.y & 0xffffu), f16_bits_to_f32(r.ks.y >> 16)};
-        vsc[0] = f16_bits_to_f32(r.vs.x & 0xffffu);
-        vsc[1] = f16_bits_to_f32(r.vs.x >> 16);
-        vsc[2] = f16_bits_to_f32(r.vs.y & 0xffffu);
-        vsc[3] = f16_bits_to_f32(r.vs.y >> 16);
+        const uint32_t pr[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+        float k4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          k4[i] = f16_bits_to_f32(pr[i] & 0xffffu);
+          vsc[i] = f16_bits_to_f32(pr[i] >> 16);
+        }
         kscale_own[0] = (hf ? k4[1] : k4[0]) * a.scale_log2e;
         kscale_own[1] = (hf ? k4[3] : k4[2]) * a.scale_log2e;
       } else {
@@ -541,12 +560,39 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
       }
     }
   }
+  // p . v over this lane's 8 dims; V of tokens outside [lo, len) is zeroed
+  // first (only partial blocks pay the masks)
+  if constexpr (FMT == kBf16) {
+    uint2 vv[8];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    uint32_t v01, v23;
-    v_pairs<FMT>(r, vmask, j, v01, v23);
+    for (int j = 0; j < 8; j++) vv[j] = r.v[j];
+    if (partial) {
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) st.o[gi][j] = dot2_bf16(v23, w23[gi], dot2_bf16(v01, w01[gi], st.o[gi][j]));
+      for (int j = 0; j < 8; j++) {
+        vv[j].x &= vmask[0];
+        vv[j].y &= vmask[1];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int gi = 0; gi < G; gi++)
+        st.o[gi][j] = dot2_bf16(vv[j].y, w23[gi], dot2_bf16(vv[j].x, w01[gi], st.o[gi][j]));
+  } else {
+    uint32_t vv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) vv[j] = r.v[j];
+    if (partial) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) vv[j] &= vmask[0];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t v01, v23;
+      v_code_pairs<FMT>(vv[j], v01, v23);
+#pragma unroll
+      for (int gi = 0; gi < G; gi++) st.o[gi][j] = dot2_bf16(v23, w23[gi], dot2_bf16(v01, w01[gi], st.o[gi][j]));
+    }
   }
 }
 
@@ -586,6 +632,64 @@ __device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int la
         qw[gi][4 * i + 3] = t.w;
       }
     }
+  }
+}
+
+// Turns the bf16 q words of load_q into the operands compute_block uses and
+// returns this lane's fixed-point step (1 where q stays bf16).  Split from the
+// loads so that a caller can issue its next block's loads in between.
+//
+// int8 pools in the token-lane layout take q . k on v_dot4_i32_i8: each head's
+// q becomes q16 = round(q * 2^-e) with e = exponent(max |q|) - 13, so |q16| <=
+// 16320 and |q - q16 * 2^e| <= 2^-14 * max |q| (bf16 elements within 2^-6 of
+// the largest one's binade are exact).  Words k = 0..7 then hold
+// hi = floor((q16 + 128) / 256) and words 8..15 lo = q16 - 256 hi (both in int8
+// range) for dims 32c + 4k .. +3, the dims of the lane's K word k, so that
+// q . k = 2^e (256 hi . k + lo . k) in int32 without rounding.  The step is NaN
+// when the head's q holds an infinity or NaN, so its scores are NaN as in f32.
+template <int G, int FMT>
+__device__ __forceinline__ float prep_q(int lane, uint32_t (&qw)[G][kQWords<G, FMT>]) {
+  if constexpr (FMT == kInt8 && kTokenLanes<G, FMT>) {
+    typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+    // q * 2^-e + 1.5 * 2^23 + 128, rounded once (fma): the float's low 16 bits
+    // are q16 + 128 in two's complement, byte 0 = lo + 128, byte 1 = hi
+    constexpr float kRound = 12583040.0f;
+    float own = 1.0f;
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      u16x2_t mv = {0, 0};
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        mv = __builtin_elementwise_max(mv, __builtin_bit_cast(u16x2_t, qw[gi][k] & 0x7fff7fffu));
+      // |q| bits order as integers (NaN above infinity); the head's 128 dims lie in the lane's quad
+      int mx = max((int)mv.x, (int)mv.y);
+      mx = max(mx, dpp_i32<0xB1>(mx));
+      mx = max(mx, dpp_i32<0x4E>(mx));
+      const int ex = mx >> 7;                  // biased exponent of the largest |q|
+      const int inv_b = min(267 - ex, 253);    // 2^-e, with e >= -126
+      const float inv = __int_as_float(inv_b << 23);
+      const float step = ex == 255 ? __builtin_nanf("") : __int_as_float((254 - inv_b) << 23);
+      uint32_t t[16];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t p0 = qw[gi][2 * k], p1 = qw[gi][2 * k + 1];
+        const uint32_t f0 = __float_as_uint(fmaf(bf16_lo(p0), inv, kRound));
+        const uint32_t f1 = __float_as_uint(fmaf(bf16_hi(p0), inv, kRound));
+        const uint32_t f2 = __float_as_uint(fmaf(bf16_lo(p1), inv, kRound));
+        const uint32_t f3 = __float_as_uint(fmaf(bf16_hi(p1), inv, kRound));
+        // bytes (hi0, hi1, lo0 + 128, lo1 + 128) and (hi2, hi3, lo2 + 128, lo3 + 128)
+        const uint32_t t01 = __builtin_amdgcn_perm(f1, f0, 0x04000501u);
+        const uint32_t t23 = __builtin_amdgcn_perm(f3, f2, 0x04000501u);
+        t[k] = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+        t[8 + k] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; k++) qw[gi][k] = t[k];
+      if (gi == 0 || ((lane & 3) & (G - 1)) == gi) own = step;
+    }
+    return own;
+  } else {
+    return 1.0f;
   }
 }
 
@@ -720,9 +824,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   if (takes_new) load_new_token(a, b, kvh, lane, nt);
 
   // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
+  float qstep = 1.0f;
   if (nbw > 0) {
     BlockRegs<FMT> r[2];
     load_block<FMT, TL>(a, entry(0), kvh, lane, r[0]);
+    qstep = prep_q<G, FMT>(lane, qw);
     int e_next = nbw > 1 ? entry(1) : -1;
     // every step inside the loop issues the next block's loads before its math,
     // so the wait before the math always leaves them in flight
@@ -731,7 +837,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
         load_block<FMT, TL>(a, e_next, kvh, lane, nxt);
         e_next = k + 2 < nbw ? entry(k + 2) : -1;
       }
-      compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len_kv, lane, qw, st);
+      compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len_kv, lane, qw, qstep, st);
     };
     int k = 0;
     for (; k + 2 < nbw; k += 2) {
@@ -1029,6 +1135,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
 
   BlockRegs<FMT> r[2];
   load_block<FMT, TL>(a, next_entry(), l_kvh, lane, r[0]);
+  float qstep = prep_q<G, FMT>(lane, qw);
   // fused append: a segment's new-token rows are loaded with its last unit, into
   // the buffer that travels with that unit's registers (r[0] / r[1])
   NewToken nt[2];
@@ -1060,15 +1167,13 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   };
 
   // One unit: a new segment's q is loaded first, then unit k+1's loads are
-  // issued, then unit k is computed.  Every step inside the loop issues the
-  // next unit's loads after any q load, so the wait before the math always
-  // leaves the next unit's loads in flight.
+  // issued, then q is prepared (prep_q) and unit k is computed.  Every step
+  // inside the loop issues the next unit's loads after any q load, so the wait
+  // before the math always leaves the next unit's loads in flight.
   auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, NewToken &cur_nt, NewToken &nxt_nt, bool issue)
                   __attribute__((always_inline)) {
-    if (need_q) {
-      load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
-      need_q = false;
-    }
+    const bool new_q = need_q;
+    if (new_q) load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
     if (issue) {
       load_block<FMT, TL>(a, e_next, l_kvh, lane, nxt);
       if constexpr (FMT == kBf16)
@@ -1079,7 +1184,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
         l_kvh++;
       }
     }
-    compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len_kv, lane, qw, st);
+    if (new_q) {
+      qstep = prep_q<G, FMT>(lane, qw);
+      need_q = false;
+    }
+    compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len_kv, lane, qw, qstep, st);
     if (++c_j == nb) {  // the segment ends with this unit
       if constexpr (FMT == kBf16)
         if (fused) add_new_token<G>(a, st, b, seg_kvh, len, lane, qw, cur_nt);

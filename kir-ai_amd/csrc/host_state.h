@@ -200,7 +200,7 @@ struct llh_kv_pool {
 inline size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 ? 2 : 1; }
 
 // int8 pools keep the K and V scales in one allocation (int8_scale_index): the V
-// scale pointer is inside the K scales' allocation, block_tokens fp16 further.
+// scale pointer is inside the K scales' allocation, one fp16 further.
 inline bool scales_interleaved(int32_t format) { return format == LLH_KV_INT8; }
 
 inline size_t scale_bytes_per_block(int32_t format, int32_t kv_heads, int32_t block_tokens) {

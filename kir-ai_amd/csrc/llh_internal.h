@@ -16,12 +16,14 @@ constexpr int kMatvecColsMultiple = kMatvecWaves * 16;  // cols the projection k
 
 enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2, kInt8Row = 3 };
 
-// int8 (per (token, head)) scales: one allocation, per (block, head) bh the
-// block_tokens K scales then the block_tokens V scales (fp16), so a decode unit
-// reads both from one 64-byte run; the pool's V scale pointer is the K scale
-// pointer + block_tokens.  Index of token t's scale of bh in either.
+// int8 (per (token, head)) scales: one allocation holding, for each (block,
+// head) bh and token t, the fp16 pair (K scale, V scale).  A decode lane reads
+// its token's two scales with one 4-byte load and a block-head's 16 pairs are
+// one 64-byte run.  The pool's V scale pointer is the K scale pointer + one
+// fp16 (kInt8VScaleOffsetBytes); index of token t's scale of bh in either.
+constexpr size_t kInt8VScaleOffsetBytes = 2;
 __host__ __device__ constexpr size_t int8_scale_index(size_t bh, int t, int block_tokens) {
-  return bh * 2 * (size_t)block_tokens + (size_t)t;
+  return (bh * (size_t)block_tokens + (size_t)t) * 2;
 }
 
 // Device error flags (bit set by kernels, read back by the host).

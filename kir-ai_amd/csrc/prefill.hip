@@ -104,7 +104,7 @@ struct TileRegs {
   uint2 k[NB];
   uint2 v[NB];
   uint32_t ks[NB];  // int8: fp16 bits of the K token's scale; fp8: f32 bits of the block's K scale
-  uint4 vs[NB];     // int8: eight fp16 V scales (tokens 8*(tid&1)..); fp8: .x = f32 bits of the V scale
+  uint4 vs[NB][2];  // int8: the (K, V) fp16 scale pairs of tokens 8*(tid&1) .. +7; fp8: [0].x = f32 bits of the V scale
 };
 
 // Block-table entries of the tile starting at kt: lane kb of every wavefront
@@ -149,12 +149,13 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
                                                 (tid >> 1) * BT + (tid & 1) * 8);
       if constexpr (FMT == kInt8) {
         r.ks[i] = reinterpret_cast<const uint16_t *>(a.pool.k_scales)[int8_scale_index(bh, tid >> 4, BT)];
-        r.vs[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.v_scales) +
-                                                   int8_scale_index(bh, 0, BT) +
-                                                   (tid & 1) * 8);
+        const uint4 *sp = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales) +
+                                                          int8_scale_index(bh, (tid & 1) * 8, BT));
+        r.vs[i][0] = sp[0];
+        r.vs[i][1] = sp[1];
       } else {
         r.ks[i] = reinterpret_cast<const uint32_t *>(a.pool.k_scales)[bh];
-        r.vs[i].x = reinterpret_cast<const uint32_t *>(a.pool.v_scales)[bh];
+        r.vs[i][0].x = reinterpret_cast<const uint32_t *>(a.pool.v_scales)[bh];
       }
     }
   }
@@ -190,11 +191,12 @@ __device__ __forceinline__ void tile_bf16(const TileRegs<FMT, NB> &r, int i, u32
 #pragma unroll
     for (int e = 0; e < 8; e++) kf[e] = code_f32<FMT>(r.k[i], e) * ks;
     if constexpr (FMT == kInt8) {
-      const uint32_t sw[4] = {r.vs[i].x, r.vs[i].y, r.vs[i].z, r.vs[i].w};
+      const uint32_t pr[8] = {r.vs[i][0].x, r.vs[i][0].y, r.vs[i][0].z, r.vs[i][0].w,
+                              r.vs[i][1].x, r.vs[i][1].y, r.vs[i][1].z, r.vs[i][1].w};
 #pragma unroll
-      for (int e = 0; e < 8; e++) vf[e] = code_f32<FMT>(r.v[i], e) * half_bits_f32(sw[e >> 1] >> (16 * (e & 1)));
+      for (int e = 0; e < 8; e++) vf[e] = code_f32<FMT>(r.v[i], e) * half_bits_f32(pr[e] >> 16);
     } else {
-      const float vs = __uint_as_float(r.vs[i].x);
+      const float vs = __uint_as_float(r.vs[i][0].x);
 #pragma unroll
       for (int e = 0; e < 8; e++) vf[e] = code_f32<FMT>(r.v[i], e) * vs;
     }

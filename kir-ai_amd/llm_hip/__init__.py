@@ -649,8 +649,8 @@ class KvPool:
 
         out = {"k": dl(i.d_k, i.k_bytes), "v": dl(i.d_v, i.k_bytes)}
         if i.scale_bytes and i.format == KV_INT8:
-            # one allocation, per (block, head) the K scales then the V scales
-            both = dl(i.d_k_scales, 2 * i.scale_bytes).reshape(-1, 2, i.block_tokens * 2)
+            # one allocation, per (block, head, token) the pair (K scale, V scale)
+            both = dl(i.d_k_scales, 2 * i.scale_bytes).reshape(-1, 2, 2)
             out["k_scales"] = np.ascontiguousarray(both[:, 0]).ravel()
             out["v_scales"] = np.ascontiguousarray(both[:, 1]).ravel()
         elif i.scale_bytes:

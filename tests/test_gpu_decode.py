@@ -249,6 +249,51 @@ def test_decode_quantized_gqa_groups(ctx, decode_kernel, fmt, Hq, Hkv):
     check(ctx, batch, Hq, Hkv, fmt, window=250, seed=14, what=f"fmt={fmt} Hq={Hq} Hkv={Hkv} W=250")
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+def test_decode_int8_query_magnitudes(ctx, decode_kernel, Hq, Hkv):
+    """int8 pools score q . k on integer dot products against q in 16-bit fixed
+    point, one step per query head (2^e from the head's largest |q|).  Heads of
+    very different magnitude side by side (so a lane taking another head's step
+    would be off by orders of magnitude), outlier elements 100x the rest, bf16
+    subnormal and all-zero heads all meet the oracle bar."""
+    lens = [300, 700, 1200]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=Hq + Hkv)
+    pool, q = build_case(ctx, batch, Hq, Hkv, llm_hip.KV_INT8, seed=31)
+    B = len(lens)
+    qf = oracle.bf16_to_f32(q).reshape(B, Hq, D).copy()
+    mags = [1.0, 1e-30, 6.0, 1e-3, 1e-39, 0.0, 3e4, 0.25]
+    for h in range(Hq):
+        qf[:, h, :] *= np.float32(mags[h % len(mags)])
+        if h % 3 == 1:
+            qf[:, h, 5 + h] *= np.float32(100.0)
+    qb = oracle.f32_to_bf16(qf.ravel())
+    scale = 1.0 / math.sqrt(D)
+    for window in (0, 250):
+        out = run_decode(ctx, pool, batch, qb, Hq, window, scale)
+        assert ctx.device_errors() == 0, ctx.last_error()
+        ref = oracle_decode(pool, batch, llm_hip.KV_INT8, Hq, Hkv, window, qb, scale)
+        assert_parity(out, ref, what=f"Hq={Hq} Hkv={Hkv} W={window}")
+
+
+def test_decode_int8_nan_query_stays_in_its_head(ctx, decode_kernel):
+    """A NaN in one query head's q makes that head's output NaN (as f32 scores
+    would) and leaves every other head of the sequence at the oracle bar."""
+    Hq, Hkv = 32, 8
+    lens = [500, 900]
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=41)
+    pool, q = build_case(ctx, batch, Hq, Hkv, llm_hip.KV_INT8, seed=42)
+    qn = q.reshape(len(lens), Hq, D).copy()
+    qn[1, 5, 17] = 0x7FC0  # NaN in sequence 1, head 5
+    scale = 1.0 / math.sqrt(D)
+    out = run_decode(ctx, pool, batch, qn.ravel(), Hq, 0, scale).reshape(len(lens), Hq, D)
+    assert ctx.device_errors() == 0, ctx.last_error()
+    assert np.all(np.isnan(oracle.bf16_to_f32(out[1, 5])))
+    ref = oracle_decode(pool, batch, llm_hip.KV_INT8, Hq, Hkv, 0, q, scale).reshape(len(lens), Hq, D)
+    keep = np.ones((len(lens), Hq), bool)
+    keep[1, 5] = False
+    assert_parity(out[keep], ref[keep], what="heads without the NaN")
+
+
 @pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
 def test_decode_bad_block_is_masked_and_flagged(ctx, decode_kernel, fmt):
     """A table entry outside the pool raises the sticky flag, its tokens are
