@@ -159,7 +159,10 @@ int llh_ctx_kernel_time(llh_ctx *ctx, int32_t kind, double *total_ms, int64_t *c
  *                its token's two scales with one 4-byte load
  *                (d_v_scales = d_k_scales + 2 bytes; both have a stride of
  *                4 bytes per token)
- *   fp8 scales : f32  [n_blocks][kv_heads]               for K and for V
+ *   fp8 scales : f32  [n_blocks][kv_heads][2] in one allocation: the pair
+ *                (K scale, V scale) of (block, head), one 8-byte load per
+ *                decode unit (d_v_scales = d_k_scales + 4 bytes; both have a
+ *                stride of 8 bytes per (block, head))
  *   int8 row scales (LLH_KV_INT8_ROW): f32 [n_blocks][block_tokens] for K and for V
  * Position p of a sequence lives in block_table[(p / block_tokens) % max_blocks]
  * at offset p % block_tokens.  The modulus lets a ring of blocks serve a
@@ -174,10 +177,10 @@ typedef struct llh_kv_pool_info {
   void *d_k;
   void *d_v;
   void *d_k_scales; /* NULL for bf16 */
-  void *d_v_scales; /* NULL for bf16; int8: inside d_k_scales' allocation (see above) */
+  void *d_v_scales; /* NULL for bf16; int8, fp8: inside d_k_scales' allocation (see above) */
   size_t k_bytes;   /* bytes of d_k (and of d_v) */
-  size_t scale_bytes; /* bytes of the K (and of the V) scales; int8: the allocation at d_k_scales
-                         holds both, 2 * scale_bytes, interleaved per token */
+  size_t scale_bytes; /* bytes of the K (and of the V) scales; int8, fp8: the allocation at
+                         d_k_scales holds both, 2 * scale_bytes, as (K, V) pairs */
 } llh_kv_pool_info;
 
 int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32_t kv_heads,

@@ -115,10 +115,9 @@ SplitPlan plan_splits(const llh_ctx *ctx, int num_seqs, int kv_heads, int max_se
 // all resident at once, the best grid measured on MI355X for C2 (one and three
 // per CU run 2-8% slower) and for C5 int8 / fp8 (three and four per CU, which
 // run in rounds, 2-4% slower).  It is chosen when the step has at least
-// kStreamMinUnitsPerWave units (block x kv head) per wavefront and its 32-bit
-// partition arithmetic (units * wavefronts < 2^31) is exact; smaller steps
-// (C1, C4 decode) use split-K.  LLH_OPT_DECODE_KERNEL overrides the choice,
-// LLH_OPT_DECODE_STREAM_WGS the grid.
+// kStreamMinUnitsPerWave units (block x kv head) per wavefront (and fewer than
+// 2^31 units); smaller steps (C1, C4 decode) use split-K.
+// LLH_OPT_DECODE_KERNEL overrides the choice, LLH_OPT_DECODE_STREAM_WGS the grid.
 constexpr int kStreamWgsPerCu = 2;
 constexpr int kStreamMaxWgs = 1024;
 constexpr int kStreamMinUnitsPerWave = 8;
@@ -136,9 +135,8 @@ int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int 
   if (want_split) return 0;
   const int wgs = stream_grid(ctx);
   const long long waves = 4LL * wgs;
-  const long long max_units_seq = (long long)kv_heads * est_blocks;
-  const long long max_units = max_units_seq * num_seqs;
-  if (2LL * num_seqs >= waves || max_units_seq * waves >= (1LL << 31) || max_units >= (1LL << 31)) return 0;
+  const long long max_units = (long long)kv_heads * est_blocks * num_seqs;
+  if (max_units >= (1LL << 31)) return 0;
   if (want_stream) return wgs;
   const long long units = total_tokens_hint > 0
                               ? (long long)kv_heads * ((long long)total_tokens_hint / kFastBlockTokens + num_seqs)
@@ -361,7 +359,7 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
   if (scales_interleaved(format)) {
     if (e == hipSuccess) e = hipMalloc(&pool->ks, 2 * pool->s_bytes);
     if (e == hipSuccess) e = hipMemset(pool->ks, 0, 2 * pool->s_bytes);
-    if (e == hipSuccess) pool->vs = static_cast<char *>(pool->ks) + kInt8VScaleOffsetBytes;
+    if (e == hipSuccess) pool->vs = static_cast<char *>(pool->ks) + v_scale_offset_bytes(format);
   } else {
     if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->ks, pool->s_bytes);
     if (e == hipSuccess && pool->s_bytes) e = hipMalloc(&pool->vs, pool->s_bytes);
@@ -925,7 +923,7 @@ struct BlockStore {
       if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, kscale * capacity, hipMemcpyDeviceToDevice);
       if (e == hipSuccess && sblock && !il) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
     }
-    if (il && nks) nvs = static_cast<char *>(nks) + kInt8VScaleOffsetBytes;
+    if (il && nks) nvs = static_cast<char *>(nks) + v_scale_offset_bytes(format);
     // the memsets and device-to-device copies above run on the null stream,
     // asynchronously to the host: they must land before the caches' own
     // (non-blocking) streams touch the new buffers, and before the old ones go

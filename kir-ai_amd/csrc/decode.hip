@@ -220,8 +220,12 @@ __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kv
         r.sc = *reinterpret_cast<const uint4 *>(sp + int8_scale_index(bh, 4 * g, BT));
       }
     } else {
-      r.ksb = reinterpret_cast<const float *>(a.pool.k_scales)[bh];
-      r.vsb = reinterpret_cast<const float *>(a.pool.v_scales)[bh];
+      // the block-head's (K, V) scale pair: bh is wave-uniform, so a scalar load
+      // (constant address space: nothing writes the scales during the launch)
+      typedef const __attribute__((address_space(4))) float scale_elem_t;
+      const scale_elem_t *sp = (const scale_elem_t *)a.pool.k_scales + fp8_scale_index(bh);
+      r.ksb = sp[0];
+      r.vsb = sp[1];
     }
   }
 }
@@ -913,16 +917,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 // ---------------------------------------------------------------------------
 // Persistent stream decode.
 //
-// The attended blocks of one (sequence, kv head) are that segment's "units";
-// sequence b has Hkv * nblk(b) units, ordered (kv head, block).  Every
-// non-empty sequence gets one wavefront of the grid plus a share of the
-// remaining wavefronts proportional to its units (at most one per unit), and
-// each of its wavefronts streams an equal, contiguous range of its units,
-// loading one unit ahead of the math across kv-head boundaries.  Every
-// workgroup has the same amount of work however ragged the lengths are, and
-// there is no workgroup barrier and no wait on another workgroup, so results
-// do not depend on how many workgroups are resident at once (the default grid
-// is all resident).
+// The attended blocks of one (sequence, kv head) are that segment's "units".
+// All units of the step, U of them, are ordered (sequence, kv head, block) and
+// wavefront w < W' = min(W, U) of the W in the grid streams the contiguous
+// range [w * U / W', (w + 1) * U / W'), across kv-head and sequence
+// boundaries, loading one unit ahead of the math.  Every wavefront has the same number of units to
+// within one however ragged the lengths are, there is no workgroup barrier and
+// no wait on another workgroup, so results do not depend on how many
+// workgroups are resident at once (the default grid is all resident).
 //
 // A segment that lies wholly inside one wavefront's range is written out
 // directly.  A segment cut between wavefronts leaves one (max, sum, output)
@@ -950,77 +952,91 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
-struct SeqShare {
-  int b;   // sequence (-1: none)
-  int nb;  // its attended blocks
-  int wb;  // its wavefronts
-  int w0;  // its first wavefront
-};
-
-// Wavefronts of a sequence of ub units: one, plus its share of the spare
-// wavefronts, capped at one per unit so that every range is non-empty.  The
-// host keeps ub * W below 2^31, so 32-bit products are exact.
-__device__ __forceinline__ int seq_waves(int ub, int spare, int total) {
-  return ub > 0 ? min(ub, 1 + (int)(((unsigned)spare * (unsigned)ub) / (unsigned)total)) : 0;
+// floor(x / d) for x < 2^63, d > 0: 32-bit division when x fits (the usual
+// case; a 64-bit division is several times longer and sits on the path to the
+// first load)
+__device__ __forceinline__ int div_u64(unsigned long long x, unsigned d) {
+  return (int)((x >> 32) == 0 ? (unsigned)x / d : x / d);
 }
 
-// First unit of wavefront omega of a sequence: ranges are [omega*ub/wb, (omega+1)*ub/wb).
-__device__ __forceinline__ int range_begin(int omega, int ub, int wb) {
-  return (int)(((unsigned)omega * (unsigned)ub) / (unsigned)wb);
+// First global unit of wavefront omega's range [omega * U / W, (omega + 1) * U / W).
+__device__ __forceinline__ int range_begin(int omega, int U, int W) {
+  return div_u64((unsigned long long)omega * (unsigned)U, (unsigned)W);
 }
 
-// The wavefront of a sequence whose range holds unit r.
-__device__ __forceinline__ int wave_of_unit(int r, int ub, int wb) {
-  return (int)(((unsigned)(r + 1) * (unsigned)wb + (unsigned)ub - 1u) / (unsigned)ub) - 1;
+// The wavefront whose range holds global unit r.
+__device__ __forceinline__ int wave_of_unit(int r, int U, int W) {
+  return div_u64((unsigned long long)(r + 1) * (unsigned)W + (unsigned)U - 1u, (unsigned)U) - 1;
 }
 
-// The sequence whose wavefronts include wavefront w (W in the grid).  Lane l
-// of the first chunk reads sequence l, so batches up to 64 need one load.
 // Attended tokens of a sequence of length len.
 __device__ __forceinline__ int attended_tokens(const DecodeArgs &a, int len) {
   return a.window > 0 ? min(len, a.window) : len;
 }
 
-// Returns b = -1 when w is spare; sets *units = 0 when nothing is attended and
-// *bad_flags to kErrTooManySplits when a length exceeds the host's max_seq_len
-// bound, kErrSpan when a sequence attends more tokens than its table row holds.
-__device__ __forceinline__ SeqShare stream_share(const DecodeArgs &a, int W, int w, int lane, int *units,
-                                                 int *bad_flags) {
+// This wavefront's share of the step, a pure function of seq_lens that every
+// wavefront computes (lane l of a 64-sequence chunk reads sequence l; len0 is
+// chunk 0, already loaded).  The ranges are cut for Wu = min(W, U) wavefronts,
+// so that every range is non-empty and the pieces of a cut segment lie in
+// consecutive wavefronts (the merge reads them so); wavefronts w >= Wu idle.
+struct StreamRange {
+  int U;     // units of the step
+  int Wu;    // wavefronts that take units
+  int r0;    // first global unit of the range
+  int n;     // units in the range (0: none)
+  int b;     // sequence of unit r0
+  int base;  // global index of that sequence's first unit
+};
+
+// Sets *bad_flags to kErrTooManySplits when a length exceeds the host's
+// max_seq_len bound and to kErrSpan when a sequence attends more tokens than
+// its table row holds (then n = 0).
+__device__ __forceinline__ StreamRange stream_range(const DecodeArgs &a, int W, int w, int lane, int len0,
+                                                    int *bad_flags) {
   const int B = a.num_seqs;
+  const int Hkv = a.pool.kv_heads;
   const int row_tokens = a.max_blocks * BT;
-  int len0 = lane < B ? a.seq_lens[lane] : 0;
-  int nb0 = attended_blocks(a, len0);
-  int u = wave_sum(nb0), nz = __popcll(__ballot(nb0 > 0));
-  bool too_long = __ballot(len0 > a.max_seq_len) != 0;
-  bool span = __ballot(attended_tokens(a, len0) > row_tokens) != 0;
-  for (int cb = 64; cb < B; cb += 64) {
-    const int len = cb + lane < B ? a.seq_lens[cb + lane] : 0;
-    const int nb = attended_blocks(a, len);
-    u += wave_sum(nb);
-    nz += __popcll(__ballot(nb > 0));
+  int blocks = 0;
+  bool too_long = false, span = false;
+  for (int cb = 0; cb < B; cb += 64) {
+    const int len = cb == 0 ? len0 : (cb + lane < B ? a.seq_lens[cb + lane] : 0);
+    blocks += wave_sum(attended_blocks(a, len));
     too_long |= __ballot(len > a.max_seq_len) != 0;
     span |= __ballot(attended_tokens(a, len) > row_tokens) != 0;
   }
   *bad_flags = (too_long ? kErrTooManySplits : 0) | (span ? kErrSpan : 0);
-  *units = u * a.pool.kv_heads;
-  if (*bad_flags || u == 0) return {-1, 0, 0, 0};
-  const int spare = W - 2 * nz;  // the host sizes W above 2B, so spare > 0
-  int cw = 0;
+  StreamRange r = {blocks * Hkv, min(W, blocks * Hkv), 0, 0, -1, 0};
+  if (*bad_flags || r.U == 0 || w >= r.Wu) return r;
+  r.r0 = range_begin(w, r.U, r.Wu);
+  r.n = range_begin(w + 1, r.U, r.Wu) - r.r0;
+  // the sequence whose units hold r0: inclusive scan of units per sequence
+  int before = 0;  // units of the chunks already scanned
   for (int cb = 0; cb < B; cb += 64) {
-    const int nb = cb == 0 ? nb0 : (cb + lane < B ? attended_blocks(a, a.seq_lens[cb + lane]) : 0);
-    const int wb = seq_waves(a.pool.kv_heads * nb, spare, *units);
-    const int incl = wave_incl_scan(wb, lane);
-    const int lo = cw + incl - wb;
-    const unsigned long long hit = __ballot(w >= lo && w < cw + incl);
+    const int len = cb == 0 ? len0 : (cb + lane < B ? a.seq_lens[cb + lane] : 0);
+    const int ub = Hkv * attended_blocks(a, len);
+    const int incl = before + wave_incl_scan(ub, lane);
+    const unsigned long long hit = __ballot(r.r0 >= incl - ub && r.r0 < incl);
     if (hit) {
       const int src = __ffsll((long long)hit) - 1;
-      return {cb + src, __builtin_amdgcn_readlane(nb, src), __builtin_amdgcn_readlane(wb, src),
-              __builtin_amdgcn_readlane(lo, src)};
+      r.b = cb + src;
+      r.base = __builtin_amdgcn_readlane(incl - ub, src);
+      return r;
     }
-    cw += __builtin_amdgcn_readlane(incl, 63);
+    before = __builtin_amdgcn_readlane(incl, 63);
   }
-  return {-1, 0, 0, 0};
+  r.n = 0;  // not reached: r0 < U lies in some sequence
+  return r;
 }
+
+// A position in the stream order (all fields wave-uniform): sequence b, kv
+// head kvh, attended block j of the sequence's nb; base is the global index of
+// (b, 0, 0) and tab the block-table index of block j.
+struct UnitCursor {
+  int b, kvh, j, nb;
+  int len, lo;     // the sequence's length and first attended position
+  int tab, tab0;   // table index of block j and of block 0: (lo / BT + j) % max_blocks
+  int base;
+};
 
 // Ends a segment: merges the wavefront's four token groups, then writes the
 // bf16 output (complete segment) or the partial in `slot`; resets the state.
@@ -1071,97 +1087,112 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int W = gridDim.x * 4;
   const int Hkv = a.pool.kv_heads;
-  int units;
+  const int B = a.num_seqs;
+  const int len0 = lane < B ? a.seq_lens[lane] : 0;  // sequences 0..63, one per lane
   int bad_flags;
-  const SeqShare sh = stream_share(a, W, w, lane, &units, &bad_flags);
+  const StreamRange sr = stream_range(a, W, w, lane, len0, &bad_flags);
   if (bad_flags) {
     if (w == 0 && lane == 0) atomicOr(a.err, bad_flags);
     return;
   }
   // empty sequences: zero output (weighted sum of nothing), nothing to merge
-  for (int b = w; b < a.num_seqs; b += W) {
+  for (int b = w; b < B; b += W) {
     if (attended_blocks(a, a.seq_lens[b]) == 0) {
       for (int idx = lane; idx < a.q_heads * D; idx += 64) a.out[(size_t)b * a.q_heads * D + idx] = 0;
       for (int idx = lane; idx < 2 * Hkv; idx += 64) a.seg_desc[(size_t)b * Hkv * 2 + idx] = 0;
     }
   }
-  if (sh.b < 0) return;
-  // readfirstlane: these are wave-uniform, so the loop's cursors, branches and
-  // load addresses stay in scalar registers
-  const int b = __builtin_amdgcn_readfirstlane(sh.b);
-  const int nb = __builtin_amdgcn_readfirstlane(sh.nb);
-  const int wb = __builtin_amdgcn_readfirstlane(sh.wb);
-  const int w0 = __builtin_amdgcn_readfirstlane(sh.w0);
-  const int ub = Hkv * nb;
-  const int r0 = __builtin_amdgcn_readfirstlane(range_begin(w - w0, ub, wb));
-  const int n = __builtin_amdgcn_readfirstlane(range_begin(w - w0 + 1, ub, wb)) - r0;  // >= 1
-  const int len = __builtin_amdgcn_readfirstlane(a.seq_lens[b]);
+  const int n = __builtin_amdgcn_readfirstlane(sr.n);
+  if (n == 0) return;
+  const int U = __builtin_amdgcn_readfirstlane(sr.U);
+  const int Wu = __builtin_amdgcn_readfirstlane(sr.Wu);
   // fused append: the pool part attends [lo, len - 1); the new token comes from a.k_new
   constexpr bool fused = FUSED;
-  const int len_kv = fused ? len - 1 : len;
-  const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-  const int first_blk = lo / BT;
-  const int32_t *table = a.tables + (size_t)b * a.max_blocks;
 
-  // Pool index of a unit's block (it depends on the block only): a scalar load
-  // from the block-table row, which no one writes during the launch, fetched one
-  // unit ahead.  Scalar loads keep the table out of the vector-memory counter,
-  // so the waits before the math cover K/V loads only.
-  typedef const __attribute__((address_space(4))) int32_t table_elem_t;
-  const table_elem_t *stable = (const table_elem_t *)table;
-  const int tab_first = first_blk % a.max_blocks;
-  int e_j = r0 % nb;                               // entry cursor: block (in segment) of the next entry
-  int e_tab = (first_blk + e_j) % a.max_blocks;    // and its table index
-  auto next_entry = [&]() __attribute__((always_inline)) -> int {
-    const int e = stable[e_tab];
-    if (++e_j == nb) {
-      e_j = 0;
-      e_tab = tab_first;
-    } else if (++e_tab == a.max_blocks) {
-      e_tab = 0;
+  // Lengths, block-table entries: scalar loads (constant address space: no
+  // one writes them during the launch), so the waits before the math cover
+  // K/V loads only.  Sequences 0..63 take their length from len0's lanes.
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const const_i32 *slens = (const const_i32 *)a.seq_lens;
+  const const_i32 *stable = (const const_i32 *)a.tables;
+  auto set_seq = [&](UnitCursor &c, int b) __attribute__((always_inline)) {
+    c.b = b;
+    c.len = b < 64 ? __builtin_amdgcn_readlane(len0, b) : slens[b];
+    c.nb = attended_blocks(a, c.len);
+    c.lo = a.window > 0 ? max(0, c.len - a.window) : 0;
+    c.tab0 = (c.lo / BT) % a.max_blocks;
+  };
+  // the next unit in stream order; past the last sequence nb stays 0 and nothing is read
+  auto advance = [&](UnitCursor &c) __attribute__((always_inline)) {
+    if (++c.j < c.nb) {
+      if (++c.tab == a.max_blocks) c.tab = 0;
+      return;
     }
+    c.j = 0;
+    c.tab = c.tab0;
+    if (++c.kvh < Hkv) return;
+    c.kvh = 0;
+    c.base += Hkv * c.nb;
+    for (;;) {
+      if (++c.b >= B) {
+        c.nb = 0;
+        return;
+      }
+      set_seq(c, c.b);
+      if (c.nb > 0) {
+        c.tab = c.tab0;
+        return;
+      }
+    }
+  };
+  UnitCursor c0;
+  set_seq(c0, __builtin_amdgcn_readfirstlane(sr.b));
+  c0.base = __builtin_amdgcn_readfirstlane(sr.base);
+  {
+    const int u = __builtin_amdgcn_readfirstlane(sr.r0) - c0.base;
+    c0.kvh = u / c0.nb;
+    c0.j = u - c0.kvh * c0.nb;
+    c0.tab = c0.tab0 + c0.j;
+    if (c0.tab >= a.max_blocks) c0.tab -= a.max_blocks;
+  }
+  // three cursors: the next block-table entry to fetch (one unit ahead of the
+  // loads), the next unit to load, the next unit to compute
+  UnitCursor E = c0, L = c0, C = c0;
+  auto next_entry = [&]() __attribute__((always_inline)) -> int {
+    const int e = stable[(size_t)E.b * a.max_blocks + E.tab];
+    advance(E);
     return e;
   };
 
-  int l_j = r0 % nb, l_kvh = r0 / nb;  // load cursor: block and kv head of the next unit to load
-  int c_j = l_j;                      // compute cursor: block (within its segment) of the next unit
-  int seg_kvh = l_kvh;
-  bool seg_from_start = c_j == 0;
+  bool seg_from_start = C.j == 0;
   bool first_seg = true;
   bool need_q = false;
   constexpr bool TL = kTokenLanes<G, FMT>;
   uint32_t qw[G][kQWords<G, FMT>];
-  load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
+  load_q<G, FMT>(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G, lane, qw);
 
   BlockRegs<FMT> r[2];
-  load_block<FMT, TL>(a, next_entry(), l_kvh, lane, r[0]);
-  float qstep = prep_q<G, FMT>(lane, qw);
+  load_block<FMT, TL>(a, next_entry(), L.kvh, lane, r[0]);
   // fused append: a segment's new-token rows are loaded with its last unit, into
   // the buffer that travels with that unit's registers (r[0] / r[1])
   NewToken nt[2];
   if constexpr (FMT == kBf16)
-    if (fused && l_j == nb - 1) load_new_token(a, b, l_kvh, lane, nt[0]);
+    if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nt[0]);
+  float qstep = prep_q<G, FMT>(lane, qw);
   int e_next = n > 1 ? next_entry() : -1;
-  if (++l_j == nb) {
-    l_j = 0;
-    l_kvh++;
-  }
+  advance(L);
   SoftmaxState<G> st;
   reset_state(st);
 
   auto end_segment = [&](bool complete) __attribute__((always_inline)) {
     const int slot = w * 2 + (first_seg ? 0 : 1);
     finalize_state<G, FMT>(st);
-    stream_flush<G>(a, st, b, seg_kvh, complete, slot, lane);
+    stream_flush<G>(a, st, C.b, C.kvh, complete, slot, lane);
     if (lane == 0 && (complete || seg_from_start)) {
       // this wavefront holds the segment's first unit: record how to merge it
       int2 d = make_int2(0, 0);
-      if (!complete) {
-        const int wf = w - w0;
-        const int wl = wave_of_unit((seg_kvh + 1) * nb - 1, ub, wb);
-        d = make_int2(slot, wl - wf + 1);
-      }
-      reinterpret_cast<int2 *>(a.seg_desc)[(size_t)b * Hkv + seg_kvh] = d;
+      if (!complete) d = make_int2(slot, wave_of_unit(C.base + (C.kvh + 1) * C.nb - 1, U, Wu) - w + 1);
+      reinterpret_cast<int2 *>(a.seg_desc)[(size_t)C.b * Hkv + C.kvh] = d;
     }
     first_seg = false;
   };
@@ -1173,31 +1204,27 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, NewToken &cur_nt, NewToken &nxt_nt, bool issue)
                   __attribute__((always_inline)) {
     const bool new_q = need_q;
-    if (new_q) load_q<G, FMT>(a, (size_t)b * a.q_heads + (size_t)seg_kvh * G, lane, qw);
+    if (new_q) load_q<G, FMT>(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G, lane, qw);
     if (issue) {
-      load_block<FMT, TL>(a, e_next, l_kvh, lane, nxt);
+      load_block<FMT, TL>(a, e_next, L.kvh, lane, nxt);
       if constexpr (FMT == kBf16)
-        if (fused && l_j == nb - 1) load_new_token(a, b, l_kvh, lane, nxt_nt);
+        if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nxt_nt);
       e_next = k + 2 < n ? next_entry() : -1;
-      if (++l_j == nb) {
-        l_j = 0;
-        l_kvh++;
-      }
+      advance(L);
     }
     if (new_q) {
       qstep = prep_q<G, FMT>(lane, qw);
       need_q = false;
     }
-    compute_block<G, FMT>(a, cur, first_blk + c_j, lo, len_kv, lane, qw, qstep, st);
-    if (++c_j == nb) {  // the segment ends with this unit
+    compute_block<G, FMT>(a, cur, C.lo / BT + C.j, C.lo, fused ? C.len - 1 : C.len, lane, qw, qstep, st);
+    if (C.j == C.nb - 1) {  // the segment ends with this unit
       if constexpr (FMT == kBf16)
-        if (fused) add_new_token<G>(a, st, b, seg_kvh, len, lane, qw, cur_nt);
+        if (fused) add_new_token<G>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);
       end_segment(seg_from_start);
-      c_j = 0;
-      seg_kvh++;
       seg_from_start = true;
       need_q = true;
     }
+    advance(C);
   };
   int k = 0;
   for (; k + 2 < n; k += 2) {
@@ -1210,7 +1237,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   } else {
     step(k, r[0], r[1], nt[0], nt[1], false);
   }
-  if (c_j != 0) end_segment(false);  // the range ends inside a segment
+  if (C.j != 0) end_segment(false);  // the range ends inside a segment
 }
 
 // One round of the stream merge over partials i0 .. i0+cnt-1 (1 <= cnt <= N <=

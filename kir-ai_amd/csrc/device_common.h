@@ -30,7 +30,7 @@ __device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_
   if (p.format == kInt8Row)  // one f32 scale per token row of the block (all heads)
     return (float)reinterpret_cast<const int8_t *>(base)[idx] * reinterpret_cast<const float *>(sc)[blk * p.block_tokens + t];
   const uint32_t code = reinterpret_cast<const uint8_t *>(base)[idx];
-  return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * reinterpret_cast<const float *>(sc)[bh];
+  return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * reinterpret_cast<const float *>(sc)[fp8_scale_index(bh)];
 }
 
 }  // namespace llh

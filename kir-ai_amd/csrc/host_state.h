@@ -199,9 +199,13 @@ struct llh_kv_pool {
 
 inline size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 ? 2 : 1; }
 
-// int8 pools keep the K and V scales in one allocation (int8_scale_index): the V
-// scale pointer is inside the K scales' allocation, one fp16 further.
-inline bool scales_interleaved(int32_t format) { return format == LLH_KV_INT8; }
+// int8 and fp8 pools keep the K and V scales in one allocation as (K, V) pairs
+// (int8_scale_index, fp8_scale_index): the V scale pointer is inside the K
+// scales' allocation, one element further.
+inline bool scales_interleaved(int32_t format) { return format == LLH_KV_INT8 || format == LLH_KV_FP8_E4M3; }
+inline size_t v_scale_offset_bytes(int32_t format) {
+  return format == LLH_KV_INT8 ? llh::kInt8VScaleOffsetBytes : llh::kFp8VScaleOffsetBytes;
+}
 
 inline size_t scale_bytes_per_block(int32_t format, int32_t kv_heads, int32_t block_tokens) {
   if (format == LLH_KV_INT8) return (size_t)kv_heads * block_tokens * 2;

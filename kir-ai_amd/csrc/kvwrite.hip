@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
       }
       codes[tensor][0] = q[0];
       codes[tensor][1] = q[1];
-      if (tid == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[bh] = sc;
+      if (tid == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[fp8_scale_index(bh)] = sc;
     }
   } else {
   // int8 with per (token, head) fp16 scales
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
       else
         kd[(bh * BT + t) * Dh + d] = code;
     }
-    if (threadIdx.x == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[bh] = s;
+    if (threadIdx.x == 0) reinterpret_cast<float *>(tensor ? a.vs_dst : a.ks_dst)[fp8_scale_index(bh)] = s;
   }
 }
 
@@ -433,7 +433,8 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
       const bool same = j < i && a.slots[j] >= 0 && a.slots[j] / BT == blk;
       if (__any(same)) return;
     }
-    float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[bh], reinterpret_cast<const float *>(a.vs_dst)[bh]};
+    float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[fp8_scale_index(bh)],
+                      reinterpret_cast<const float *>(a.vs_dst)[fp8_scale_index(bh)]};
     for (int j = i; j < a.n; j++) {
       const int64_t sj = a.slots[j];
       if (sj < 0 || sj / BT != blk) continue;
@@ -452,8 +453,8 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
       scale[1] = append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
     }
     if (lane == 0) {
-      reinterpret_cast<float *>(a.ks_dst)[bh] = scale[0];
-      reinterpret_cast<float *>(a.vs_dst)[bh] = scale[1];
+      reinterpret_cast<float *>(a.ks_dst)[fp8_scale_index(bh)] = scale[0];
+      reinterpret_cast<float *>(a.vs_dst)[fp8_scale_index(bh)] = scale[1];
     }
     return;
   }
@@ -501,7 +502,7 @@ __device__ __forceinline__ float load_f32(const PoolView &p, const void *base, c
     return (float)reinterpret_cast<const int8_t *>(base)[idx] *
            reinterpret_cast<const float *>(sc)[(bh / p.kv_heads) * p.block_tokens + off];
   return __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)reinterpret_cast<const uint8_t *>(base)[idx], false)[0] *
-         reinterpret_cast<const float *>(sc)[bh];
+         reinterpret_cast<const float *>(sc)[fp8_scale_index(bh)];
 }
 
 // One wavefront per (slot, kv head): K and V of that token as f32 rows

@@ -26,6 +26,13 @@ __host__ __device__ constexpr size_t int8_scale_index(size_t bh, int t, int bloc
   return (bh * (size_t)block_tokens + (size_t)t) * 2;
 }
 
+// fp8 (per (block, head)) scales: one allocation holding, for each (block,
+// head) bh, the f32 pair (K scale, V scale), read with one 8-byte load per
+// decode unit.  The V scale pointer is the K scale pointer + one f32; index of
+// bh's scale in either.
+constexpr size_t kFp8VScaleOffsetBytes = 4;
+__host__ __device__ constexpr size_t fp8_scale_index(size_t bh) { return bh * 2; }
+
 // Device error flags (bit set by kernels, read back by the host).
 enum ErrFlag : int32_t {
   kErrBadBlock = 1,      // block table entry outside the pool

@@ -154,8 +154,10 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
         r.vs[i][0] = sp[0];
         r.vs[i][1] = sp[1];
       } else {
-        r.ks[i] = reinterpret_cast<const uint32_t *>(a.pool.k_scales)[bh];
-        r.vs[i][0].x = reinterpret_cast<const uint32_t *>(a.pool.v_scales)[bh];
+        const uint2 s2 = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint32_t *>(a.pool.k_scales) +
+                                                          fp8_scale_index(bh));
+        r.ks[i] = s2.x;
+        r.vs[i][0].x = s2.y;
       }
     }
   }

@@ -648,9 +648,11 @@ class KvPool:
             return buf.cpu().numpy()
 
         out = {"k": dl(i.d_k, i.k_bytes), "v": dl(i.d_v, i.k_bytes)}
-        if i.scale_bytes and i.format == KV_INT8:
-            # one allocation, per (block, head, token) the pair (K scale, V scale)
-            both = dl(i.d_k_scales, 2 * i.scale_bytes).reshape(-1, 2, 2)
+        if i.scale_bytes and i.format in (KV_INT8, KV_FP8_E4M3):
+            # one allocation of (K scale, V scale) pairs: fp16 per (block, head, token)
+            # for int8, f32 per (block, head) for fp8
+            esz = 2 if i.format == KV_INT8 else 4
+            both = dl(i.d_k_scales, 2 * i.scale_bytes).reshape(-1, 2, esz)
             out["k_scales"] = np.ascontiguousarray(both[:, 0]).ravel()
             out["v_scales"] = np.ascontiguousarray(both[:, 1]).ravel()
         elif i.scale_bytes:
