@@ -87,6 +87,19 @@ __device__ __forceinline__ float row_mirror(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
 }
 
+// Value of lane l ^ 16 / l ^ 32 without an LDS round trip: v_permlane16_swap
+// (v_permlane32_swap) of a register with itself leaves the even rows' (low
+// half's) values in both rows of each pair in r[0] and the odd rows' (high
+// half's) in r[1].
+__device__ __forceinline__ float xor16_other(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_other(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 32) ? r[0] : r[1]);
+}
+
 // Sum over the 16 lanes of a DPP row; every lane receives the total.
 __device__ __forceinline__ float row_sum16(float v) {
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -866,18 +879,18 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   __shared__ float s_l[4][G];
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
-    mm = fmaxf(mm, __shfl_xor(mm, 32));
+    float mm = fmaxf(st.m[gi], xor16_other(st.m[gi], lane));
+    mm = fmaxf(mm, xor32_other(mm, lane));
     const float mref = (mm == -INFINITY) ? 0.0f : mm;
     const float f = fast_exp2(st.m[gi] - mref);
     float ll = st.l[gi] * f;
-    ll += __shfl_xor(ll, 16);
-    ll += __shfl_xor(ll, 32);
+    ll += xor16_other(ll, lane);
+    ll += xor32_other(ll, lane);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       float v = st.o[gi][j] * f;
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v += xor16_other(v, lane);
+      v += xor32_other(v, lane);
       st.o[gi][j] = v;
     }
     if (g == 0) {
@@ -937,20 +950,21 @@ __device__ __forceinline__ int attended_blocks(const DecodeArgs &a, int len) {
   return len > lo ? (len - 1) / BT - lo / BT + 1 : 0;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Inclusive prefix sum over the wavefront in the VALU (DPP, no LDS round trip):
+// a Hillis-Steele scan inside each 16-lane row (row_shr 1, 2, 4, 8), then row
+// 15's last lane added to rows 1 and 3 and lane 31 to rows 2 and 3 (row_bcast).
+// Lanes whose source is outside the row, and rows outside the row mask, add 0.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
+__device__ __forceinline__ int wave_sum(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 
 // floor(x / d) for x < 2^63, d > 0: 32-bit division when x fits (the usual
 // case; a 64-bit division is several times longer and sits on the path to the
@@ -1014,7 +1028,7 @@ __device__ __forceinline__ StreamRange stream_range(const DecodeArgs &a, int W, 
   for (int cb = 0; cb < B; cb += 64) {
     const int len = cb == 0 ? len0 : (cb + lane < B ? a.seq_lens[cb + lane] : 0);
     const int ub = Hkv * attended_blocks(a, len);
-    const int incl = before + wave_incl_scan(ub, lane);
+    const int incl = before + wave_incl_scan(ub);
     const unsigned long long hit = __ballot(r.r0 >= incl - ub && r.r0 < incl);
     if (hit) {
       const int src = __ffsll((long long)hit) - 1;
@@ -1048,19 +1062,19 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
   const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G;
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    float mm = fmaxf(st.m[gi], __shfl_xor(st.m[gi], 16));
-    mm = fmaxf(mm, __shfl_xor(mm, 32));
+    float mm = fmaxf(st.m[gi], xor16_other(st.m[gi], lane));
+    mm = fmaxf(mm, xor32_other(mm, lane));
     const float mref = (mm == -INFINITY) ? 0.0f : mm;
     const float f = fast_exp2(st.m[gi] - mref);
     float ll = st.l[gi] * f;
-    ll += __shfl_xor(ll, 16);
-    ll += __shfl_xor(ll, 32);
+    ll += xor16_other(ll, lane);
+    ll += xor32_other(ll, lane);
     float o2[2];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       float v = st.o[gi][j] * f;
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v += xor16_other(v, lane);
+      v += xor32_other(v, lane);
       if (j == 2 * g) o2[0] = v;
       if (j == 2 * g + 1) o2[1] = v;
     }
@@ -1096,8 +1110,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     return;
   }
   // empty sequences: zero output (weighted sum of nothing), nothing to merge
+  // (lengths of sequences 0..63 come from len0's lanes: no load on the way to
+  // the first unit)
   for (int b = w; b < B; b += W) {
-    if (attended_blocks(a, a.seq_lens[b]) == 0) {
+    if (attended_blocks(a, b < 64 ? __builtin_amdgcn_readlane(len0, b) : a.seq_lens[b]) == 0) {
       for (int idx = lane; idx < a.q_heads * D; idx += 64) a.out[(size_t)b * a.q_heads * D + idx] = 0;
       for (int idx = lane; idx < 2 * Hkv; idx += 64) a.seg_desc[(size_t)b * Hkv * 2 + idx] = 0;
     }
