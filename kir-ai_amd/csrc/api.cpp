@@ -905,7 +905,7 @@ struct BlockStore {
   hipError_t allocate(int64_t cap) {
     kblock = (size_t)kv_heads * kRingBlockTokens * head_dim * elem_bytes(format);
     sblock = scale_bytes_per_block(format, kv_heads, kRingBlockTokens);
-    // scale bytes per block in the K scales' allocation (int8: K and V interleaved)
+    // scale bytes per block in the K scales' allocation (int8, fp8: K and V scale pairs)
     const bool il = scales_interleaved(format);
     const size_t kscale = il ? 2 * sblock : sblock;
     void *nk = nullptr, *nv = nullptr, *nks = nullptr, *nvs = nullptr;

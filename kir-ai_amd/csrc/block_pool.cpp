@@ -279,7 +279,7 @@ struct llh_block_pool {
       e = hipMemcpy((char *)pool->k + kb * dst, (char *)pool->k + kb * src, kb, hipMemcpyDeviceToDevice);
     if (e == hipSuccess)
       e = hipMemcpy((char *)pool->v + kb * dst, (char *)pool->v + kb * src, kb, hipMemcpyDeviceToDevice);
-    const size_t ksb = scales_interleaved(v.format) ? 2 * sb : sb;  // int8: K and V scales in one run
+    const size_t ksb = scales_interleaved(v.format) ? 2 * sb : sb;  // int8, fp8: K and V scale pairs in one run
     if (e == hipSuccess && sb)
       e = hipMemcpy((char *)pool->ks + ksb * dst, (char *)pool->ks + ksb * src, ksb, hipMemcpyDeviceToDevice);
     if (e == hipSuccess && sb && !scales_interleaved(v.format))
