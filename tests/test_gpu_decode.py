@@ -396,6 +396,22 @@ def test_stream_small_grids_cut_segments_everywhere(ctx, wgs, opts):
     check(ctx, batch, 16, 8, seed=41 + wgs, what=f"stream wgs={wgs}")
 
 
+@pytest.mark.parametrize("wgs", [1, 3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+def test_stream_ranges_span_many_sequences(ctx, wgs, fmt, opts):
+    """The partition runs over all units of the step, so one wavefront's range crosses
+    sequence boundaries: on 4 or 12 wavefronts, 100 short sequences (empty ones among
+    them, lengths taken from beyond the first 64 lanes too) give ranges holding dozens of
+    sequences, some starting or ending inside one; with and without a window."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
+    opts(llm_hip.OPT_DECODE_STREAM_WGS, wgs)
+    lens = workloads.uniform_lengths(100, 0, 40, 48 + wgs)
+    lens[::17] = 0
+    batch = workloads.paged_batch(lens, BT, 0.10, seed=49 + wgs)
+    check(ctx, batch, 16, 8, fmt, seed=50 + wgs, what=f"stream wgs={wgs} fmt={fmt}")
+    check(ctx, batch, 16, 8, fmt, window=20, seed=51 + wgs, what=f"stream wgs={wgs} fmt={fmt} W=20")
+
+
 def test_stream_many_partials_per_segment(ctx, opts):
     """Few long sequences on a large grid: ~64 partials per segment, merged in rounds of 16."""
     opts(llm_hip.OPT_DECODE_KERNEL, "stream")
