@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 3
+#define LLH_ABI_VERSION 4  /* 4: int8 and fp8 pools store their scales as (K, V) pairs */
 
 /* Status codes.  Mirrors MathError / KvCacheError
  * (crates/llm-backend/src/core/math.rs:10-15, crates/llm-kv-cache/src/lib.rs). */
