@@ -9,6 +9,10 @@ K/V/Q are synthetic N(0,1) bf16 already resident in HBM when timing starts.
 `value` is the decode kernel's achieved HBM bandwidth in GB/s: the algorithmic
 bytes of one step (K+V rows attended, q, out, block tables, lengths) divided by
 the mean step time from HIP events on the launch stream over --steps steps.
+Every timed run starts from the GPU's steady state under load: before its
+--warmup steps the step is repeated, untimed, for --settle-ms of wall time
+(the clocks ramp up over the first 15-40 ms of sustained work after the GPU
+has idled, e.g. while the host builds a workload).
 `secondary` adds the other BASELINE configs (C1, C3 prefill MFMA utilisation,
 C4 window decode/prefill, C5 int8/fp8 decode) measured the same way.
 `cpu_baseline` times the CPU oracle (a C restatement of the reference's
@@ -17,7 +21,7 @@ single-threaded per-head loop) on the same pool, on this host, on one thread
 process's host threads (at most 16); each secondary config carries the same
 two timings under `cpu` (C5 and the prefills on a stated, scaled sample).
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--settle-ms 150] [--no-secondary] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -36,6 +40,7 @@ BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode attn: HBM GB/s (% of peak) + µs/step at B=32; prefill MFMA util"
 D = 128
 BT = 16
+SETTLE = {"s": 0.15}  # untimed settle before each timed run (--settle-ms)
 
 
 def log(msg: str) -> None:
@@ -127,14 +132,36 @@ class DecodeWorkload:
         return B * self.Hkv * D * 2 * 2 + B * self.Hkv * D * elem * 2 + scales + B * 8
 
 
+def settle(fn, stream, seconds: float) -> None:
+    """Repeats the step, untimed, for `seconds` of wall time with the GPU kept
+    busy (at most three batches of 8 steps queued ahead): after an idle spell
+    the GPU's clocks ramp up over the first 15-40 ms of sustained load (C2 step
+    48.8 -> 47.3 us, C5 fp8 240 -> 187 us), so a run timed from a cold start
+    measures the ramp, not the kernels."""
+    import torch
+
+    t0 = time.perf_counter()
+    pending = []
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn(stream)
+        e = torch.cuda.Event()
+        e.record(stream)
+        pending.append(e)
+        if len(pending) > 3:
+            pending.pop(0).synchronize()
+
+
 def time_steps(fn, steps: int, warmup: int, kernel_timing=None):
     """Mean ms per step from HIP events recorded on the launch stream.
 
+    The timed steps follow a settle phase (`settle`) and `warmup` untimed steps.
     With kernel_timing = (ctx, kind), the library also records HIP events around
     its main kernel in every timed step (same stream); returns (step ms, kernel ms)."""
     import torch
 
     stream = torch.cuda.Stream()  # default priority
+    settle(fn, stream, SETTLE["s"])
     for _ in range(warmup):
         fn(stream)
     torch.cuda.synchronize()
@@ -793,6 +820,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=150.0,
+                    help="untimed wall time of repeated steps before each timed run (GPU clock ramp)")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -806,6 +835,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.summarize:
         return summarize(args.summarize)
+    SETTLE["s"] = max(0.0, args.settle_ms / 1e3)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (the batch shards by sequence with "
               "no communication). Run with --gpus 1.", file=sys.stderr)
@@ -868,6 +898,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
