@@ -530,9 +530,9 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         state["i"] += 1
 
     # step time over all timed steps, then the decode kernel alone (library-recorded events)
-    streamed0 = ctx.metrics()["stream_decode_calls"]
+    streamed0, calls0 = ctx.metrics()["stream_decode_calls"], state["i"]
     ms = time_steps(step, steps, warmup)
-    streamed = ctx.metrics()["stream_decode_calls"] - streamed0
+    streamed, calls = ctx.metrics()["stream_decode_calls"] - streamed0, state["i"] - calls0
     _, kms = time_steps(step, steps, 0, kernel_timing=(ctx, "decode"))
     if ctx.device_errors() != 0:
         raise RuntimeError(f"{name}: device error flags set during timing")
@@ -550,7 +550,7 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
         "bytes_per_step": nbytes,
         "rotating_copies": len(copies),
-        "kernel": "paged_decode_stream_kernel" if streamed == steps + warmup else "paged_decode_kernel (split-K)",
+        "kernel": "paged_decode_stream_kernel" if streamed == calls else "paged_decode_kernel (split-K)",
     }
 
 
@@ -649,11 +649,11 @@ def summarize(root: str) -> int:
                 got = rows_of(sec, sub, "counter_collection.csv")
                 if got and sub != "ctr":
                     cmds.append(f"    cd /tmp && rocprofv3 --pmc {sub.upper()}_SIZE --output-format csv "
-                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2")
+                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2 --settle-ms 20")
                 elif got:
                     names = sorted({r["Counter_Name"] for r in got})
                     cmds.append(f"    cd /tmp && rocprofv3 --pmc {' '.join(names)} --output-format csv "
-                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2")
+                                f"-d <dir>/{sec}/{sub} -o run -- {run} --steps 10 --warmup 2 --settle-ms 20")
                 for r in got:
                     k = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
                     ctr.setdefault((k, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
