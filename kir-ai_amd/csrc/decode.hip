@@ -1336,34 +1336,65 @@ __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArg
 // the (max, sum) pairs, the pairs are reduced through LDS, and any remaining
 // partials follow 32 at a time.
 constexpr int kMergeMaxSplits = 1024;
-constexpr int kMergeOneRound = 64;  // splits merged from one round of loads, all in registers
-constexpr int kMergePrefetch = 96;  // partials loaded up front on the LDS path
+constexpr int kMergeOneRound = 128;  // splits merged from one round of loads, all in registers
+constexpr int kMergePrefetch = 96;   // partials loaded up front on the LDS path
 
-// Merge of n <= N splits from one round of loads, all in registers.  Loads
-// past the last split re-read the last split (no branch between the loads and
-// their use, so they are all in flight at once) and are weighted 0.
+// Merge of n <= N <= 128 splits from one round of loads, all in registers.
+// Partial rows past the last split re-read the last split (no branch between
+// the loads and their use, so they are all in flight at once) and are weighted
+// 0.  The (max, sum) pairs are spread over the lanes: lane i of each wavefront
+// loads those of splits i and 64 + i with vector loads, the wavefront reduces
+// them with DPP and row exchanges, and the split weights reach every lane
+// through LDS.  (Loaded as uniform values they became scalar loads, and
+// the scalar queue's depth split them into several dependent rounds: a merge
+// of 64 splits took ~7 us.)
 template <int N>
 __device__ __forceinline__ void merge_in_registers(const DecodeArgs &a, size_t row0, int last, int d, size_t orow) {
+  static_assert(N <= 128, "at most two (max, sum) pairs per lane");
+  constexpr int P = (N + 63) / 64;  // pairs per lane
   float o_sp[N];
-  float2 ml[N];
 #pragma unroll
   for (int i = 0; i < N; i++) o_sp[i] = a.ws_o[(row0 + min(i, last)) * D + d];
+  const int li = d & 63;
+  float mx[P], ly[P];
 #pragma unroll
-  for (int i = 0; i < N; i++) ml[i] = a.ws_ml[row0 + min(i, last)];
-#pragma unroll
-  for (int i = 0; i < N; i++)
-    if (i > last) ml[i] = make_float2(-INFINITY, 0.0f);
-  float mm = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < N; i++) mm = fmaxf(mm, ml[i].x);
-  const float mref = (mm == -INFINITY) ? 0.0f : mm;
-  float ll = 0.0f, oo = 0.0f;
-#pragma unroll
-  for (int i = 0; i < N; i++) {
-    const float f = fast_exp2(ml[i].x - mref);
-    ll += ml[i].y * f;
-    oo += o_sp[i] * f;
+  for (int p = 0; p < P; p++) {
+    const float2 ml = a.ws_ml[row0 + min(64 * p + li, last)];
+    mx[p] = 64 * p + li <= last ? ml.x : -INFINITY;
+    ly[p] = ml.y;
   }
+  // wavefront max and sum: DPP within rows of 16, then row exchanges (no LDS)
+  float mm = mx[0];
+#pragma unroll
+  for (int p = 1; p < P; p++) mm = fmaxf(mm, mx[p]);
+  mm = fmaxf(mm, dpp<0xB1>(mm));   // quad_perm [1,0,3,2]
+  mm = fmaxf(mm, dpp<0x4E>(mm));   // quad_perm [2,3,0,1]
+  mm = fmaxf(mm, dpp<0x141>(mm));  // row_half_mirror
+  mm = fmaxf(mm, dpp<0x140>(mm));  // row_mirror
+  mm = fmaxf(mm, xor16_other(mm, li));
+  mm = fmaxf(mm, xor32_other(mm, li));
+  const float mref = (mm == -INFINITY) ? 0.0f : mm;
+  float f[P];
+  float lsum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < P; p++) {
+    f[p] = 64 * p + li <= last ? fast_exp2(mx[p] - mref) : 0.0f;
+    lsum += ly[p] * f[p];
+  }
+  float ll = row_sum16(lsum);
+  ll += xor16_other(ll, li);
+  ll += xor32_other(ll, li);
+  // the weights to every lane through LDS (broadcast reads)
+  __shared__ __attribute__((aligned(16))) float s_w[N];
+  if (d < 64) {
+#pragma unroll
+    for (int p = 0; p < P; p++)
+      if (64 * p + li < N) s_w[64 * p + li] = f[p];
+  }
+  __syncthreads();
+  float oo = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; i++) oo += o_sp[i] * s_w[i];
   a.out[orow * D + d] = f32_to_bf16_rne(oo / ll);
 }
 
@@ -1380,6 +1411,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   if (n_splits <= 8) return merge_in_registers<8>(a, row0, last, d, orow);
   if (n_splits <= 16) return merge_in_registers<16>(a, row0, last, d, orow);
   if (n_splits <= 32) return merge_in_registers<32>(a, row0, last, d, orow);
+  if (n_splits <= 64) return merge_in_registers<64>(a, row0, last, d, orow);
   if (n_splits <= kMergeOneRound) return merge_in_registers<kMergeOneRound>(a, row0, last, d, orow);
   // partials of the first splits: in flight while the (max, sum) pairs are reduced
   float o_pre[kMergePrefetch];
