@@ -61,7 +61,7 @@ void read_env_options(llh_ctx *ctx) {
 //  * bf16 pools are memory-bound: 8 blocks (two per wavefront, so each
 //    wavefront has a block in flight behind the one it computes) beat larger
 //    splits on ragged and on long contexts (C2 52 us at 8 against 59-65 at
-//    16-64, C4 decode 17 us against 27 at 4); steps too small to give 512
+//    16-64, C4 decode 15.9 us against 18.6 at 4); steps too small to give 512
 //    workgroups that way use 4;
 //  * int8 / fp8 pools are bound by their per-block arithmetic: the split that
 //    brings the workgroup count closest to 2048 (C5: 128 blocks, 278 us
