@@ -1276,16 +1276,20 @@ __device__ __forceinline__ void stream_merge_round(const DecodeArgs &a, int firs
     a1[i] = a.ws_o[row * D + 64 + lane];
   }
   __builtin_amdgcn_sched_barrier(0);  // every load of the round is issued before the first wait
+  static_assert(N == 16 || N == 32, "one or two DPP rows of partials");
+  // max and sum over lanes 0 .. N-1: DPP within rows, then a row exchange (no LDS)
   const float m = lane < cnt ? ml.x : -INFINITY;
   float nm = m;
-#pragma unroll
-  for (int o = N / 2; o > 0; o >>= 1) nm = fmaxf(nm, __shfl_xor(nm, o));
+  nm = fmaxf(nm, dpp<0xB1>(nm));   // quad_perm [1,0,3,2]
+  nm = fmaxf(nm, dpp<0x4E>(nm));   // quad_perm [2,3,0,1]
+  nm = fmaxf(nm, dpp<0x141>(nm));  // row_half_mirror
+  nm = fmaxf(nm, dpp<0x140>(nm));  // row_mirror
+  if constexpr (N == 32) nm = fmaxf(nm, xor16_other(nm, lane));
   nm = fmaxf(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nm))), mm);
   const float mref = (nm == -INFINITY) ? 0.0f : nm;
   const float f = fast_exp2(m - mref);  // 0 on lanes past the last partial
-  float ls = ml.y * f;
-#pragma unroll
-  for (int o = N / 2; o > 0; o >>= 1) ls += __shfl_xor(ls, o);
+  float ls = row_sum16(ml.y * f);
+  if constexpr (N == 32) ls += xor16_other(ls, lane);
   const float f0 = fast_exp2(mm - mref);
   ll = ll * f0 + __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ls)));
   o0 *= f0;
@@ -1330,11 +1334,10 @@ __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArg
 // Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
 // dim) per (query head, sequence) whose sequence used more than one split.
 // The merge is latency-bound, so it is laid out as few dependent memory round
-// trips as possible: up to 64 splits, each lane loads every (max, sum) pair
-// and its partial of every split at once and combines them in registers;
-// beyond that the partials of the first 96 splits are loaded together with
-// the (max, sum) pairs, the pairs are reduced through LDS, and any remaining
-// partials follow 32 at a time.
+// trips as possible: up to 128 splits from one round of loads
+// (merge_in_registers); beyond that the partials of the first 96 splits are
+// loaded together with the (max, sum) pairs, the pairs are reduced through
+// LDS, and any remaining partials follow 32 at a time.
 constexpr int kMergeMaxSplits = 1024;
 constexpr int kMergeOneRound = 128;  // splits merged from one round of loads, all in registers
 constexpr int kMergePrefetch = 96;   // partials loaded up front on the LDS path
