@@ -59,12 +59,6 @@ __device__ __forceinline__ uint8_t encode_e4m3(float x) {
   return (uint8_t)(sign | q);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
 // Max over the 16 lanes of a DPP row (lanes 16g .. 16g+15), in every lane of
 // the row: quad butterflies (quad_perm [1,0,3,2] and [2,3,0,1]), then the row
 // rotated by 4 and by 8 lanes.  No LDS round trip.
@@ -78,6 +72,18 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, row_dpp<0x124>(v));
   v = fmaxf(v, row_dpp<0x128>(v));
   return v;
+}
+
+// Max over the wavefront, in every lane: the row maxima, then v_permlane16_swap
+// and v_permlane32_swap of the register with itself (each leaves one row, or
+// half, of every pair in each result register, so the max of the two covers
+// the pair).  No LDS round trip.
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
 }
 
 // Whole 16-token blocks of head_dim 128, any pool format: one workgroup of
