@@ -441,22 +441,33 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     }
     float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[fp8_scale_index(bh)],
                       reinterpret_cast<const float *>(a.vs_dst)[fp8_scale_index(bh)]};
-    for (int j = i; j < a.n; j++) {
-      const int64_t sj = a.slots[j];
-      if (sj < 0 || sj / BT != blk) continue;
-      const int offj = (int)(sj % BT);
-      const ST *kj = reinterpret_cast<const ST *>(a.k) + ((size_t)j * Hkv + h) * Dh;
-      const ST *vj = reinterpret_cast<const ST *>(a.v) + ((size_t)j * Hkv + h) * Dh;
-      bool finite = true;
-      for (int d = lane; d < Dh; d += 64) finite = finite && isfinite(ld(kj, d)) && isfinite(ld(vj, d));
-      if (__any(!finite)) {
-        if (lane == 0) atomicOr(a.err, kErrNonFinite);
-        continue;
+    // this call's tokens of the block, in call order: the slots are read 64 at a
+    // time (one vector load per lane) and walked through a ballot mask
+    for (int j0 = i; j0 < a.n; j0 += 64) {
+      const int64_t sl = j0 + lane < a.n ? a.slots[j0 + lane] : (int64_t)-1;
+      uint64_t pending = __ballot(sl >= 0 && sl / BT == blk);
+      while (pending) {
+        const int k = __builtin_ctzll(pending);
+        pending &= pending - 1;
+        const int j = j0 + k;
+        const int64_t sj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sl >> 32), k) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sl, k));
+        const int offj = (int)(sj % BT);
+        const ST *kj = reinterpret_cast<const ST *>(a.k) + ((size_t)j * Hkv + h) * Dh;
+        const ST *vj = reinterpret_cast<const ST *>(a.v) + ((size_t)j * Hkv + h) * Dh;
+        bool finite = true;
+        for (int d = lane; d < Dh; d += 64) finite = finite && isfinite(ld(kj, d)) && isfinite(ld(vj, d));
+        if (__any(!finite)) {
+          if (lane == 0) atomicOr(a.err, kErrNonFinite);
+          continue;
+        }
+        // this wavefront's earlier stores to the block are complete before it reads the block again
+        if (j > i) __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+        scale[0] =
+            append_fp8_row(reinterpret_cast<uint8_t *>(a.k_dst), false, bh, BT, Dh, offj, kj, ld, scale[0], lane);
+        scale[1] =
+            append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
       }
-      // this wavefront's earlier stores to the block are complete before it reads the block again
-      if (j > i) __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-      scale[0] = append_fp8_row(reinterpret_cast<uint8_t *>(a.k_dst), false, bh, BT, Dh, offj, kj, ld, scale[0], lane);
-      scale[1] = append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
     }
     if (lane == 0) {
       reinterpret_cast<float *>(a.ks_dst)[fp8_scale_index(bh)] = scale[0];
