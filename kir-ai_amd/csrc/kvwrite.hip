@@ -405,15 +405,6 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
   const int BT = a.pool.block_tokens;
   const int Hkv = a.pool.kv_heads;
   const int Dh = a.pool.head_dim;
-  const int64_t slot = a.slots[i];
-  if (slot == kNoSlot) return;  // a sequence with no new token (fused-append fallback)
-  const int64_t blk = slot / BT;
-  const int off = (int)(slot % BT);
-  if (slot < 0 || blk >= a.pool.n_blocks) {
-    if (lane == 0) atomicOr(a.err, kErrBadBlock);
-    return;
-  }
-  const size_t bh = (size_t)blk * Hkv + h;
   const ST *ks = reinterpret_cast<const ST *>(a.k) + ((size_t)i * Hkv + h) * Dh;
   const ST *vs = reinterpret_cast<const ST *>(a.v) + ((size_t)i * Hkv + h) * Dh;
   auto ld = [](const ST *p, int d) -> float {
@@ -422,13 +413,58 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     else
       return bf16_to_f32(p[d]);
   };
+  // head_dim <= 128: the token's rows (two elements per lane) do not depend on
+  // the slot, so they are loaded together with it and one memory round trip
+  // covers both (the empty asm takes all five values, so neither load is
+  // deferred behind the slot checks)
+  const bool rows_in_regs = Dh <= 128;
+  const int64_t slot = a.slots[i];
+  uint32_t kraw[2] = {0u, 0u}, vraw[2] = {0u, 0u};  // the elements' bits as stored in k / v
+  if (rows_in_regs) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {  // unconditional (clamped) loads: all four in flight at once
+      const int d = min(lane + 64 * r, Dh - 1);
+      if constexpr (sizeof(ST) == 4) {
+        kraw[r] = __float_as_uint(ks[d]);
+        vraw[r] = __float_as_uint(vs[d]);
+      } else {
+        kraw[r] = ks[d];
+        vraw[r] = vs[d];
+      }
+    }
+  }
+  asm volatile("" ::"v"(kraw[0]), "v"(kraw[1]), "v"(vraw[0]), "v"(vraw[1]), "s"(slot));
+  float kx[2], vx[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    kx[r] = sizeof(ST) == 4 ? __uint_as_float(kraw[r]) : bf16_to_f32((uint16_t)kraw[r]);
+    vx[r] = sizeof(ST) == 4 ? __uint_as_float(vraw[r]) : bf16_to_f32((uint16_t)vraw[r]);
+  }
+  if (slot == kNoSlot) return;  // a sequence with no new token (fused-append fallback)
+  const int64_t blk = slot / BT;
+  const int off = (int)(slot % BT);
+  if (slot < 0 || blk >= a.pool.n_blocks) {
+    if (lane == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  // calls f(d, k, v) for each element d of this lane's share of the rows
+  auto for_elems = [&](auto f) __attribute__((always_inline)) {
+    if (rows_in_regs) {
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        if (lane + 64 * r < Dh) f(lane + 64 * r, kx[r], vx[r]);
+    } else {
+      for (int d = lane; d < Dh; d += 64) f(d, ld(ks, d), ld(vs, d));
+    }
+  };
   if (a.pool.format == kBf16) {
     uint16_t *kd = reinterpret_cast<uint16_t *>(a.k_dst);
     uint16_t *vd = reinterpret_cast<uint16_t *>(a.v_dst);
-    for (int d = lane; d < Dh; d += 64) {
-      kd[(bh * BT + off) * Dh + d] = f32_to_bf16_rne(ld(ks, d));
-      vd[(bh * Dh + d) * BT + off] = f32_to_bf16_rne(ld(vs, d));
-    }
+    for_elems([&](int d, float k, float v) __attribute__((always_inline)) {
+      kd[(bh * BT + off) * Dh + d] = f32_to_bf16_rne(k);
+      vd[(bh * Dh + d) * BT + off] = f32_to_bf16_rne(v);
+    });
     return;
   }
   if (a.pool.format == kFp8) {
@@ -479,14 +515,13 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
   int8_t *kd = reinterpret_cast<int8_t *>(a.k_dst);
   int8_t *vd = reinterpret_cast<int8_t *>(a.v_dst);
   for (int tensor = 0; tensor < 2; tensor++) {
-    const ST *src = tensor ? vs : ks;
     float mx = 0.0f;
     bool finite = true;
-    for (int d = lane; d < Dh; d += 64) {
-      const float x = ld(src, d);
+    for_elems([&](int, float k, float v) __attribute__((always_inline)) {
+      const float x = tensor ? v : k;
       finite = finite && isfinite(x);
       mx = fmaxf(mx, fabsf(x));
-    }
+    });
     mx = wave_max(mx);
     if (__any(!finite)) {
       if (lane == 0) atomicOr(a.err, kErrNonFinite);
@@ -494,13 +529,13 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     }
     const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
     const float s = (float)s16;
-    for (int d = lane; d < Dh; d += 64) {
-      const int8_t code = quant_int8(ld(src, d), s);
+    for_elems([&](int d, float k, float v) __attribute__((always_inline)) {
+      const int8_t code = quant_int8(tensor ? v : k, s);
       if (tensor)
         vd[(bh * Dh + d) * BT + off] = code;
       else
         kd[(bh * BT + off) * Dh + d] = code;
-    }
+    });
     if (lane == 0)
       reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[int8_scale_index(bh, off, BT)] =
           __builtin_bit_cast(uint16_t, s16);
