@@ -721,10 +721,12 @@ __device__ __forceinline__ float prep_q(int lane, uint32_t (&qw)[G][kQWords<G, F
 struct NewToken {
   uint4 k;
   uint32_t v[8];
+  int blk;  // block-table entry of the block that receives the token (the segment's last unit's)
 };
 
-__device__ __forceinline__ void load_new_token(const DecodeArgs &a, int b, int kvh, int lane, NewToken &nt) {
+__device__ __forceinline__ void load_new_token(const DecodeArgs &a, int b, int kvh, int lane, NewToken &nt, int blk) {
   const int c = lane & 15;
+  nt.blk = blk;
   const size_t row = (size_t)b * a.pool.kv_heads + kvh;
   nt.k = *reinterpret_cast<const uint4 *>(a.k_new + row * D + 8 * c);
 #pragma unroll
@@ -766,7 +768,7 @@ __device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<
     }
   }
   const int pos = len - 1;
-  const int e = a.tables[(size_t)b * a.max_blocks + (pos / BT) % a.max_blocks];
+  const int e = nt.blk;
   if (g == 0 && e >= 0 && (int64_t)e < a.pool.n_blocks) {
     const size_t bh = (size_t)e * a.pool.kv_heads + kvh;
     uint16_t *kd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.k));
@@ -838,7 +840,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   const int last_blk = first_blk + n_blk - 1;
   const bool takes_new = fused && last_blk >= blk_begin && last_blk < blk_end && (last_blk - blk_begin) % 4 == wave;
   NewToken nt;
-  if (takes_new) load_new_token(a, b, kvh, lane, nt);
+  if (takes_new) load_new_token(a, b, kvh, lane, nt, stable[((len - 1) / BT) % a.max_blocks]);
 
   // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
   float qstep = 1.0f;
@@ -1188,12 +1190,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   load_q<G, FMT>(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G, lane, qw);
 
   BlockRegs<FMT> r[2];
-  load_block<FMT, TL>(a, next_entry(), L.kvh, lane, r[0]);
+  const int e_first = next_entry();
+  load_block<FMT, TL>(a, e_first, L.kvh, lane, r[0]);
   // fused append: a segment's new-token rows are loaded with its last unit, into
-  // the buffer that travels with that unit's registers (r[0] / r[1])
+  // the buffer that travels with that unit's registers (r[0] / r[1]), with that
+  // unit's block-table entry (the block the token goes to)
   NewToken nt[2];
   if constexpr (FMT == kBf16)
-    if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nt[0]);
+    if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nt[0], e_first);
   float qstep = prep_q<G, FMT>(lane, qw);
   int e_next = n > 1 ? next_entry() : -1;
   advance(L);
@@ -1224,7 +1228,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     if (issue) {
       load_block<FMT, TL>(a, e_next, L.kvh, lane, nxt);
       if constexpr (FMT == kBf16)
-        if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nxt_nt);
+        if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nxt_nt, e_next);
       e_next = k + 2 < n ? next_entry() : -1;
       advance(L);
     }
