@@ -733,7 +733,25 @@ __device__ __forceinline__ void load_new_token(const DecodeArgs &a, int b, int k
   for (int j = 0; j < 8; j++) nt.v[j] = a.v_new[row * D + 16 * j + c];
 }
 
-template <int G>
+// Writes a sequence's new token (position len - 1) into its pool slot: K as
+// one 256-byte row, V as one 2-byte element in each of the 128 dim rows.
+__device__ __forceinline__ void store_new_token(const DecodeArgs &a, int kvh, int len, int lane, const NewToken &nt) {
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int pos = len - 1;
+  const int e = nt.blk;
+  if (g == 0 && e >= 0 && (int64_t)e < a.pool.n_blocks) {
+    const size_t bh = (size_t)e * a.pool.kv_heads + kvh;
+    uint16_t *kd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.k));
+    uint16_t *vd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.v));
+    *reinterpret_cast<uint4 *>(kd + (bh * BT + pos % BT) * D + 8 * c) = nt.k;
+#pragma unroll
+    for (int j = 0; j < 8; j++) vd[(bh * D + 16 * j + c) * BT + pos % BT] = (uint16_t)nt.v[j];
+  }
+}
+
+// Adds the new token to the state (STORE: and writes it to the pool).
+template <int G, bool STORE = true>
 __device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<G> &st, int b, int kvh, int len,
                                               int lane, const uint32_t (&qw)[G][kQWords<G, kBf16>],
                                               const NewToken &nt) {
@@ -767,16 +785,7 @@ __device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<
       for (int j = 0; j < 8; j++) st.o[gi][j] = dot2_bf16(vn[j], w, st.o[gi][j]);
     }
   }
-  const int pos = len - 1;
-  const int e = nt.blk;
-  if (g == 0 && e >= 0 && (int64_t)e < a.pool.n_blocks) {
-    const size_t bh = (size_t)e * a.pool.kv_heads + kvh;
-    uint16_t *kd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.k));
-    uint16_t *vd = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.v));
-    *reinterpret_cast<uint4 *>(kd + (bh * BT + pos % BT) * D + 8 * c) = kn;
-#pragma unroll
-    for (int j = 0; j < 8; j++) vd[(bh * D + 16 * j + c) * BT + pos % BT] = (uint16_t)vn[j];
-  }
+  if constexpr (STORE) store_new_token(a, kvh, len, lane, nt);
 }
 
 template <int G, int FMT, bool FUSED = false>
@@ -1196,6 +1205,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   // the buffer that travels with that unit's registers (r[0] / r[1]), with that
   // unit's block-table entry (the block the token goes to)
   NewToken nt[2];
+  NewToken pend;  // a computed segment's new token, not yet written to the pool
+  int pend_kvh = 0, pend_len = 0;
+  bool have_pend = false;
   if constexpr (FMT == kBf16)
     if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nt[0], e_first);
   float qstep = prep_q<G, FMT>(lane, qw);
@@ -1239,7 +1251,17 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     compute_block<G, FMT>(a, cur, C.lo / BT + C.j, C.lo, fused ? C.len - 1 : C.len, lane, qw, qstep, st);
     if (C.j == C.nb - 1) {  // the segment ends with this unit
       if constexpr (FMT == kBf16)
-        if (fused) add_new_token<G>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);
+        if (fused) {
+          // The token's pool write waits for the end of the range (or the range's
+          // next new token): stores count in vmcnt like loads, so one issued in
+          // the loop would be waited for by the next unit's load wait.
+          add_new_token<G, false>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);
+          if (have_pend) store_new_token(a, pend_kvh, pend_len, lane, pend);
+          pend = cur_nt;
+          pend_kvh = C.kvh;
+          pend_len = C.len;
+          have_pend = true;
+        }
       end_segment(seg_from_start);
       seg_from_start = true;
       need_q = true;
@@ -1258,6 +1280,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     step(k, r[0], r[1], nt[0], nt[1], false);
   }
   if (C.j != 0) end_segment(false);  // the range ends inside a segment
+  if constexpr (FMT == kBf16)
+    if (fused && have_pend) store_new_token(a, pend_kvh, pend_len, lane, pend);
 }
 
 // One round of the stream merge over partials i0 .. i0+cnt-1 (1 <= cnt <= N <=
