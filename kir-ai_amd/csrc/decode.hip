@@ -1252,15 +1252,19 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
     if (C.j == C.nb - 1) {  // the segment ends with this unit
       if constexpr (FMT == kBf16)
         if (fused) {
-          // The token's pool write waits for the end of the range (or the range's
-          // next new token): stores count in vmcnt like loads, so one issued in
-          // the loop would be waited for by the next unit's load wait.
-          add_new_token<G, false>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);
-          if (have_pend) store_new_token(a, pend_kvh, pend_len, lane, pend);
-          pend = cur_nt;
-          pend_kvh = C.kvh;
-          pend_len = C.len;
-          have_pend = true;
+          if constexpr (G > 4) {
+            add_new_token<G, true>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);  // no registers to spare
+          } else {
+            // The token's pool write waits for the end of the range (or the range's
+            // next new token): stores count in vmcnt like loads, so one issued in
+            // the loop would be waited for by the next unit's load wait.
+            add_new_token<G, false>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);
+            if (have_pend) store_new_token(a, pend_kvh, pend_len, lane, pend);
+            pend = cur_nt;
+            pend_kvh = C.kvh;
+            pend_len = C.len;
+            have_pend = true;
+          }
         }
       end_segment(seg_from_start);
       seg_from_start = true;
