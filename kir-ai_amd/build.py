@@ -31,6 +31,12 @@ def hipcc() -> str:
     return path
 
 
+# The prefill's MFMA loop is scheduled for instruction-level parallelism
+# (measured on MI355X: C4 prefill 157.0 -> 156.0 us, C3 over int8 blocks
+# 165.9 -> 163.6 us, C3 bf16 unchanged, all against the default scheduler).
+PER_FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
+
+
 def common_flags() -> list[str]:
     return [
         "-O3",
@@ -50,6 +56,7 @@ def compile_one(src: str) -> str:
     cmd = [hipcc()] + common_flags()
     if src.endswith(".cpp"):
         cmd += ["-x", "hip"]
+    cmd += PER_FILE_FLAGS.get(src, [])
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; that warning is expected

@@ -756,7 +756,6 @@ __device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<
                                               int lane, const uint32_t (&qw)[G][kQWords<G, kBf16>],
                                               const NewToken &nt) {
   const int g = lane >> 4;
-  const int c = lane & 15;
   const uint4 kn = nt.k;
   const uint32_t(&vn)[8] = nt.v;
   float s[G];
