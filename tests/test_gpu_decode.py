@@ -163,11 +163,13 @@ def test_decode_split_sizes(ctx, opts, split_blocks):
     check(ctx, batch, 32, 8, seed=17, what=f"split={split_blocks}")
 
 
-@pytest.mark.parametrize("n_splits", [2, 33, 64, 65, 96, 97, 130])
+@pytest.mark.parametrize("n_splits", [2, 8, 9, 17, 33, 64, 65, 97, 128, 129, 130, 200])
 def test_decode_merge_split_counts(ctx, opts, n_splits):
-    """The merge launch's three layouts: every partial in registers (<= 64 splits),
-    LDS-reduced pairs with all partials loaded up front (<= 96) and the chunked tail;
-    one sequence per count at the boundaries, 4-block splits."""
+    """The merge launch's layouts: every partial in registers with one (<= 64 splits)
+    or two (<= 128) (max, sum) pairs per lane, in register sets of 8 / 16 / 32 / 64 /
+    128; beyond 128 the pairs reduced through LDS with the first 96 partials loaded up
+    front and the rest in chunks of 32.  Two sequences per count (n and n - 1 splits)
+    at the boundaries, 4-block splits."""
     opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, 4)
     opts(llm_hip.OPT_DECODE_KERNEL, "split")
     lens = np.array([BT * 4 * n_splits - 5, BT * 4 * (n_splits - 1) + 1], np.int32)  # n_splits each
