@@ -335,3 +335,33 @@ def test_fp8_decode_table(ctx):
     ref = oracle.fp8_decode_table()
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan) and np.array_equal(got[~nan], ref[~nan])
+
+
+def test_fp8_append_one_call_equals_token_by_token_calls(ctx):
+    """A call of 128 tokens whose blocks' tokens are interleaved across the whole call
+    (token i goes to block i % 8 at offset i // 8, so each block's tokens sit in both
+    64-slot scans of the call) leaves the pool bit-identical to 128 calls of one token
+    in the same order: the tokens of one block are appended in call order."""
+    import torch
+
+    Hkv, n_tok, nb = 2, 128, 8
+    rng = np.random.default_rng(11)
+    mag = np.exp(rng.uniform(-3, 2, n_tok)).astype(np.float32)
+    k = oracle.f32_to_bf16(rng.standard_normal((n_tok, Hkv, D)).astype(np.float32) * mag[:, None, None])
+    v = oracle.f32_to_bf16(rng.standard_normal((n_tok, Hkv, D)).astype(np.float32) * mag[::-1, None, None])
+    blocks = [6, 2, 9, 0, 4, 11, 7, 1]
+    slots = np.array([blocks[i % nb] * BT + i // nb for i in range(n_tok)], np.int64)
+    one = ctx.pool(llm_hip.KV_FP8_E4M3, BT, Hkv, D, 12)
+    many = ctx.pool(llm_hip.KV_FP8_E4M3, BT, Hkv, D, 12)
+    ctx.append(one, to_dev(slots), to_dev(k), to_dev(v))
+    for i in range(n_tok):
+        ctx.append(many, to_dev(slots[i:i + 1]), to_dev(k[i:i + 1]), to_dev(v[i:i + 1]))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    a, b = one.raw(), many.raw()
+    used = np.array(blocks)  # the other blocks were never written (their contents are unspecified)
+    for key, shape in (("k", (12, Hkv, BT, D)), ("v", (12, Hkv, D, BT))):
+        assert np.array_equal(a[key].reshape(shape)[used], b[key].reshape(shape)[used]), key
+    for key in ("k_scales", "v_scales"):
+        sa, sb = a[key].view(np.float32).reshape(12, Hkv), b[key].view(np.float32).reshape(12, Hkv)
+        assert np.array_equal(sa[used], sb[used]), key
