@@ -433,11 +433,16 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     // the normaliser sums the weights p . v really applies to the dequantised value
     // (code * scale): bf16(p * scale) / scale, the same bf16 rounding as the packs below
     st.l_own += vs_own != 0.0f ? bf16_round(wv) * __builtin_amdgcn_rcpf(vs_own) : p;
-    // every lane of the row gathers the row's 4 tokens' value weights of each head
+    // every lane of the row gathers the row's 4 tokens' value weights of each
+    // head: each lane packs its weight with the next token's (same head, 4 lanes
+    // on: DPP row_shl:4), so the pairs (t0, t1) and (t2, t3) of head gi sit in
+    // row lanes gi and 8 + gi and one broadcast per pair reaches the row
+    const uint32_t pr = pack_bf16(wv, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(wv), 0x104, 0xF, 0xF,
+                                                                              false)));
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-      w01[gi] = pack_bf16(row_bcast(wv, gi), row_bcast(wv, 4 + gi));
-      w23[gi] = pack_bf16(row_bcast(wv, 8 + gi), row_bcast(wv, 12 + gi));
+      w01[gi] = __float_as_uint(row_bcast(__uint_as_float(pr), gi));
+      w23[gi] = __float_as_uint(row_bcast(__uint_as_float(pr), 8 + gi));
     }
   } else {
     float s[G][4];
