@@ -40,7 +40,8 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 4  /* 4: int8 and fp8 pools store their scales as (K, V) pairs */
+#define LLH_ABI_VERSION 5  /* 5: per-stream device error words, llh_layer_cache_create_from_rows;
+                              4: int8 and fp8 pools store their scales as (K, V) pairs */
 
 /* Status codes.  Mirrors MathError / KvCacheError
  * (crates/llm-backend/src/core/math.rs:10-15, crates/llm-kv-cache/src/lib.rs). */
@@ -127,15 +128,28 @@ typedef struct llh_metrics {
   uint64_t trait_tuned_calls;   /* trait-mirror attention calls served by the tuned decode kernels */
   uint64_t generic_prefill_calls; /* prefill calls that ran the element-wise kernel */
   uint64_t fused_append_calls;    /* llh_paged_decode_append calls served by one launch */
+  uint64_t stream_slots;          /* streams holding a workspace slot (scratch and error word) now */
+  uint64_t workspace_bytes;       /* device bytes of those slots' scratch now */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
-/* Waits for the device, then reads (and optionally clears) the sticky error
- * flags the batched kernels raise instead of faulting: 1 = a block table entry
- * outside the pool, 2 = a sequence longer than the call's max_seq_len allows,
- * 4 = a non-finite score, 8 = a sequence's attended span needs more blocks
- * than its block-table row holds (the row is read modulo its length, so the
- * span would alias its own blocks).  The flags are shared by every stream. */
+/* Sticky error flags the batched kernels raise instead of faulting: 1 = a
+ * block table entry outside the pool, 2 = a sequence longer than the call's
+ * max_seq_len allows, 4 = a non-finite value (score, or a row given to an
+ * int8 write / append), 8 = a sequence's attended span needs more blocks than
+ * its block-table row holds (the row is read modulo its length, so the span
+ * would alias its own blocks).  Each stream has its own flag word (the calls
+ * made on it raise flags there; MetalBackendMetrics records fallbacks per
+ * call in the reference, native_metrics.rs:81-112), created with the stream's
+ * workspace slot; calls that cannot have one (llh_paged_decode_noalloc on a
+ * stream without a slot, a stream under graph capture without one) use the
+ * context's word.
+ * llh_ctx_device_errors waits for the whole device and returns the OR of every
+ * word (the context's, every stream's, and those of released streams),
+ * optionally clearing them all. */
 int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset);
+/* One stream's flags: waits for that stream only, then reads (and optionally
+ * clears) the word of the calls made on it; 0 for a stream that has none. */
+int llh_ctx_stream_device_errors(llh_ctx *ctx, void *stream, int32_t *flags, int32_t reset);
 /* Kernel timing for measurement: while enabled, each llh_paged_decode /
  * llh_paged_prefill call records a pair of HIP events on its stream around its
  * main kernel (the split-K or stream decode kernel, not the merge; the prefill
@@ -342,7 +356,37 @@ int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int
  * UNSUPPORTED. */
 int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, size_t head_dim, int32_t format,
                            llh_layer_cache **out);
+/* Also releases the workspace slot of the cache's own stream. */
 int llh_layer_cache_destroy(llh_layer_cache *cache);
+
+/* A device mirror of a host LayerKvCache that already holds rows:
+ * LayerKvCache::from_snapshot (crates/llm-kv-cache/src/layer.rs:467-507, with
+ * window_start = 0) and from_prefix_cache_state (layer.rs:544-581) -- the
+ * caches the driver restores on a prefix-cache hit
+ * (crates/llm-native-runtime/src/native_text/driver.rs:694-703).  The rows are
+ * the cache's logical rows (keys() / values(), layer.rs:1046-1052): logical row
+ * i goes to ring slot (window_start + i) % max_tokens, stored as appending it
+ * would store it (bf16 rounding, int8 quantisation).  The new cache has a
+ * fresh id and block ids, and the given revision, token count, tokens seen
+ * and window start, so its state and active_blocks() are those of the host
+ * cache.  Errors as the reference: a state failing from_prefix_cache_state's
+ * checks (zero sizes, token_count > max_tokens, tokens_seen < token_count,
+ * window_start >= max_tokens) or rows of the wrong length -> INVALID_SHAPE,
+ * non-finite rows of an int8 cache -> NON_FINITE, fp8 -> UNSUPPORTED. */
+typedef struct llh_layer_cache_rows {
+  uint64_t max_tokens;
+  uint64_t kv_heads;
+  uint64_t head_dim;
+  int32_t format;         /* LLH_KV_BF16, LLH_KV_INT8 or LLH_KV_INT8_ROW */
+  uint64_t revision;      /* revision() */
+  uint64_t token_count;   /* token_count() */
+  uint64_t tokens_seen;   /* next_position() */
+  uint64_t window_start;  /* physical slot of logical token 0: active_blocks()[0].physical_token_start() */
+  const float *h_keys;    /* [token_count][kv_heads * head_dim] f32 host rows, logical order */
+  const float *h_values;
+  size_t keys_len;        /* elements of h_keys and of h_values: token_count * kv_heads * head_dim */
+} llh_layer_cache_rows;
+int llh_layer_cache_create_from_rows(llh_ctx *ctx, const llh_layer_cache_rows *rows, llh_layer_cache **out);
 /* Clone with a fresh cache id that shares blocks until written (layer.rs:237-259, block.rs:124-130). */
 int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out);
 /* clear() (layer.rs:1068-1086) */

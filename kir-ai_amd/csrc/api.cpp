@@ -186,8 +186,10 @@ int llh_ctx_destroy(llh_ctx *ctx) {
       (void)hipEventDestroy(ev.second);
     }
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
-  for (auto &w : ctx->workspaces)
+  for (auto &w : ctx->workspaces) {
     if (w->ptr) (void)hipFree(w->ptr);
+    if (w->err) (void)hipFree(w->err);
+  }
   if (ctx->d_err) (void)hipFree(ctx->d_err);
   delete ctx;
   return LLH_OK;
@@ -208,7 +210,7 @@ int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes) {
   std::vector<std::shared_ptr<StreamWorkspace>> slots;
   {
     std::lock_guard<std::mutex> g(ctx->ws_mu);
-    ctx->ws_min_bytes = std::max(ctx->ws_min_bytes, kCounterBytes + bytes);
+    ctx->ws_min_bytes = std::max(ctx->ws_min_bytes, bytes);
     slots = ctx->workspaces;
   }
   for (auto &w : slots) {
@@ -222,11 +224,17 @@ int llh_ctx_reserve_workspace(llh_ctx *ctx, size_t bytes) {
 int llh_ctx_reserve_stream_workspace(llh_ctx *ctx, void *stream, size_t bytes) {
   if (!ctx) return LLH_ERR_NULL;
   WsLease lease;
-  return lease.acquire(ctx, static_cast<hipStream_t>(stream), kCounterBytes + bytes);
+  return lease.acquire(ctx, static_cast<hipStream_t>(stream), bytes);
 }
 
-int llh_ctx_release_stream(llh_ctx *ctx, void *stream) {
-  if (!ctx) return LLH_ERR_NULL;
+}  // extern "C"
+
+// Drops the workspace slot of `stream` (scratch and error word).  A stream the
+// caller may already have destroyed is waited for with the whole device; a live
+// one (a layer cache's own) with its own synchronisation.  Flags still set in
+// the slot's word are folded into the context's word, so llh_ctx_device_errors
+// keeps seeing them.
+static int release_slot(llh_ctx *ctx, hipStream_t stream, bool stream_alive) {
   std::shared_ptr<StreamWorkspace> w;
   {
     std::lock_guard<std::mutex> g(ctx->ws_mu);
@@ -237,16 +245,29 @@ int llh_ctx_release_stream(llh_ctx *ctx, void *stream) {
     ctx->workspaces.erase(it);
   }
   std::lock_guard<std::mutex> g(w->mu);  // waits for a call still holding it
-  if (w->ptr) {
-    // the stream may already be gone: wait for the whole device before freeing
-    hipError_t e = hipSetDevice(ctx->device);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) return ctx->hip_fail(e, "release stream workspace");
-    (void)hipFree(w->ptr);
-    w->ptr = nullptr;
-    w->bytes = 0;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = stream_alive ? hipStreamSynchronize(stream) : hipDeviceSynchronize();
+  int32_t flags = 0;
+  if (e == hipSuccess && w->err) e = hipMemcpy(&flags, w->err, sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return ctx->hip_fail(e, "release stream workspace");
+  if (flags) {
+    std::lock_guard<std::mutex> g2(ctx->ws_mu);
+    ctx->retired_flags |= flags;
   }
+  if (w->ptr) (void)hipFree(w->ptr);
+  if (w->err) (void)hipFree(w->err);
+  w->ptr = nullptr;
+  w->err = nullptr;
+  w->bytes = 0;
   return LLH_OK;
+}
+
+extern "C" {
+
+int llh_ctx_release_stream(llh_ctx *ctx, void *stream) {
+  if (!ctx) return LLH_ERR_NULL;
+  // the stream may already be gone: the whole device is waited for
+  return release_slot(ctx, static_cast<hipStream_t>(stream), false);
 }
 
 int llh_ctx_set_option(llh_ctx *ctx, int32_t option, int32_t value) {
@@ -289,17 +310,52 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->trait_tuned_calls = ctx->trait_tuned_calls.load();
   out->generic_prefill_calls = ctx->generic_prefill_calls.load();
   out->fused_append_calls = ctx->fused_append_calls.load();
+  std::lock_guard<std::mutex> g(const_cast<llh_ctx *>(ctx)->ws_mu);
+  out->stream_slots = ctx->workspaces.size();
+  out->workspace_bytes = 0;
+  for (auto &w : ctx->workspaces) out->workspace_bytes += w->bytes;
   return LLH_OK;
 }
 
 int llh_ctx_device_errors(llh_ctx *ctx, int32_t *flags, int32_t reset) {
   if (!ctx || !flags) return LLH_ERR_NULL;
+  *flags = 0;
+  std::lock_guard<std::mutex> g(ctx->ws_mu);  // no slot comes or goes meanwhile
   hipError_t e = hipSetDevice(ctx->device);
   if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (e == hipSuccess) e = hipMemcpy(flags, ctx->d_err, sizeof(int32_t), hipMemcpyDeviceToHost);
-  if (e == hipSuccess && reset) e = hipMemset(ctx->d_err, 0, sizeof(int32_t));
-  if (e == hipSuccess && reset) e = hipDeviceSynchronize();  // the reset lands before any later kernel
+  std::vector<int32_t *> words{ctx->d_err};
+  for (auto &w : ctx->workspaces)
+    if (w->err) words.push_back(w->err);
+  for (int32_t *word : words) {
+    int32_t f = 0;
+    if (e == hipSuccess) e = hipMemcpy(&f, word, sizeof(int32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && reset && f) e = hipMemset(word, 0, sizeof(int32_t));
+    *flags |= f;
+  }
+  *flags |= ctx->retired_flags;
+  if (reset) ctx->retired_flags = 0;
+  if (e == hipSuccess && reset) e = hipDeviceSynchronize();  // the resets land before any later kernel
   if (e != hipSuccess) return ctx->hip_fail(e, "device error flags");
+  return LLH_OK;
+}
+
+int llh_ctx_stream_device_errors(llh_ctx *ctx, void *stream, int32_t *flags, int32_t reset) {
+  if (!ctx || !flags) return LLH_ERR_NULL;
+  *flags = 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t *word = nullptr;
+  {
+    std::lock_guard<std::mutex> g(ctx->ws_mu);
+    for (auto &w : ctx->workspaces)
+      if (w->stream == s) word = w->err;
+  }
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e == hipSuccess && word) e = hipMemcpyAsync(flags, word, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && word) e = hipStreamSynchronize(s);
+  if (e == hipSuccess && word && reset && *flags) e = hipMemsetAsync(word, 0, sizeof(int32_t), s);
+  if (e == hipSuccess && word && reset && *flags) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return ctx->hip_fail(e, "stream device error flags");
   return LLH_OK;
 }
 
@@ -421,7 +477,7 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
   a.k = static_cast<const uint16_t *>(d_k);
   a.v = static_cast<const uint16_t *>(d_v);
   a.n = n;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(static_cast<hipStream_t>(stream));
   hipError_t e = launch_write_blocks(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "write_blocks launch");
   return LLH_OK;
@@ -444,7 +500,7 @@ static int kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, co
   a.v = d_v;
   a.n = n;
   a.src_f32 = src_f32;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(static_cast<hipStream_t>(stream));
   ctx->append_calls++;
   hipError_t e = launch_append(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "append launch");
@@ -473,7 +529,7 @@ int llh_kv_export_rows_f32(llh_ctx *ctx, const llh_kv_pool *pool, const int64_t 
   a.k = d_k;
   a.v = d_v;
   a.n = (int32_t)n;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(static_cast<hipStream_t>(stream));
   hipError_t e = launch_export_rows(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "export launch");
   return LLH_OK;
@@ -534,8 +590,7 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   plan->group = group;
   plan->fast = pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
                rows_aligned &&
-               (group == 1 || group == 2 || group == 4 || group == 8) &&
-               (size_t)desc->num_seqs * pv.kv_heads <= kCounterSlots && !ctx->opt(LLH_OPT_FORCE_GENERIC);
+               (group == 1 || group == 2 || group == 4 || group == 8) && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   if (plan->fast) {
     const SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
                                      desc->total_tokens_hint, pv.format);
@@ -548,7 +603,7 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     // partial rows: split-K [B][Hq][max_splits]; stream [2 * waves][G]
     const size_t rows = plan->stream_wgs ? (size_t)2 * 4 * plan->stream_wgs * group
                                          : (size_t)desc->num_seqs * desc->num_q_heads * sp.max_splits;
-    plan->ml_off = kCounterBytes;
+    plan->ml_off = 0;
     plan->o_off = plan->ml_off + align_up(rows * sizeof(float2));
     plan->desc_off = align_up(plan->o_off + rows * kFastHeadDim * sizeof(float));
     plan->bytes = align_up(plan->desc_off +
@@ -558,7 +613,7 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   // any other shape: the reference-order kernel, with a score row per (sequence, head)
   const int span = desc->window > 0 ? std::min(desc->window, desc->max_seq_len) : desc->max_seq_len;
   plan->score_stride = std::max(1, span);
-  plan->scores_off = kCounterBytes;
+  plan->scores_off = 0;
   plan->bytes = align_up(plan->scores_off + (size_t)desc->num_seqs * desc->num_q_heads * plan->score_stride *
                                                  sizeof(float));
   return LLH_OK;
@@ -567,7 +622,8 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
 // Launches a planned decode step with its workspace at `ws` (plan.bytes long).
 int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc,
                                const DecodePlan &plan, const void *d_q, void *d_out, float score_scale,
-                               hipStream_t s, char *ws, bool timed, const uint16_t *k_new, const uint16_t *v_new) {
+                               hipStream_t s, char *ws, int32_t *err, bool timed, const uint16_t *k_new,
+                               const uint16_t *v_new) {
   const PoolView &pv = pool->view;
   ctx->decode_calls++;
   if (plan.fast) {
@@ -579,7 +635,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
     a.tables = desc->d_block_tables;
     a.ws_o = reinterpret_cast<float *>(ws + plan.o_off);
     a.ws_ml = reinterpret_cast<float2 *>(ws + plan.ml_off);
-    a.err = ctx->d_err;
+    a.err = err;
     a.num_seqs = desc->num_seqs;
     a.q_heads = desc->num_q_heads;
     a.max_blocks = desc->max_blocks_per_seq;
@@ -616,7 +672,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
   g.starts = nullptr;
   g.tables = desc->d_block_tables;
   g.scores = reinterpret_cast<float *>(ws + plan.scores_off);
-  g.err = ctx->d_err;
+  g.err = err;
   g.num_seqs = desc->num_seqs;
   g.q_heads = desc->num_q_heads;
   g.max_blocks = desc->max_blocks_per_seq;
@@ -647,7 +703,7 @@ static int paged_decode_impl(llh_ctx *ctx, const llh_kv_pool *pool, const llh_de
   char *ws = lease.base();
   if (extra_ptr) *extra_ptr = ws + plan.bytes;
   if (!d_out) d_out = ws + plan.bytes;
-  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws);
+  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, lease.err());
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -717,6 +773,18 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   if (st != LLH_OK || plan.empty) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const PoolView &pv = pool->view;
+  // fp8 blocks keep one scale per (block, head) that a token at offset 0 restarts
+  // and a later token may grow, re-encoding only the tokens before it: a block
+  // that still holds live (in-window) tokens of an older pass round the ring
+  // must never receive the new token.  That holds when the row outlasts the
+  // window by a block's worth of slots (window + block_tokens - 1 <= row) or the
+  // ring never wraps (max_seq_len <= row).
+  const int64_t row_tokens = (int64_t)desc->max_blocks_per_seq * pv.block_tokens;
+  if (pv.format == LLH_KV_FP8_E4M3 && desc->max_seq_len > row_tokens &&
+      (int64_t)desc->window + pv.block_tokens - 1 > row_tokens)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE,
+                     "fp8 append over a window ring needs window + block_tokens - 1 <= max_blocks_per_seq * "
+                     "block_tokens (one block more than the window)");
   // one launch for bf16 pools on the tuned kernels (new-token rows 16-byte aligned);
   // any other case appends through the append kernel first, then decodes
   const bool fused = plan.fast && pv.format == LLH_KV_BF16 && aligned16(d_k_new) && aligned16(d_v_new);
@@ -727,7 +795,7 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   char *ws = lease.base();
   if (fused) {
     ctx->fused_append_calls++;
-    return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, true,
+    return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, lease.err(), true,
                                  static_cast<const uint16_t *>(d_k_new), static_cast<const uint16_t *>(d_v_new));
   }
   int64_t *slots = reinterpret_cast<int64_t *>(ws + plan.bytes);
@@ -736,7 +804,7 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   if (e != hipSuccess) return ctx->hip_fail(e, "new-token slot launch");
   st = kv_append(ctx, pool, slots, d_k_new, d_v_new, desc->num_seqs, 0, stream);
   if (st != LLH_OK) return st;
-  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws);
+  return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, lease.err());
 }
 
 int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t cols, const void *d_x, int32_t x_f32,
@@ -760,10 +828,10 @@ int llh_matvec_bf16_f32(llh_ctx *ctx, const void *d_w, int32_t rows, int32_t col
   a.x_f32 = x_f32 ? 1 : 0;
   a.ksplit = matvec_ksplit(rows, cols, n, ctx->cus);
   WsLease lease;
-  if (a.ksplit > 1) {  // partial tiles after the counters at the front of the stream's workspace
-    st = lease.acquire(ctx, static_cast<hipStream_t>(stream), kCounterBytes + (size_t)a.ksplit * n * rows * sizeof(float));
+  if (a.ksplit > 1) {  // partial tiles in the stream's workspace
+    st = lease.acquire(ctx, static_cast<hipStream_t>(stream), (size_t)a.ksplit * n * rows * sizeof(float));
     if (st != LLH_OK) return st;
-    a.partial = reinterpret_cast<float *>(lease.base() + kCounterBytes);
+    a.partial = reinterpret_cast<float *>(lease.base());
   }
   hipError_t e = launch_matvec_bf16(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "projection launch");
@@ -807,7 +875,7 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   a.chunk_starts = desc->d_chunk_starts;
   a.context_lens = desc->d_context_lens;
   a.tables = desc->d_block_tables;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(static_cast<hipStream_t>(stream));
   a.num_seqs = desc->num_seqs;
   a.q_heads = desc->num_q_heads;
   a.max_blocks = desc->max_blocks_per_seq;
@@ -850,7 +918,7 @@ int llh_debug_gather(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   a.tensor = tensor;
   a.ring_tokens = 0;
   a.out = d_out;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(static_cast<hipStream_t>(stream));
   hipError_t e = launch_gather(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "gather launch");
   return LLH_OK;
@@ -901,8 +969,10 @@ struct BlockStore {
   PoolView view() const {
     return PoolView{format, kRingBlockTokens, kv_heads, head_dim, capacity, k, v, ks, vs};
   }
-  // Grows the store; callers hold `mu` and no kernel on the store is in flight.
-  hipError_t allocate(int64_t cap) {
+  // Grows the store with its copies on stream s (waited for before the old
+  // buffers go); callers hold `mu`, so no kernel of any cache of the store is
+  // in flight (every trait call waits for its own stream before releasing it).
+  hipError_t allocate(int64_t cap, hipStream_t s) {
     kblock = (size_t)kv_heads * kRingBlockTokens * head_dim * elem_bytes(format);
     sblock = scale_bytes_per_block(format, kv_heads, kRingBlockTokens);
     // scale bytes per block in the K scales' allocation (int8, fp8: K and V scale pairs)
@@ -913,21 +983,22 @@ struct BlockStore {
     if (e == hipSuccess) e = hipMalloc(&nv, kblock * cap);
     if (e == hipSuccess && sblock) e = hipMalloc(&nks, kscale * cap);
     if (e == hipSuccess && sblock && !il) e = hipMalloc(&nvs, sblock * cap);
-    if (e == hipSuccess) e = hipMemset(nk, 0, kblock * cap);
-    if (e == hipSuccess) e = hipMemset(nv, 0, kblock * cap);
-    if (e == hipSuccess && sblock) e = hipMemset(nks, 0, kscale * cap);
-    if (e == hipSuccess && sblock && !il) e = hipMemset(nvs, 0, sblock * cap);
+    if (e == hipSuccess) e = hipMemsetAsync(nk, 0, kblock * cap, s);
+    if (e == hipSuccess) e = hipMemsetAsync(nv, 0, kblock * cap, s);
+    if (e == hipSuccess && sblock) e = hipMemsetAsync(nks, 0, kscale * cap, s);
+    if (e == hipSuccess && sblock && !il) e = hipMemsetAsync(nvs, 0, sblock * cap, s);
     if (e == hipSuccess && capacity > 0) {
-      e = hipMemcpy(nk, k, kblock * capacity, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess) e = hipMemcpy(nv, v, kblock * capacity, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess && sblock) e = hipMemcpy(nks, ks, kscale * capacity, hipMemcpyDeviceToDevice);
-      if (e == hipSuccess && sblock && !il) e = hipMemcpy(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice);
+      e = hipMemcpyAsync(nk, k, kblock * capacity, hipMemcpyDeviceToDevice, s);
+      if (e == hipSuccess) e = hipMemcpyAsync(nv, v, kblock * capacity, hipMemcpyDeviceToDevice, s);
+      if (e == hipSuccess && sblock) e = hipMemcpyAsync(nks, ks, kscale * capacity, hipMemcpyDeviceToDevice, s);
+      if (e == hipSuccess && sblock && !il)
+        e = hipMemcpyAsync(nvs, vs, sblock * capacity, hipMemcpyDeviceToDevice, s);
     }
     if (il && nks) nvs = static_cast<char *>(nks) + v_scale_offset_bytes(format);
-    // the memsets and device-to-device copies above run on the null stream,
-    // asynchronously to the host: they must land before the caches' own
-    // (non-blocking) streams touch the new buffers, and before the old ones go
-    if (e == hipSuccess) e = hipDeviceSynchronize();
+    // the copies must land before any cache's stream touches the new buffers
+    // (the next trait call, on whichever stream, starts after this wait) and
+    // before the old buffers are freed
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
       for (void *p : {nk, nv, nks, il ? nullptr : nvs})
         if (p) (void)hipFree(p);
@@ -944,10 +1015,10 @@ struct BlockStore {
     capacity = cap;
     return hipSuccess;
   }
-  // returns a pool index with refcount 1, growing the store when full
-  hipError_t take(int32_t &out) {
+  // returns a pool index with refcount 1, growing the store (on stream s) when full
+  hipError_t take(int32_t &out, hipStream_t s) {
     if (free_list.empty()) {
-      hipError_t e = allocate(capacity * 2);
+      hipError_t e = allocate(capacity * 2, s);
       if (e != hipSuccess) return e;
     }
     out = free_list.back();
@@ -1072,10 +1143,10 @@ int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, siz
   c->store->head_dim = (int32_t)head_dim;
   hipError_t e = hipSetDevice(ctx->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = c->store->allocate((int64_t)nb * 2 + 2);
+  if (e == hipSuccess) e = c->store->allocate((int64_t)nb * 2 + 2, c->stream);
   for (size_t i = 0; e == hipSuccess && i < nb; i++) {
     int32_t idx;
-    e = c->store->take(idx);
+    e = c->store->take(idx, c->stream);
     c->table.push_back(idx);
     c->ids.push_back(next_block_id());
   }
@@ -1087,6 +1158,96 @@ int llh_layer_cache_create(llh_ctx *ctx, size_t max_tokens, size_t kv_heads, siz
   return LLH_OK;
 }
 
+// LayerKvCache::from_snapshot (layer.rs:467-507) and from_prefix_cache_state
+// (layer.rs:544-581) on the device: a fresh cache (new id) whose ring holds the
+// given logical rows, logical row i in ring slot (window_start + i) % max_tokens,
+// with the given revision, token count, tokens seen and window start.  The rows
+// go through the append kernel (bf16 rounding, int8 quantisation), in chunks, so
+// the ring holds exactly what appending them one by one would write.
+int llh_layer_cache_create_from_rows(llh_ctx *ctx, const llh_layer_cache_rows *r, llh_layer_cache **out) {
+  if (!ctx || !r || !out) return LLH_ERR_NULL;
+  *out = nullptr;
+  // from_prefix_cache_state's checks, in its order (layer.rs:545-553)
+  if (r->max_tokens == 0 || r->kv_heads == 0 || r->head_dim == 0 || r->token_count > r->max_tokens ||
+      r->tokens_seen < r->token_count || r->window_start >= r->max_tokens)
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "invalid KV cache state");
+  llh_layer_cache *c = nullptr;
+  int st = llh_layer_cache_create(ctx, r->max_tokens, r->kv_heads, r->head_dim, r->format, &c);
+  if (st != LLH_OK) return st;
+  const size_t vl = c->vector_len();
+  const size_t n = r->token_count;
+  // from_snapshot's length check (layer.rs:482-496): KvCacheError::ShapeMismatch
+  if (r->keys_len != n * vl) {
+    llh_layer_cache_destroy(c);
+    return ctx->fail(LLH_ERR_INVALID_SHAPE, "KV rows do not match token_count * key_value_heads * head_dim");
+  }
+  if (n > 0 && (!r->h_keys || !r->h_values)) {
+    llh_layer_cache_destroy(c);
+    return ctx->fail(LLH_ERR_NULL, "null row pointer");
+  }
+  bool finite = true;
+  for (size_t i = 0; i < n * vl && finite; i++) finite = std::isfinite(r->h_keys[i]) && std::isfinite(r->h_values[i]);
+  if (!finite && (r->format == LLH_KV_INT8 || r->format == LLH_KV_INT8_ROW)) {
+    llh_layer_cache_destroy(c);
+    return ctx->fail(LLH_ERR_NON_FINITE, "int8 KV cache rows must be finite");
+  }
+  hipError_t e = hipSuccess;
+  if (n > 0) {
+    BlockStore &bs = *c->store;
+    std::lock_guard<std::mutex> gs(bs.mu);  // through the stream waits
+    const size_t chunk = std::max<size_t>(1, std::min<size_t>(n, ((size_t)16 << 20) / (vl * sizeof(float))));
+    const size_t k_off = align_up(chunk * sizeof(int64_t));
+    const size_t v_off = k_off + align_up(chunk * vl * sizeof(float));
+    void *tmp = nullptr;
+    e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc(&tmp, v_off + chunk * vl * sizeof(float));
+    std::vector<int64_t> slots(chunk);
+    int32_t *err = ctx->err_word(c->stream);
+    for (size_t i0 = 0; e == hipSuccess && i0 < n; i0 += chunk) {
+      const size_t m = std::min(chunk, n - i0);
+      for (size_t i = 0; i < m; i++) {
+        const size_t phys = (r->window_start + i0 + i) % r->max_tokens;
+        slots[i] = (int64_t)c->table[phys / kRingBlockTokens] * kRingBlockTokens + (int64_t)(phys % kRingBlockTokens);
+      }
+      char *d = static_cast<char *>(tmp);
+      e = hipMemcpyAsync(d, slots.data(), m * sizeof(int64_t), hipMemcpyHostToDevice, c->stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(d + k_off, r->h_keys + i0 * vl, m * vl * sizeof(float), hipMemcpyHostToDevice, c->stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(d + v_off, r->h_values + i0 * vl, m * vl * sizeof(float), hipMemcpyHostToDevice,
+                           c->stream);
+      AppendArgs a{};
+      a.pool = bs.view();
+      a.k_dst = bs.k;
+      a.v_dst = bs.v;
+      a.ks_dst = bs.ks;
+      a.vs_dst = bs.vs;
+      a.slots = reinterpret_cast<const int64_t *>(d);
+      a.k = d + k_off;
+      a.v = d + v_off;
+      a.n = (int32_t)m;
+      a.src_f32 = 1;
+      a.err = err;
+      if (e == hipSuccess) e = launch_append(a, c->stream);
+      // the host slot list is refilled for the next chunk only after this one's copies
+      if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    }
+    if (tmp) (void)hipFree(tmp);
+  }
+  if (e != hipSuccess) {
+    llh_layer_cache_destroy(c);
+    return ctx->hip_fail(e, "layer cache rows");
+  }
+  ctx->append_calls += n;
+  c->token_count = n;
+  c->tokens_seen = r->tokens_seen;
+  c->window_start = r->window_start;
+  c->revision = r->revision;
+  c->non_finite_rows = !finite;
+  *out = c;
+  return LLH_OK;
+}
+
 int llh_layer_cache_destroy(llh_layer_cache *cache) {
   if (!cache) return LLH_ERR_NULL;
   {
@@ -1094,8 +1255,11 @@ int llh_layer_cache_destroy(llh_layer_cache *cache) {
     for (int32_t idx : cache->table) cache->store->release(idx);
   }
   (void)hipSetDevice(cache->ctx->device);
+  // the workspace slot of the cache's stream (its tuned trait calls' scratch and
+  // error word) goes before the stream does
+  const int st = release_slot(cache->ctx, cache->stream, true);
   delete cache;
-  return LLH_OK;
+  return st;
 }
 
 int llh_layer_cache_clone(const llh_layer_cache *cache, llh_layer_cache **out) {
@@ -1226,7 +1390,7 @@ static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key
   const int32_t idx = cache->table[bi];
   if (bs.refs[idx] > 1) {
     int32_t fresh;
-    e = bs.take(fresh);
+    e = bs.take(fresh, cache->stream);
     if (e == hipSuccess) e = bs.copy_block(idx, fresh, cache->stream);
     if (e != hipSuccess) return ctx->hip_fail(e, "copy-on-write block");
     bs.release(idx);
@@ -1252,7 +1416,7 @@ static int layer_append(llh_ctx *ctx, llh_layer_cache *cache, const float *h_key
   a.v = sb + v_off;
   a.n = 1;
   a.src_f32 = 1;
-  a.err = ctx->d_err;
+  a.err = ctx->err_word(cache->stream);
   e = launch_append(a, cache->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "append");
@@ -1318,8 +1482,10 @@ static int cache_mix_tuned(llh_ctx *ctx, llh_layer_cache *cache, const float *h_
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
   char *hb = static_cast<char *>(cache->scratch.host);
   char *sb = static_cast<char *>(cache->scratch.dev);
-  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
-  const int32_t len = (int32_t)(abs_start + (int64_t)row_count);
+  // logical row i lives in ring slot (window_start + i) % max_tokens
+  // (layer.rs:1080-1095): the kernels address it as position window_start + i,
+  // whose block is table[(p / 16) % blocks] at offset p % 16 (whole-block ring)
+  const int32_t len = (int32_t)(cache->window_start + row_count);
   std::memcpy(hb, &len, sizeof(len));
   std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
   auto *qh = reinterpret_cast<uint16_t *>(hb + off_q);
@@ -1412,9 +1578,9 @@ static int cache_mix_impl(llh_ctx *ctx, const llh_layer_cache *cache_c, const fl
   if (e != hipSuccess) return ctx->hip_fail(e, "scratch allocation");
   char *hb = static_cast<char *>(cache->scratch.host);
   char *sb = static_cast<char *>(cache->scratch.dev);
-  // header: err flag, start, end
-  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
-  const int32_t hdr[4] = {0, (int32_t)abs_start, (int32_t)(abs_start + (int64_t)row_count), 0};
+  // header: err flag, start, end; logical row i is ring slot (window_start + i) % max_tokens
+  // (layer.rs:1080-1095), addressed as position window_start + i modulo the ring
+  const int32_t hdr[4] = {0, (int32_t)cache->window_start, (int32_t)(cache->window_start + row_count), 0};
   std::memcpy(hb, hdr, sizeof(hdr));
   std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
   std::memcpy(hb + off_q, h_query, qdim * sizeof(float));
@@ -1525,7 +1691,8 @@ int llh_select_kv_cache_head_rows_f32_in_place(llh_ctx *ctx, const llh_layer_cac
   std::memcpy(hb + off_table, cache->table.data(), nb * sizeof(int32_t));
   e = hipMemcpyAsync(sb, hb, off_out, hipMemcpyHostToDevice, cache->stream);
   if (e != hipSuccess) return ctx->hip_fail(e, "upload");
-  const int64_t abs_start = (int64_t)cache->tokens_seen - (int64_t)cache->token_count;
+  // logical row i is ring slot (window_start + i) % max_tokens (layer.rs:1080-1095)
+  const int64_t abs_start = (int64_t)cache->window_start;
   GatherArgs a{};
   a.pool = bs.view();
   a.table = reinterpret_cast<const int32_t *>(sb + off_table);

@@ -19,8 +19,6 @@
 
 namespace llh {
 
-constexpr size_t kCounterSlots = 65536;  // (sequence, kv head) arrival counters at the front of a workspace
-constexpr size_t kCounterBytes = kCounterSlots * sizeof(int32_t);
 constexpr size_t kAlign = 256;
 
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
@@ -29,14 +27,19 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // crates/llm-kv-cache/src/block_id.rs:11-41).
 uint64_t next_block_id();
 
-// Device scratch of one stream: split partials, merge descriptors, counters and
-// the fused projection's staging.  A call holds `mu` from planning through its
-// last launch, so two threads on one stream never interleave their use of it,
-// and a growth (which frees the old buffer) never happens under another call.
+// Device scratch of one stream: split partials, merge descriptors and the
+// fused projection's staging, plus the stream's own device error word (the
+// sticky flags the kernels of this stream's calls raise).  A call holds `mu`
+// from planning through its last launch, so two threads on one stream never
+// interleave their use of the scratch, and a growth (which frees the old
+// buffer) never happens under another call.  `err` is allocated with the slot
+// and lives as long as it: calls that need no scratch (writes, appends,
+// gathers) take it without the lock.
 struct StreamWorkspace {
   hipStream_t stream = nullptr;
   void *ptr = nullptr;
   size_t bytes = 0;
+  int32_t *err = nullptr;
   std::mutex mu;
 };
 
@@ -50,10 +53,11 @@ struct llh_ctx {
       shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0}, fused_append_calls{0};
   std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
 
-  // per-stream workspaces; ws_mu guards the list and ws_min_bytes
+  // per-stream workspaces; ws_mu guards the list, ws_min_bytes and retired_flags
   std::mutex ws_mu;
   std::vector<std::shared_ptr<llh::StreamWorkspace>> workspaces;
   size_t ws_min_bytes = 0;
+  int32_t retired_flags = 0;  // flags the error words of released slots held
 
   std::mutex err_mu;
   std::string last_error;
@@ -105,22 +109,46 @@ struct llh_ctx {
     return fail(LLH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
   }
 
-  // The workspace slot of stream s (created on first use).
+  // The workspace slot of stream s, created (with its zeroed error word) on
+  // first use; nullptr when the error word cannot be allocated.
   std::shared_ptr<llh::StreamWorkspace> slot(hipStream_t s) {
     std::lock_guard<std::mutex> g(ws_mu);
     for (auto &w : workspaces)
       if (w->stream == s) return w;
-    workspaces.push_back(std::make_shared<llh::StreamWorkspace>());
-    workspaces.back()->stream = s;
-    return workspaces.back();
+    auto w = std::make_shared<llh::StreamWorkspace>();
+    w->stream = s;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipMalloc(&w->err, sizeof(int32_t));
+    // zeroed on the slot's own stream, so it lands before the stream's first kernel
+    if (e == hipSuccess) e = hipMemsetAsync(w->err, 0, sizeof(int32_t), s);
+    if (e != hipSuccess) {
+      if (w->err) (void)hipFree(w->err);
+      return nullptr;
+    }
+    workspaces.push_back(w);
+    return w;
+  }
+  // The error word the kernels of a call on stream s raise their flags in: the
+  // stream's own, or the context's when it cannot be had -- also while s is
+  // being captured into a graph and has no slot yet (creating one allocates).
+  int32_t *err_word(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+      std::lock_guard<std::mutex> g(ws_mu);
+      for (auto &w : workspaces)
+        if (w->stream == s) return w->err;
+      return d_err;
+    }
+    auto w = slot(s);
+    return w ? w->err : d_err;
   }
   size_t min_ws() {
     std::lock_guard<std::mutex> g(ws_mu);
     return ws_min_bytes;
   }
-  // Grows a locked slot to at least `bytes` (plus the counter region, zeroed on
-  // every allocation).  The old buffer is freed once the slot's stream has
-  // drained, so no kernel still reads it.
+  // Grows a locked slot to at least `bytes` (zeroed on every allocation).  The
+  // old buffer is freed once the slot's stream has drained, so no kernel still
+  // reads it.
   int grow_locked(llh::StreamWorkspace &w, size_t bytes) {
     bytes = std::max(bytes, min_ws());
     if (w.ptr && bytes <= w.bytes) return LLH_OK;
@@ -133,7 +161,7 @@ struct llh_ctx {
       w.ptr = nullptr;
       w.bytes = 0;
     }
-    const size_t nb = llh::align_up(std::max(bytes, llh::kCounterBytes + llh::kAlign));
+    const size_t nb = llh::align_up(std::max(bytes, llh::kAlign));
     e = hipMalloc(&w.ptr, nb);
     if (e != hipSuccess) {
       w.ptr = nullptr;
@@ -156,9 +184,11 @@ struct WsLease {
   std::unique_lock<std::mutex> lock;
   int acquire(llh_ctx *ctx, hipStream_t s, size_t bytes) {
     w = ctx->slot(s);
+    if (!w) return ctx->fail(LLH_ERR_DEVICE, "stream error word allocation failed");
     lock = std::unique_lock<std::mutex>(w->mu);
     return ctx->grow_locked(*w, bytes);
   }
+  int32_t *err() const { return w->err; }
   char *base() const { return static_cast<char *>(w->ptr); }
 };
 
@@ -180,10 +210,11 @@ struct DecodePlan {
 };
 int plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
                 const void *d_out, float score_scale, DecodePlan *plan);
-// timed = false leaves out the kernel-timing events (no event is created or recorded);
-// k_new / v_new (bf16 pools, tuned kernels): fused append of each sequence's new token
+// err: the device error word the kernels raise flags in; timed = false leaves out
+// the kernel-timing events (no event is created or recorded); k_new / v_new
+// (tuned kernels): fused append of each sequence's new token
 int launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const DecodePlan &plan,
-                          const void *d_q, void *d_out, float score_scale, hipStream_t s, char *ws,
+                          const void *d_q, void *d_out, float score_scale, hipStream_t s, char *ws, int32_t *err,
                           bool timed = true, const uint16_t *k_new = nullptr, const uint16_t *v_new = nullptr);
 // Resolves this device's address of the no-allocation scratch (device current).
 int noalloc_init(int device);

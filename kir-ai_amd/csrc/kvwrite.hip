@@ -125,6 +125,20 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
         make_uint4(w[0], w[1], w[2], w[3]);
     return;
   }
+  // quantised blocks: a NaN or an infinity in the block's rows is NonFiniteValue
+  // in the reference (format.rs:713-716): flagged, and the block is left as it was
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t u[2] = {(&kw.x)[j], (&vw.x)[j]};
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+      bad = bad || (u[k] & 0x7f80u) == 0x7f80u || (u[k] & 0x7f800000u) == 0x7f800000u;
+  }
+  if (__syncthreads_or(bad)) {
+    if (tid == 0) atomicOr(a.err, kErrNonFinite);
+    return;
+  }
   __shared__ uint8_t lq[BT][Dh + 16];
   uint32_t codes[2][2];
   if (a.pool.format == kFp8) {
@@ -224,6 +238,18 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
     }
     return;
   }
+  {
+    // quantised blocks: a NaN or an infinity in the block's rows is flagged
+    // (NonFiniteValue, format.rs:713-716) and the block is left as it was
+    bool bad = false;
+    for (int e = threadIdx.x; e < n; e += blockDim.x)
+      bad = bad || !isfinite(bf16_to_f32(a.k[src_idx(e / Dh, e % Dh)])) ||
+            !isfinite(bf16_to_f32(a.v[src_idx(e / Dh, e % Dh)]));
+    if (__syncthreads_or(bad)) {
+      if (threadIdx.x == 0) atomicOr(a.err, kErrNonFinite);
+      return;
+    }
+  }
   if (a.pool.format == kInt8) {
     // one wavefront per token row of this head
     const int lane = threadIdx.x & 63;
@@ -298,6 +324,17 @@ __global__ __launch_bounds__(256) void write_blocks_row_kernel(const WriteBlocks
   }
   const int vl = Hkv * Dh;
   for (int t = wave; t < BT; t += 4) {
+    // a row holding a NaN or an infinity is NonFiniteValue in the reference
+    // (format.rs:713-716): flagged, and the token's rows are left as they were
+    bool finite = true;
+    for (int tensor = 0; tensor < 2; tensor++) {
+      const uint16_t *src = (tensor ? a.v : a.k) + ((size_t)i * BT + t) * vl;
+      for (int e = lane; e < vl; e += 64) finite = finite && isfinite(bf16_to_f32(src[e]));
+    }
+    if (__any(!finite)) {
+      if (lane == 0) atomicOr(a.err, kErrNonFinite);
+      continue;
+    }
     for (int tensor = 0; tensor < 2; tensor++) {
       const uint16_t *src = (tensor ? a.v : a.k) + ((size_t)i * BT + t) * vl;  // [h][d] of token t
       float mx = 0.0f;
@@ -370,14 +407,24 @@ __global__ __launch_bounds__(64) void append_row_kernel(const AppendArgs a) {
     return;
   }
   const int vl = Hkv * Dh;
-  for (int tensor = 0; tensor < 2; tensor++) {
+  auto ld_row = [&](int tensor, int e) -> float {
     const ST *src = reinterpret_cast<const ST *>(tensor ? a.v : a.k) + (size_t)i * vl;
-    auto ld = [&](int e) -> float {
-      if constexpr (sizeof(ST) == 4)
-        return src[e];
-      else
-        return bf16_to_f32(src[e]);
-    };
+    if constexpr (sizeof(ST) == 4)
+      return src[e];
+    else
+      return bf16_to_f32(src[e]);
+  };
+  // a row holding a NaN or an infinity is NonFiniteValue in the reference
+  // (format.rs:713-716): flagged, and the slot is left as it was
+  bool finite = true;
+  for (int tensor = 0; tensor < 2; tensor++)
+    for (int e = lane; e < vl; e += 64) finite = finite && isfinite(ld_row(tensor, e));
+  if (__any(!finite)) {
+    if (lane == 0) atomicOr(a.err, kErrNonFinite);
+    return;
+  }
+  for (int tensor = 0; tensor < 2; tensor++) {
+    auto ld = [&](int e) -> float { return ld_row(tensor, e); };
     float mx = 0.0f;
     for (int e = lane; e < vl; e += 64) mx = fmaxf(mx, fabsf(ld(e)));
     mx = wave_max(mx);
@@ -511,22 +558,20 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     }
     return;
   }
-  // int8 with per (token, head) fp16 scale
+  // int8 with per (token, head) fp16 scale; a NaN or an infinity in either row
+  // is flagged and nothing of the token is written
   int8_t *kd = reinterpret_cast<int8_t *>(a.k_dst);
   int8_t *vd = reinterpret_cast<int8_t *>(a.v_dst);
+  bool finite = true;
+  for_elems([&](int, float k, float v) __attribute__((always_inline)) { finite = finite && isfinite(k) && isfinite(v); });
+  if (__any(!finite)) {
+    if (lane == 0) atomicOr(a.err, kErrNonFinite);
+    return;
+  }
   for (int tensor = 0; tensor < 2; tensor++) {
     float mx = 0.0f;
-    bool finite = true;
-    for_elems([&](int, float k, float v) __attribute__((always_inline)) {
-      const float x = tensor ? v : k;
-      finite = finite && isfinite(x);
-      mx = fmaxf(mx, fabsf(x));
-    });
+    for_elems([&](int, float k, float v) __attribute__((always_inline)) { mx = fmaxf(mx, fabsf(tensor ? v : k)); });
     mx = wave_max(mx);
-    if (__any(!finite)) {
-      if (lane == 0) atomicOr(a.err, kErrNonFinite);
-      return;
-    }
     const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
     const float s = (float)s16;
     for_elems([&](int d, float k, float v) __attribute__((always_inline)) {

@@ -63,6 +63,14 @@ extern "C" int llh_paged_decode_noalloc(llh_ctx *ctx, const llh_kv_pool *pool, c
                                            std::to_string(kScratchBytes) + " (use llh_paged_decode)");
   char *base = static_cast<char *>(scratch_of(ctx->device));
   if (!base) return ctx->fail(LLH_ERR_DEVICE, "no-allocation scratch not resolved for this device");
+  // flags go to the stream's own error word if it has one (finding it allocates
+  // nothing), else to the context's
+  int32_t *err = ctx->d_err;
+  {
+    std::lock_guard<std::mutex> g(ctx->ws_mu);
+    for (auto &w : ctx->workspaces)
+      if (w->stream == static_cast<hipStream_t>(stream) && w->err) err = w->err;
+  }
   return llh::launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, static_cast<hipStream_t>(stream),
-                                    base, /*timed=*/false);
+                                    base, err, /*timed=*/false);
 }

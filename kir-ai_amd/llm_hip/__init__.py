@@ -132,6 +132,8 @@ class Metrics(ctypes.Structure):
         ("trait_tuned_calls", ctypes.c_uint64),
         ("generic_prefill_calls", ctypes.c_uint64),
         ("fused_append_calls", ctypes.c_uint64),
+        ("stream_slots", ctypes.c_uint64),
+        ("workspace_bytes", ctypes.c_uint64),
     ]
 
 
@@ -148,6 +150,22 @@ class LayerCacheState(ctypes.Structure):
         ("block_count", ctypes.c_uint64),
         ("format", ctypes.c_int32),
         ("block_tokens", ctypes.c_int32),
+    ]
+
+
+class LayerCacheRows(ctypes.Structure):
+    _fields_ = [
+        ("max_tokens", ctypes.c_uint64),
+        ("kv_heads", ctypes.c_uint64),
+        ("head_dim", ctypes.c_uint64),
+        ("format", ctypes.c_int32),
+        ("revision", ctypes.c_uint64),
+        ("token_count", ctypes.c_uint64),
+        ("tokens_seen", ctypes.c_uint64),
+        ("window_start", ctypes.c_uint64),
+        ("h_keys", ctypes.POINTER(ctypes.c_float)),
+        ("h_values", ctypes.POINTER(ctypes.c_float)),
+        ("keys_len", ctypes.c_size_t),
     ]
 
 
@@ -279,6 +297,7 @@ SIGNATURES = {
     "llh_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "llh_ctx_metrics": (ctypes.c_int, [_P, ctypes.POINTER(Metrics)]),
     "llh_ctx_device_errors": (ctypes.c_int, [_P, ctypes.POINTER(_I32), _I32]),
+    "llh_ctx_stream_device_errors": (ctypes.c_int, [_P, _P, ctypes.POINTER(_I32), _I32]),
     "llh_ctx_set_kernel_timing": (ctypes.c_int, [_P, _I32]),
     "llh_ctx_kernel_time": (ctypes.c_int, [_P, _I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
                                            _I32]),
@@ -298,6 +317,7 @@ SIGNATURES = {
     "llh_debug_decode_fp8": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
     "llh_layer_cache_create": (ctypes.c_int, [_P, _SZ, _SZ, _SZ, _I32, ctypes.POINTER(_P)]),
     "llh_layer_cache_destroy": (ctypes.c_int, [_P]),
+    "llh_layer_cache_create_from_rows": (ctypes.c_int, [_P, ctypes.POINTER(LayerCacheRows), ctypes.POINTER(_P)]),
     "llh_layer_cache_clone": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
     "llh_layer_cache_clear": (ctypes.c_int, [_P]),
     "llh_layer_cache_get_state": (ctypes.c_int, [_P, ctypes.POINTER(LayerCacheState)]),
@@ -456,8 +476,16 @@ class Context:
         return {f: getattr(m, f) for f, _ in Metrics._fields_}
 
     def device_errors(self, reset: bool = True) -> int:
+        """OR of every stream's sticky device flags (waits for the device)."""
         flags = _I32()
         self.check(self.lib.llh_ctx_device_errors(self.handle, ctypes.byref(flags), 1 if reset else 0))
+        return flags.value
+
+    def stream_device_errors(self, stream=None, reset: bool = True) -> int:
+        """The flags raised by the calls made on one stream (waits for that stream only)."""
+        flags = _I32()
+        self.check(self.lib.llh_ctx_stream_device_errors(self.handle, _stream(stream), ctypes.byref(flags),
+                                                         1 if reset else 0))
         return flags.value
 
     def set_kernel_timing(self, enable: bool) -> None:
@@ -688,6 +716,26 @@ class LayerKvCache:
         h = _P()
         ctx.check(ctx.lib.llh_layer_cache_create(ctx.handle, max_tokens, key_value_heads, head_dim, fmt,
                                                  ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def from_rows(cls, ctx: Context, max_tokens: int, key_value_heads: int, head_dim: int, keys, values,
+                  revision: int = 0, tokens_seen: Optional[int] = None, window_start: int = 0,
+                  fmt: int = KV_BF16) -> "LayerKvCache":
+        """A cache that already holds rows: LayerKvCache::from_snapshot (window_start 0) and
+        from_prefix_cache_state (layer.rs:467-507, 544-581).  keys / values: the logical rows
+        (keys() / values()), token_count x (key_value_heads * head_dim) f32."""
+        k = np.ascontiguousarray(keys, dtype=np.float32).ravel()
+        v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        vl = key_value_heads * head_dim
+        n = k.size // vl if vl else 0
+        r = LayerCacheRows(max_tokens=max_tokens, kv_heads=key_value_heads, head_dim=head_dim, format=fmt,
+                           revision=revision, token_count=n, tokens_seen=n if tokens_seen is None else tokens_seen,
+                           window_start=window_start, h_keys=_f32_ptr(k), h_values=_f32_ptr(v), keys_len=k.size)
+        if v.size != k.size:
+            raise LlhError(ERR_INVALID_SHAPE, "key and value lengths differ")
+        h = _P()
+        ctx.check(ctx.lib.llh_layer_cache_create_from_rows(ctx.handle, ctypes.byref(r), ctypes.byref(h)))
         return cls(ctx, h)
 
     def close(self) -> None:

@@ -44,6 +44,7 @@ STRUCTS = {
     "llh_kv_pool_info": llm_hip.PoolInfo,
     "llh_metrics": llm_hip.Metrics,
     "llh_layer_cache_state": llm_hip.LayerCacheState,
+    "llh_layer_cache_rows": llm_hip.LayerCacheRows,
     "llh_block_run": llm_hip.BlockRun,
     "llh_block_pool_counts": llm_hip.BlockPoolCounts,
     "llh_paged_kv_metrics": llm_hip.PagedKvMetrics,

@@ -141,3 +141,65 @@ def test_decode_append_quantized_pools_equal_two_calls(ctx, fmt):
     assert_pools_equal(batch, raw_f, raw_t)
     assert np.array_equal(fused, two)
     assert_parity(fused, ref, what=f"fmt {fmt}")
+
+
+def test_fp8_append_over_a_window_ring_needs_one_block_more(ctx):
+    """An fp8 block keeps one scale per (block, head) that a token at offset 0 restarts: in a
+    window ring of exactly W/16 blocks the new token's block still holds live tokens of the
+    previous pass round the ring, so the call is refused; with W/16 + 1 blocks the step runs,
+    the appended block equals the oracle's per-token rule (oracle.append_fp8_token) bit for
+    bit and the output meets the bar of the oracle run on the pool."""
+    import torch
+
+    W, Hq, Hkv = 64, 16, 8
+    lens = np.array([1000, 77, 129, 97], np.int32)  # new tokens at offsets 7, 12, 0, 0
+    B = lens.size
+    for nb, ok in ((W // BT, False), (W // BT + 1, True)):
+        n_pool = 23  # prime: the entries i * 5 + 1 (mod 23) of the B * nb <= 20 table slots are distinct
+        tables = ((np.arange(B * nb, dtype=np.int32) * 5 + 1) % n_pool).reshape(B, nb)
+        assert np.unique(tables).size == B * nb
+        pool = ctx.pool(llm_hip.KV_FP8_E4M3, BT, Hkv, D, n_pool)
+        slots, ks, vs = [], [], []
+        for b in range(B):
+            for p in range(max(0, int(lens[b]) - W), int(lens[b]) - 1):  # the window before the new token
+                slots.append(int(tables[b, (p // BT) % nb]) * BT + p % BT)
+                ks.append(oracle.normal_bf16(600 + b, Hkv * D, p * Hkv * D).reshape(Hkv, D))
+                vs.append(oracle.normal_bf16(700 + b, Hkv * D, p * Hkv * D).reshape(Hkv, D))
+        ctx.append(pool, to_dev(np.array(slots, np.int64)), to_dev(np.stack(ks)), to_dev(np.stack(vs)))
+        torch.cuda.synchronize()
+        before = pool.raw()
+        kn = oracle.normal_bf16(801, B * Hkv * D).reshape(B, Hkv, D)
+        vn = oracle.normal_bf16(802, B * Hkv * D).reshape(B, Hkv, D)
+        q = oracle.normal_bf16(803, B * Hq * D)
+        out = torch.zeros(B * Hq * D, dtype=torch.int16, device="cuda")
+        desc = ctx.decode_desc(to_dev(lens), to_dev(tables), Hq, int(lens.max()), W)
+        if not ok:
+            with pytest.raises(llm_hip.LlhError) as e:
+                ctx.paged_decode_append(pool, desc, to_dev(kn), to_dev(vn), to_dev(q), out, 0.09)
+            assert e.value.status == llm_hip.ERR_INVALID_SHAPE
+            continue
+        ctx.paged_decode_append(pool, desc, to_dev(kn), to_dev(vn), to_dev(q), out, 0.09)
+        torch.cuda.synchronize()
+        assert ctx.device_errors() == 0, ctx.last_error()
+        after = pool.raw()
+        kc0, vc0 = before["k"].reshape(n_pool, Hkv, BT, D), before["v"].reshape(n_pool, Hkv, D, BT)
+        ks0 = before["k_scales"].view(np.float32).reshape(n_pool, Hkv)
+        vs0 = before["v_scales"].view(np.float32).reshape(n_pool, Hkv)
+        kc1, vc1 = after["k"].reshape(n_pool, Hkv, BT, D), after["v"].reshape(n_pool, Hkv, D, BT)
+        ks1 = after["k_scales"].view(np.float32).reshape(n_pool, Hkv)
+        vs1 = after["v_scales"].view(np.float32).reshape(n_pool, Hkv)
+        for b in range(B):
+            p = int(lens[b]) - 1
+            blk, off = int(tables[b, (p // BT) % nb]), p % BT
+            for h in range(Hkv):
+                for src, c0, s0, c1, s1 in ((kn, kc0[blk, h], ks0[blk, h], kc1[blk, h], ks1[blk, h]),
+                                            (vn, vc0[blk, h].T, vs0[blk, h], vc1[blk, h].T, vs1[blk, h])):
+                    codes = np.ascontiguousarray(c0).copy()
+                    st, s = oracle.append_fp8_token(codes, float(s0), off, oracle.bf16_to_f32(src[b, h]))
+                    assert st == oracle.OK
+                    assert np.float32(s) == s1, (b, h)
+                    assert np.array_equal(codes[:off + 1], c1[:off + 1]), (b, h)
+        opool = oracle.Pool.from_raw(llm_hip.KV_FP8_E4M3, BT, Hkv, D, n_pool, after)
+        st, ref = opool.decode(Hq, lens, tables, W, q, 0.09)
+        assert st == oracle.OK
+        assert_parity(from_dev_bf16(out), ref, what=f"fp8 window ring of {nb} blocks")

@@ -365,3 +365,76 @@ def test_fp8_append_one_call_equals_token_by_token_calls(ctx):
     for key in ("k_scales", "v_scales"):
         sa, sb = a[key].view(np.float32).reshape(12, Hkv), b[key].view(np.float32).reshape(12, Hkv)
         assert np.array_equal(sa[used], sb[used]), key
+
+
+@pytest.mark.parametrize("src_f32", [0, 1])
+def test_int8_row_append_flags_non_finite_rows(ctx, src_f32):
+    """A NaN or an infinity in a row appended to an LLH_KV_INT8_ROW pool is the reference's
+    NonFiniteValue (format.rs:713-716): the flag is raised and the slot keeps what it held;
+    finite rows of the same call are written."""
+    import torch
+
+    Hkv = 2
+    pool = ctx.pool(llm_hip.KV_INT8_ROW, BT, Hkv, D, 4)
+    before = pool.raw()
+    rows = oracle.normal_bf16(91, 3 * Hkv * D).reshape(3, Hkv, D)
+    rf = oracle.bf16_to_f32(rows.ravel()).reshape(3, Hkv, D).copy()
+    rf[1, 1, 7] = np.nan if src_f32 else np.inf
+    k = rf if src_f32 else oracle.f32_to_bf16(rf.ravel()).reshape(3, Hkv, D)
+    slots = np.array([0 * BT + 3, 1 * BT + 4, 2 * BT + 5], np.int64)
+    (ctx.append_f32 if src_f32 else ctx.append)(pool, to_dev(slots), to_dev(k), to_dev(k))
+    torch.cuda.synchronize()
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_NON_FINITE
+    after = pool.raw()
+    kc0, kc1 = before["k"].reshape(4, Hkv, BT, D), after["k"].reshape(4, Hkv, BT, D)
+    assert np.array_equal(kc1[1, :, 4], kc0[1, :, 4])  # the non-finite row's slot untouched
+    assert np.array_equal(after["k_scales"].view(np.float32).reshape(4, BT)[1, 4], 0.0)
+    st, codes, scales = oracle.quantize_int8_rows(oracle.bf16_to_f32(rows[0].ravel()), Hkv * D)
+    assert st == oracle.OK and np.array_equal(kc1[0, :, 3].view(np.int8).ravel(), codes)
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_INT8_ROW])
+@pytest.mark.parametrize("misalign", [False, True])
+def test_quantised_block_write_flags_non_finite_rows(ctx, fmt, misalign):
+    """Whole-block writes into quantised pools (the head_dim-128 vector kernel and, with the
+    source 2 bytes off alignment, the element-wise kernels): a NaN or an infinity raises the
+    non-finite flag, and the (block, head) holding it -- the token row, for the reference's
+    row layout -- is left as it was; the other blocks of the call are written as the oracle
+    quantises them."""
+    import torch
+
+    Hkv, n = 2, 3
+    pool = ctx.pool(fmt, BT, Hkv, D, 4)
+    before = pool.raw()
+    k = oracle.normal_bf16(95, n * BT * Hkv * D).reshape(n, BT, Hkv, D).copy()
+    v = oracle.normal_bf16(96, n * BT * Hkv * D).reshape(n, BT, Hkv, D).copy()
+    v[1, 9, 1, 100] = 0x7F80  # +inf in block 1's values
+    dk, dv = to_dev(k), to_dev(v)
+    if misalign:
+        def shifted(t):
+            flat = torch.zeros(t.numel() + 1, dtype=torch.int16, device="cuda")
+            flat[1:].copy_(t.view(-1))
+            return flat[1:]
+        dk, dv = shifted(dk), shifted(dv)
+    ctx.write_blocks(pool, to_dev(np.array([0, 2, 3], np.int32)), dk, dv)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() & llm_hip.ERR_FLAG_NON_FINITE
+    after = pool.raw()
+    if fmt == llm_hip.KV_INT8_ROW:
+        # the reference's row layout quantises per token row over all heads: only the
+        # non-finite token (9 of pool block 2) is skipped
+        vc0, vc1 = before["v"].reshape(4, Hkv, D, BT), after["v"].reshape(4, Hkv, D, BT)
+        assert np.array_equal(vc1[2, :, :, 9], vc0[2, :, :, 9])
+        assert after["v_scales"].view(np.float32).reshape(4, BT)[2, 9] == 0.0
+    else:
+        # per (block, head) workgroups: head 1 of pool block 2 (codes and scales) is untouched
+        for key in after:
+            assert np.array_equal(after[key].reshape(4, Hkv, -1)[2, 1], before[key].reshape(4, Hkv, -1)[2, 1]), key
+    # block 0 of the call (pool block 0) is written as the oracle quantises it
+    opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, 4, after)
+    st, kf, _ = opool.gather_f32(np.array([0], np.int32), 0, BT)
+    assert st == oracle.OK
+    x = oracle.bf16_to_f32(k[0].ravel()).reshape(BT, Hkv, D)
+    err = np.abs(kf.reshape(BT, Hkv, D) - x)
+    # one e4m3 rounding (3 mantissa bits) or half an int8 step of the row's absmax / 127
+    assert np.all(err <= 0.0625 * np.abs(x) + 0.03), err.max()
