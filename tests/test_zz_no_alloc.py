@@ -80,13 +80,12 @@ def test_noalloc_decode_matches_paged_decode_on_two_calls(ctx):
 
 
 def test_noalloc_decode_rejects_steps_beyond_its_scratch(ctx, opts):
-    """A stream step with G = 8 on a 1024-workgroup grid plans 2 x 8 partial rows of 520 bytes
-    per wavefront (34 MB), twice the array's partial part: the call is refused before any
-    launch; llh_paged_decode takes the same step."""
+    """A split-K step of 32 sequences of 2048-4096 tokens with 64 query heads plans 33
+    partial rows of 520 bytes per (sequence, head) (35 MB), twice the array: the call is
+    refused before any launch; llh_paged_decode takes the same step."""
     import torch
 
-    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
-    opts(llm_hip.OPT_DECODE_STREAM_WGS, 1024)
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
     lens = workloads.uniform_lengths(32, 2048, 4096, 902)
     batch, pool, q, keep, desc = _case(ctx, lens, 64, 8, 902)
     out = torch.zeros(batch.seq_lens.size * 64 * D, dtype=torch.int16, device="cuda")
