@@ -41,6 +41,7 @@ METRIC = "paged decode attn: HBM GB/s (% of peak) + µs/step at B=32; prefill MF
 D = 128
 BT = 16
 SETTLE = {"s": 0.15}  # untimed settle before each timed run (--settle-ms)
+HOST = {"us": None}   # host time per call of the last time_steps run (issue loop wall time / steps)
 
 
 def log(msg: str) -> None:
@@ -86,6 +87,7 @@ class DecodeWorkload:
         if ctx.device_errors() != 0:
             raise RuntimeError("device error flags set while building the workload")
         self.llm_hip = llm_hip
+        self._bound = {}
 
     def attended_rows(self):
         import numpy as np
@@ -97,8 +99,16 @@ class DecodeWorkload:
     def algorithmic_bytes(self) -> int:
         return decode_bytes(self.batch.seq_lens, self.Hq, self.Hkv, self.fmt, self.window)
 
+    def bound(self, key, name, *args):
+        """The C call `name` with its arguments converted once (Context.bind), per stream."""
+        f = self._bound.get(key)
+        if f is None:
+            f = self._bound[key] = self.ctx.bind(name, *args)
+        return f
+
     def step(self, stream):
-        self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
+        self.bound(("decode", stream), "llh_paged_decode", self.pool, self.desc, self.q, self.out, self.scale,
+                   stream)()
 
     def prepare_append(self):
         """The new token of every sequence (position len-1): its pool slot and N(0,1) K/V rows."""
@@ -116,13 +126,14 @@ class DecodeWorkload:
 
     def append_step(self, stream):
         """kir-ai's decode step order (native_attention.rs:307-329): append the new token, then attend."""
-        self.ctx.append(self.pool, self.d_slots, self.k_new, self.v_new, stream=stream)
-        self.ctx.paged_decode(self.pool, self.desc, self.q, self.out, self.scale, stream=stream)
+        self.bound(("append", stream), "llh_kv_append", self.pool, self.d_slots, self.k_new, self.v_new,
+                   self.d_slots.numel(), stream)()
+        self.step(stream)
 
     def fused_step(self, stream):
         """The same step as append_step in one call (llh_paged_decode_append)."""
-        self.ctx.paged_decode_append(self.pool, self.desc, self.k_new, self.v_new, self.q, self.out, self.scale,
-                                     stream=stream)
+        self.bound(("fused", stream), "llh_paged_decode_append", self.pool, self.desc, self.k_new, self.v_new, self.q,
+                   self.out, self.scale, stream)()
 
     def append_bytes(self) -> int:
         """Algorithmic bytes of the append: the new rows read (bf16) and written (pool format), slots."""
@@ -171,8 +182,10 @@ def time_steps(fn, steps: int, warmup: int, kernel_timing=None):
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
+    t0 = time.perf_counter()
     for _ in range(steps):
         fn(stream)
+    HOST["us"] = round((time.perf_counter() - t0) / steps * 1e6, 2)  # the host's issue cost per call
     e1.record(stream)
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
@@ -181,6 +194,42 @@ def time_steps(fn, steps: int, warmup: int, kernel_timing=None):
     kernel_timing[0].set_kernel_timing(False)
     total, n = kernel_timing[0].kernel_time(kernel_timing[1], reset=True)
     return step_ms, total / max(n, 1)
+
+
+def time_graph(fns, replays: int, min_calls: int = 128):
+    """Mean ms per step of a HIP graph holding the calls fn(stream) of fns, in order,
+    repeated until it holds at least min_calls of them (a graph launch costs about as much
+    as ten small kernels, so short graphs would time the launch), replayed `replays` times
+    after a settle phase: the GPU's own time per step, without the host's per-call launch
+    cost."""
+    import torch
+
+    fns = list(fns) * max(1, -(-min_calls // len(fns)))
+    replays = max(3, replays // len(fns) + 1)
+    s = torch.cuda.Stream()  # default priority
+    for f in fns:  # eager once, outside the capture
+        f(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for f in fns:
+            f(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < SETTLE["s"]:
+            g.replay()
+            s.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(replays):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (replays * len(fns))
+    del g
+    return ms
 
 
 def cpu_baseline_decode(w: DecodeWorkload, budget_s: float):
@@ -359,6 +408,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     (32 rows into 16-token blocks; bf16, and int8 quantised on write) and the o_proj of
     Qwen3-0.6B (W bf16 1024 x 2048, 32 attention outputs), alone and fused behind the decode.
     W rotates over copies totalling > 2 x 256 MB so each step reads it from HBM."""
+    import numpy as np
     import torch
     import llm_hip
     from llm_hip import workloads
@@ -381,7 +431,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: nblk * H * 4 * 2}.get(fmt, 0)
         nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + scales
         out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
-                    "us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
+                    "us_per_step": round(ms * 1e3, 2), "host_us_per_call": HOST["us"], "bytes_per_step": nbytes,
                     "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_d128_kernel"})
         del pool
@@ -392,12 +442,19 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         k = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
         v = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.append(pool, slots, k, v, stream=s), steps, warmup)
+        host_us = HOST["us"]
+        # the same append replayed from a HIP graph (the GPU's own time per call); appending the
+        # same rows again leaves the pool as it was, which the replay must reproduce
+        before = pool.raw()
+        gms = time_graph([lambda s: ctx.append(pool, slots, k, v, stream=s)], steps)
+        if any(not np.array_equal(a, b) for a, b in zip(before.values(), pool.raw().values())):
+            raise RuntimeError("append: graph replay changed the pool")
         esz = 2 if fmt == llm_hip.KV_BF16 else 1
         # fp8: the block's scale is read and written per token (an earlier row re-encode is not counted)
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: T * H * 4 * 2 * 2}.get(fmt, 0)
         nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + T * 8 + scales
         out.append({"config": f"KV append C2 batch ({T} tokens, Hkv{H}, {nm})", "us_per_step": round(ms * 1e3, 2),
-                    "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "host_us_per_call": host_us, "graph_us_per_step": round(gms * 1e3, 2), "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "kernel": "append_kernel (launch-bound at this size)"})
         if ctx.device_errors() != 0:
@@ -418,6 +475,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     ms = time_steps(proj, steps, warmup)
     nbytes = wbytes + B * cols * 2 + B * rows * 4
     out.append({"config": f"o_proj matvec W {rows}x{cols} bf16, {B} rows", "us_per_step": round(ms * 1e3, 2),
+                "host_us_per_call": HOST["us"],
                 "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                 "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "w_copies": len(ws),
                 "kernel": "matvec_bf16_kernel (MFMA)"})
@@ -502,13 +560,16 @@ LLC_BYTES = 256 << 20  # MI355X Infinity Cache (memory-side last-level cache)
 
 
 def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10,
-                   append=False, fused=False):
+                   append=False, fused=False, graph=False):
     """Mean step time over `steps` decode steps.  Steps rotate over enough independent
     copies of the workload (same lengths, own pool, own block permutation and data) that
     the bytes read between two visits of one copy exceed the 256 MB Infinity Cache: every
     step reads its K/V from HBM, not from cache.  append=True times kir-ai's whole decode
     step instead: the new token's K/V append, then attention over the cache holding it.  fused=True
-    times the same step through llh_paged_decode_append (one call)."""
+    times the same step through llh_paged_decode_append (one call).  graph=True also times
+    the step replayed from a HIP graph (llh_paged_decode_noalloc, one call per copy): the
+    GPU's own time per step, free of the host's per-call launch cost, which sets the pace of
+    small steps issued one call at a time (host_us_per_call)."""
     first = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free)
     nbytes = first.algorithmic_bytes() + (first.append_bytes() if append or fused else 0)
     copies = [first]
@@ -532,6 +593,7 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     # step time over all timed steps, then the decode kernel alone (library-recorded events)
     streamed0, calls0 = ctx.metrics()["stream_decode_calls"], state["i"]
     ms = time_steps(step, steps, warmup)
+    host_us = HOST["us"]
     streamed, calls = ctx.metrics()["stream_decode_calls"] - streamed0, state["i"] - calls0
     _, kms = time_steps(step, steps, 0, kernel_timing=(ctx, "decode"))
     if ctx.device_errors() != 0:
@@ -540,6 +602,24 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     # the event pair around the main kernel also spans its dispatch; a figure above the step
     # time is not a kernel duration and is not reported (rocprof's trace gives the duration)
     kernel_ok = kms <= ms
+    extra = {}
+    if graph:
+        import torch
+
+        def noalloc(c):
+            return lambda s: ctx.paged_decode_noalloc(c.pool, c.desc, c.q, c.out, c.scale, stream=s)
+
+        eager = []
+        for c in copies:
+            c.step(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        eager = [c.out.clone() for c in copies]
+        gms = time_graph([noalloc(c) for c in copies], steps)
+        same = all(torch.equal(c.out, e) for c, e in zip(copies, eager))
+        if not same or ctx.device_errors() != 0:
+            raise RuntimeError(f"{name}: graph replay output differs from the eager call")
+        extra = {"graph_us_per_step": round(gms * 1e3, 2),
+                 "graph_hbm_frac": round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return first, {
         "config": name,
         "us_per_step": round(ms * 1e3, 2),
@@ -551,6 +631,8 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         "bytes_per_step": nbytes,
         "rotating_copies": len(copies),
         "kernel": "paged_decode_stream_kernel" if streamed == calls else "paged_decode_kernel (split-K)",
+        "host_us_per_call": host_us,
+        **extra,
     }
 
 
@@ -746,7 +828,7 @@ def run_sections(ctx, args, lens, sel) -> list:
     sec_steps, sec_warm = max(100, args.steps), max(10, args.warmup)
     if sel("c1"):
         w1, r = measure_decode(ctx, "C1 B=1 L=512", [512], 16, 8, llm_hip.KV_BF16, sec_steps, sec_warm,
-                               seed=workloads.SEED_BASE, free=0.0)
+                               seed=workloads.SEED_BASE, free=0.0, graph=True)
         if not args.no_cpu:
             r["cpu"] = cpu_decode_times(w1, 1.0)
         del w1
@@ -768,7 +850,8 @@ def run_sections(ctx, args, lens, sel) -> list:
     if sel("c4"):
         L, W = 32768, 4096
         _, r = measure_decode(ctx, "C4 decode 4x32768 W=4096", [L] * 4, 16, 8, llm_hip.KV_BF16, sec_steps,
-                              sec_warm, window=W, resident_from=[(L - W) // BT] * 4, seed=workloads.SEED_BASE + 3)
+                              sec_warm, window=W, resident_from=[(L - W) // BT] * 4, seed=workloads.SEED_BASE + 3,
+                              graph=True)
         secondary.append(r)
         log(f"C4 decode: {r}")
     for fmt, nm in ((llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
@@ -798,6 +881,7 @@ def run_sections(ctx, args, lens, sel) -> list:
             continue
         step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res, fmt)
         pms = time_steps(step, sec_steps, sec_warm)
+        host_us = HOST["us"]
         _, pkms = time_steps(step, sec_steps, 0, kernel_timing=(ctx, "prefill"))
         if ctx.device_errors() != 0:
             raise RuntimeError(f"{name}: device error flags set")
@@ -805,7 +889,7 @@ def run_sections(ctx, args, lens, sel) -> list:
         r = {"config": name, "us_per_step": round(pms * 1e3, 2),
              "kernel_us": round(pkms * 1e3, 2) if pkms <= pms else None, "tflops": round(tf, 1),
              "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
-             "flops_per_step": flops}
+             "flops_per_step": flops, "host_us_per_call": host_us}
         if not args.no_cpu and fmt == llm_hip.KV_BF16:
             r["cpu"] = cpu_prefill_times(keep, B, prefix, chunk, Hq, Hkv, window, 16, 1.0)
         secondary.append(r)
@@ -867,7 +951,7 @@ def main() -> int:
     # ---- headline: C2 batched paged decode ----
     log(f"C2 decode: B=32 sum(L)={int(lens.sum())}")
     w, c2 = measure_decode(ctx, "C2", lens, 16, 8, llm_hip.KV_BF16, args.steps, args.warmup,
-                           seed=workloads.SEED_BASE + 1)
+                           seed=workloads.SEED_BASE + 1, graph=True)
     ms = c2["us_per_step"] / 1e3
     value = c2["hbm_gbs"]
     log(f"C2: {c2['us_per_step']} us/step, {value} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of 8 TB/s); "
@@ -913,6 +997,8 @@ def main() -> int:
             "sum_context_tokens": int(lens.sum()),
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
             "us_per_step": c2["us_per_step"],
+            "host_us_per_call": c2["host_us_per_call"],
+            "graph_us_per_step": c2["graph_us_per_step"],
             "tokens_per_s": c2["tokens_per_s"],
             "bytes_per_step": c2["bytes_per_step"],
             "parallelism": "single GPU",

@@ -564,6 +564,37 @@ class Context:
             )
         )
 
+    def bind(self, name: str, *args):
+        """A zero-argument call of the C entry point `name` with the context handle and the
+        given arguments converted to ctypes values once (device tensors become their
+        pointers, DecodeDesc / PrefillDesc are passed by reference, streams by handle), for
+        loops that issue the same call many times: the per-call Python work is one C call and
+        the status check.  The tensors and descriptors must outlive the returned call."""
+        fn = getattr(self.lib, name)
+        conv = [self.handle]
+        for a in args:
+            if isinstance(a, (DecodeDesc, PrefillDesc)):
+                conv.append(ctypes.byref(a))
+            elif isinstance(a, (KvPool, LayerKvCache)):
+                conv.append(a.handle)
+            elif isinstance(a, float):
+                conv.append(ctypes.c_float(a))
+            elif hasattr(a, "data_ptr"):
+                conv.append(_P(a.data_ptr()))
+            elif hasattr(a, "cuda_stream"):
+                conv.append(_P(a.cuda_stream))
+            else:
+                conv.append(a)
+        conv = tuple(conv)
+        keep = args
+
+        def call():
+            st = fn(*conv)
+            if st < 0:
+                raise LlhError(st, self.lib.llh_ctx_last_error(self.handle).decode() + f" ({len(keep)} args)")
+
+        return call
+
     def paged_decode_append(self, pool: "KvPool", desc: DecodeDesc, k_new, v_new, q, out, score_scale: float,
                             stream=None) -> None:
         """llh_paged_decode_append: append each sequence's new token (position len - 1), then attend."""
