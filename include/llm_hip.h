@@ -249,6 +249,10 @@ typedef struct llh_decode_desc {
   int32_t total_tokens_hint;  /* host-known sum of attended tokens (sizes split-K); 0 = unknown */
   const int32_t *d_seq_lens;     /* [num_seqs] tokens incl. the new one (appended first, native_attention.rs:307-309) */
   const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] pool block indices */
+  /* NULL, or the attention output gate of Qwen3.5 / 3.6 (attn_output_gate), bf16
+   * [num_seqs][num_q_heads][head_dim]: out = attention * sigmoid(gate) element-wise, in f32
+   * before the output's bf16 rounding (apply_attention_gate, native_attention.rs:765-781). */
+  const void *d_gate;
 } llh_decode_desc;
 
 /* One decode step: out[b][h] = softmax(scale * q[b][h] . K^T) V over the
@@ -300,6 +304,8 @@ typedef struct llh_prefill_desc {
   const int32_t *d_chunk_starts; /* [num_seqs + 1] */
   const int32_t *d_context_lens; /* [num_seqs] */
   const int32_t *d_block_tables; /* [num_seqs][max_blocks_per_seq] */
+  const void *d_gate;            /* NULL, or bf16 [total_q_rows][num_q_heads][head_dim]: out = attention *
+                                    sigmoid(gate), as llh_decode_desc.d_gate */
 } llh_prefill_desc;
 
 /* d_q, d_out: [total_q_rows][Hq][head_dim] bf16 (2-byte aligned).  Every pool

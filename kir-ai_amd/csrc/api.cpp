@@ -649,6 +649,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
     a.scale_log2e = score_scale * 1.4426950408889634f;
     a.k_new = k_new;
     a.v_new = v_new;
+    a.gate = static_cast<const uint16_t *>(desc->d_gate);
     struct TimingHook {
       llh_ctx *ctx;
       std::pair<hipEvent_t, hipEvent_t> ev;
@@ -680,6 +681,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
   g.ring_tokens = 0;
   g.score_stride = plan.score_stride;
   g.scale = score_scale;
+  g.gate = static_cast<const uint16_t *>(desc->d_gate);
   hipError_t e = launch_decode_generic(g, 0, 0, s);
   if (e != hipSuccess) return ctx->hip_fail(e, "generic decode launch");
   return LLH_OK;
@@ -883,6 +885,7 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
   a.q_tiles = std::max(1, (desc->max_chunk_len + 127) / 128);
   a.scale_log2e = score_scale * 1.4426950408889634f;
   a.scale = score_scale;
+  a.gate = static_cast<const uint16_t *>(desc->d_gate);
   ctx->prefill_calls++;
   auto ev = ctx->timing_begin(static_cast<hipStream_t>(stream));
   hipError_t e;

@@ -933,7 +933,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       oo += s_o[w][gi][d] * f;
     }
     if (n_splits == 1) {
-      a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(oo / ll);
+      a.out[(qrow0 + gi) * D + d] = f32_to_bf16_rne(gated(oo / ll, a.gate, (qrow0 + gi) * D + d));
     } else {
       const size_t row = (qrow0 + gi) * a.max_splits + split;
       a.ws_o[row * D + d] = oo;
@@ -1096,8 +1096,9 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
     // every group now holds the totals; group g writes dims 16j + c for j = 2g, 2g + 1
     if (complete) {
       const float inv = 1.0f / ll;
-      a.out[(qrow0 + gi) * D + 16 * (2 * g) + c] = f32_to_bf16_rne(o2[0] * inv);
-      a.out[(qrow0 + gi) * D + 16 * (2 * g + 1) + c] = f32_to_bf16_rne(o2[1] * inv);
+      const size_t o0 = (qrow0 + gi) * D + 16 * (2 * g) + c;
+      a.out[o0] = f32_to_bf16_rne(gated(o2[0] * inv, a.gate, o0));
+      a.out[o0 + 16] = f32_to_bf16_rne(gated(o2[1] * inv, a.gate, o0 + 16));
     } else {
       const size_t row = (size_t)slot * G + gi;
       a.ws_o[row * D + 16 * (2 * g) + c] = o2[0];
@@ -1363,8 +1364,8 @@ __global__ __launch_bounds__(64) void decode_stream_merge_kernel(const DecodeArg
   }
   const float inv = 1.0f / ll;
   const size_t orow = (size_t)b * a.q_heads + h;
-  a.out[orow * D + lane] = f32_to_bf16_rne(o0 * inv);
-  a.out[orow * D + 64 + lane] = f32_to_bf16_rne(o1 * inv);
+  a.out[orow * D + lane] = f32_to_bf16_rne(gated(o0 * inv, a.gate, orow * D + lane));
+  a.out[orow * D + 64 + lane] = f32_to_bf16_rne(gated(o1 * inv, a.gate, orow * D + 64 + lane));
 }
 
 // Log-sum-exp merge of the split partials: one workgroup of 128 lanes (one per
@@ -1434,7 +1435,7 @@ __device__ __forceinline__ void merge_in_registers(const DecodeArgs &a, size_t r
   float oo = 0.0f;
 #pragma unroll
   for (int i = 0; i < N; i++) oo += o_sp[i] * s_w[i];
-  a.out[orow * D + d] = f32_to_bf16_rne(oo / ll);
+  a.out[orow * D + d] = f32_to_bf16_rne(gated(oo / ll, a.gate, orow * D + d));
 }
 
 __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
@@ -1495,7 +1496,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 32; i++) oo += o_sp[i] * (sp0 + i <= last ? s_f[min(sp0 + i, last)] : 0.0f);
   }
-  a.out[orow * D + d] = f32_to_bf16_rne(oo / l_tot);
+  a.out[orow * D + d] = f32_to_bf16_rne(gated(oo / l_tot, a.gate, orow * D + d));
 }
 
 // ---------------------------------------------------------------------------
@@ -1611,6 +1612,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(const GenericDecode
       const float w = __fdiv_rn(sc[r], sum);
       acc = __fadd_rn(acc, __fmul_rn(pool_elem(a.pool, 1, blk, kvh, off, d), w));
     }
+    acc = gated(acc, a.gate, qoff + d);
     if constexpr (sizeof(OT) == 4)
       reinterpret_cast<float *>(a.out)[qoff + d] = acc;
     else

@@ -13,6 +13,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
   return (uint16_t)(u >> 16);
 }
 
+// The attention output gate of Qwen3.5 / 3.6 (attn_output_gate): attention * sigmoid(g)
+// per output element, sigmoid_f32(g) = 1 / (1 + exp(-g)) (crates/llm-backend/src/core/
+// math.rs:472-474, applied at native_attention.rs:765-770,775-781).  gate: bf16 bits, or
+// null for no gate.
+__device__ __forceinline__ float gated(float v, const uint16_t *gate, size_t idx) {
+  if (!gate) return v;
+  const float g = __uint_as_float((uint32_t)gate[idx] << 16);
+  return v * (1.0f / (1.0f + expf(-g)));
+}
+
 // One dequantised K (tensor 0) or V (tensor 1) element of any pool format and
 // shape: token t of block blk, kv head h, dim d (K rows token-major, V rows
 // dim-major).

@@ -78,6 +78,7 @@ struct DecodeArgs {
   // computes the sequence's last block; null: plain decode
   const uint16_t *k_new;
   const uint16_t *v_new;
+  const uint16_t *gate;     // null, or [B][Hq][128] bf16: out = attention * sigmoid(gate)
 };
 
 // Reference-order decode for any head_dim / block size / group size.
@@ -97,6 +98,7 @@ struct GenericDecodeArgs {
   int32_t ring_tokens;      // >0: position p lives in slot p % ring_tokens (ring cache mirror)
   int32_t score_stride;
   float scale;
+  const uint16_t *gate;     // null, or [B][Hq][D] bf16: out = attention * sigmoid(gate)
 };
 
 struct PrefillArgs {
@@ -114,6 +116,7 @@ struct PrefillArgs {
   int32_t q_tiles;          // tiles of 128 rows per sequence in the grid
   float scale_log2e;
   float scale;              // score_scale (generic kernel)
+  const uint16_t *gate;     // null, or [T][Hq][D] bf16: out = attention * sigmoid(gate)
 };
 
 struct WriteBlocksArgs {

@@ -459,15 +459,17 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
   const float l_tot = l_run + xor32_other(l_run);
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  uint16_t *orow = a.out + ((size_t)(c0 + my_row) * Hq + qh) * D;
+  const size_t obase = ((size_t)(c0 + my_row) * Hq + qh) * D;
+  uint16_t *orow = a.out + obase;
 #pragma unroll
   for (int mt = 0; mt < 4; mt++) {
 #pragma unroll
     for (int jq = 0; jq < 4; jq++) {
       const int d0 = mt * 32 + jq * 8 + 4 * h;
-      const uint2 w2 = make_uint2(pack_bf16(oacc[mt][4 * jq + 0] * inv, oacc[mt][4 * jq + 1] * inv),
-                                  pack_bf16(oacc[mt][4 * jq + 2] * inv, oacc[mt][4 * jq + 3] * inv));
-      *reinterpret_cast<uint2 *>(orow + d0) = w2;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = gated(oacc[mt][4 * jq + e] * inv, a.gate, obase + d0 + e);
+      *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
     }
   }
 }
@@ -583,7 +585,7 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(const PrefillArgs 
 #pragma unroll
   for (int j = 0; j < kGenericPrefillMaxDim / 256; j++) {
     const int d = tid + 256 * j;
-    if (d < Dh) a.out[row + d] = f32_to_bf16_rne(acc[j] * inv);
+    if (d < Dh) a.out[row + d] = f32_to_bf16_rne(gated(acc[j] * inv, a.gate, row + d));
   }
 }
 

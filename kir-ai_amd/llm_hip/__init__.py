@@ -87,6 +87,7 @@ class DecodeDesc(ctypes.Structure):
         ("total_tokens_hint", ctypes.c_int32),
         ("d_seq_lens", ctypes.c_void_p),
         ("d_block_tables", ctypes.c_void_p),
+        ("d_gate", ctypes.c_void_p),
     ]
 
 
@@ -101,6 +102,7 @@ class PrefillDesc(ctypes.Structure):
         ("d_chunk_starts", ctypes.c_void_p),
         ("d_context_lens", ctypes.c_void_p),
         ("d_block_tables", ctypes.c_void_p),
+        ("d_gate", ctypes.c_void_p),
     ]
 
 
@@ -521,9 +523,10 @@ class Context:
     # ---- batched hot path ----
     @staticmethod
     def decode_desc(seq_lens, block_tables, num_q_heads: int, max_seq_len: int, window: int = 0,
-                    total_tokens_hint: int = 0) -> DecodeDesc:
+                    total_tokens_hint: int = 0, gate=None) -> DecodeDesc:
         """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers).
-        total_tokens_hint: the sum of attended tokens if the caller knows it (sizes split-K)."""
+        total_tokens_hint: the sum of attended tokens if the caller knows it (sizes split-K);
+        gate: None, or a bf16 [num_seqs][num_q_heads][head_dim] tensor (out *= sigmoid(gate))."""
         d = DecodeDesc(
             num_seqs=seq_lens.shape[0],
             num_q_heads=num_q_heads,
@@ -533,14 +536,16 @@ class Context:
             total_tokens_hint=total_tokens_hint,
             d_seq_lens=_ptr(seq_lens),
             d_block_tables=_ptr(block_tables),
+            d_gate=_ptr(gate),
         )
-        d._keep = (seq_lens, block_tables)
+        d._keep = (seq_lens, block_tables, gate)
         return d
 
     @staticmethod
     def prefill_desc(chunk_starts, context_lens, block_tables, num_q_heads: int, max_chunk_len: int,
-                     window: int = 0, total_q_rows: Optional[int] = None) -> PrefillDesc:
-        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers)."""
+                     window: int = 0, total_q_rows: Optional[int] = None, gate=None) -> PrefillDesc:
+        """Descriptor over device int32 tensors; it keeps them alive (it stores raw pointers).
+        gate: None, or a bf16 [total_q_rows][num_q_heads][head_dim] tensor (out *= sigmoid(gate))."""
         if total_q_rows is None:
             total_q_rows = int(chunk_starts[-1].item())
         d = PrefillDesc(
@@ -553,8 +558,9 @@ class Context:
             d_chunk_starts=_ptr(chunk_starts),
             d_context_lens=_ptr(context_lens),
             d_block_tables=_ptr(block_tables),
+            d_gate=_ptr(gate),
         )
-        d._keep = (chunk_starts, context_lens, block_tables)
+        d._keep = (chunk_starts, context_lens, block_tables, gate)
         return d
 
     def paged_decode(self, pool: "KvPool", desc: DecodeDesc, q, out, score_scale: float, stream=None) -> None:

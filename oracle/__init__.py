@@ -102,6 +102,8 @@ _SIGS = {
     "orc_weighted_sum": (None, [_P, _P, _SZ, _SZ, _P]),
     "orc_select_head_rows": (None, [_P, _SZ, _SZ, _SZ, _SZ, _P]),
     "orc_attention_mix": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _F, _P]),
+    "orc_sigmoid": (_F, [_F]),
+    "orc_apply_gate": (None, [_P, _P, _SZ]),
     "orc_attention_mix_f64": (ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, _P]),
     "orc_ring_init": (ctypes.c_int, [ctypes.POINTER(_Ring), _I64, _I64, _I64, _P, _P, _P, _I64]),
     "orc_ring_append_sliding": (ctypes.c_int, [ctypes.POINTER(_Ring), _P, _P, _P, _P]),
@@ -198,6 +200,21 @@ def softmax(scores) -> tuple[int, np.ndarray]:
     out = np.zeros_like(s)
     st = lib().orc_softmax(_p(s), s.size, _p(out))
     return st, out
+
+
+def sigmoid(x: float) -> float:
+    """sigmoid_f32 (math.rs:472-474)."""
+    return lib().orc_sigmoid(float(x))
+
+
+def apply_gate(attended, gate) -> np.ndarray:
+    """apply_attention_gate (native_attention.rs:775-781): attended * sigmoid(gate), element-wise,
+    on a copy (f32)."""
+    out = np.ascontiguousarray(attended, dtype=np.float32).ravel().copy()
+    g = np.ascontiguousarray(gate, dtype=np.float32).ravel()
+    assert g.size == out.size
+    lib().orc_apply_gate(_p(out), _p(g), out.size)
+    return out
 
 
 def attention_mix(query, keys, values, row_count, q_heads, kv_heads, head_dim, scale) -> tuple[int, np.ndarray]:

@@ -223,6 +223,15 @@ int orc_softmax(const float *scores, size_t n, float *out) {
   return ORC_OK;
 }
 
+/* math.rs:472-474 sigmoid_f32 */
+float orc_sigmoid(float value) { return 1.0f / (1.0f + expf(-value)); }
+
+/* native_attention.rs:775-781 apply_attention_gate: each attended value times the
+ * sigmoid of its gate (the per-head loop at :765-770 applies the same product) */
+void orc_apply_gate(float *attended, const float *gate, size_t n) {
+  for (size_t i = 0; i < n; i++) attended[i] = attended[i] * orc_sigmoid(gate[i]);
+}
+
 /* math.rs:260-287 weighted_sum_f32_in_place */
 void orc_weighted_sum(const float *values, const float *weights, size_t rows, size_t vector_len, float *out) {
   for (size_t d = 0; d < vector_len; d++) out[d] = 0.0f;

@@ -79,6 +79,11 @@ void orc_matvec_row_major(const float *x, const float *w, size_t rows, size_t co
 void orc_matvec_bf16_f32(const uint16_t *w, size_t rows, size_t cols, const float *x, float *out);
 /* softmax_f32_in_place: error on non-finite input or invalid denominator */
 int orc_softmax(const float *scores, size_t n, float *out);
+/* math.rs:472-474 sigmoid_f32: 1 / (1 + exp(-value)) */
+float orc_sigmoid(float value);
+/* native_attention.rs:775-781 apply_attention_gate (and the per-head form of :765-770):
+ * attended[i] *= sigmoid_f32(gate[i]) for i < n */
+void orc_apply_gate(float *attended, const float *gate, size_t n);
 /* weighted_sum_f32_in_place */
 void orc_weighted_sum(const float *values, const float *weights, size_t rows, size_t vector_len, float *out);
 /* select_head_rows_f32_in_place */

@@ -121,7 +121,8 @@ def test_sliding_window_two():
     keys = [[1.0, 0.0]] * len(c["values"])
     outs = ring_step_outputs([[1.0, 0.0]] * 3, keys, c["values"], 1, 1, 2, 1.0 / math.sqrt(2), c["max_tokens"])
     assert close(outs[-1], c["expected_attention"], 1e-6)
-    assert close(np.array(outs[-1]) * 0.5, c["expected_after_gate"], 1e-6)
+    # the q projection's gate half is zero in the reference test: attention * sigmoid(0)
+    assert close(oracle.apply_gate(outs[-1], np.zeros(2, np.float32)), c["expected_after_gate"], 1e-6)
     r = oracle.Ring(c["max_tokens"], 2)
     for k, v in zip(keys, c["values"]):
         r.append_sliding(k, v)
@@ -598,3 +599,27 @@ def test_bf16_matvec_matches_float64():
     assert np.max(np.abs(got - ref)) < 1e-4
     # a transposed operand or a dropped row fails this
     assert not np.allclose(got[:-1], ref[1:], atol=1e-2)
+
+
+def test_sigmoid_and_gate():
+    """sigmoid_f32 (math.rs:472-474) and apply_attention_gate (native_attention.rs:775-781):
+    sigmoid(0) is exactly one half, the f32 result is within 2 ulp of float64 1 / (1 + e^-x)
+    over [-30, 30], the symmetry sigmoid(-x) = 1 - sigmoid(x) holds to f32 rounding, the tails
+    saturate to 0 and 1 (exp overflow gives 0, not NaN), and the gate multiplies element-wise
+    (a gate of a different element must not leak: one planted swap fails)."""
+    assert oracle.sigmoid(0.0) == 0.5
+    xs = np.linspace(-30.0, 30.0, 6001).astype(np.float32)
+    got = np.array([oracle.sigmoid(float(x)) for x in xs], np.float32)
+    ref = 1.0 / (1.0 + np.exp(-xs.astype(np.float64)))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2 * ulp)
+    mid = np.abs(xs) < 8
+    assert np.all(np.abs(got[mid] + got[mid][::-1] - 1.0) <= 2 * np.spacing(np.float32(1.0)))
+    assert oracle.sigmoid(200.0) == 1.0 and oracle.sigmoid(-200.0) == 0.0
+    att = np.arange(1, 9, dtype=np.float32)
+    gate = np.array([0, 0, 1, -1, 30, -30, 2, -2], np.float32)
+    out = oracle.apply_gate(att, gate)
+    assert np.all(out == np.array([att[i] * oracle.sigmoid(float(gate[i])) for i in range(8)], np.float32))
+    swapped = gate.copy()
+    swapped[[2, 3]] = swapped[[3, 2]]
+    assert not np.array_equal(oracle.apply_gate(att, swapped), out)
