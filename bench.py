@@ -865,6 +865,16 @@ def run_sections(ctx, args, lens, sel) -> list:
         log(f"C5 {nm}: {r}")
         del wq
         torch.cuda.empty_cache()
+        # kir-ai's step order on the same shape: append the new token (quantised), then attend, in one call
+        _, r = measure_decode(ctx, f"C5 {nm} append + attend in one call (llh_paged_decode_append)", [8192] * 64, 32,
+                              8, fmt, sec_steps, sec_warm, seed=workloads.SEED_BASE + 4, free=0.0, fused=True)
+        r["decode_alone_us"] = secondary[-1]["us_per_step"]
+        # int8: the stream kernel quantises the token itself (+ merge); fp8: slot and append
+        # kernels, then the stream kernel and merge
+        r["launches"] = 2 if fmt == llm_hip.KV_INT8 else 4
+        secondary.append(r)
+        log(f"C5 {nm} fused append+attend: {r}")
+        torch.cuda.empty_cache()
     if sel("neighbours"):
         secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))
     if sel("trait"):

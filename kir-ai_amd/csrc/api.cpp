@@ -787,9 +787,14 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
     return ctx->fail(LLH_ERR_INVALID_SHAPE,
                      "fp8 append over a window ring needs window + block_tokens - 1 <= max_blocks_per_seq * "
                      "block_tokens (one block more than the window)");
-  // one launch for bf16 pools on the tuned kernels (new-token rows 16-byte aligned);
-  // any other case appends through the append kernel first, then decodes
-  const bool fused = plan.fast && pv.format == LLH_KV_BF16 && aligned16(d_k_new) && aligned16(d_v_new);
+  // one launch on the tuned kernels (new-token rows 16-byte aligned): bf16 pools attend
+  // the new token from its rows, int8 / fp8 pools quantise it into the block that
+  // receives it.  fp8 pools on the persistent stream kernel are the exception: the
+  // scale-growth re-encode doubles that kernel's code and costs more than the
+  // separate append launch it saves.  Every other case appends through the append
+  // kernel first, then decodes.
+  const bool fused = plan.fast && aligned16(d_k_new) && aligned16(d_v_new) &&
+                     !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0);
   const size_t slot_bytes = fused ? 0 : align_up((size_t)desc->num_seqs * sizeof(int64_t));
   WsLease lease;
   st = lease.acquire(ctx, s, plan.bytes + slot_bytes);

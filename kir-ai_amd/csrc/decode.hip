@@ -792,9 +792,299 @@ __device__ __forceinline__ void add_new_token(const DecodeArgs &a, SoftmaxState<
   if constexpr (STORE) store_new_token(a, kvh, len, lane, nt);
 }
 
+// ---------------------------------------------------------------------------
+// Fused append for int8 / fp8 pools.  The new token must be attended as stored
+// (quantised), so the wavefront that computes the sequence's last block
+// quantises it exactly as append_kernel would -- int8: codes with the fp16
+// scale absmax / 127 of the token's head row; fp8: the block's scale becomes
+// max(old, absmax / 448) (restarted at offset 0) and, when it grows, the
+// block's earlier tokens are re-encoded from their dequantised values -- patches
+// the codes and scales into the block registers it loaded from the pool (whose
+// slot of the new position is stale), attends the block, and writes the token
+// (and re-encoded tokens) back.  The pool ends byte-identical to llh_kv_append,
+// and the attention equals the two calls' (the same registers meet the same
+// arithmetic).  A non-finite row is flagged and not appended, as append_kernel
+// does.
+// Each lane holds two dims of the new rows (2l, 2l+1 of K and of V, one bf16
+// pair each); the codes reach the lanes that hold the slot in the block layout
+// through ds_bpermute.
+struct NewTokenQ {
+  uint32_t k2, v2;  // bf16 pairs: dims 2 * lane, 2 * lane + 1
+  int blk;          // block-table entry of the block that receives the token
+};
+
+__device__ __forceinline__ void load_new_token_q(const DecodeArgs &a, int b, int kvh, int lane, NewTokenQ &nt,
+                                                 int blk) {
+  const size_t row = ((size_t)b * a.pool.kv_heads + kvh) * D;
+  nt.blk = blk;
+  nt.k2 = reinterpret_cast<const uint32_t *>(a.k_new + row)[lane];
+  nt.v2 = reinterpret_cast<const uint32_t *>(a.v_new + row)[lane];
+}
+
+// Max over the wavefront, in every lane (DPP within rows, then row exchanges).
+__device__ __forceinline__ float wave_max_f(float v, int lane) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, xor16_other(v, lane));
+  return fmaxf(v, xor32_other(v, lane));
+}
+
+__device__ __forceinline__ uint32_t bperm(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+
+// Re-encodes the fp8 codes of a 16-byte run from scale s_old to s_new (append_fp8_row's
+// rule, encode(decode(code) * s_old / s_new)); byte i is re-encoded when bit i of mask is set.
+// (The bytes of a word are walked by a loop that is not unrolled: the path is rare, and
+// 64 unrolled software encodes per lane would bloat the decode loop's code.)
+__device__ __forceinline__ uint32_t fp8_rescale_word(uint32_t w, float s_old, float s_new, uint32_t mask4) {
+#pragma unroll 1
+  for (int i = 0; i < 4; i++)
+    if (mask4 & (1u << i)) {
+      const uint32_t code = (w >> (8 * i)) & 0xffu;
+      const float x = s_old == 0.0f ? 0.0f : decode_e4m3(code) * s_old;
+      const uint32_t nc = encode_e4m3(__fdiv_rn(x, s_new));
+      w = (w & ~(0xffu << (8 * i))) | (nc << (8 * i));
+    }
+  return w;
+}
+__device__ __forceinline__ uint4 fp8_rescale16(uint4 w, float s_old, float s_new, uint32_t mask) {
+  return make_uint4(fp8_rescale_word(w.x, s_old, s_new, mask & 15u), fp8_rescale_word(w.y, s_old, s_new, (mask >> 4) & 15u),
+                    fp8_rescale_word(w.z, s_old, s_new, (mask >> 8) & 15u),
+                    fp8_rescale_word(w.w, s_old, s_new, (mask >> 12) & 15u));
+}
+
+// fp8 block scale growth (rare): the append done in the pool itself, as append_fp8_row
+// does it -- tokens before `off` re-encoded (K: lane = token lane / 4, dims 32 (lane % 4)
+// .. + 31; V: dim rows 2 lane, 2 lane + 1, tokens 0 .. off - 1), the new token's codes
+// (kc / vc: dims 2 lane, 2 lane + 1) and the scale pair written -- then the block's codes
+// read back into r.  Called by the whole wavefront (uniform condition).
+template <int FMT, bool TL>
+__device__ __forceinline__ void fp8_append_in_pool(const DecodeArgs &a, BlockRegs<FMT> &r, int blk, int kvh, int off,
+                                                   float ks_old, float ks, float vs_old, float vs, uint32_t kc,
+                                                   uint32_t vc, int lane) {
+  const size_t bh = (size_t)blk * a.pool.kv_heads + kvh;
+  uint8_t *kb = const_cast<uint8_t *>(reinterpret_cast<const uint8_t *>(a.pool.k)) + bh * (BT * D);
+  uint8_t *vb = const_cast<uint8_t *>(reinterpret_cast<const uint8_t *>(a.pool.v)) + bh * (BT * D);
+  const int tok = lane >> 2;
+  uint4 k0 = *reinterpret_cast<const uint4 *>(kb + lane * 32);
+  uint4 k1 = *reinterpret_cast<const uint4 *>(kb + lane * 32 + 16);
+  uint4 v0 = *reinterpret_cast<const uint4 *>(vb + (2 * lane) * BT);
+  uint4 v1 = *reinterpret_cast<const uint4 *>(vb + (2 * lane + 1) * BT);
+  if (ks != ks_old && tok < off) {
+    k0 = fp8_rescale16(k0, ks_old, ks, 0xffffu);
+    k1 = fp8_rescale16(k1, ks_old, ks, 0xffffu);
+  }
+  if (vs != vs_old) {
+    const uint32_t m = (1u << off) - 1u;
+    v0 = fp8_rescale16(v0, vs_old, vs, m);
+    v1 = fp8_rescale16(v1, vs_old, vs, m);
+  }
+  *reinterpret_cast<uint4 *>(kb + lane * 32) = k0;
+  *reinterpret_cast<uint4 *>(kb + lane * 32 + 16) = k1;
+  *reinterpret_cast<uint4 *>(vb + (2 * lane) * BT) = v0;
+  *reinterpret_cast<uint4 *>(vb + (2 * lane + 1) * BT) = v1;
+  // the new token: K row bytes 2 lane, 2 lane + 1; V byte `off` of dim rows 2 lane, 2 lane + 1
+  *reinterpret_cast<uint16_t *>(kb + off * D + 2 * lane) = (uint16_t)kc;
+  vb[(2 * lane) * BT + off] = (uint8_t)(vc & 0xffu);
+  vb[(2 * lane + 1) * BT + off] = (uint8_t)(vc >> 8);
+  if (lane == 0)
+    *reinterpret_cast<float2 *>(const_cast<float *>(reinterpret_cast<const float *>(a.pool.k_scales)) +
+                                fp8_scale_index(bh)) = make_float2(ks, vs);
+  // this wavefront's stores are complete before it reads the block again
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+  const bool valid = r.valid;
+  load_block<FMT, TL>(a, blk, kvh, lane, r);
+  r.valid = valid;
+  r.ksb = ks;  // (the scalar load of load_block may read the scale pair through the scalar cache)
+  r.vsb = vs;
+}
+
+// What a patched block writes back to the pool after it is computed.
+struct NewTokenStore {
+  bool any;          // this wavefront appends (finite rows, valid block)
+  uint32_t k_rows;   // token-lane layout: the lane's token row is written; row layout: bit i = r.k[i]
+  uint32_t v_words;  // the lane's V words are written (its group holds a changed token)
+  bool scale;        // this lane writes the scale pair(s)
+};
+
+// Patches the new token (offset off of block r) into the registers; returns what to store.
+template <int G, int FMT>
+__device__ __forceinline__ NewTokenStore patch_new_token_q(const DecodeArgs &a, BlockRegs<FMT> &r,
+                                                           const NewTokenQ &nt, int kvh, int off, int lane) {
+  static_assert(FMT == kInt8 || FMT == kFp8, "quantised pools");
+  constexpr bool TL = kTokenLanes<G, FMT>;
+  NewTokenStore out{false, 0u, 0u, false};
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const float kx[2] = {bf16_lo(nt.k2), bf16_hi(nt.k2)};
+  const float vx[2] = {bf16_lo(nt.v2), bf16_hi(nt.v2)};
+  const bool finite = isfinite(kx[0]) && isfinite(kx[1]) && isfinite(vx[0]) && isfinite(vx[1]);
+  if (__any(!finite)) {  // append_kernel: NonFiniteValue, nothing of the token written
+    if (lane == 0) atomicOr(a.err, kErrNonFinite);
+    return out;
+  }
+  if (!r.valid) return out;  // the append flags the slot (compute_block flags the block)
+  const float kmax = wave_max_f(fmaxf(fabsf(kx[0]), fabsf(kx[1])), lane);
+  const float vmax = wave_max_f(fmaxf(fabsf(vx[0]), fabsf(vx[1])), lane);
+  float ks, vs;            // the token's scales
+  float ks_old = 0.0f, vs_old = 0.0f;
+  uint32_t s16pair = 0u;   // int8: the (K, V) fp16 scale pair
+  if constexpr (FMT == kInt8) {
+    const _Float16 k16 = (_Float16)(kmax == 0.0f ? 0.0f : __fdiv_rn(kmax, 127.0f));
+    const _Float16 v16 = (_Float16)(vmax == 0.0f ? 0.0f : __fdiv_rn(vmax, 127.0f));
+    ks = (float)k16;
+    vs = (float)v16;
+    s16pair = (uint32_t)__builtin_bit_cast(uint16_t, k16) | ((uint32_t)__builtin_bit_cast(uint16_t, v16) << 16);
+  } else {
+    ks_old = off == 0 ? 0.0f : r.ksb;
+    vs_old = off == 0 ? 0.0f : r.vsb;
+    ks = fmaxf(ks_old, kmax == 0.0f ? 0.0f : __fdiv_rn(kmax, 448.0f));
+    vs = fmaxf(vs_old, vmax == 0.0f ? 0.0f : __fdiv_rn(vmax, 448.0f));
+  }
+  auto code = [&](float x, float sc) -> uint32_t {
+    if constexpr (FMT == kInt8)
+      return (uint32_t)(uint8_t)quant_int8(x, sc);
+    else
+      return sc == 0.0f ? 0u : (uint32_t)encode_e4m3(__fdiv_rn(x, sc));
+  };
+  // this lane's two codes of each row (dims 2 * lane, 2 * lane + 1)
+  const uint32_t kc = code(kx[0], ks) | (code(kx[1], ks) << 8);
+  const uint32_t vc = code(vx[0], vs) | (code(vx[1], vs) << 8);
+  if constexpr (FMT == kFp8) {
+    if (off > 0 && (ks != ks_old || vs != vs_old)) {  // the block's scale grows: the rare path, in the pool
+      fp8_append_in_pool<FMT, TL>(a, r, nt.blk, kvh, off, ks_old, ks, vs_old, vs, kc, vc, lane);
+      return out;  // written already
+    }
+  }
+  // ---- K ----
+  if constexpr (TL) {
+    // lane 16g + 4tq + c4 holds token 4g + tq at dims 32 c4 .. + 31: codes of lanes 16 c4 .. + 15
+    const int c4 = lane & 3;
+    const int tok = 4 * g + ((lane >> 2) & 3);
+    uint32_t w[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+      w[m] = (bperm(kc, 16 * c4 + 2 * m) & 0xffffu) | (bperm(kc, 16 * c4 + 2 * m + 1) << 16);
+    if (tok == off) {
+      r.k[0] = make_uint4(w[0], w[1], w[2], w[3]);
+      r.k[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      out.k_rows = 1u;
+      if constexpr (FMT == kInt8) {
+        r.sc.x = s16pair;
+        out.scale = c4 == 0;
+      }
+    }
+  } else {
+    // lane 16g + 8hf + c8 holds tokens 4g + 2i + hf (i = 0, 1) at dims 16 c8 .. + 15: codes of lanes 8 c8 .. + 7
+    const int hf = (lane >> 3) & 1;
+    const int c8 = lane & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+      w[m] = (bperm(kc, 8 * c8 + 2 * m) & 0xffffu) | (bperm(kc, 8 * c8 + 2 * m + 1) << 16);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int tok = 4 * g + 2 * i + hf;
+      if (tok == off) {
+        r.k[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        out.k_rows |= 1u << i;
+      }
+    }
+    if constexpr (FMT == kInt8) {
+      if (g == off / 4) {
+        if ((off & 3) == 0) r.sc.x = s16pair;
+        if ((off & 3) == 1) r.sc.y = s16pair;
+        if ((off & 3) == 2) r.sc.z = s16pair;
+        if ((off & 3) == 3) r.sc.w = s16pair;
+        out.scale = (lane & 15) == 0;
+      }
+    }
+  }
+  // ---- V: lane (g, c) holds tokens 4g .. 4g+3 (bytes) of dims 16j + c ----
+  const int shift = 8 * (off & 3);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int dim = 16 * j + c;
+    const uint32_t cv = (bperm(vc, dim >> 1) >> (8 * (dim & 1))) & 0xffu;
+    if (g == off / 4) r.v[j] = (r.v[j] & ~(0xffu << shift)) | (cv << shift);
+  }
+  out.v_words = g == off / 4 ? 1u : 0u;
+  if constexpr (FMT == kFp8) {
+    r.ksb = ks;
+    r.vsb = vs;
+    out.scale = lane == 0;
+  }
+  out.any = true;
+  return out;
+}
+
+// Writes what patch_new_token_q changed (block nt.blk, kv head kvh, offset off).
+template <int G, int FMT>
+__device__ __forceinline__ void store_new_token_q(const DecodeArgs &a, const BlockRegs<FMT> &r, const NewTokenQ &nt,
+                                                  const NewTokenStore &w, int kvh, int off, int lane) {
+  if (!w.any) return;
+  constexpr bool TL = kTokenLanes<G, FMT>;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const size_t bh = (size_t)nt.blk * a.pool.kv_heads + kvh;
+  char *kb = const_cast<char *>(reinterpret_cast<const char *>(a.pool.k)) + bh * (BT * D);
+  char *vb = const_cast<char *>(reinterpret_cast<const char *>(a.pool.v)) + bh * (BT * D);
+  if constexpr (TL) {
+    if (w.k_rows) {
+      *reinterpret_cast<uint4 *>(kb + lane * 32) = r.k[0];
+      *reinterpret_cast<uint4 *>(kb + lane * 32 + 16) = r.k[1];
+    }
+  } else {
+    const int hf = (lane >> 3) & 1;
+    const int c8 = lane & 7;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (w.k_rows & (1u << i)) *reinterpret_cast<uint4 *>(kb + (4 * g + 2 * i + hf) * D + c8 * 16) = r.k[i];
+  }
+  if (w.v_words) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) *reinterpret_cast<uint32_t *>(vb + (16 * j + c) * BT + g * 4) = r.v[j];
+  }
+  if (w.scale) {
+    if constexpr (FMT == kInt8) {
+      uint32_t pair;
+      if constexpr (TL) {
+        pair = r.sc.x;
+      } else {
+        const uint32_t p4[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+        pair = p4[off & 3];
+      }
+      uint16_t *sp = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(a.pool.k_scales));
+      *reinterpret_cast<uint32_t *>(sp + int8_scale_index(bh, off, BT)) = pair;
+    } else {
+      float *sp = const_cast<float *>(reinterpret_cast<const float *>(a.pool.k_scales));
+      *reinterpret_cast<float2 *>(sp + fp8_scale_index(bh)) = make_float2(r.ksb, r.vsb);
+    }
+  }
+}
+
+// The new-token registers of the fused append: bf16 rows as the row layout holds
+// a block (NewToken), or two dims per lane for quantised pools (NewTokenQ).
+template <int FMT>
+struct NtOf {
+  typedef NewTokenQ type;
+};
+template <>
+struct NtOf<kBf16> {
+  typedef NewToken type;
+};
+__device__ __forceinline__ void load_nt(const DecodeArgs &a, int b, int kvh, int lane, NewToken &nt, int blk) {
+  load_new_token(a, b, kvh, lane, nt, blk);
+}
+__device__ __forceinline__ void load_nt(const DecodeArgs &a, int b, int kvh, int lane, NewTokenQ &nt, int blk) {
+  load_new_token_q(a, b, kvh, lane, nt, blk);
+}
+
 template <int G, int FMT, bool FUSED = false>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeArgs a) {
-  static_assert(!FUSED || FMT == kBf16, "fused append: bf16 pools");
   // consecutive workgroups are consecutive splits of one (kv head, sequence):
   // they share its query rows and block-table row in L2 (measured faster on
   // MI355X than dispatching all first splits first)
@@ -845,15 +1135,18 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 
   SoftmaxState<G> st;
   reset_state(st);
-  // fused append: the pool part attends [lo, len - 1); the new token comes from a.k_new
+  // fused append, bf16: the pool part attends [lo, len - 1) and the new token comes from
+  // a.k_new; int8 / fp8: the token is quantised into the registers of the block that
+  // receives it, which is then attended up to len as stored
   constexpr bool fused = FUSED;
-  const int len_kv = fused ? len - 1 : len;
+  constexpr bool qfused = FUSED && FMT != kBf16;
+  const int len_kv = fused && !qfused ? len - 1 : len;
   // the wavefront that walks the sequence's last block takes the new token: its rows
   // are loaded now, ahead of the block loop
   const int last_blk = first_blk + n_blk - 1;
   const bool takes_new = fused && last_blk >= blk_begin && last_blk < blk_end && (last_blk - blk_begin) % 4 == wave;
-  NewToken nt;
-  if (takes_new) load_new_token(a, b, kvh, lane, nt, stable[((len - 1) / BT) % a.max_blocks]);
+  typename NtOf<FMT>::type nt;
+  if (takes_new) load_nt(a, b, kvh, lane, nt, stable[((len - 1) / BT) % a.max_blocks]);
 
   // ---- two-stage block pipeline: block k+1's loads are in flight during block k's math ----
   float qstep = 1.0f;
@@ -869,7 +1162,15 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
         load_block<FMT, TL>(a, e_next, kvh, lane, nxt);
         e_next = k + 2 < nbw ? entry(k + 2) : -1;
       }
+      // int8 / fp8 fused append: the block that receives the new token gets it patched in
+      // first (one compute_block below either way: the block math is not duplicated)
+      NewTokenStore nw{false, 0u, 0u, false};
+      const bool patch = qfused && takes_new && blk_begin + wave + 4 * k == last_blk;
+      if constexpr (qfused)
+        if (patch) nw = patch_new_token_q<G, FMT>(a, cur, nt, kvh, (len - 1) % BT, lane);
       compute_block<G, FMT>(a, cur, blk_begin + wave + 4 * k, lo, len_kv, lane, qw, qstep, st);
+      if constexpr (qfused)
+        if (patch) store_new_token_q<G, FMT>(a, cur, nt, nw, kvh, (len - 1) % BT, lane);
     };
     int k = 0;
     for (; k + 2 < nbw; k += 2) {
@@ -1109,9 +1410,15 @@ __device__ __forceinline__ void stream_flush(const DecodeArgs &a, SoftmaxState<G
   reset_state(st);
 }
 
+// Waves per SIMD the stream kernel is built for: two (its grid of two workgroups
+// per CU all resident) for up to four query heads per kv head; the quantised fused
+// append's extra registers would otherwise push it to one.
+template <int G>
+constexpr int kStreamWavesPerSimd = G <= 4 ? 2 : 1;
+
 template <int G, int FMT, bool FUSED = false>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(const DecodeArgs a) {
-  static_assert(!FUSED || FMT == kBf16, "fused append: bf16 pools");
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(kStreamWavesPerSimd<G>)))
+void paged_decode_stream_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
   const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
@@ -1138,8 +1445,11 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   if (n == 0) return;
   const int U = __builtin_amdgcn_readfirstlane(sr.U);
   const int Wu = __builtin_amdgcn_readfirstlane(sr.Wu);
-  // fused append: the pool part attends [lo, len - 1); the new token comes from a.k_new
+  // fused append, bf16: the pool part attends [lo, len - 1) and the new token comes from
+  // a.k_new; int8 / fp8: the token is quantised into the registers of the segment's last
+  // unit (the block that receives it), which is attended up to len as stored
   constexpr bool fused = FUSED;
+  constexpr bool qfused = FUSED && FMT != kBf16;
 
   // Lengths, block-table entries: scalar loads (constant address space: no
   // one writes them during the launch), so the waits before the math cover
@@ -1209,12 +1519,13 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   // fused append: a segment's new-token rows are loaded with its last unit, into
   // the buffer that travels with that unit's registers (r[0] / r[1]), with that
   // unit's block-table entry (the block the token goes to)
-  NewToken nt[2];
-  NewToken pend;  // a computed segment's new token, not yet written to the pool
+  typedef typename NtOf<FMT>::type NT;
+  NT nt[2];
+  NewToken pend;  // bf16: a computed segment's new token, not yet written to the pool
   int pend_kvh = 0, pend_len = 0;
   bool have_pend = false;
-  if constexpr (FMT == kBf16)
-    if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nt[0], e_first);
+  if constexpr (fused)
+    if (L.j == L.nb - 1) load_nt(a, L.b, L.kvh, lane, nt[0], e_first);
   float qstep = prep_q<G, FMT>(lane, qw);
   int e_next = n > 1 ? next_entry() : -1;
   advance(L);
@@ -1238,14 +1549,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
   // issued, then q is prepared (prep_q) and unit k is computed.  Every step
   // inside the loop issues the next unit's loads after any q load, so the wait
   // before the math always leaves the next unit's loads in flight.
-  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, NewToken &cur_nt, NewToken &nxt_nt, bool issue)
+  auto step = [&](int k, BlockRegs<FMT> &cur, BlockRegs<FMT> &nxt, NT &cur_nt, NT &nxt_nt, bool issue)
                   __attribute__((always_inline)) {
     const bool new_q = need_q;
     if (new_q) load_q<G, FMT>(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G, lane, qw);
     if (issue) {
       load_block<FMT, TL>(a, e_next, L.kvh, lane, nxt);
-      if constexpr (FMT == kBf16)
-        if (fused && L.j == L.nb - 1) load_new_token(a, L.b, L.kvh, lane, nxt_nt, e_next);
+      if constexpr (fused)
+        if (L.j == L.nb - 1) load_nt(a, L.b, L.kvh, lane, nxt_nt, e_next);
       e_next = k + 2 < n ? next_entry() : -1;
       advance(L);
     }
@@ -1253,10 +1564,16 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_stream_kernel(con
       qstep = prep_q<G, FMT>(lane, qw);
       need_q = false;
     }
-    compute_block<G, FMT>(a, cur, C.lo / BT + C.j, C.lo, fused ? C.len - 1 : C.len, lane, qw, qstep, st);
+    // int8 / fp8 fused append: the segment's last unit (the block that receives the new
+    // token) gets it patched in first (one compute_block either way)
+    NewTokenStore nw{false, 0u, 0u, false};
+    if constexpr (qfused)
+      if (C.j == C.nb - 1) nw = patch_new_token_q<G, FMT>(a, cur, cur_nt, C.kvh, (C.len - 1) % BT, lane);
+    compute_block<G, FMT>(a, cur, C.lo / BT + C.j, C.lo, fused && !qfused ? C.len - 1 : C.len, lane, qw, qstep, st);
+    if constexpr (qfused)
+      if (C.j == C.nb - 1) store_new_token_q<G, FMT>(a, cur, cur_nt, nw, C.kvh, (C.len - 1) % BT, lane);
     if (C.j == C.nb - 1) {  // the segment ends with this unit
-      if constexpr (FMT == kBf16)
-        if (fused) {
+      if constexpr (fused && FMT == kBf16) {
           if constexpr (G > 4) {
             add_new_token<G, true>(a, st, C.b, C.kvh, C.len, lane, qw, cur_nt);  // no registers to spare
           } else {
@@ -1631,8 +1948,14 @@ hipError_t launch_decode_t(const DecodeArgs &a, int max_seq_len, hipStream_t s, 
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
   if (hook) hook(hu, 0, s);
   if (a.stream_wgs > 0) {
-    hipLaunchKernelGGL((paged_decode_stream_kernel<G, FMT, FUSED>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s,
-                       a);
+    // fp8 appends on the stream plan go through the append kernel (the host never
+    // asks for this instantiation)
+    if constexpr (FUSED && FMT == kFp8) {
+      return hipErrorInvalidValue;
+    } else {
+      hipLaunchKernelGGL((paged_decode_stream_kernel<G, FMT, FUSED>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
+                         s, a);
+    }
     hipError_t e = hipGetLastError();
     if (hook) hook(hu, 1, s);
     if (e != hipSuccess) return e;
@@ -1655,9 +1978,11 @@ hipError_t launch_decode_fmt(const DecodeArgs &a, int max_seq_len, hipStream_t s
       return a.k_new ? launch_decode_t<G, kBf16, true>(a, max_seq_len, s, hu, hook)
                      : launch_decode_t<G, kBf16, false>(a, max_seq_len, s, hu, hook);
     case kInt8:
-      return a.k_new ? hipErrorInvalidValue : launch_decode_t<G, kInt8, false>(a, max_seq_len, s, hu, hook);
+      return a.k_new ? launch_decode_t<G, kInt8, true>(a, max_seq_len, s, hu, hook)
+                     : launch_decode_t<G, kInt8, false>(a, max_seq_len, s, hu, hook);
     case kFp8:
-      return a.k_new ? hipErrorInvalidValue : launch_decode_t<G, kFp8, false>(a, max_seq_len, s, hu, hook);
+      return a.k_new ? launch_decode_t<G, kFp8, true>(a, max_seq_len, s, hu, hook)
+                     : launch_decode_t<G, kFp8, false>(a, max_seq_len, s, hu, hook);
   }
   return hipErrorInvalidValue;
 }

@@ -13,6 +13,48 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
   return (uint16_t)(u >> 16);
 }
 
+// int8 code of x with scale s: clamp(round_half_away(x / s), -127, 127), 0 for
+// s = 0 -- the symmetric rule of crates/llm-kv-cache/src/format.rs:711-735 (Rust
+// f32::round rounds half away from zero, as roundf does).  Shared by the KV
+// writes and the fused append of the decode kernels, so both store identical bytes.
+__device__ __forceinline__ int8_t quant_int8(float x, float s) {
+  if (s == 0.0f) return 0;
+  float c = roundf(__fdiv_rn(x, s));
+  c = fminf(fmaxf(c, -127.0f), 127.0f);
+  return (int8_t)c;
+}
+
+// OCP e4m3fn encode, round to nearest even, saturate to +-448, NaN -> 0x7f.
+__device__ __forceinline__ uint8_t encode_e4m3(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t au = u & 0x7fffffffu;
+  if (au > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+  if (__uint_as_float(au) >= 448.0f) return (uint8_t)(sign | 0x7eu);
+  const uint32_t exp = au >> 23;
+  uint32_t man = au & 0x7fffffu;
+  const int e = (int)exp - 127 + 7;
+  if (e <= 0) {
+    if (exp == 0) return (uint8_t)sign;
+    man |= 0x800000u;
+    const int shift = 21 - e;
+    if (shift > 24) return (uint8_t)sign;
+    uint32_t q = man >> shift;
+    const uint32_t rem = man & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint8_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)e << 3) | (man >> 20);
+  const uint32_t rem = man & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q++;
+  if (q > 0x7eu) q = 0x7eu;
+  return (uint8_t)(sign | q);
+}
+
+// fp8 e4m3 code as f32 (exact).
+__device__ __forceinline__ float decode_e4m3(uint32_t code) { return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0]; }
+
 // The attention output gate of Qwen3.5 / 3.6 (attn_output_gate): attention * sigmoid(g)
 // per output element, sigmoid_f32(g) = 1 / (1 + exp(-g)) (crates/llm-backend/src/core/
 // math.rs:472-474, applied at native_attention.rs:765-770,775-781).  gate: bf16 bits, or

@@ -24,41 +24,6 @@ namespace {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-__device__ __forceinline__ int8_t quant_int8(float x, float s) {
-  if (s == 0.0f) return 0;
-  float c = roundf(__fdiv_rn(x, s));
-  c = fminf(fmaxf(c, -127.0f), 127.0f);
-  return (int8_t)c;
-}
-
-// OCP e4m3fn encode, round to nearest even, saturate to +-448, NaN -> 0x7f.
-__device__ __forceinline__ uint8_t encode_e4m3(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t au = u & 0x7fffffffu;
-  if (au > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
-  if (__uint_as_float(au) >= 448.0f) return (uint8_t)(sign | 0x7eu);
-  const uint32_t exp = au >> 23;
-  uint32_t man = au & 0x7fffffu;
-  const int e = (int)exp - 127 + 7;
-  if (e <= 0) {
-    if (exp == 0) return (uint8_t)sign;
-    man |= 0x800000u;
-    const int shift = 21 - e;
-    if (shift > 24) return (uint8_t)sign;
-    uint32_t q = man >> shift;
-    const uint32_t rem = man & ((1u << shift) - 1u);
-    const uint32_t half = 1u << (shift - 1);
-    if (rem > half || (rem == half && (q & 1u))) q++;
-    return (uint8_t)(sign | q);
-  }
-  uint32_t q = ((uint32_t)e << 3) | (man >> 20);
-  const uint32_t rem = man & 0xfffffu;
-  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q++;
-  if (q > 0x7eu) q = 0x7eu;
-  return (uint8_t)(sign | q);
-}
-
 // Max over the 16 lanes of a DPP row (lanes 16g .. 16g+15), in every lane of
 // the row: quad butterflies (quad_perm [1,0,3,2] and [2,3,0,1]), then the row
 // rotated by 4 and by 8 lanes.  No LDS round trip.
@@ -356,8 +321,6 @@ __global__ __launch_bounds__(256) void write_blocks_row_kernel(const WriteBlocks
   }
 }
 
-// fp8 e4m3 code as f32 (exact).
-__device__ __forceinline__ float decode_e4m3(uint32_t code) { return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0]; }
 
 // Appends one token row (this wavefront's kv head) into an fp8 block whose
 // scale is per (block, head) and tensor: the block's scale becomes

@@ -2,12 +2,16 @@
 replaces: llh_kv_append of each sequence's new token at position len - 1, then
 llh_paged_decode (crates/llm-backend/src/core/native_attention.rs:307-329).
 
-bf16 pools on the tuned kernels run it as one launch (the new token is attended
-from the input rows and written to its slot by the wavefront that computes the
-sequence's last block); the pool must end up bit-identical to the two-call
-path's and the output within the parity bar of the oracle run on that pool.
-Other pool formats take the append kernel, then the decode: bit-identical to
-the two calls.
+Every pool format runs it as one launch on the tuned kernels, except fp8 pools on
+the persistent stream kernel, which append through the append kernel first (the
+fused fp8 re-encode made that kernel slower than the launch it saves).  bf16: the new
+token is attended from the input rows and written to its slot by the wavefront
+that computes the sequence's last block; the pool must end up bit-identical to
+the two-call path's and the output within the parity bar of the oracle run on
+that pool.  int8 / fp8: that wavefront quantises the token into the block it
+loaded, exactly as the append kernel would (fp8: re-encoding the block's earlier
+tokens when the block scale grows), attends the block as stored and writes it
+back: pool and output bit-identical to the two calls.
 """
 import math
 
@@ -49,13 +53,18 @@ def assert_pools_equal(batch, raw_a, raw_b):
         assert np.array_equal(a, b), key
 
 
-def run_both(ctx, batch, Hq, Hkv, fmt, window, seed):
-    """Returns (fused output, two-call output, fused pool raw, two-call pool raw, ref)."""
+def run_both(ctx, batch, Hq, Hkv, fmt, window, seed, mag=None):
+    """Returns (fused output, two-call output, fused pool raw, two-call pool raw, ref).
+    mag: optional per-sequence factors for the new rows (> 1 grows an fp8 block's scale)."""
     import torch
 
     scale = 1.0 / math.sqrt(D)
     B = batch.seq_lens.size
     kn, vn = new_rows(seed, B, Hkv)
+    if mag is not None:
+        f = np.asarray(mag, np.float32)[:, None, None]
+        kn = oracle.f32_to_bf16(oracle.bf16_to_f32(kn.ravel()).reshape(kn.shape) * f).reshape(kn.shape)
+        vn = oracle.f32_to_bf16(oracle.bf16_to_f32(vn.ravel()).reshape(vn.shape) * f[::-1]).reshape(vn.shape)
     outs, raws = [], []
     for fused in (True, False):
         pool, q = build_case(ctx, batch, Hq, Hkv, fmt, seed)
@@ -129,18 +138,71 @@ def test_decode_append_single_token_is_its_value(ctx):
         assert np.array_equal(k[blk, :, 0, :], kn[b])
 
 
+@pytest.mark.parametrize("kernel", ["split", "stream"])
 @pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
-def test_decode_append_quantized_pools_equal_two_calls(ctx, fmt):
-    """int8 / fp8 pools take the append kernel, then the decode: bit-identical to the
-    two calls, pool and output."""
-    lens = np.array([40, 1, 500, 16, 1777], np.int32)
-    batch = workloads.paged_batch(lens, BT, 0.10, 21)
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (32, 8), (8, 8), (64, 8)])
+def test_decode_append_quantized_one_launch(ctx, opts, kernel, fmt, Hq, Hkv):
+    """int8 / fp8 pools, one launch (fp8 on the stream kernel: two), both kernels, the
+    token-lane (G <= 4) and row (G = 8) layouts: pool and output bit-identical to
+    llh_kv_append + llh_paged_decode.  New tokens land at every offset class (0,
+    mid-block, 15); half of them are 4x larger than the block's rows, so fp8 block scales
+    grow and earlier tokens are re-encoded."""
+    opts(llm_hip.OPT_DECODE_KERNEL, kernel)
+    launches = 0 if (fmt == llm_hip.KV_FP8_E4M3 and kernel == "stream") else 1
+    lens = np.array([40, 1, 500, 16, 1777, 17, 33, 2048, 4095, 129, 64, 300], np.int32)
+    batch = workloads.paged_batch(lens, BT, 0.10, 21 + Hq)
+    mag = [4.0 if i % 2 else 1.0 for i in range(lens.size)]
+    for window in (0, 300):
+        before = ctx.metrics()["fused_append_calls"]
+        fused, two, raw_f, raw_t, ref = run_both(ctx, batch, Hq, Hkv, fmt, window, 50 + fmt + window, mag)
+        assert ctx.metrics()["fused_append_calls"] == before + launches
+        assert_pools_equal(batch, raw_f, raw_t)
+        assert np.array_equal(fused, two), f"fmt {fmt} {kernel} Hq{Hq} W={window}"
+        assert_parity(fused, ref, what=f"fmt {fmt} {kernel} Hq{Hq} W={window}")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_append_quantized_c5_full_launch(ctx, opts, fmt):
+    """The C5 step (64 x 8192, Hq32/Hkv8) on the stream kernel: one fused launch for
+    int8, the append kernel then the decode for fp8."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "auto")
+    batch = workloads.paged_batch(np.full(64, 8192, np.int32), BT, 0.0, 22)
     before = ctx.metrics()["fused_append_calls"]
-    fused, two, raw_f, raw_t, ref = run_both(ctx, batch, 16, 8, fmt, 0, 50 + fmt)
-    assert ctx.metrics()["fused_append_calls"] == before
+    fused, two, raw_f, raw_t, ref = run_both(ctx, batch, 32, 8, fmt, 0, 60 + fmt)
+    assert ctx.metrics()["fused_append_calls"] == before + (fmt == llm_hip.KV_INT8)
     assert_pools_equal(batch, raw_f, raw_t)
     assert np.array_equal(fused, two)
-    assert_parity(fused, ref, what=f"fmt {fmt}")
+    assert_parity(fused, ref, what=f"C5 fused fmt {fmt}")
+
+
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+def test_decode_append_quantized_non_finite_row(ctx, fmt):
+    """A NaN in one sequence's new row: flagged and not appended (as llh_kv_append), and the
+    other sequences' pool bytes and outputs still equal the two calls'."""
+    import torch
+
+    Hq, Hkv = 16, 8
+    lens = np.array([40, 300, 77], np.int32)
+    batch = workloads.paged_batch(lens, BT, 0.10, 23)
+    kn, vn = new_rows(70, lens.size, Hkv)
+    kn = kn.copy()
+    kn[1, 3, 7] = 0x7FC0
+    outs, raws = [], []
+    for fused in (True, False):
+        pool, q = build_case(ctx, batch, Hq, Hkv, fmt, 71)
+        desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(batch.tables), Hq, int(lens.max()))
+        out = torch.zeros(lens.size * Hq * D, dtype=torch.int16, device="cuda")
+        if fused:
+            ctx.paged_decode_append(pool, desc, to_dev(kn), to_dev(vn), to_dev(q), out, 0.09)
+        else:
+            ctx.append(pool, to_dev(slots_of(batch)), to_dev(kn), to_dev(vn))
+            ctx.paged_decode(pool, desc, to_dev(q), out, 0.09)
+        torch.cuda.synchronize()
+        assert ctx.device_errors() & llm_hip.ERR_FLAG_NON_FINITE
+        outs.append(from_dev_bf16(out).reshape(lens.size, -1))
+        raws.append(pool.raw())
+    assert_pools_equal(batch, raws[0], raws[1])
+    assert np.array_equal(outs[0][[0, 2]], outs[1][[0, 2]])
 
 
 def test_fp8_append_over_a_window_ring_needs_one_block_more(ctx):
