@@ -51,7 +51,7 @@ def log(msg: str) -> None:
 class DecodeWorkload:
     """A paged batch resident on the device plus its descriptor."""
 
-    def __init__(self, ctx, lens, Hq, Hkv, fmt, window=0, resident_from=None, seed=0, free_frac=0.10):
+    def __init__(self, ctx, lens, Hq, Hkv, fmt, window=0, resident_from=None, seed=0, free_frac=0.10, head_dim=D):
         import torch
         import llm_hip
         from llm_hip import workloads
@@ -59,6 +59,7 @@ class DecodeWorkload:
         self.torch = torch
         self.ctx = ctx
         self.Hq, self.Hkv, self.fmt, self.window = Hq, Hkv, fmt, window
+        self.D = D = head_dim
         self.batch = workloads.paged_batch(lens, BT, free_frac, seed, resident_from)
         b = self.batch
         self.pool = ctx.pool(fmt, BT, Hkv, D, b.n_blocks)
@@ -97,7 +98,7 @@ class DecodeWorkload:
         return lens - lo, lo
 
     def algorithmic_bytes(self) -> int:
-        return decode_bytes(self.batch.seq_lens, self.Hq, self.Hkv, self.fmt, self.window)
+        return decode_bytes(self.batch.seq_lens, self.Hq, self.Hkv, self.fmt, self.window, self.D)
 
     def bound(self, key, name, *args):
         """The C call `name` with its arguments converted once (Context.bind), per stream."""
@@ -121,8 +122,8 @@ class DecodeWorkload:
         self.d_slots = self.torch.from_numpy(blocks * BT + pos % BT).cuda()
         g = self.torch.Generator(device="cuda")
         g.manual_seed(int(lens.sum()))
-        self.k_new = self.torch.randn((lens.size, self.Hkv, D), generator=g, device="cuda").to(self.torch.bfloat16)
-        self.v_new = self.torch.randn((lens.size, self.Hkv, D), generator=g, device="cuda").to(self.torch.bfloat16)
+        self.k_new = self.torch.randn((lens.size, self.Hkv, self.D), generator=g, device="cuda").to(self.torch.bfloat16)
+        self.v_new = self.torch.randn((lens.size, self.Hkv, self.D), generator=g, device="cuda").to(self.torch.bfloat16)
 
     def append_step(self, stream):
         """kir-ai's decode step order (native_attention.rs:307-329): append the new token, then attend."""
@@ -140,7 +141,7 @@ class DecodeWorkload:
         B = self.batch.seq_lens.size
         elem = 2 if self.fmt == self.llm_hip.KV_BF16 else 1
         scales = B * self.Hkv * 2 * 2 if self.fmt == self.llm_hip.KV_INT8 else 0
-        return B * self.Hkv * D * 2 * 2 + B * self.Hkv * D * elem * 2 + scales + B * 8
+        return B * self.Hkv * self.D * 2 * 2 + B * self.Hkv * self.D * elem * 2 + scales + B * 8
 
 
 def settle(fn, stream, seconds: float) -> None:
@@ -560,7 +561,7 @@ LLC_BYTES = 256 << 20  # MI355X Infinity Cache (memory-side last-level cache)
 
 
 def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resident_from=None, seed=0, free=0.10,
-                   append=False, fused=False, graph=False):
+                   append=False, fused=False, graph=False, head_dim=D):
     """Mean step time over `steps` decode steps.  Steps rotate over enough independent
     copies of the workload (same lengths, own pool, own block permutation and data) that
     the bytes read between two visits of one copy exceed the 256 MB Infinity Cache: every
@@ -570,11 +571,12 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     the step replayed from a HIP graph (llh_paged_decode_noalloc, one call per copy): the
     GPU's own time per step, free of the host's per-call launch cost, which sets the pace of
     small steps issued one call at a time (host_us_per_call)."""
-    first = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free)
+    first = DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed, free, head_dim)
     nbytes = first.algorithmic_bytes() + (first.append_bytes() if append or fused else 0)
     copies = [first]
     while (len(copies) - 1) * nbytes < 2 * LLC_BYTES:
-        copies.append(DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed + 1000 * len(copies), free))
+        copies.append(DecodeWorkload(ctx, lens, Hq, Hkv, fmt, window, resident_from, seed + 1000 * len(copies), free,
+                                     head_dim))
     if append or fused:
         for c in copies:
             c.prepare_append()
@@ -636,7 +638,7 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
     }
 
 
-def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0) -> int:
+def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0, head_dim: int = D) -> int:
     """Algorithmic bytes of one decode step: K and V of every attended position (+ int8 /
     fp8 scales), q and out, the block-table entries read and the lengths."""
     import numpy as np
@@ -645,10 +647,10 @@ def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0) -> int:
     lo = np.maximum(0, lens - window) if window > 0 else np.zeros_like(lens)
     rows = lens - lo
     elem = 2 if fmt == 0 else 1
-    kv = int(rows.sum()) * Hkv * D * elem * 2
+    kv = int(rows.sum()) * Hkv * head_dim * elem * 2
     blocks = ((lens + BT - 1) // BT) - lo // BT
     scales = int(rows.sum()) * Hkv * 4 if fmt == 1 else (int(blocks.sum()) * Hkv * 8 if fmt == 2 else 0)
-    return kv + scales + 2 * lens.size * Hq * D * 2 + int(blocks.sum()) * 4 + lens.size * 4
+    return kv + scales + 2 * lens.size * Hq * head_dim * 2 + int(blocks.sum()) * 4 + lens.size * 4
 
 
 def prefill_flops(B: int, prefix: int, chunk: int, Hq: int, window: int) -> int:
@@ -813,8 +815,8 @@ def traffic_from_profile(kernel: str):
 
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
-SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "neighbours", "trait", "c3", "c4prefill", "c3int8",
-            "c3fp8")
+SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "q36", "neighbours", "trait", "c3", "c4prefill",
+            "c3int8", "c3fp8")
 
 
 def run_sections(ctx, args, lens, sel) -> list:
@@ -875,6 +877,13 @@ def run_sections(ctx, args, lens, sel) -> list:
         secondary.append(r)
         log(f"C5 {nm} fused append+attend: {r}")
         torch.cuda.empty_cache()
+    if sel("q36"):
+        # Qwen3.6 full-attention layer (fixtures/qwen36/config.json: Hq16 / Hkv2, head_dim 256) on C2's
+        # lengths, bf16 blocks: the head_dim-256 kernel
+        _, r = measure_decode(ctx, "Q36 decode B=32 L~U[256,4096] Hq16/Hkv2 D=256", lens, 16, 2, llm_hip.KV_BF16,
+                              sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, head_dim=256)
+        secondary.append(r)
+        log(f"Q36 decode: {r}")
     if sel("neighbours"):
         secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))
     if sel("trait"):

@@ -40,7 +40,8 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 5  /* 5: per-stream device error words, llh_layer_cache_create_from_rows;
+#define LLH_ABI_VERSION 6  /* 6: head_dim-256 decode kernel, llh_metrics.d256_decode_calls, gate fields;
+                              5: per-stream device error words, llh_layer_cache_create_from_rows;
                               4: int8 and fp8 pools store their scales as (K, V) pairs */
 
 /* Status codes.  Mirrors MathError / KvCacheError
@@ -113,7 +114,7 @@ typedef enum llh_option {
 } llh_option;
 int llh_ctx_set_option(llh_ctx *ctx, int32_t option, int32_t value);
 int llh_ctx_get_option(const llh_ctx *ctx, int32_t option, int32_t *value);
-/* Workspace bytes a llh_paged_decode call with these bounds needs. */
+/* Workspace bytes a llh_paged_decode call with these bounds needs (any head_dim up to 256). */
 size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len);
 /* Fallback/attempt counters, as MetalBackendMetrics' attention counters
  * (crates/llm-native-runtime/src/native_metrics.rs:73-112). */
@@ -130,6 +131,7 @@ typedef struct llh_metrics {
   uint64_t fused_append_calls;    /* llh_paged_decode_append calls served by one launch */
   uint64_t stream_slots;          /* streams holding a workspace slot (scratch and error word) now */
   uint64_t workspace_bytes;       /* device bytes of those slots' scratch now */
+  uint64_t d256_decode_calls;     /* decode calls that ran the head_dim-256 kernel */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Sticky error flags the batched kernels raise instead of faulting: 1 = a

@@ -69,6 +69,7 @@ void read_env_options(llh_ctx *ctx) {
 // The total work comes from the caller's hint when given, else from the
 // max_seq_len bound.
 constexpr int kMaxDecodeSplits = 1024;  // partials one merge workgroup combines
+constexpr int kD256MaxSplits = 64;      // partials the head_dim-256 merge combines
 
 struct SplitPlan {
   int split_blocks;
@@ -295,7 +296,10 @@ size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t
   const size_t srows = (size_t)2 * 4 * kStreamMaxWgs * std::min(num_q_heads, 8);
   const size_t stream = align_up(srows * sizeof(float2)) + align_up(srows * kFastHeadDim * sizeof(float)) +
                         align_up((size_t)num_seqs * num_q_heads * 2 * sizeof(int32_t));
-  return std::max({align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic, stream});
+  // head_dim-256 kernel: at most kD256MaxSplits partial rows per (sequence, head), 256 floats each
+  const size_t rows256 = (size_t)num_seqs * num_q_heads * std::min<size_t>(max_splits, kD256MaxSplits);
+  const size_t d256 = align_up(rows256 * sizeof(float2)) + rows256 * kD256HeadDim * sizeof(float);
+  return std::max({align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic, stream, d256});
 }
 
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
@@ -310,6 +314,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->trait_tuned_calls = ctx->trait_tuned_calls.load();
   out->generic_prefill_calls = ctx->generic_prefill_calls.load();
   out->fused_append_calls = ctx->fused_append_calls.load();
+  out->d256_decode_calls = ctx->d256_decode_calls.load();
   std::lock_guard<std::mutex> g(const_cast<llh_ctx *>(ctx)->ws_mu);
   out->stream_slots = ctx->workspaces.size();
   out->workspace_bytes = 0;
@@ -591,6 +596,26 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   plan->fast = pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
                rows_aligned &&
                (group == 1 || group == 2 || group == 4 || group == 8) && !ctx->opt(LLH_OPT_FORCE_GENERIC);
+  // head_dim 256 (Qwen3.5 / 3.6 full attention: Hq16 / Hkv2): bf16 pools, G = 8
+  plan->d256 = pv.format == LLH_KV_BF16 && pv.head_dim == kD256HeadDim && pv.block_tokens == kFastBlockTokens &&
+               rows_aligned && group == 8 && !ctx->opt(LLH_OPT_FORCE_GENERIC);
+  if (plan->d256) {
+    plan->fast = true;
+    SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
+                               desc->total_tokens_hint, pv.format);
+    // the merge takes at most kD256MaxSplits partials: longer spans get longer splits
+    while (sp.max_splits > kD256MaxSplits) {
+      sp.split_blocks *= 2;
+      sp.max_splits = (sp.est_blocks + sp.split_blocks - 1) / sp.split_blocks;
+    }
+    plan->split_blocks = sp.split_blocks;
+    plan->max_splits = sp.max_splits;
+    const size_t rows = (size_t)desc->num_seqs * desc->num_q_heads * sp.max_splits;
+    plan->ml_off = 0;
+    plan->o_off = align_up(rows * sizeof(float2));
+    plan->bytes = align_up(plan->o_off + rows * kD256HeadDim * sizeof(float));
+    return LLH_OK;
+  }
   if (plan->fast) {
     const SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
                                      desc->total_tokens_hint, pv.format);
@@ -646,6 +671,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
     a.max_seq_len = desc->max_seq_len;
     a.seg_desc = plan.stream_wgs ? reinterpret_cast<int32_t *>(ws + plan.desc_off) : nullptr;
     if (plan.stream_wgs) ctx->stream_decode_calls++;
+    if (plan.d256) ctx->d256_decode_calls++;
     a.scale_log2e = score_scale * 1.4426950408889634f;
     a.k_new = k_new;
     a.v_new = v_new;
@@ -661,7 +687,9 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
       else
         t->ctx->timing_end(0, t->ev, st);
     };
-    hipError_t e = launch_decode(a, plan.group, desc->max_seq_len, s, timed ? &th : nullptr, timed ? hook : nullptr);
+    hipError_t e = plan.d256 ? launch_decode_d256(a, desc->max_seq_len, s, timed ? &th : nullptr, timed ? hook : nullptr)
+                             : launch_decode(a, plan.group, desc->max_seq_len, s, timed ? &th : nullptr,
+                                             timed ? hook : nullptr);
     if (e != hipSuccess) return ctx->hip_fail(e, "decode launch");
     return LLH_OK;
   }
@@ -793,7 +821,7 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   // scale-growth re-encode doubles that kernel's code and costs more than the
   // separate append launch it saves.  Every other case appends through the append
   // kernel first, then decodes.
-  const bool fused = plan.fast && aligned16(d_k_new) && aligned16(d_v_new) &&
+  const bool fused = plan.fast && !plan.d256 && aligned16(d_k_new) && aligned16(d_v_new) &&
                      !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0);
   const size_t slot_bytes = fused ? 0 : align_up((size_t)desc->num_seqs * sizeof(int64_t));
   WsLease lease;

@@ -1,0 +1,405 @@
+// Paged GQA decode attention for head_dim 256 on gfx950 (MI355X): the
+// full-attention layers of Qwen3.5 / 3.6 (fixtures/qwen36/config.json: 16 query
+// heads, 2 kv heads, head_dim 256, so G = 8 query heads per kv head), bf16 K/V in
+// 16-token blocks.  Same contract as the head_dim-128 kernels in decode.hip: per
+// sequence b and query head h,
+//   out[b][h] = sum_t softmax_t(scale * q[b][h] . K[t][kv]) V[t][kv]
+// over the attended positions [lo, len) (crates/llm-backend/src/core/
+// native_attention.rs:731-771; window rule qwen/ops/cache.rs:116-121), times
+// sigmoid(gate) when the call carries a gate (native_attention.rs:765-781).
+//
+// Split-K: one workgroup per (split, kv head, sequence); a split is
+// `split_blocks` consecutive blocks and its four wavefronts take them
+// round-robin.  A single-split sequence writes its output directly, otherwise
+// decode_merge_d256_kernel merges the splits' (max, sum, output) partials.
+//
+// Lane roles per block (64 lanes, row g = lane / 16, c = lane % 16):
+//   K: lane loads token 4g + i (i = 0..3) at dims 8c..8c+7 and 128+8c..+7
+//      (two 256-byte runs per instruction and row) and forms 32 partial dot
+//      products (8 heads x 4 tokens) over its 16 dims.  Query slot s of lane c
+//      holds head s ^ fold(c), fold linear over the bits of c, so the 16-lane
+//      sum becomes a reduce-scatter of three DPP adds on 16, 8 and 4 values
+//      (row_mirror, row_half_mirror, quad swap) and one lane-pair exchange:
+//      afterwards lane c holds the scores of head fold(c) for tokens
+//      4g + 2 (c % 2) + {0, 1}, each computed once per wavefront.
+//   V: lane owns dims 64 j + lane (j = 0..3), all 16 tokens (two 16-byte
+//      loads per dim row): no two lanes accumulate the same output element.
+//   The 64 packed bf16 weight pairs (8 heads x 8 token pairs, one per lane)
+//   reach every lane as scalar registers (v_readlane), the scalar operand of
+//   p . v's dot2 instructions.
+// Running max / sum live in the 8 lanes that score a head; outputs in
+// registers (8 heads x 4 dims per lane).  HBM-bound; no MFMA.
+#include "device_common.h"
+#include "wave_ops.h"
+
+namespace llh {
+
+namespace {
+
+constexpr int D2 = kD256HeadDim;
+constexpr int BT = kFastBlockTokens;
+constexpr int G2 = 8;
+constexpr int kBlockBytes2 = BT * D2 * 2;  // one (block, kv head) of K (and of V), bf16
+constexpr int kMerge256MaxSplits = 64;
+
+// Head of query slot 0 in lane c of a row (and of slot s: s ^ fold(c)).  fold is
+// linear over GF(2) in the bits of c with fold(15) = 4, fold(7) = 2, fold(2) = 1
+// and fold(1) = 0: the lane that a reduce step pairs c with (c ^ 15, c ^ 7,
+// c ^ 2, c ^ 1) holds the same head in the slot 4, 2, 1 (0) places away.
+__host__ __device__ constexpr int fold(int c) {
+  return ((c >> 1) & 1) ^ (((c >> 2) & 1) * 3) ^ (((c >> 3) & 1) * 6);
+}
+// The lane pair (2x, 2x + 1) of a row whose slot-0 head is h.
+__host__ __device__ constexpr int pair_of_head(int h) {
+  int x = 0;
+  while (fold(2 * x) != h) x++;
+  return x;
+}
+static_assert(fold(15) == 4 && fold(7) == 2 && fold(2) == 1 && fold(1) == 0, "reduce-scatter pairing");
+
+struct Kregs {
+  uint4 k[8];  // token 4g + i/2 ... : k[2i] dims 8c..8c+7, k[2i+1] dims 128+8c..+7
+};
+struct Vregs {
+  uint4 v[8];  // v[2j + h]: dim 64j + lane, tokens 8h .. 8h+7
+};
+
+__device__ __forceinline__ const char *block_base(const void *base, int phys, int kvh, int kv_heads) {
+  return reinterpret_cast<const char *>(base) + ((size_t)phys * kv_heads + kvh) * kBlockBytes2;
+}
+
+__device__ __forceinline__ void load_k(const DecodeArgs &a, int phys, int kvh, int lane, Kregs &r) {
+  const char *kb = block_base(a.pool.k, phys, kvh, a.pool.kv_heads) + (lane >> 4) * 4 * (D2 * 2) + (lane & 15) * 16;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    r.k[2 * i] = ld_nt16(kb + i * (D2 * 2));
+    r.k[2 * i + 1] = ld_nt16(kb + i * (D2 * 2) + 256);
+  }
+}
+
+__device__ __forceinline__ void load_v(const DecodeArgs &a, int phys, int kvh, int lane, Vregs &r) {
+  const char *vb = block_base(a.pool.v, phys, kvh, a.pool.kv_heads) + lane * (BT * 2);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    r.v[2 * j] = ld_nt16(vb + j * 64 * (BT * 2));
+    r.v[2 * j + 1] = ld_nt16(vb + j * 64 * (BT * 2) + 16);
+  }
+}
+
+struct State256 {
+  float m;        // running max (log2 units) of this lane's head fold(c)
+  float l;        // this lane's share of that head's weight sum
+  float o[G2][4]; // head h, dim 64j + lane
+};
+
+// First half of one block: scores, online softmax.  jb: the block's index in the
+// sequence (positions 16 jb ..); valid: its table entry is inside the pool.
+// Returns this lane's packed weight pair (head fold(c), tokens 4g + 2 (c % 2) + {0, 1})
+// and, per token pair, the mask that zeroes V of unattended tokens.
+__device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kregs &kr, bool valid, int jb, int lo,
+                                                 int len, int lane, const uint32_t (&qw)[G2][8], State256 &st,
+                                                 uint32_t (&vm)[8]) {
+  const int g = lane >> 4;
+  const int b0 = lane & 1;
+  // ---- partial q . k: slot s, token 4g + i, over this lane's 16 dims ----
+  float p[G2][4];
+#pragma unroll
+  for (int s = 0; s < G2; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint4 lo4 = kr.k[2 * i], hi4 = kr.k[2 * i + 1];
+      float acc = dot2_bf16(lo4.x, qw[s][0], 0.0f);
+      acc = dot2_bf16(lo4.y, qw[s][1], acc);
+      acc = dot2_bf16(lo4.z, qw[s][2], acc);
+      acc = dot2_bf16(lo4.w, qw[s][3], acc);
+      acc = dot2_bf16(hi4.x, qw[s][4], acc);
+      acc = dot2_bf16(hi4.y, qw[s][5], acc);
+      acc = dot2_bf16(hi4.z, qw[s][6], acc);
+      acc = dot2_bf16(hi4.w, qw[s][7], acc);
+      p[s][i] = acc;
+    }
+  // ---- reduce-scatter over the row (see fold) ----
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[s][i] += row_mirror(p[s + 4][i]);
+#pragma unroll
+  for (int s = 0; s < 2; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[s][i] += dpp<0x141>(p[s + 2][i]);  // row_half_mirror
+#pragma unroll
+  for (int i = 0; i < 4; i++) p[0][i] += dpp<0x4E>(p[1][i]);  // quad_perm [2,3,0,1]
+  float sc[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const float keep = b0 ? p[0][2 + k] : p[0][k];
+    const float send = b0 ? p[0][k] : p[0][2 + k];
+    sc[k] = (keep + dpp<0xB1>(send)) * a.scale_log2e;  // quad_perm [1,0,3,2]
+  }
+  // ---- mask: tokens outside [lo, len) or in a block outside the pool ----
+  const bool partial = (jb * BT < lo) || (jb * BT + BT > len) || !valid;
+  // per token pair of V: zero what is not attended (slots may hold garbage)
+#pragma unroll
+  for (int t = 0; t < 8; t++) vm[t] = 0xffffffffu;
+  if (partial) {
+    const int pos = jb * BT + 4 * g + 2 * b0;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+      if (!(valid && pos + k >= lo && pos + k < len)) sc[k] = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const int p0 = jb * BT + 2 * t;
+      const bool ok0 = valid && p0 >= lo && p0 < len;
+      const bool ok1 = valid && p0 + 1 >= lo && p0 + 1 < len;
+      vm[t] = (ok0 ? 0xffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
+    }
+  }
+  // ---- online softmax per head (the 8 lanes of a head agree on every value) ----
+  float mx = fmaxf(sc[0], sc[1]);
+  mx = fmaxf(mx, dpp<0xB1>(mx));
+  mx = fmaxf(mx, xor16_other(mx, lane));
+  mx = fmaxf(mx, xor32_other(mx, lane));
+  const bool grow = mx > st.m + 8.0f;  // lazy rescale: weights stay below 2^8; true on the first finite block
+  if (__any(grow)) {
+    const float nm = grow ? mx : st.m;
+    const float alpha = grow ? fast_exp2(st.m - nm) : 1.0f;  // 0 when st.m = -inf
+    st.m = nm;
+    st.l *= alpha;
+#pragma unroll
+    for (int h = 0; h < G2; h++) {
+      const float al = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), 2 * pair_of_head(h)));
+#pragma unroll
+      for (int j = 0; j < 4; j++) st.o[h][j] *= al;
+    }
+  }
+  const float mref = (st.m == -INFINITY) ? 0.0f : st.m;
+  const uint32_t w = pack_bf16(fast_exp2(sc[0] - mref), fast_exp2(sc[1] - mref));
+  st.l = dot2_ones(w, st.l);  // the normaliser sums exactly the bf16 weights that enter p . v
+  return w;
+}
+
+// Second half: p . v over this lane's 4 dims for every head, head h's weights as
+// scalars read from the lanes that hold them.
+__device__ __forceinline__ void block_accumulate(const Vregs &vr, uint32_t w, const uint32_t (&vm)[8], State256 &st) {
+  uint32_t vv[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint4 a0 = vr.v[2 * j], a1 = vr.v[2 * j + 1];
+    vv[j][0] = a0.x & vm[0];
+    vv[j][1] = a0.y & vm[1];
+    vv[j][2] = a0.z & vm[2];
+    vv[j][3] = a0.w & vm[3];
+    vv[j][4] = a1.x & vm[4];
+    vv[j][5] = a1.y & vm[5];
+    vv[j][6] = a1.z & vm[6];
+    vv[j][7] = a1.w & vm[7];
+  }
+#pragma unroll
+  for (int h = 0; h < G2; h++) {
+    uint32_t sw[8];  // pair t of head h: lane 16 (t / 2) + 2 pair_of_head(h) + t % 2
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+      sw[t] = (uint32_t)__builtin_amdgcn_readlane((int)w, 16 * (t >> 1) + 2 * pair_of_head(h) + (t & 1));
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float acc = st.o[h][j];
+#pragma unroll
+      for (int t = 0; t < 8; t++) acc = dot2_bf16(vv[j][t], sw[t], acc);
+      st.o[h][j] = acc;
+    }
+  }
+}
+
+__device__ __forceinline__ void seq_range256(const DecodeArgs &a, int b, int &len, int &lo, int &first_blk,
+                                             int &n_blk, int &n_splits) {
+  len = a.seq_lens[b];
+  lo = a.window > 0 ? max(0, len - a.window) : 0;
+  first_blk = lo / BT;
+  n_blk = len > lo ? (len - 1) / BT - first_blk + 1 : 0;
+  n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
+}
+
+__global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(const DecodeArgs a) {
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  int len, lo, first_blk, n_blk, n_splits;
+  seq_range256(a, b, len, lo, first_blk, n_blk, n_splits);
+  if (n_splits > a.max_splits) {
+    if (threadIdx.x == 0 && split == 0) atomicOr(a.err, kErrTooManySplits);
+    return;
+  }
+  if (len - lo > a.max_blocks * BT) {  // the span would alias its own table entries
+    if (threadIdx.x == 0 && split == 0) atomicOr(a.err, kErrSpan);
+    return;
+  }
+  if (split >= max(n_splits, 1)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G2;
+  if (n_blk == 0) {  // empty context: zero output (weighted sum of nothing)
+    for (int idx = tid; idx < G2 * D2; idx += kDecodeThreads) a.out[qrow0 * D2 + idx] = 0;
+    return;
+  }
+
+  const int blk_begin = first_blk + split * a.split_blocks;
+  const int blk_end = min(blk_begin + a.split_blocks, first_blk + n_blk);
+  const int nbw = max(0, (blk_end - blk_begin - wave + 3) / 4);
+  typedef const __attribute__((address_space(4))) int32_t table_elem_t;
+  const table_elem_t *stable = (const table_elem_t *)(a.tables + (size_t)b * a.max_blocks);
+  auto entry = [&](int k) __attribute__((always_inline)) -> int {
+    return stable[(blk_begin + wave + 4 * k) % a.max_blocks];
+  };
+
+  // query slot s of this lane: head s ^ fold(c), dims 8c..8c+7 and 128+8c..+7
+  uint32_t qw[G2][8];
+  {
+    const int c = lane & 15;
+#pragma unroll
+    for (int s = 0; s < G2; s++) {
+      const uint16_t *qr = a.q + (qrow0 + (size_t)(s ^ fold(c))) * D2 + 8 * c;
+      const uint4 x = *reinterpret_cast<const uint4 *>(qr);
+      const uint4 y = *reinterpret_cast<const uint4 *>(qr + 128);
+      qw[s][0] = x.x, qw[s][1] = x.y, qw[s][2] = x.z, qw[s][3] = x.w;
+      qw[s][4] = y.x, qw[s][5] = y.y, qw[s][6] = y.z, qw[s][7] = y.w;
+    }
+  }
+
+  State256 st;
+  st.m = -INFINITY;
+  st.l = 0.0f;
+#pragma unroll
+  for (int h = 0; h < G2; h++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) st.o[h][j] = 0.0f;
+
+  if (nbw > 0) {
+    // K of the next block loads behind this block's p . v, V of the next block
+    // behind the next block's q . k: one block's registers, always a load in flight
+    int e = entry(0);
+    bool valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
+    int phys = valid ? e : 0;
+    Kregs kr;
+    Vregs vr;
+    load_k(a, phys, kvh, lane, kr);
+    load_v(a, phys, kvh, lane, vr);
+    for (int k = 0; k < nbw; k++) {
+      const int jb = blk_begin + wave + 4 * k;
+      if (!valid && lane == 0) atomicOr(a.err, kErrBadBlock);  // its tokens are all masked
+      uint32_t vm[8];
+      const uint32_t w = block_scores(a, kr, valid, jb, lo, len, lane, qw, st, vm);
+      const bool more = k + 1 < nbw;
+      if (more) {
+        e = entry(k + 1);
+        valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
+        phys = valid ? e : 0;
+        load_k(a, phys, kvh, lane, kr);
+      }
+      block_accumulate(vr, w, vm, st);
+      if (more) load_v(a, phys, kvh, lane, vr);
+    }
+  }
+
+  // ---- wavefront totals, then merge the four wavefronts through LDS ----
+  float l = st.l + dpp<0xB1>(st.l);
+  l += xor16_other(l, lane);
+  l += xor32_other(l, lane);
+  __shared__ float s_o[4][G2][D2];
+  __shared__ float s_m[4][G2];
+  __shared__ float s_l[4][G2];
+#pragma unroll
+  for (int h = 0; h < G2; h++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) s_o[wave][h][64 * j + lane] = st.o[h][j];
+  if (lane < 16 && (lane & 1) == 0) {
+    s_m[wave][fold(lane)] = st.m;
+    s_l[wave][fold(lane)] = l;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G2 * D2; idx += kDecodeThreads) {
+    const int gi = idx / D2;
+    const int d = idx % D2;
+    const float mm = fmaxf(fmaxf(s_m[0][gi], s_m[1][gi]), fmaxf(s_m[2][gi], s_m[3][gi]));
+    const float mref = (mm == -INFINITY) ? 0.0f : mm;
+    float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float f = fast_exp2(s_m[w][gi] - mref);
+      ll += s_l[w][gi] * f;
+      oo += s_o[w][gi][d] * f;
+    }
+    if (n_splits == 1) {
+      a.out[(qrow0 + gi) * D2 + d] = f32_to_bf16_rne(gated(oo / ll, a.gate, (qrow0 + gi) * D2 + d));
+    } else {
+      const size_t row = (qrow0 + gi) * a.max_splits + split;
+      a.ws_o[row * D2 + d] = oo;
+      if (d == 0) a.ws_ml[row] = make_float2(mm, ll);
+    }
+  }
+}
+
+// Merge of n <= N <= 64 split partials of one (sequence, query head): every
+// partial row in flight at once, the (max, sum) pairs one per lane, reduced
+// with DPP and row exchanges; split weights reach the lanes through v_readlane.
+template <int N>
+__device__ __forceinline__ void merge256(const DecodeArgs &a, size_t row0, int last, int d, size_t orow) {
+  float o_sp[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) o_sp[i] = a.ws_o[(row0 + min(i, last)) * D2 + d];
+  const int li = d & 63;
+  const float2 ml = a.ws_ml[row0 + min(li, last)];
+  const float mx = li <= last ? ml.x : -INFINITY;
+  float mm = fmaxf(mx, dpp<0xB1>(mx));
+  mm = fmaxf(mm, dpp<0x4E>(mm));
+  mm = fmaxf(mm, dpp<0x141>(mm));
+  mm = fmaxf(mm, dpp<0x140>(mm));
+  mm = fmaxf(mm, xor16_other(mm, li));
+  mm = fmaxf(mm, xor32_other(mm, li));
+  const float mref = (mm == -INFINITY) ? 0.0f : mm;
+  const float f = li <= last ? fast_exp2(mx - mref) : 0.0f;
+  float ll = f * ml.y;
+  ll = row_sum16(ll);
+  ll += xor16_other(ll, li);
+  ll += xor32_other(ll, li);
+  float oo = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; i++) oo += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), i)) * o_sp[i];
+  a.out[orow * D2 + d] = f32_to_bf16_rne(gated(oo / ll, a.gate, orow * D2 + d));
+}
+
+__global__ __launch_bounds__(D2) void decode_merge_d256_kernel(const DecodeArgs a) {
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  int len, lo, first_blk, n_blk, n_splits;
+  seq_range256(a, b, len, lo, first_blk, n_blk, n_splits);
+  if (n_splits <= 1 || n_splits > a.max_splits || n_splits > kMerge256MaxSplits || len - lo > a.max_blocks * BT)
+    return;
+  const int d = threadIdx.x;
+  const size_t row0 = ((size_t)b * a.q_heads + h) * a.max_splits;
+  const size_t orow = (size_t)b * a.q_heads + h;
+  const int last = n_splits - 1;
+  if (n_splits <= 8) return merge256<8>(a, row0, last, d, orow);
+  if (n_splits <= 16) return merge256<16>(a, row0, last, d, orow);
+  if (n_splits <= 32) return merge256<32>(a, row0, last, d, orow);
+  return merge256<64>(a, row0, last, d, orow);
+}
+
+}  // namespace
+
+hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
+  if (a.max_splits > kMerge256MaxSplits) return hipErrorInvalidValue;
+  const int max_blk = (max_seq_len + BT - 1) / BT + 1;
+  const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
+  if (hook) hook(hu, 0, s);
+  dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
+  hipLaunchKernelGGL(paged_decode_d256_kernel, grid, dim3(kDecodeThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (hook) hook(hu, 1, s);
+  if (e != hipSuccess || a.max_splits <= 1) return e;
+  hipLaunchKernelGGL(decode_merge_d256_kernel, dim3(a.q_heads, a.num_seqs), dim3(D2), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace llh

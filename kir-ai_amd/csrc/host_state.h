@@ -50,7 +50,8 @@ struct llh_ctx {
   int cus = 256;  // compute units of the device (sizes the persistent decode grid)
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
-      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0}, fused_append_calls{0};
+      shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0}, fused_append_calls{0},
+      d256_decode_calls{0};
   std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
 
   // per-stream workspaces; ws_mu guards the list, ws_min_bytes and retired_flags
@@ -201,6 +202,7 @@ namespace llh {
 struct DecodePlan {
   bool empty = false;  // nothing to launch (no sequences)
   bool fast = false;   // tuned kernels (else the reference-order kernel)
+  bool d256 = false;   // tuned: the head_dim-256 (G = 8, bf16) split-K kernel
   int group = 0;
   int split_blocks = 0, max_splits = 0, stream_wgs = 0;
   size_t ml_off = 0, o_off = 0, desc_off = 0;  // tuned: partial (max, sum), partial outputs, segment descriptors

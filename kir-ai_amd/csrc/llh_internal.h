@@ -8,6 +8,7 @@
 namespace llh {
 
 constexpr int kFastHeadDim = 128;   // head_dim of the tuned kernels
+constexpr int kD256HeadDim = 256;   // head_dim of the tuned G = 8 bf16 decode kernel (decode256.hip)
 constexpr int kFastBlockTokens = 16;  // block_tokens of the tuned kernels
 constexpr int kDecodeThreads = 256;   // 4 wavefronts
 constexpr int kPrefillThreads = 256;  // 4 wavefronts, 32 query rows each
@@ -56,11 +57,11 @@ struct PoolView {
 // Split-K decode over the tuned shape (head_dim 128, 16-token blocks).
 struct DecodeArgs {
   PoolView pool;
-  const uint16_t *q;        // [B][Hq][128] bf16
-  uint16_t *out;            // [B][Hq][128] bf16
+  const uint16_t *q;        // [B][Hq][D] bf16 (D = 128, or 256 on the head_dim-256 kernel)
+  uint16_t *out;            // [B][Hq][D] bf16
   const int32_t *seq_lens;  // [B]
   const int32_t *tables;    // [B][max_blocks]
-  float *ws_o;              // [B][Hq][max_splits][128]
+  float *ws_o;              // [B][Hq][max_splits][D]
   float2 *ws_ml;            // [B][Hq][max_splits]  (running max in log2 units, sum)
   int32_t *err;             // error flags
   int32_t num_seqs;
@@ -78,7 +79,7 @@ struct DecodeArgs {
   // computes the sequence's last block; null: plain decode
   const uint16_t *k_new;
   const uint16_t *v_new;
-  const uint16_t *gate;     // null, or [B][Hq][128] bf16: out = attention * sigmoid(gate)
+  const uint16_t *gate;     // null, or [B][Hq][D] bf16: out = attention * sigmoid(gate)
 };
 
 // Reference-order decode for any head_dim / block size / group size.
@@ -192,6 +193,9 @@ int matvec_ksplit(int rows, int cols, int n, int cus);
 typedef void (*LaunchHook)(void *user, int phase, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int group, int max_seq_len, hipStream_t s, void *hook_user = nullptr,
                          LaunchHook hook = nullptr);
+// head_dim 256, G = 8, bf16 pools, split-K (a.stream_wgs = 0, a.max_splits <= 64, no fused append)
+hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hook_user = nullptr,
+                              LaunchHook hook = nullptr);
 hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_f32, hipStream_t s);
 // heads_per_wg: query heads of one kv head that share a workgroup's K/V tiles (1 or 2; 2 needs an even group)
 // prefill kernels: one query head per workgroup, or two heads of a kv head

@@ -136,6 +136,7 @@ class Metrics(ctypes.Structure):
         ("fused_append_calls", ctypes.c_uint64),
         ("stream_slots", ctypes.c_uint64),
         ("workspace_bytes", ctypes.c_uint64),
+        ("d256_decode_calls", ctypes.c_uint64),
     ]
 
 

@@ -50,19 +50,20 @@ def code(pos, kvh: int):
     return ((pos >> 4) * 37 + (pos & 15) * 11) & 127
 
 
-def coded_rows(lo: int, hi: int, kv_heads: int, dims: int = D) -> np.ndarray:
-    """Value rows of positions [lo, hi): uint16 bf16 [hi-lo][kv_heads][dims]."""
+def coded_rows(lo: int, hi: int, kv_heads: int, dims: int = D, code_base: int = 0) -> np.ndarray:
+    """Value rows of positions [lo, hi): uint16 bf16 [hi-lo][kv_heads][dims]; kv head h
+    carries code code_base + h (modulo 4) in dims 0..127, zeros above."""
     pos = np.arange(lo, hi, dtype=np.int64)
     r = np.zeros((hi - lo, kv_heads, dims), np.uint16)
     for h in range(kv_heads):
-        r[np.arange(hi - lo), h, code(pos, h)] = ONE_BF16
+        r[np.arange(hi - lo), h, code(pos, code_base + h)] = ONE_BF16
     return r
 
 
-def counts(lo: int, hi: int, kv_heads: int) -> np.ndarray:
+def counts(lo: int, hi: int, kv_heads: int, code_base: int = 0) -> np.ndarray:
     """int64 [kv_heads][128]: how many positions of [lo, hi) carry each code."""
     pos = np.arange(max(lo, 0), max(hi, lo, 0), dtype=np.int64)
-    return np.stack([np.bincount(code(pos, h), minlength=D)[:D] for h in range(kv_heads)])
+    return np.stack([np.bincount(code(pos, code_base + h), minlength=D)[:D] for h in range(kv_heads)])
 
 
 def prefix_counts(lo: int, hi: int, kv_heads: int) -> np.ndarray:
@@ -88,7 +89,7 @@ def recover(out_f32: np.ndarray, n: int, value: float) -> np.ndarray:
     return c.astype(np.int64)
 
 
-def expected_decode(seq_lens, window: int, q_heads: int, kv_heads: int):
+def expected_decode(seq_lens, window: int, q_heads: int, kv_heads: int, code_base: int = 0):
     """(counts [B][Hq][128], n [B]) of the decode step's attended sets."""
     lens = np.asarray(seq_lens, np.int64)
     G = q_heads // kv_heads
@@ -97,19 +98,23 @@ def expected_decode(seq_lens, window: int, q_heads: int, kv_heads: int):
     for b, L in enumerate(lens):
         lo = max(0, int(L) - window) if window > 0 else 0
         n[b] = int(L) - lo
-        c = counts(lo, int(L), kv_heads)
+        c = counts(lo, int(L), kv_heads, code_base)
         out[b] = np.repeat(c, G, axis=0)
     return out, n
 
 
 def check_decode(out_bf16_bits: np.ndarray, seq_lens, window: int, q_heads: int, kv_heads: int, value: float,
-                 what: str = "") -> None:
-    """Recovered counts of every (sequence, query head) equal the reference set's, exactly."""
+                 what: str = "", head_dim: int = D, code_base: int = 0) -> None:
+    """Recovered counts of every (sequence, query head) equal the reference set's, exactly
+    (head_dim > 128: the dims above 128, whose value rows are zero, must be exactly 0)."""
     from oracle import bf16_to_f32
 
     lens = np.asarray(seq_lens, np.int64)
-    got = bf16_to_f32(np.ascontiguousarray(out_bf16_bits).ravel()).reshape(lens.size, q_heads, D)
-    exp, n = expected_decode(lens, window, q_heads, kv_heads)
+    got = bf16_to_f32(np.ascontiguousarray(out_bf16_bits).ravel()).reshape(lens.size, q_heads, head_dim)
+    if head_dim > D:
+        assert np.all(got[:, :, D:] == 0.0), f"{what}: dims above {D} must be zero"
+        got = got[:, :, :D]
+    exp, n = expected_decode(lens, window, q_heads, kv_heads, code_base)
     for b in range(lens.size):
         rec = recover(got[b], int(n[b]), value)
         if not np.array_equal(rec, exp[b]):

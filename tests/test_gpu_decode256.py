@@ -1,0 +1,193 @@
+"""The head_dim-256 decode kernel (decode256.hip): Qwen3.5 / 3.6 full-attention layers,
+16 query heads over 2 kv heads, head_dim 256 (fixtures/qwen36/config.json), bf16 blocks
+of 16 tokens.  Checked against the oracle (the per-head loop of crates/llm-backend/
+src/core/native_attention.rs:731-771, head_dim taken from the call) at the parity bar,
+its attended set bit-exactly with the position-coded probe (tests/attended_set.py), the
+output gate (native_attention.rs:765-781), split counts from 1 to the merge's 64, and
+the entry points that share the plan (noalloc, decode+append)."""
+import math
+
+import numpy as np
+import pytest
+
+import llm_hip
+import oracle
+from attended_set import check_decode, coded_rows
+from helpers import assert_parity, from_dev_bf16, to_dev
+from llm_hip import workloads
+from test_gpu_decode import build_case, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+D = 256
+BT = 16
+HQ, HKV = 16, 2
+
+
+def run(ctx, pool, batch, q, window, scale, Hq=HQ, gate=None, fn="decode", kv_new=None, expect_d256=True):
+    import torch
+
+    B = batch.seq_lens.size
+    out = torch.full((B * Hq * D,), 0x7FC0, dtype=torch.int16, device="cuda")
+    desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(batch.tables), Hq, int(batch.seq_lens.max()), window,
+                           gate=to_dev(gate) if gate is not None else None)
+    before = ctx.metrics()["d256_decode_calls"]
+    if fn == "decode":
+        ctx.paged_decode(pool, desc, to_dev(q), out, scale)
+    elif fn == "noalloc":
+        ctx.paged_decode_noalloc(pool, desc, to_dev(q), out, scale)
+    else:
+        ctx.paged_decode_append(pool, desc, to_dev(kv_new[0]), to_dev(kv_new[1]), to_dev(q), out, scale)
+    torch.cuda.synchronize()
+    assert ctx.device_errors() == 0, ctx.last_error()
+    assert ctx.metrics()["d256_decode_calls"] == before + (1 if expect_d256 else 0)
+    return from_dev_bf16(out)
+
+
+def case(ctx, lens, seed, free=0.10, Hq=HQ):
+    batch = workloads.paged_batch(np.asarray(lens, np.int32), BT, free, seed)
+    pool, q = build_case(ctx, batch, Hq, HKV, llm_hip.KV_BF16, seed, head_dim=D)
+    return batch, pool, q
+
+
+def test_decode256_qwen36_step(ctx):
+    """The Qwen3.6-shaped step: 32 sequences, lengths in [256, 4096], edges included."""
+    lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
+    lens[:6] = [1, 16, 17, 32, 33, 4096]
+    batch, pool, q = case(ctx, lens, 101)
+    scale = 1.0 / math.sqrt(D)
+    out = run(ctx, pool, batch, q, 0, scale)
+    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, scale, head_dim=D),
+                  what="qwen36 step")
+
+
+@pytest.mark.parametrize("window", [1, 17, 100, 4096])
+def test_decode256_windows(ctx, window):
+    lens = np.array([1, 15, 16, 17, 100, 101, 700, 4100, 5000], np.int32)
+    batch, pool, q = case(ctx, lens, 102 + window)
+    out = run(ctx, pool, batch, q, window, 0.0625)
+    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, window, q, 0.0625, head_dim=D),
+                  what=f"W={window}")
+
+
+@pytest.mark.parametrize("split_blocks", [4, 8, 64, 256])
+def test_decode256_split_counts(ctx, opts, split_blocks):
+    """One split (split_blocks 256 over 4096 tokens) up to 64 (4 blocks a split), and the
+    planner's growth of the split past 64 partials for a 20000-token context."""
+    opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, split_blocks)
+    lens = np.array([4096, 20000, 1, 333], np.int32)
+    batch, pool, q = case(ctx, lens, 103)
+    out = run(ctx, pool, batch, q, 0, 0.0625)
+    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"split_blocks {split_blocks}")
+
+
+def test_decode256_is_deterministic(ctx):
+    lens = workloads.uniform_lengths(8, 256, 4096, 104)
+    batch, pool, q = case(ctx, lens, 104)
+    a = run(ctx, pool, batch, q, 0, 0.0625)
+    b = run(ctx, pool, batch, q, 0, 0.0625)
+    assert np.array_equal(a, b)
+
+
+def test_decode256_empty_sequence_is_zero(ctx):
+    lens = np.array([0, 20, 0, 300], np.int32)
+    batch, pool, q = case(ctx, lens, 105)
+    out = run(ctx, pool, batch, q, 0, 0.0625).reshape(4, -1)
+    assert np.all(oracle.bf16_to_f32(out[0]) == 0.0) and np.all(oracle.bf16_to_f32(out[2]) == 0.0)
+    assert_parity(out.ravel(), oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what="empty rows")
+
+
+def test_decode256_bad_block_is_masked_and_flagged(ctx):
+    import torch
+
+    lens = np.array([100, 300], np.int32)
+    batch, pool, q = case(ctx, lens, 106)
+    tables = batch.tables.copy()
+    tables[1, 3] = batch.n_blocks + 5  # outside the pool
+    out = torch.zeros(2 * HQ * D, dtype=torch.int16, device="cuda")
+    desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(tables), HQ, 300, 0)
+    ctx.paged_decode(pool, desc, to_dev(q), out, 0.0625)
+    torch.cuda.synchronize()
+    assert ctx.device_errors(reset=True) & llm_hip.ERR_FLAG_BAD_BLOCK
+    # sequence 0 is untouched by the bad entry
+    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D)
+    assert_parity(from_dev_bf16(out)[: HQ * D], ref[: HQ * D], what="sequence beside the bad block")
+
+
+def gate_rows(seed, n):
+    return oracle.f32_to_bf16(oracle.bf16_to_f32(oracle.normal_bf16(seed, n)) * np.float32(2.0))
+
+
+@pytest.mark.parametrize("window", [0, 333])
+def test_decode256_gate(ctx, window):
+    """The Qwen3.6 attention output gate: out * sigmoid(gate), applied before the bf16 rounding."""
+    lens = workloads.uniform_lengths(16, 1, 3000, 107)
+    batch, pool, q = case(ctx, lens, 107)
+    gate = gate_rows(108, lens.size * HQ * D)
+    out = run(ctx, pool, batch, q, window, 0.0625, gate=gate)
+    ref = oracle.apply_gate(oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, window, q, 0.0625, head_dim=D),
+                            oracle.bf16_to_f32(gate))
+    assert_parity(out, ref, what=f"gated W={window}")
+
+
+def test_decode256_noalloc_matches_decode(ctx):
+    lens = workloads.uniform_lengths(16, 256, 4096, 109)  # partials within the static scratch
+    batch, pool, q = case(ctx, lens, 109)
+    a = run(ctx, pool, batch, q, 0, 0.0625)
+    b = run(ctx, pool, batch, q, 0, 0.0625, fn="noalloc")
+    assert np.array_equal(a, b)
+
+
+def test_decode256_append_then_attend(ctx):
+    """llh_paged_decode_append at head_dim 256: the append kernel, then this kernel; the
+    pool holds the new rows and the output matches the oracle on that pool."""
+    lens = np.array([1, 17, 256, 999, 4096], np.int32)
+    batch, pool, q = case(ctx, lens, 110)
+    kn = oracle.normal_bf16(111, lens.size * HKV * D).reshape(lens.size, HKV, D)
+    vn = oracle.normal_bf16(112, lens.size * HKV * D).reshape(lens.size, HKV, D)
+    out = run(ctx, pool, batch, q, 0, 0.0625, fn="append", kv_new=(kn, vn))
+    raw = pool.raw()
+    k = raw["k"].view(np.uint16).reshape(batch.n_blocks, HKV, BT, D)
+    for b, L in enumerate(lens):
+        p = int(L) - 1
+        blk = batch.tables[b, p // BT]
+        assert np.array_equal(k[blk, :, p % BT, :], kn[b])
+    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D)
+    assert_parity(out, ref, what="append + attend")
+
+
+def coded_case(ctx, lens, seed, code_base):
+    """K random, V one-hot codes of the absolute position (attended_set.coded_rows) in
+    dims 0..127, zeros above."""
+    batch = workloads.paged_batch(np.asarray(lens, np.int32), BT, 0.10, seed)
+    ids, src_k = workloads.block_sources(
+        batch, lambda b, lo, hi: oracle.normal_bf16(seed + b, (hi - lo) * HKV * D).reshape(hi - lo, HKV, D), HKV, D)
+    _, src_v = workloads.block_sources(batch, lambda b, lo, hi: coded_rows(lo, hi, HKV, D, code_base), HKV, D)
+    pool = ctx.pool(llm_hip.KV_BF16, BT, HKV, D, batch.n_blocks)
+    ctx.write_blocks(pool, to_dev(ids), to_dev(src_k), to_dev(src_v))
+    return batch, pool
+
+
+@pytest.mark.parametrize("code_base", [0, 2])
+@pytest.mark.parametrize("window", [0, 1, 17, 100, 4096])
+def test_decode256_attended_set(ctx, code_base, window):
+    """q = 0: every attended token weighs exactly 1 and the output counts the position codes
+    of the attended set, compared exactly with the reference's set."""
+    lens = workloads.uniform_lengths(32, 256, 4096, 113)
+    lens[:8] = [1, 15, 16, 17, 33, 4096, 5000, 8191]
+    batch, pool = coded_case(ctx, lens, 114, code_base)
+    q = np.zeros(lens.size * HQ * D, np.uint16)
+    out = run(ctx, pool, batch, q, window, 0.0625)
+    check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 W={window}", head_dim=D, code_base=code_base)
+
+
+def test_decode256_other_shapes_stay_generic(ctx):
+    """head_dim 256 with another group size, and int8 pools, take the reference-order kernel."""
+    lens = np.array([5, 77, 300], np.int32)
+    for Hq, fmt in ((8, llm_hip.KV_BF16), (HQ, llm_hip.KV_INT8)):
+        batch = workloads.paged_batch(lens, BT, 0.10, 115)
+        pool, q = build_case(ctx, batch, Hq, HKV, fmt, 115, head_dim=D)
+        out = run(ctx, pool, batch, q, 0, 0.0625, Hq=Hq, expect_d256=False)
+        assert_parity(out, oracle_decode(pool, batch, fmt, Hq, HKV, 0, q, 0.0625, head_dim=D), what=f"Hq{Hq} fmt{fmt}")
