@@ -632,7 +632,8 @@ def measure_decode(ctx, name, lens, Hq, Hkv, fmt, steps, warmup, window=0, resid
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
         "bytes_per_step": nbytes,
         "rotating_copies": len(copies),
-        "kernel": "paged_decode_stream_kernel" if streamed == calls else "paged_decode_kernel (split-K)",
+        "kernel": ("paged_decode_stream_kernel" if streamed == calls else
+                   "paged_decode_d256_kernel (split-K)" if head_dim == 256 else "paged_decode_kernel (split-K)"),
         "host_us_per_call": host_us,
         **extra,
     }
@@ -881,7 +882,7 @@ def run_sections(ctx, args, lens, sel) -> list:
         # Qwen3.6 full-attention layer (fixtures/qwen36/config.json: Hq16 / Hkv2, head_dim 256) on C2's
         # lengths, bf16 blocks: the head_dim-256 kernel
         _, r = measure_decode(ctx, "Q36 decode B=32 L~U[256,4096] Hq16/Hkv2 D=256", lens, 16, 2, llm_hip.KV_BF16,
-                              sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, head_dim=256)
+                              sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, graph=True, head_dim=256)
         secondary.append(r)
         log(f"Q36 decode: {r}")
     if sel("neighbours"):

@@ -603,6 +603,20 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
     plan->fast = true;
     SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
                                desc->total_tokens_hint, pv.format);
+    if (ctx->opt(LLH_OPT_DECODE_SPLIT_BLOCKS) <= 0) {
+      // Long splits: each wavefront keeps one block in flight, so a workgroup's
+      // start (q, first loads) and its merge are paid once per split.  The longest
+      // split of at most 64 blocks that still gives >= 160 workgroups (measured on
+      // MI355X for the Qwen3.6 step, 32 x U[256, 4096]: 64 blocks 38.2 us, 32 41.7,
+      // 16 43.1, 8 41.0; 128 61.2).
+      long long blocks = (long long)desc->num_seqs * sp.est_blocks;
+      if (desc->total_tokens_hint > 0) blocks = (long long)desc->total_tokens_hint / kFastBlockTokens + desc->num_seqs;
+      auto wgs = [&](int s) { return (double)pv.kv_heads * (double)(blocks + (long long)desc->num_seqs * (s / 2)) / s; };
+      int split = 64;
+      while (split > 4 && wgs(split) < 160.0) split /= 2;
+      sp.split_blocks = split;
+      sp.max_splits = (sp.est_blocks + split - 1) / split;
+    }
     // the merge takes at most kD256MaxSplits partials: longer spans get longer splits
     while (sp.max_splits > kD256MaxSplits) {
       sp.split_blocks *= 2;

@@ -284,22 +284,33 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
     Kregs kr;
     Vregs vr;
     load_k(a, phys, kvh, lane, kr);
+    // K before V, as in the loop, so the loop's first wait (for K) leaves V in flight
+    __builtin_amdgcn_sched_barrier(0);
     load_v(a, phys, kvh, lane, vr);
-    for (int k = 0; k < nbw; k++) {
-      const int jb = blk_begin + wave + 4 * k;
-      if (!valid && lane == 0) atomicOr(a.err, kErrBadBlock);  // its tokens are all masked
+    // A block outside the pool is masked and flagged after the loop (a store in
+    // the loop would make every wait there wait for all loads in flight), and
+    // the last block is peeled off (loads under a condition made the compiler
+    // copy the block registers every iteration, waiting for loads in flight).
+    bool bad = false;
+    int k = 0;
+    for (; k + 1 < nbw; k++) {
+      bad |= !valid;
       uint32_t vm[8];
-      const uint32_t w = block_scores(a, kr, valid, jb, lo, len, lane, qw, st, vm);
-      const bool more = k + 1 < nbw;
-      if (more) {
-        e = entry(k + 1);
-        valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
-        phys = valid ? e : 0;
-        load_k(a, phys, kvh, lane, kr);
-      }
+      const uint32_t w = block_scores(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm);
+      e = entry(k + 1);
+      valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
+      phys = valid ? e : 0;
+      load_k(a, phys, kvh, lane, kr);
+      // nothing of p . v (which waits for V) moves above the K loads
+      __builtin_amdgcn_sched_barrier(0);
       block_accumulate(vr, w, vm, st);
-      if (more) load_v(a, phys, kvh, lane, vr);
+      load_v(a, phys, kvh, lane, vr);
     }
+    bad |= !valid;
+    uint32_t vm[8];
+    const uint32_t w = block_scores(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm);
+    block_accumulate(vr, w, vm, st);
+    if (bad && lane == 0) atomicOr(a.err, kErrBadBlock);
   }
 
   // ---- wavefront totals, then merge the four wavefronts through LDS ----
