@@ -698,6 +698,7 @@ def summarize(root: str) -> int:
         "c4": {"paged_decode_kernel": ("B", decode_bytes([32768] * 4, 16, 8, 0, 4096))},
         "c5int8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 1))},
         "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
+        "q36": {"paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
         "c3": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "c3int8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "c3fp8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
@@ -711,6 +712,8 @@ def summarize(root: str) -> int:
          ("c1", "c4")),
         ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
                                   "scales) and fp8 e4m3 (per (block, head) scales)", ("c5int8", "c5fp8")),
+        ("decode_q36_d256.md", "Paged GQA decode at head_dim 256, the Qwen3.6 full-attention shape (Hq16/Hkv2, "
+                               "bf16 KV) on C2's lengths (B=32, L~U[256,4096])", ("q36",)),
         ("prefill_mfma.md", "Chunked causal prefill (MFMA): C3 (8 x (1536 + 512), Hq32/Hkv4) over bf16, int8 and fp8 "
                             "blocks, C4 (4 x (31744 + 1024), window 4096)", ("c3", "c3int8", "c3fp8", "c4prefill")),
         ("kv_write_oproj.md", "KV writes (whole blocks, per-token append) and the output projection",
@@ -769,7 +772,8 @@ def summarize(root: str) -> int:
                          f"{statistics.mean(d):.2f} | {unit[1] if unit else '-'} | {rate} | "
                          f"{med(f) if f else float('nan'):.0f} | {med(w) if w else float('nan'):.0f} | "
                          f"{traffic if traffic else float('nan'):.0f} | {ratio} |\n")
-            mf = [(k, c) for (k, c) in ctr if not c.endswith("_SIZE") and not k[0].startswith("__amd")]
+            mf = [(k, c) for (k, c) in ctr if not c.endswith("_SIZE") and not k[0].startswith("__amd")
+                  and "::" not in k[0] and not k[0].startswith("_ZN")]  # library kernels of the set-up and checks
             for k, c in sorted(mf):
                 body += f"| {sec.upper()} | `{k[0]}` | {k[1]} | counter `{c}` | {med(ctr[(k, c)]):.4g} per dispatch |  |  |  |  |  |  |  |\n"
             for k in sorted({k for (k, c) in mf}):
@@ -872,9 +876,9 @@ def run_sections(ctx, args, lens, sel) -> list:
         _, r = measure_decode(ctx, f"C5 {nm} append + attend in one call (llh_paged_decode_append)", [8192] * 64, 32,
                               8, fmt, sec_steps, sec_warm, seed=workloads.SEED_BASE + 4, free=0.0, fused=True)
         r["decode_alone_us"] = secondary[-1]["us_per_step"]
-        # int8: the stream kernel quantises the token itself (+ merge); fp8: slot and append
-        # kernels, then the stream kernel and merge
-        r["launches"] = 2 if fmt == llm_hip.KV_INT8 else 4
+        # int8: the stream kernel quantises the token itself (+ merge); fp8: the append
+        # kernel (slots from the descriptor), then the stream kernel and merge
+        r["launches"] = 2 if fmt == llm_hip.KV_INT8 else 3
         secondary.append(r)
         log(f"C5 {nm} fused append+attend: {r}")
         torch.cuda.empty_cache()

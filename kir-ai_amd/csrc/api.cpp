@@ -488,12 +488,16 @@ int llh_kv_write_blocks(llh_ctx *ctx, llh_kv_pool *pool, const int32_t *d_blocks
   return LLH_OK;
 }
 
+// d_slots null: row i is sequence i's new token, appended at position
+// seq_lens[i] - 1 through block-table row i (the decode step's append).
 static int kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, const void *d_k, const void *d_v,
-                     int32_t n, int32_t src_f32, void *stream) {
+                     int32_t n, int32_t src_f32, void *stream, const int32_t *d_seq_lens = nullptr,
+                     const int32_t *d_tables = nullptr, int32_t max_blocks = 0) {
   if (!ctx || !pool) return LLH_ERR_NULL;
   if (n < 0) return ctx->fail(LLH_ERR_INVALID_SHAPE, "negative token count");
   if (n == 0) return LLH_OK;
-  if (!d_slots || !d_k || !d_v) return ctx->fail(LLH_ERR_NULL, "null device pointer");
+  if ((!d_slots && (!d_seq_lens || !d_tables)) || !d_k || !d_v)
+    return ctx->fail(LLH_ERR_NULL, "null device pointer");
   AppendArgs a{};
   a.pool = pool->view;
   a.k_dst = pool->k;
@@ -506,6 +510,9 @@ static int kv_append(llh_ctx *ctx, llh_kv_pool *pool, const int64_t *d_slots, co
   a.n = n;
   a.src_f32 = src_f32;
   a.err = ctx->err_word(static_cast<hipStream_t>(stream));
+  a.seq_lens = d_seq_lens;
+  a.tables = d_tables;
+  a.max_blocks = max_blocks;
   ctx->append_calls++;
   hipError_t e = launch_append(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return ctx->hip_fail(e, "append launch");
@@ -837,9 +844,8 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   // kernel first, then decodes.
   const bool fused = plan.fast && !plan.d256 && aligned16(d_k_new) && aligned16(d_v_new) &&
                      !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0);
-  const size_t slot_bytes = fused ? 0 : align_up((size_t)desc->num_seqs * sizeof(int64_t));
   WsLease lease;
-  st = lease.acquire(ctx, s, plan.bytes + slot_bytes);
+  st = lease.acquire(ctx, s, plan.bytes);
   if (st != LLH_OK) return st;
   char *ws = lease.base();
   if (fused) {
@@ -847,11 +853,9 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
     return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, lease.err(), true,
                                  static_cast<const uint16_t *>(d_k_new), static_cast<const uint16_t *>(d_v_new));
   }
-  int64_t *slots = reinterpret_cast<int64_t *>(ws + plan.bytes);
-  hipError_t e = launch_new_token_slots(desc->d_seq_lens, desc->d_block_tables, desc->max_blocks_per_seq,
-                                        pv.block_tokens, desc->num_seqs, slots, s);
-  if (e != hipSuccess) return ctx->hip_fail(e, "new-token slot launch");
-  st = kv_append(ctx, pool, slots, d_k_new, d_v_new, desc->num_seqs, 0, stream);
+  // the append kernel finds each new token's slot through the descriptor's table rows
+  st = kv_append(ctx, pool, nullptr, d_k_new, d_v_new, desc->num_seqs, 0, stream, desc->d_seq_lens,
+                 desc->d_block_tables, desc->max_blocks_per_seq);
   if (st != LLH_OK) return st;
   return launch_planned_decode(ctx, pool, desc, plan, d_q, d_out, score_scale, s, ws, lease.err());
 }

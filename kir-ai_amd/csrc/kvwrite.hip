@@ -352,6 +352,17 @@ __device__ __forceinline__ float append_fp8_row(uint8_t *dst, bool dim_major, si
   return s_new;
 }
 
+// Pool slot of append row i: a.slots[i], or (a.slots null) the new token of
+// sequence i, position seq_lens[i] - 1 through its block-table row (kNoSlot when
+// seq_lens[i] <= 0).
+__device__ __forceinline__ int64_t append_slot(const AppendArgs &a, int i) {
+  if (a.slots) return a.slots[i];
+  const int pos = a.seq_lens[i] - 1;
+  const int bt = a.pool.block_tokens;
+  return pos < 0 ? kNoSlot
+                 : (int64_t)a.tables[(size_t)i * a.max_blocks + (pos / bt) % a.max_blocks] * bt + pos % bt;
+}
+
 // One wavefront per token row i: the reference's int8 row layout (one f32
 // scale over all kv heads of the row; write_blocks_row_kernel's rule).
 template <typename ST>
@@ -361,7 +372,7 @@ __global__ __launch_bounds__(64) void append_row_kernel(const AppendArgs a) {
   const int BT = a.pool.block_tokens;
   const int Hkv = a.pool.kv_heads;
   const int Dh = a.pool.head_dim;
-  const int64_t slot = a.slots[i];
+  const int64_t slot = append_slot(a, i);
   if (slot == kNoSlot) return;
   const int64_t blk = slot / BT;
   const int off = (int)(slot % BT);
@@ -428,7 +439,7 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
   // covers both (the empty asm takes all five values, so neither load is
   // deferred behind the slot checks)
   const bool rows_in_regs = Dh <= 128;
-  const int64_t slot = a.slots[i];
+  const int64_t slot = append_slot(a, i);
   uint32_t kraw[2] = {0u, 0u}, vraw[2] = {0u, 0u};  // the elements' bits as stored in k / v
   if (rows_in_regs) {
 #pragma unroll
@@ -482,7 +493,8 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     // in call order appends them all, in that order (each may rescale the block).
     for (int j0 = 0; j0 < i; j0 += 64) {
       const int j = j0 + lane;
-      const bool same = j < i && a.slots[j] >= 0 && a.slots[j] / BT == blk;
+      const int64_t sj = j < i ? append_slot(a, j) : (int64_t)-1;
+      const bool same = sj >= 0 && sj / BT == blk;
       if (__any(same)) return;
     }
     float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[fp8_scale_index(bh)],
@@ -490,7 +502,7 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     // this call's tokens of the block, in call order: the slots are read 64 at a
     // time (one vector load per lane) and walked through a ballot mask
     for (int j0 = i; j0 < a.n; j0 += 64) {
-      const int64_t sl = j0 + lane < a.n ? a.slots[j0 + lane] : (int64_t)-1;
+      const int64_t sl = j0 + lane < a.n ? append_slot(a, j0 + lane) : (int64_t)-1;
       uint64_t pending = __ballot(sl >= 0 && sl / BT == blk);
       while (pending) {
         const int k = __builtin_ctzll(pending);
@@ -630,23 +642,6 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   hipLaunchKernelGGL(export_rows_kernel, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
-  return hipGetLastError();
-}
-
-__global__ __launch_bounds__(64) void new_token_slots_kernel(const int32_t *seq_lens, const int32_t *tables,
-                                                             int32_t max_blocks, int32_t bt, int32_t n,
-                                                             int64_t *slots) {
-  const int b = blockIdx.x * 64 + threadIdx.x;
-  if (b >= n) return;
-  const int pos = seq_lens[b] - 1;
-  slots[b] = pos < 0 ? kNoSlot : (int64_t)tables[(size_t)b * max_blocks + (pos / bt) % max_blocks] * bt + pos % bt;
-}
-
-hipError_t launch_new_token_slots(const int32_t *seq_lens, const int32_t *tables, int32_t max_blocks,
-                                  int32_t block_tokens, int32_t n, int64_t *slots, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(new_token_slots_kernel, dim3((n + 63) / 64), dim3(64), 0, s, seq_lens, tables, max_blocks,
-                     block_tokens, n, slots);
   return hipGetLastError();
 }
 

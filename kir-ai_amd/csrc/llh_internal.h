@@ -139,12 +139,17 @@ struct AppendArgs {
   void *v_dst;
   void *ks_dst;
   void *vs_dst;
-  const int64_t *slots;     // [n] block * BT + offset
+  const int64_t *slots;     // [n] block * BT + offset, or null: row i is sequence i's new token
   const void *k;            // [n][Hkv][D], bf16 or f32
   const void *v;
   int32_t n;
   int32_t src_f32;
   int32_t *err;
+  // slots == null: row i goes to position seq_lens[i] - 1 through table row i
+  // (no row when seq_lens[i] <= 0), as the decode step's new token
+  const int32_t *seq_lens;
+  const int32_t *tables;
+  int32_t max_blocks;
 };
 
 struct GatherArgs {
@@ -208,12 +213,8 @@ constexpr int kGenericPrefillMaxDim = 512;  // head_dim bound of the generic pre
 hipError_t launch_prefill_generic(const PrefillArgs &a, int total_rows, hipStream_t s);
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
-// slots[b] = the pool slot of position seq_lens[b] - 1 through table row b (kNoSlot
-// when seq_lens[b] <= 0: the append kernel skips it), for an append of each
-// sequence's new token
+// no new token for a sequence whose length is <= 0 (the append kernel skips its row)
 constexpr int64_t kNoSlot = INT64_MIN;
-hipError_t launch_new_token_slots(const int32_t *seq_lens, const int32_t *tables, int32_t max_blocks,
-                                  int32_t block_tokens, int32_t n, int64_t *slots, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s);
 hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);
