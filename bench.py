@@ -361,13 +361,14 @@ def host_info() -> str:
     return f"{model} (nproc={os.cpu_count()})"
 
 
-def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos=None, fmt=None):
+def prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, seed, resident_from_pos=None, fmt=None, head_dim=D):
     """Prefill workload: B sequences of prefix + chunk tokens, all K/V resident (bf16 pool
     unless fmt names a quantised one)."""
     import torch
     import llm_hip
     from llm_hip import workloads
 
+    D = head_dim
     fmt = llm_hip.KV_BF16 if fmt is None else fmt
     ctxlen = prefix + chunk
     lens = [ctxlen] * B
@@ -654,14 +655,14 @@ def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0, head_dim: i
     return kv + scales + 2 * lens.size * Hq * head_dim * 2 + int(blocks.sum()) * 4 + lens.size * 4
 
 
-def prefill_flops(B: int, prefix: int, chunk: int, Hq: int, window: int) -> int:
-    """4 * D FLOPs per unmasked (query, key) pair per head."""
+def prefill_flops(B: int, prefix: int, chunk: int, Hq: int, window: int, head_dim: int = D) -> int:
+    """4 * head_dim FLOPs per unmasked (query, key) pair per head."""
     pairs = 0
     for i in range(chunk):
         pos = prefix + i
         lo = max(0, pos - window + 1) if window > 0 else 0
         pairs += pos - lo + 1
-    return 4 * D * pairs * Hq * B
+    return 4 * head_dim * pairs * Hq * B
 
 
 def summarize(root: str) -> int:
@@ -699,6 +700,7 @@ def summarize(root: str) -> int:
         "c5int8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 1))},
         "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
         "q36": {"paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
+        "q36prefill": {"paged_prefill_d256_kernel": ("F", prefill_flops(8, 1536, 512, 16, 0, 256))},
         "c3": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "c3int8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "c3fp8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
@@ -713,7 +715,8 @@ def summarize(root: str) -> int:
         ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
                                   "scales) and fp8 e4m3 (per (block, head) scales)", ("c5int8", "c5fp8")),
         ("decode_q36_d256.md", "Paged GQA decode at head_dim 256, the Qwen3.6 full-attention shape (Hq16/Hkv2, "
-                               "bf16 KV) on C2's lengths (B=32, L~U[256,4096])", ("q36",)),
+                               "bf16 KV): decode on C2's lengths (B=32, L~U[256,4096]) and prefill on C3's chunking "
+                               "(8 x (1536 + 512))", ("q36", "q36prefill")),
         ("prefill_mfma.md", "Chunked causal prefill (MFMA): C3 (8 x (1536 + 512), Hq32/Hkv4) over bf16, int8 and fp8 "
                             "blocks, C4 (4 x (31744 + 1024), window 4096)", ("c3", "c3int8", "c3fp8", "c4prefill")),
         ("kv_write_oproj.md", "KV writes (whole blocks, per-token append) and the output projection",
@@ -821,7 +824,7 @@ def traffic_from_profile(kernel: str):
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
 SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "q36", "neighbours", "trait", "c3", "c4prefill",
-            "c3int8", "c3fp8")
+            "c3int8", "c3fp8", "q36prefill")
 
 
 def run_sections(ctx, args, lens, sel) -> list:
@@ -895,15 +898,19 @@ def run_sections(ctx, args, lens, sel) -> list:
         r = measure_trait_c1(ctx, 200, 2.0, not args.no_cpu)
         secondary.append(r)
         log(f"trait C1: {r}")
-    for key, name, B, prefix, chunk, Hq, Hkv, window, res, fmt in (
-            ("c3", "C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_BF16),
+    for key, name, B, prefix, chunk, Hq, Hkv, window, res, fmt, hd in (
+            ("c3", "C3 prefill 8x(1536+512) Hq32/Hkv4", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_BF16, D),
             ("c4prefill", "C4 prefill 4x(31744+1024) W=4096", 4, 31744, 1024, 16, 8, 4096, 31744 - 4096,
-             llm_hip.KV_BF16),
-            ("c3int8", "C3 prefill over int8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_INT8),
-            ("c3fp8", "C3 prefill over fp8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_FP8_E4M3)):
+             llm_hip.KV_BF16, D),
+            ("c3int8", "C3 prefill over int8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_INT8, D),
+            ("c3fp8", "C3 prefill over fp8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_FP8_E4M3, D),
+            # Qwen3.6 full-attention layer (Hq16 / Hkv2, head_dim 256) on C3's chunking: the head_dim-256 kernel
+            ("q36prefill", "Q36 prefill 8x(1536+512) Hq16/Hkv2 D=256", 8, 1536, 512, 16, 2, 0, None, llm_hip.KV_BF16,
+             256)):
         if not sel(key):
             continue
-        step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res, fmt)
+        step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res, fmt,
+                                         hd)
         pms = time_steps(step, sec_steps, sec_warm)
         host_us = HOST["us"]
         _, pkms = time_steps(step, sec_steps, 0, kernel_timing=(ctx, "prefill"))
@@ -914,7 +921,7 @@ def run_sections(ctx, args, lens, sel) -> list:
              "kernel_us": round(pkms * 1e3, 2) if pkms <= pms else None, "tflops": round(tf, 1),
              "mfma_util": round(tf / BF16_PEAK_TFLOPS, 4), "tokens_per_s": round(B * chunk / (pms * 1e-3), 1),
              "flops_per_step": flops, "host_us_per_call": host_us}
-        if not args.no_cpu and fmt == llm_hip.KV_BF16:
+        if not args.no_cpu and fmt == llm_hip.KV_BF16 and hd == D:
             r["cpu"] = cpu_prefill_times(keep, B, prefix, chunk, Hq, Hkv, window, 16, 1.0)
         secondary.append(r)
         log(f"{name}: {r}")

@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "llm_hip", "libllm_hip.so")
-SOURCES = ["api.cpp", "block_pool.cpp", "prefix_cache.cpp", "disk_codec.cpp", "sha256.cpp", "decode.hip", "decode256.hip", "prefill.hip", "kvwrite.hip", "oproj.hip", "noalloc.hip"]
+SOURCES = ["api.cpp", "block_pool.cpp", "prefix_cache.cpp", "disk_codec.cpp", "sha256.cpp", "decode.hip", "decode256.hip", "prefill.hip", "prefill256.hip", "kvwrite.hip", "oproj.hip", "noalloc.hip"]
 ARCH = "gfx950"
 
 

@@ -207,6 +207,8 @@ hipError_t launch_decode_generic(const GenericDecodeArgs &a, int q_f32, int out_
 // sharing the K/V tiles
 enum { kPrefillOneHead = 1, kPrefillTwoHeads = 2 };
 hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s);
+// head_dim 256, bf16 pools, 16-token blocks (one query head per workgroup)
+hipError_t launch_prefill_d256(const PrefillArgs &a, hipStream_t s);
 constexpr int kGenericPrefillMaxDim = 512;  // head_dim bound of the generic prefill kernel
 // Element-wise prefill for every other shape (any head_dim <= 512, block size,
 // row alignment); total_rows = chunk_starts[num_seqs].

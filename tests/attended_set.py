@@ -66,13 +66,13 @@ def counts(lo: int, hi: int, kv_heads: int, code_base: int = 0) -> np.ndarray:
     return np.stack([np.bincount(code(pos, code_base + h), minlength=D)[:D] for h in range(kv_heads)])
 
 
-def prefix_counts(lo: int, hi: int, kv_heads: int) -> np.ndarray:
+def prefix_counts(lo: int, hi: int, kv_heads: int, code_base: int = 0) -> np.ndarray:
     """int32 [kv_heads][hi - lo + 1][128]: counts of positions [lo, lo + i) for every i."""
     pos = np.arange(lo, hi, dtype=np.int64)
     out = np.zeros((kv_heads, hi - lo + 1, D), np.int32)
     for h in range(kv_heads):
         one_hot = np.zeros((hi - lo, D), np.int32)
-        one_hot[np.arange(hi - lo), code(pos, h)] = 1
+        one_hot[np.arange(hi - lo), code(pos, code_base + h)] = 1
         out[h, 1:] = np.cumsum(one_hot, axis=0)
     return out
 
@@ -125,14 +125,18 @@ def check_decode(out_bf16_bits: np.ndarray, seq_lens, window: int, q_heads: int,
 
 
 def check_prefill(out_bf16_bits: np.ndarray, chunk_starts, context_lens, window: int, q_heads: int, kv_heads: int,
-                  value: float, what: str = "") -> None:
-    """Every chunk row's recovered counts equal those of [lo(pos), pos], exactly."""
+                  value: float, what: str = "", head_dim: int = D, code_base: int = 0) -> None:
+    """Every chunk row's recovered counts equal those of [lo(pos), pos], exactly (head_dim >
+    128: the dims above 128, whose value rows are zero, must be exactly 0)."""
     from oracle import bf16_to_f32
 
     cs = np.asarray(chunk_starts, np.int64)
     cl = np.asarray(context_lens, np.int64)
     G = q_heads // kv_heads
-    got = bf16_to_f32(np.ascontiguousarray(out_bf16_bits).ravel()).reshape(int(cs[-1]), q_heads, D)
+    got = bf16_to_f32(np.ascontiguousarray(out_bf16_bits).ravel()).reshape(int(cs[-1]), q_heads, head_dim)
+    if head_dim > D:
+        assert np.all(got[:, :, D:] == 0.0), f"{what}: dims above {D} must be zero"
+        got = got[:, :, :D]
     for b in range(cl.size):
         chunk = int(cs[b + 1] - cs[b])
         if chunk == 0:
@@ -140,7 +144,7 @@ def check_prefill(out_bf16_bits: np.ndarray, chunk_starts, context_lens, window:
         pos = int(cl[b]) - chunk + np.arange(chunk)
         lo = np.maximum(0, pos - window + 1) if window > 0 else np.zeros_like(pos)
         base = int(lo.min())
-        pc = prefix_counts(base, int(pos.max()) + 1, kv_heads)  # [Hkv][span + 1][128]
+        pc = prefix_counts(base, int(pos.max()) + 1, kv_heads, code_base)  # [Hkv][span + 1][128]
         exp = pc[:, pos + 1 - base] - pc[:, lo - base]          # [Hkv][chunk][128]
         n = (pos + 1 - lo).astype(np.float64)
         rows = got[cs[b]:cs[b + 1]].astype(np.float64)           # [chunk][Hq][128]

@@ -185,7 +185,7 @@ def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm
 
 
 @pytest.mark.parametrize("head_dim,bt,Hq,Hkv,W,fmt", [
-    (256, 16, 8, 4, 0, llm_hip.KV_BF16),       # Gemma-like head_dim
+    (256, 32, 8, 4, 0, llm_hip.KV_BF16),       # head_dim 256 on 32-token blocks
     (256, 16, 8, 4, 200, llm_hip.KV_INT8),
     (64, 32, 12, 4, 48, llm_hip.KV_BF16),      # odd group (3), 32-token blocks, window
     (96, 8, 4, 1, 0, llm_hip.KV_FP8_E4M3),     # MQA, 8-token blocks
