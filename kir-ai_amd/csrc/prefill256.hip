@@ -218,8 +218,17 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
   store_tile(k_lds[0], v_lds[0], tid, next, use_next, t_begin, ctx);
   __syncthreads();
 
+  // The O^T accumulators live in AGPRs, where only the MFMAs touch them: the rare
+  // rescale (a row's max grew by more than 16 in log2 units) leaves the tile loop,
+  // multiplies them, and re-enters at the same tile, reissuing its loads and
+  // recomputing its scores.  (A rescale inside the loop made the compiler copy
+  // all 128 accumulators out of and back into AGPRs on every tile.)
   int buf = 0;
-  for (int kt = t_begin; kt < khi; kt += BN, buf ^= 1) {
+  int kt = t_begin;
+  for (;;) {
+  bool rescale = false;
+  float m_next = m_run;  // this lane's new running max when leaving to rescale
+  for (; kt < khi; kt += BN, buf ^= 1) {
     const bool has_next = kt + BN < khi;
     if (has_next)  // in flight during the math
       use_next = load_tile(a, ent_next, kvh, kt + BN, ctx, klo, tid, next, bad);
@@ -276,16 +285,15 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
       }
       tmax = fmaxf(tmax, xor32_other(tmax));
       const float m_cand = fmaxf(m_run, tmax);
-      const bool grow = m_cand > m_run + 8.0f;  // lazy rescale; true on the first finite tile
+      // a row without a finite score yet takes the tile's max (its accumulators are
+      // still zero); a row whose max grows by more than 16 needs a rescale first
+      const bool grow = m_run != -INFINITY && m_cand > m_run + 16.0f;
       if (__any(grow)) {
-        const float alpha = grow ? fast_exp2(m_run - m_cand) : 1.0f;
-        m_run = grow ? m_cand : m_run;
-        l_run *= alpha;
-#pragma unroll
-        for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-          for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
+        m_next = grow ? m_cand : m_run;
+        rescale = true;
+        break;
       }
+      if (m_run == -INFINITY) m_run = m_cand;
       const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
       u32x4_t pb[4];
 #pragma unroll
@@ -320,6 +328,18 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
 
     if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
     __syncthreads();  // next tile visible; this tile no longer read
+  }
+  if (!rescale) break;
+  {
+    const float alpha = fast_exp2(m_run - m_next);  // 1 for rows that did not grow
+    m_run = m_next;
+    l_run *= alpha;
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
+    ent_next = fetch_entries(a, table, kt + BN, lane);  // the re-entered tile's next-tile entries
+  }
   }
 
   // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
