@@ -139,7 +139,7 @@ class DecodeWorkload:
     def append_bytes(self) -> int:
         """Algorithmic bytes of the append: the new rows read (bf16) and written (pool format), slots."""
         B = self.batch.seq_lens.size
-        elem = 2 if self.fmt == self.llm_hip.KV_BF16 else 1
+        elem = 2 if self.fmt in (self.llm_hip.KV_BF16, self.llm_hip.KV_F16) else 1
         scales = B * self.Hkv * 2 * 2 if self.fmt == self.llm_hip.KV_INT8 else 0
         return B * self.Hkv * self.D * 2 * 2 + B * self.Hkv * self.D * elem * 2 + scales + B * 8
 
@@ -421,14 +421,15 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     B, Hkv, Hq = 32, 8, 16
     # decode: the C2 batch's 32 new tokens (one row per sequence, scattered slots);
     # prefill: C3's 8 x 512-token chunks, whole 16-token blocks (llh_kv_write_blocks)
-    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8")):
+    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8"),
+                    (llm_hip.KV_F16, "fp16")):
         nblk, H = 8 * 512 // BT, 4
         pool = ctx.pool(fmt, BT, H, D, 8192)
         ids = torch.randperm(8192, generator=g, device="cuda")[:nblk].to(torch.int32)
         k = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
         v = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.write_blocks(pool, ids, k, v, stream=s), steps, warmup)
-        esz = 2 if fmt == llm_hip.KV_BF16 else 1
+        esz = 2 if fmt in (llm_hip.KV_BF16, llm_hip.KV_F16) else 1
         T = nblk * BT
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: nblk * H * 4 * 2}.get(fmt, 0)
         nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + scales
@@ -438,7 +439,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_d128_kernel"})
         del pool
     for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv),
-                          (llm_hip.KV_FP8_E4M3, "fp8", B, Hkv)):
+                          (llm_hip.KV_FP8_E4M3, "fp8", B, Hkv), (llm_hip.KV_F16, "fp16", B, Hkv)):
         pool = ctx.pool(fmt, BT, H, D, 8192)
         slots = torch.randperm(8192 * BT, generator=g, device="cuda")[:T].to(torch.int64)
         k = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
@@ -451,7 +452,7 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         gms = time_graph([lambda s: ctx.append(pool, slots, k, v, stream=s)], steps)
         if any(not np.array_equal(a, b) for a, b in zip(before.values(), pool.raw().values())):
             raise RuntimeError("append: graph replay changed the pool")
-        esz = 2 if fmt == llm_hip.KV_BF16 else 1
+        esz = 2 if fmt in (llm_hip.KV_BF16, llm_hip.KV_F16) else 1
         # fp8: the block's scale is read and written per token (an earlier row re-encode is not counted)
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: T * H * 4 * 2 * 2}.get(fmt, 0)
         nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + T * 8 + scales
@@ -648,7 +649,7 @@ def decode_bytes(lens, Hq: int, Hkv: int, fmt: int, window: int = 0, head_dim: i
     lens = np.asarray(lens, np.int64)
     lo = np.maximum(0, lens - window) if window > 0 else np.zeros_like(lens)
     rows = lens - lo
-    elem = 2 if fmt == 0 else 1
+    elem = 2 if fmt in (0, 4) else 1  # bf16, fp16: 2 bytes; int8, fp8: 1
     kv = int(rows.sum()) * Hkv * head_dim * elem * 2
     blocks = ((lens + BT - 1) // BT) - lo // BT
     scales = int(rows.sum()) * Hkv * 4 if fmt == 1 else (int(blocks.sum()) * Hkv * 8 if fmt == 2 else 0)
@@ -699,6 +700,8 @@ def summarize(root: str) -> int:
         "c4": {"paged_decode_kernel": ("B", decode_bytes([32768] * 4, 16, 8, 0, 4096))},
         "c5int8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 1))},
         "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
+        "c2f16": {"paged_decode_stream_kernel": ("B", decode_bytes(c2lens, 16, 8, 4))},
+        "c3f16": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "q36": {"paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
         "q36prefill": {"paged_prefill_d256_kernel": ("F", prefill_flops(8, 1536, 512, 16, 0, 256))},
         "c3": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
@@ -714,6 +717,8 @@ def summarize(root: str) -> int:
          ("c1", "c4")),
         ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
                                   "scales) and fp8 e4m3 (per (block, head) scales)", ("c5int8", "c5fp8")),
+        ("f16_kv.md", "fp16 KV pools (the reference's Metal mirror dtype): decode on C2 (B=32, L~U[256,4096], "
+                      "Hq16/Hkv8) and prefill on C3 (8 x (1536 + 512), Hq32/Hkv4)", ("c2f16", "c3f16")),
         ("decode_q36_d256.md", "Paged GQA decode at head_dim 256, the Qwen3.6 full-attention shape (Hq16/Hkv2, "
                                "bf16 KV): decode on C2's lengths (B=32, L~U[256,4096]) and prefill on C3's chunking "
                                "(8 x (1536 + 512))", ("q36", "q36prefill")),
@@ -824,7 +829,7 @@ def traffic_from_profile(kernel: str):
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
 SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "q36", "neighbours", "trait", "c3", "c4prefill",
-            "c3int8", "c3fp8", "q36prefill")
+            "c3int8", "c3fp8", "q36prefill", "c2f16", "c3f16")
 
 
 def run_sections(ctx, args, lens, sel) -> list:
@@ -892,6 +897,13 @@ def run_sections(ctx, args, lens, sel) -> list:
                               sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, graph=True, head_dim=256)
         secondary.append(r)
         log(f"Q36 decode: {r}")
+    if sel("c2f16"):
+        # C2's shape over an fp16 pool (the element type of the reference's Metal KV mirror)
+        _, r = measure_decode(ctx, "C2 decode over fp16 blocks", lens, 16, 8, llm_hip.KV_F16, sec_steps, sec_warm,
+                              seed=workloads.SEED_BASE + 1)
+        secondary.append(r)
+        log(f"C2 f16: {r}")
+        torch.cuda.empty_cache()
     if sel("neighbours"):
         secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))
     if sel("trait"):
@@ -904,6 +916,7 @@ def run_sections(ctx, args, lens, sel) -> list:
              llm_hip.KV_BF16, D),
             ("c3int8", "C3 prefill over int8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_INT8, D),
             ("c3fp8", "C3 prefill over fp8 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_FP8_E4M3, D),
+            ("c3f16", "C3 prefill over fp16 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_F16, D),
             # Qwen3.6 full-attention layer (Hq16 / Hkv2, head_dim 256) on C3's chunking: the head_dim-256 kernel
             ("q36prefill", "Q36 prefill 8x(1536+512) Hq16/Hkv2 D=256", 8, 1536, 512, 16, 2, 0, None, llm_hip.KV_BF16,
              256)):

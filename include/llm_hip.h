@@ -40,7 +40,8 @@
 extern "C" {
 #endif
 
-#define LLH_ABI_VERSION 6  /* 6: head_dim-256 decode kernel, llh_metrics.d256_decode_calls, gate fields;
+#define LLH_ABI_VERSION 6  /* 6: head_dim-256 kernels, llh_metrics.d256_decode_calls / generic_decode_calls,
+                              gate fields, LLH_KV_F16;
                               5: per-stream device error words, llh_layer_cache_create_from_rows;
                               4: int8 and fp8 pools store their scales as (K, V) pairs */
 
@@ -67,9 +68,19 @@ typedef enum llh_kv_format {
   LLH_KV_BF16 = 0,    /* bf16 K and V */
   LLH_KV_INT8 = 1,    /* int8 codes, fp16 scale per (token, kv head): absmax/127 */
   LLH_KV_FP8_E4M3 = 2, /* OCP e4m3fn codes, f32 scale per (block, kv head) for K and for V: absmax/448 */
-  LLH_KV_INT8_ROW = 3  /* int8 codes, f32 scale per token row over all kv heads: absmax/127 -- the
+  LLH_KV_INT8_ROW = 3, /* int8 codes, f32 scale per token row over all kv heads: absmax/127 -- the
                           reference's own int8 layout (crates/llm-kv-cache/src/format.rs:702-759);
                           served by the element-wise kernels */
+  LLH_KV_F16 = 4       /* IEEE fp16 K and V: the dtype of the reference's Metal mirror
+                          (attention_scores_f16, crates/llm-metal/src/device/shaders/generic.metal:89-118;
+                          KvCacheFormat::F16, format.rs:69-120).  Rows are rounded to nearest even;
+                          a value beyond the fp16 range is stored as an infinity (as a float -> half
+                          conversion does).  The tuned decode and prefill kernels compute q . k on
+                          fp16 with each query head (prefill: each query row) scaled into fp16 by a
+                          power of two: elements within 2^-28 of the largest |q| are exact, smaller
+                          ones err by under 2^-38 of it; softmax weights enter p . v as fp16.  Device
+                          pools only: a layer cache of this format is UNSUPPORTED, as
+                          LayerKvCache::new_with_config refuses it (layer.rs:399-403) */
 } llh_kv_format;
 
 typedef struct llh_ctx llh_ctx;
@@ -132,6 +143,7 @@ typedef struct llh_metrics {
   uint64_t stream_slots;          /* streams holding a workspace slot (scratch and error word) now */
   uint64_t workspace_bytes;       /* device bytes of those slots' scratch now */
   uint64_t d256_decode_calls;     /* decode calls that ran the head_dim-256 kernel */
+  uint64_t generic_decode_calls;  /* llh_paged_decode* calls that ran the element-wise kernel */
 } llh_metrics;
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out);
 /* Sticky error flags the batched kernels raise instead of faulting: 1 = a

@@ -87,7 +87,7 @@ SplitPlan plan_splits(const llh_ctx *ctx, int num_seqs, int kv_heads, int max_se
     long long blocks = (long long)num_seqs * est_blocks;
     if (total_tokens_hint > 0) blocks = (long long)total_tokens_hint / kFastBlockTokens + num_seqs;
     auto wgs = [&](int s) { return (double)kv_heads * (double)(blocks + (long long)num_seqs * (s / 2)) / s; };
-    if (format == LLH_KV_BF16) {
+    if (format == LLH_KV_BF16 || format == LLH_KV_F16) {
       split = wgs(8) >= 512.0 ? 8 : 4;
     } else {
       const double target = 2048.0;
@@ -315,6 +315,7 @@ int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
   out->generic_prefill_calls = ctx->generic_prefill_calls.load();
   out->fused_append_calls = ctx->fused_append_calls.load();
   out->d256_decode_calls = ctx->d256_decode_calls.load();
+  out->generic_decode_calls = ctx->generic_decode_calls.load();
   std::lock_guard<std::mutex> g(const_cast<llh_ctx *>(ctx)->ws_mu);
   out->stream_slots = ctx->workspaces.size();
   out->workspace_bytes = 0;
@@ -402,11 +403,11 @@ int llh_kv_pool_create(llh_ctx *ctx, int32_t format, int32_t block_tokens, int32
                        int64_t n_blocks, llh_kv_pool **out) {
   if (!ctx || !out) return LLH_ERR_NULL;
   *out = nullptr;
-  if (format < LLH_KV_BF16 || format > LLH_KV_INT8_ROW)
+  if (format < LLH_KV_BF16 || format > LLH_KV_F16)
     return ctx->fail(LLH_ERR_UNSUPPORTED, "unsupported KV format");
   if (block_tokens <= 0 || kv_heads <= 0 || head_dim <= 0 || n_blocks <= 0)
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "kv pool sizes must be positive");
-  if (format != LLH_KV_BF16 && (block_tokens % 4 != 0 || head_dim % 4 != 0))
+  if (elem_bytes(format) == 1 && (block_tokens % 4 != 0 || head_dim % 4 != 0))
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "quantised pools need block_tokens and head_dim divisible by 4");
   if (n_blocks > INT32_MAX) return ctx->fail(LLH_ERR_INVALID_SHAPE, "block indices are int32");
   auto *pool = new llh_kv_pool();
@@ -731,6 +732,7 @@ int llh::launch_planned_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_
   g.score_stride = plan.score_stride;
   g.scale = score_scale;
   g.gate = static_cast<const uint16_t *>(desc->d_gate);
+  ctx->generic_decode_calls++;
   hipError_t e = launch_decode_generic(g, 0, 0, s);
   if (e != hipSuccess) return ctx->hip_fail(e, "generic decode launch");
   return LLH_OK;
@@ -840,10 +842,10 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
   // the new token from its rows, int8 / fp8 pools quantise it into the block that
   // receives it.  fp8 pools on the persistent stream kernel are the exception: the
   // scale-growth re-encode doubles that kernel's code and costs more than the
-  // separate append launch it saves.  Every other case appends through the append
-  // kernel first, then decodes.
-  const bool fused = plan.fast && !plan.d256 && aligned16(d_k_new) && aligned16(d_v_new) &&
-                     !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0);
+  // separate append launch it saves, and fp16 pools have no fused form.  Every
+  // other case appends through the append kernel first, then decodes.
+  const bool fused = plan.fast && !plan.d256 && pv.format != LLH_KV_F16 && aligned16(d_k_new) &&
+                     aligned16(d_v_new) && !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0);
   WsLease lease;
   st = lease.acquire(ctx, s, plan.bytes);
   if (st != LLH_OK) return st;
@@ -916,7 +918,7 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "prefill q and output must be bf16-aligned (2 bytes)");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   // the tuned MFMA kernels take 16-token blocks and 16-byte aligned rows at head_dim
-  // 128 (bf16, int8, fp8 pools) and 256 (bf16); every other call runs the
+  // 128 (bf16, int8, fp8, fp16 pools) and 256 (bf16); every other call runs the
   // element-wise kernel
   const bool tuned_shape = pv.block_tokens == kFastBlockTokens &&
                            ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) == 0 &&

@@ -53,8 +53,8 @@ constexpr int BT = kFastBlockTokens;
 // a 16-lane row.  Other shapes keep the row layout (16 dims of two tokens per
 // lane).  V is laid out the same way in both.
 template <int G, int FMT>
-constexpr bool kTokenLanes = FMT != kBf16 && G <= 4;
-// q words (packed bf16 pairs) per lane and head
+constexpr bool kTokenLanes = !is16(FMT) && G <= 4;
+// q words (packed bf16 pairs; fp16 pairs on fp16 pools) per lane and head
 template <int G, int FMT>
 constexpr int kQWords = kTokenLanes<G, FMT> ? 16 : 8;
 
@@ -62,12 +62,17 @@ constexpr int kQWords = kTokenLanes<G, FMT> ? 16 : 8;
 template <int FMT>
 struct BlockRegs;
 
-template <>
-struct BlockRegs<kBf16> {
+// 16-bit pools (bf16, fp16): 16 bytes of each of 4 K token rows, 8 bytes of
+// each of 8 V dim rows
+struct BlockRegs16 {
   uint4 k[4];
   uint2 v[8];
   bool valid;
 };
+template <>
+struct BlockRegs<kBf16> : BlockRegs16 {};
+template <>
+struct BlockRegs<kF16> : BlockRegs16 {};
 
 template <int FMT>
 struct BlockRegs {
@@ -92,11 +97,11 @@ __device__ __forceinline__ void load_block(const DecodeArgs &a, int phys, int kv
   const int c = lane & 15;
   r.valid = phys >= 0 && (int64_t)phys < a.pool.n_blocks;
   if (!r.valid) phys = 0;
-  constexpr int kBlockBytes = (FMT == kBf16 ? 2 : 1) * BT * D;
+  constexpr int kBlockBytes = (is16(FMT) ? 2 : 1) * BT * D;
   const size_t bh = (size_t)phys * a.pool.kv_heads + kvh;
   const char *kb = reinterpret_cast<const char *>(a.pool.k) + bh * kBlockBytes;
   const char *vb = reinterpret_cast<const char *>(a.pool.v) + bh * kBlockBytes;
-  if constexpr (FMT == kBf16) {
+  if constexpr (is16(FMT)) {
 #pragma unroll
     for (int i = 0; i < 4; i++) r.k[i] = ld_nt16(kb + (4 * g + i) * (D * 2) + c * 16);
 #pragma unroll
@@ -198,7 +203,9 @@ __device__ __forceinline__ void v_code_pairs(uint32_t w, uint32_t &p01, uint32_t
 
 // One 16-token block for the G query heads of this wavefront's kv head.
 // q . k and p . v run on packed bf16 dot2 with fp32 accumulation: K, V and q
-// are exact in bf16 (int8 and e4m3 codes convert exactly).  The exception is
+// are exact in bf16 (int8 and e4m3 codes convert exactly).  fp16 pools run
+// the same steps on packed fp16 dot2 against q in fp16 (q_bf16_to_f16: each
+// head's scores carry its step 2^e) with fp16 softmax weights.  The exception is
 // q . k on int8 pools in the token-lane layout, which runs on v_dot4_i32_i8
 // against q in 16-bit fixed point (prep_q; qstep is the fixed-point step of
 // this lane's head).  The softmax weights p (times the value scale for
@@ -219,7 +226,7 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     const int pos0 = jb * BT + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; i++) ok[i] = (pos0 + i >= lo) && (pos0 + i < len) && r.valid;
-    if constexpr (FMT == kBf16) {
+    if constexpr (is16(FMT)) {
       vmask[0] = (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
       vmask[1] = (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
     } else {
@@ -325,16 +332,18 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     float s[G][4];
     float vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
 
-    if constexpr (FMT == kBf16) {
+    if constexpr (is16(FMT)) {
 #pragma unroll
       for (int gi = 0; gi < G; gi++) {
+        // fp16: word 4 holds the head's q step (prep_q)
+        const float sc = FMT == kF16 ? a.scale_log2e * __uint_as_float(qw[gi][4]) : a.scale_log2e;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          float acc = dot2_bf16(r.k[i].x, qw[gi][0], 0.0f);
-          acc = dot2_bf16(r.k[i].y, qw[gi][1], acc);
-          acc = dot2_bf16(r.k[i].z, qw[gi][2], acc);
-          acc = dot2_bf16(r.k[i].w, qw[gi][3], acc);
-          s[gi][i] = row_sum16(acc) * a.scale_log2e;
+          float acc = dot2_16<FMT>(r.k[i].x, qw[gi][0], 0.0f);
+          acc = dot2_16<FMT>(r.k[i].y, qw[gi][1], acc);
+          acc = dot2_16<FMT>(r.k[i].z, qw[gi][2], acc);
+          acc = dot2_16<FMT>(r.k[i].w, qw[gi][3], acc);
+          s[gi][i] = row_sum16(acc) * sc;
         }
       }
     } else {
@@ -430,7 +439,7 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     }
     // quantized: the normaliser counts weight bf16(p * s) / s per token (see below)
     float vinv[4];
-    if constexpr (FMT != kBf16) {
+    if constexpr (!is16(FMT)) {
 #pragma unroll
       for (int i = 0; i < 4; i++) vinv[i] = vsc[i] != 0.0f ? __builtin_amdgcn_rcpf(vsc[i]) : 0.0f;
     }
@@ -440,11 +449,11 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) p[i] = fast_exp2(s[gi][i] - mref);
-      if constexpr (FMT == kBf16) {
-        w01[gi] = pack_bf16(p[0], p[1]);
-        w23[gi] = pack_bf16(p[2], p[3]);
-        // the normaliser sums exactly the bf16 weights that enter p . v
-        st.l[gi] = dot2_ones(w23[gi], dot2_ones(w01[gi], st.l[gi]));
+      if constexpr (is16(FMT)) {
+        w01[gi] = pack_16<FMT>(p[0], p[1]);
+        w23[gi] = pack_16<FMT>(p[2], p[3]);
+        // the normaliser sums exactly the 16-bit weights that enter p . v
+        st.l[gi] = dot2_ones_16<FMT>(w23[gi], dot2_ones_16<FMT>(w01[gi], st.l[gi]));
       } else {
         w01[gi] = pack_bf16(p[0] * vsc[0], p[1] * vsc[1]);
         w23[gi] = pack_bf16(p[2] * vsc[2], p[3] * vsc[3]);
@@ -461,7 +470,7 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
   }
   // p . v over this lane's 8 dims; V of tokens outside [lo, len) is zeroed
   // first (only partial blocks pay the masks)
-  if constexpr (FMT == kBf16) {
+  if constexpr (is16(FMT)) {
     uint2 vv[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) vv[j] = r.v[j];
@@ -476,7 +485,7 @@ __device__ __forceinline__ void compute_block(const DecodeArgs &a, const BlockRe
     for (int j = 0; j < 8; j++)
 #pragma unroll
       for (int gi = 0; gi < G; gi++)
-        st.o[gi][j] = dot2_bf16(vv[j].y, w23[gi], dot2_bf16(vv[j].x, w01[gi], st.o[gi][j]));
+        st.o[gi][j] = dot2_16<FMT>(vv[j].y, w23[gi], dot2_16<FMT>(vv[j].x, w01[gi], st.o[gi][j]));
   } else {
     uint32_t vv[8];
 #pragma unroll
@@ -504,7 +513,7 @@ __device__ __forceinline__ void seq_range(const DecodeArgs &a, int b, int &len, 
   n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
 }
 
-// The query words of this lane: bf16 K rows, dims 8c..8c+7 (c = lane & 15);
+// The query words of this lane: 16-bit K rows, dims 8c..8c+7 (c = lane & 15);
 // int8 / fp8 row layout, dims 16 * (lane & 7) .. +16; token-lane layout, dims
 // 32 * (lane & 3) .. +32.
 template <int G, int FMT>
@@ -512,7 +521,7 @@ __device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int la
                                        uint32_t (&qw)[G][kQWords<G, FMT>]) {
 #pragma unroll
   for (int gi = 0; gi < G; gi++) {
-    if constexpr (FMT == kBf16) {
+    if constexpr (is16(FMT)) {
       const uint4 t = *reinterpret_cast<const uint4 *>(a.q + (qrow0 + gi) * D + (lane & 15) * 8);
       qw[gi][0] = t.x;
       qw[gi][1] = t.y;
@@ -537,6 +546,9 @@ __device__ __forceinline__ void load_q(const DecodeArgs &a, size_t qrow0, int la
 // Turns the bf16 q words of load_q into the operands compute_block uses and
 // returns this lane's fixed-point step (1 where q stays bf16).  Split from the
 // loads so that a caller can issue its next block's loads in between.
+//
+// fp16 pools: each head's q becomes fp16 words (q_bf16_to_f16) and its step
+// goes to the head's word 4 (unused by the row layout's q . k), wave-uniform.
 //
 // int8 pools in the token-lane layout take q . k on v_dot4_i32_i8: each head's
 // q becomes q16 = round(q * 2^-e) with e = exponent(max |q|) - 13, so |q16| <=
@@ -587,6 +599,13 @@ __device__ __forceinline__ float prep_q(int lane, uint32_t (&qw)[G][kQWords<G, F
       if (gi == 0 || ((lane & 3) & (G - 1)) == gi) own = step;
     }
     return own;
+  } else if constexpr (FMT == kF16) {
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+      const float step = q_bf16_to_f16<4>(qw[gi]);  // every row holds the same q: uniform over the wave
+      qw[gi][4] = __builtin_amdgcn_readfirstlane(__float_as_uint(step));
+    }
+    return 1.0f;
   } else {
     return 1.0f;
   }
@@ -1860,6 +1879,9 @@ hipError_t launch_decode_fmt(const DecodeArgs &a, int max_seq_len, hipStream_t s
     case kFp8:
       return a.k_new ? launch_decode_t<G, kFp8, true>(a, max_seq_len, s, hu, hook)
                      : launch_decode_t<G, kFp8, false>(a, max_seq_len, s, hu, hook);
+    case kF16:  // appends go through the append kernel (the host never sets a.k_new here)
+      if (a.k_new) return hipErrorInvalidValue;
+      return launch_decode_t<G, kF16, false>(a, max_seq_len, s, hu, hook);
   }
   return hipErrorInvalidValue;
 }

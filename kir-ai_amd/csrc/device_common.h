@@ -13,6 +13,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
   return (uint16_t)(u >> 16);
 }
 
+// f32 -> fp16 bits, round to nearest even (v_cvt_f16_f32): beyond the fp16 range
+// an infinity, NaN stays NaN -- a float -> half conversion.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
 // int8 code of x with scale s: clamp(round_half_away(x / s), -127, 127), 0 for
 // s = 0 -- the symmetric rule of crates/llm-kv-cache/src/format.rs:711-735 (Rust
 // f32::round rounds half away from zero, as roundf does).  Shared by the KV
@@ -74,6 +78,7 @@ __device__ __forceinline__ float pool_elem(const PoolView &p, int tensor, int64_
   const void *base = tensor ? p.v : p.k;
   const void *sc = tensor ? p.v_scales : p.k_scales;
   if (p.format == kBf16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(base)[idx] << 16);
+  if (p.format == kF16) return (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(base)[idx]);
   if (p.format == kInt8) {
     const float s =
         (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(sc)[int8_scale_index(bh, t, p.block_tokens)]);

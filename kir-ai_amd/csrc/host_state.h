@@ -51,7 +51,7 @@ struct llh_ctx {
   int32_t *d_err = nullptr;
   std::atomic<uint64_t> decode_calls{0}, prefill_calls{0}, append_calls{0}, not_handled{0}, device_errors{0},
       shape_errors{0}, stream_decode_calls{0}, trait_tuned_calls{0}, generic_prefill_calls{0}, fused_append_calls{0},
-      d256_decode_calls{0};
+      d256_decode_calls{0}, generic_decode_calls{0};
   std::atomic<int32_t> options[LLH_OPT_COUNT] = {};
 
   // per-stream workspaces; ws_mu guards the list, ws_min_bytes and retired_flags
@@ -230,7 +230,7 @@ struct llh_kv_pool {
   size_t k_bytes = 0, s_bytes = 0;
 };
 
-inline size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 ? 2 : 1; }
+inline size_t elem_bytes(int32_t format) { return format == LLH_KV_BF16 || format == LLH_KV_F16 ? 2 : 1; }
 
 // int8 and fp8 pools keep the K and V scales in one allocation as (K, V) pairs
 // (int8_scale_index, fp8_scale_index): the V scale pointer is inside the K

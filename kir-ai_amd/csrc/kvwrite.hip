@@ -51,11 +51,22 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
 }
 
-// Whole 16-token blocks of head_dim 128, any pool format: one workgroup of
-// 256 lanes per (block, head).  Lane (t = lane / 16, c = lane % 16) loads the
-// 16 B of token t at dims 8c .. 8c+7 of K and of V (coalesced), writes K rows
-// straight out, and V is transposed through LDS so that every lane then writes
-// 16 B (bf16) or 8 B (int8) of one dim row: every global access is a full,
+// Eight bf16 elements as eight fp16 ones (round to nearest even).
+__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 w) {
+  uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    u[j] = (uint32_t)f32_to_f16_bits(__uint_as_float(u[j] << 16)) |
+           ((uint32_t)f32_to_f16_bits(__uint_as_float(u[j] & 0xffff0000u)) << 16);
+  return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+// Whole 16-token blocks of head_dim 128, every pool format but int8-row: one
+// workgroup of 256 lanes per (block, head).  Lane (t = lane / 16, c = lane % 16)
+// loads the 16 B of token t at dims 8c .. 8c+7 of K and of V (coalesced; fp16
+// pools convert them in registers), writes K rows straight out, and V is
+// transposed through LDS so that every lane then writes 16 B (bf16 / fp16) or
+// 8 B (int8 / fp8) of one dim row: every global access is a full,
 // coalesced vector access.  int8: the per-(token, head) scale is the 16 lanes'
 // absmax, then the same f16 rounding and code rule as the generic kernel; fp8:
 // the per-(block, head) scale is the workgroup's absmax / 448, then the generic
@@ -74,10 +85,14 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
   }
   const size_t bh = (size_t)blk * Hkv + h;
   const size_t src = (((size_t)i * BT + t) * Hkv + h) * Dh + 8 * c;
-  const uint4 kw = *reinterpret_cast<const uint4 *>(a.k + src);
-  const uint4 vw = *reinterpret_cast<const uint4 *>(a.v + src);
+  uint4 kw = *reinterpret_cast<const uint4 *>(a.k + src);
+  uint4 vw = *reinterpret_cast<const uint4 *>(a.v + src);
   const int d = tid >> 1, half = tid & 1;  // the dim row and token half this lane writes after the transpose
-  if (a.pool.format == kBf16) {
+  if (is16(a.pool.format)) {
+    if (a.pool.format == kF16) {  // each bf16 element widened (exact), then rounded to fp16
+      kw = bf16x8_to_f16x8(kw);
+      vw = bf16x8_to_f16x8(vw);
+    }
     __shared__ uint16_t lv[BT][Dh + 8];
     *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) = kw;
     *reinterpret_cast<uint4 *>(&lv[t][8 * c]) = vw;
@@ -200,6 +215,16 @@ __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs
       const int t = e / Dh, d = e % Dh;
       kd[(bh * BT + t) * Dh + d] = a.k[src_idx(t, d)];
       vd[(bh * Dh + d) * BT + t] = a.v[src_idx(t, d)];
+    }
+    return;
+  }
+  if (a.pool.format == kF16) {  // the bf16 rows converted (bf16 -> f32 exact, one rounding to fp16)
+    uint16_t *kd = reinterpret_cast<uint16_t *>(a.k_dst);
+    uint16_t *vd = reinterpret_cast<uint16_t *>(a.v_dst);
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const int t = e / Dh, d = e % Dh;
+      kd[(bh * BT + t) * Dh + d] = f32_to_f16_bits(bf16_to_f32(a.k[src_idx(t, d)]));
+      vd[(bh * Dh + d) * BT + t] = f32_to_f16_bits(bf16_to_f32(a.v[src_idx(t, d)]));
     }
     return;
   }
@@ -479,12 +504,13 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
       for (int d = lane; d < Dh; d += 64) f(d, ld(ks, d), ld(vs, d));
     }
   };
-  if (a.pool.format == kBf16) {
+  if (is16(a.pool.format)) {
     uint16_t *kd = reinterpret_cast<uint16_t *>(a.k_dst);
     uint16_t *vd = reinterpret_cast<uint16_t *>(a.v_dst);
+    const bool f16 = a.pool.format == kF16;
     for_elems([&](int d, float k, float v) __attribute__((always_inline)) {
-      kd[(bh * BT + off) * Dh + d] = f32_to_bf16_rne(k);
-      vd[(bh * Dh + d) * BT + off] = f32_to_bf16_rne(v);
+      kd[(bh * BT + off) * Dh + d] = f16 ? f32_to_f16_bits(k) : f32_to_bf16_rne(k);
+      vd[(bh * Dh + d) * BT + off] = f16 ? f32_to_f16_bits(v) : f32_to_bf16_rne(v);
     });
     return;
   }
@@ -565,6 +591,7 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
 __device__ __forceinline__ float load_f32(const PoolView &p, const void *base, const void *sc, size_t bh, size_t idx,
                                           int off) {
   if (p.format == kBf16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[idx]);
+  if (p.format == kF16) return (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t *>(base)[idx]);
   if (p.format == kInt8) {
     const float s = (float)__builtin_bit_cast(
         _Float16, reinterpret_cast<const uint16_t *>(sc)[int8_scale_index(bh, off, p.block_tokens)]);
@@ -630,7 +657,7 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
     const size_t idx = a.tensor ? (bh * Dh + d) * BT + off : (bh * BT + off) * Dh + d;
     if (a.out_f32)
       reinterpret_cast<float *>(a.out)[orow + d] = load_f32(a.pool, base, sc, bh, idx, off);
-    else if (a.pool.format == kBf16)
+    else if (is16(a.pool.format))
       reinterpret_cast<uint16_t *>(a.out)[orow + d] = reinterpret_cast<const uint16_t *>(base)[idx];
     else
       reinterpret_cast<uint8_t *>(a.out)[orow + d] = reinterpret_cast<const uint8_t *>(base)[idx];
@@ -648,7 +675,7 @@ hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const bool fast = a.pool.head_dim == 128 && a.pool.block_tokens == 16 &&
-                    (a.pool.format == kBf16 || a.pool.format == kInt8 || a.pool.format == kFp8) &&
+                    a.pool.format != kInt8Row &&
                     reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
   if (a.pool.format == kInt8Row)

@@ -15,7 +15,9 @@ constexpr int kPrefillThreads = 256;  // 4 wavefronts, 32 query rows each
 constexpr int kMatvecWaves = 8;       // wavefronts (K slices) per output-projection workgroup
 constexpr int kMatvecColsMultiple = kMatvecWaves * 16;  // cols the projection kernel takes
 
-enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2, kInt8Row = 3 };
+enum KvFormat : int32_t { kBf16 = 0, kInt8 = 1, kFp8 = 2, kInt8Row = 3, kF16 = 4 };
+// 16-bit element formats: bf16 and fp16 share the block layout and load paths
+__host__ __device__ constexpr bool is16(int fmt) { return fmt == kBf16 || fmt == kF16; }
 
 // int8 (per (token, head)) scales: one allocation holding, for each (block,
 // head) bh and token t, the fp16 pair (K scale, V scale).  A decode lane reads

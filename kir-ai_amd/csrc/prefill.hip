@@ -27,6 +27,9 @@
 // f32, rounded to bf16), so the MFMA path is the same for every format: the
 // result is attention over the dequantised cache, as the reference attends its
 // int8 cache after dequantising it (crates/llm-kv-cache/src/layer.rs:650-656).
+// fp16 pools keep K and V in fp16 and run v_mfma_f32_32x32x16_f16 instead, with
+// each query row scaled into fp16 by a power of two (f16_scaling) whose step
+// multiplies that row's scores, and fp16 softmax weights.
 //
 // Per wavefront, with v_mfma_f32_32x32x16_bf16:
 //   S^T[key][query] = K Q^T       A = K rows (token-major pool layout)
@@ -38,7 +41,7 @@
 // 16-key step is {4h..4h+3, 8+4h..8+4h+3} for lane half h; the V^T operand is
 // read from LDS with the same key order, so no transpose is ever done.
 // Softmax statistics are kept per query column in log2 units (online softmax).
-#include "device_common.h"
+#include "wave_ops.h"
 
 namespace llh {
 
@@ -55,38 +58,24 @@ constexpr int K_TILE = BN * K_STRIDE;        // bf16 elements of one K tile in L
 constexpr int V_TILE = KBLK * D * V_STRIDE;  // bf16 elements of one V^T tile in LDS
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;  // native vector: stays in registers
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
-}
-
+// 32x32x16 MFMA on packed 16-bit operands: fp16 for fp16 pools (OP = kF16),
+// bf16 for every other format
+template <int OP>
 __device__ __forceinline__ f32x16_t mfma32(const u32x4_t &a, const u32x4_t &b, const f32x16_t &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                  0, 0, 0);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Value of lane (l ^ 32): v_permlane32_swap exchanges the two 32-lane halves
-// of a pair of registers in the VALU, no LDS round trip.
-__device__ __forceinline__ float xor32_other(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  // r[0] holds the low half's values in both halves and r[1] the high half's
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
-
-// acc + lo + hi of a packed bf16 pair, exactly (dot product with (1, 1) in f32)
-__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
-                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+  if constexpr (OP == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
 }
 
 // One lane's share of a key tile: for each of the 4 blocks, the K elements of
 // token tid/16 at dims 8*(tid%16).. and the V^T elements of dim tid/2 at tokens
-// 8*(tid&1)..: 16 B each for bf16 pools; for int8 / fp8 pools 8 B of codes
+// 8*(tid&1)..: 16 B each for bf16 / fp16 pools; for int8 / fp8 pools 8 B of codes
 // each plus the scales they need (int8: the fp16 scale of the K token and the
 // eight of the V tokens; fp8: the block's f32 K and V scales), dequantised to
 // bf16 when the tile is stored to LDS.
@@ -94,10 +83,14 @@ template <int FMT, int NB>
 struct TileRegs;
 
 template <int NB>
-struct TileRegs<kBf16, NB> {
+struct TileRegs16 {
   u32x4_t k[NB];
   u32x4_t v[NB];
 };
+template <int NB>
+struct TileRegs<kBf16, NB> : TileRegs16<NB> {};
+template <int NB>
+struct TileRegs<kF16, NB> : TileRegs16<NB> {};
 
 template <int FMT, int NB>
 struct TileRegs {
@@ -137,7 +130,7 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
     use_mask |= use ? (1u << i) : 0u;
     const size_t bh = (size_t)(use ? phys : 0) * Hkv + kvh;
     const size_t base = bh * (BT * D);  // elements of this block-head
-    if constexpr (FMT == kBf16) {
+    if constexpr (is16(FMT)) {
       r.k[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base +
                                                 (tid >> 4) * D + (tid & 15) * 8);
       r.v[i] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.v) + base +
@@ -180,11 +173,12 @@ __device__ __forceinline__ float code_f32(const uint2 &w, int e) {
   }
 }
 
-// The tile's K and V^T elements of this lane as bf16 (the dequantised value,
-// code * scale in f32, rounded to nearest even).
+// The tile's K and V^T elements of this lane as 16-bit MFMA operands: the
+// stored elements of bf16 / fp16 pools; for int8 / fp8 the dequantised value
+// (code * scale in f32) rounded to bf16 (nearest even).
 template <int FMT, int NB>
-__device__ __forceinline__ void tile_bf16(const TileRegs<FMT, NB> &r, int i, u32x4_t &k, u32x4_t &v) {
-  if constexpr (FMT == kBf16) {
+__device__ __forceinline__ void tile_operands(const TileRegs<FMT, NB> &r, int i, u32x4_t &k, u32x4_t &v) {
+  if constexpr (is16(FMT)) {
     k = r.k[i];
     v = r.v[i];
   } else {
@@ -222,7 +216,7 @@ __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int
   for (int i = 0; i < NB; i++) {
     const int kb = kb0 + i;
     u32x4_t kk, v;
-    tile_bf16<FMT, NB>(r, i, kk, v);
+    tile_operands<FMT, NB>(r, i, kk, v);
     *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + (tid & 15) * 8]) = kk;
     if (!(use_mask & (1u << i))) v = u32x4_t{0u, 0u, 0u, 0u};
     if (tail) {
@@ -308,6 +302,25 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
       qb[ks] = t;
     }
   }
+  // fp16 pools: the row's q in fp16, scaled by 2^-e over its 128 dims (this lane
+  // and lane ^ 32 hold them); its scores carry the step 2^e
+  constexpr int OP = FMT == kF16 ? kF16 : kBf16;
+  float qstep = 1.0f;
+  if constexpr (FMT == kF16) {
+    uint32_t w[32];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) w[4 * ks + e] = qb[ks][e];
+    int mx = bf16_absmax_bits<32>(w);
+    mx = max(mx, __float_as_int(xor32_other(__int_as_float(mx), lane)));
+    const F16Scaling sc = f16_scaling(mx);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) qb[ks][e] = bf16x2_to_f16x2(w[4 * ks + e], sc.inv);
+    qstep = sc.step;
+  }
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][K_TILE];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][V_TILE];
@@ -362,7 +375,7 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
           const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
-          sacc[st] = mfma32(ka, qb[ks], sacc[st]);
+          sacc[st] = mfma32<OP>(ka, qb[ks], sacc[st]);
         }
       }
 
@@ -371,7 +384,7 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
       // scale (log2 units) is folded into the exp2 argument, fma(s, c, -m).
       // Masked tiles are scaled first, then masked with -inf (c_exp = 1).
       const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
-      const float c = a.scale_log2e;
+      const float c = a.scale_log2e * qstep;
       float c_exp = c;
       float tmax = -INFINITY;
       if (need_mask) {
@@ -401,11 +414,22 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
           for (int j = 0; j < 16; j++) tmin = fminf(tmin, sacc[st][j]);
         tmax = tmin * c;
       }
-      tmax = fmaxf(tmax, xor32_other(tmax));
+      // Raw scores beyond 2^26 (log2 units) once scaled: tmax, a rounded product, can
+      // fall below the fma's exact product c * s by more than the weights' headroom
+      // (|error| <= |tmax| 2^-24), so those tiles scale first, as masked tiles do:
+      // every score rounds as tmax did and the largest weight is exactly 1.
+      if (!need_mask && __any(fabsf(tmax) > 0x1p26f)) {
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) sacc[st][j] *= c;
+        c_exp = 1.0f;
+      }
+      tmax = fmaxf(tmax, xor32_other(tmax, lane));
       // Lazy rescale: the reference max m_run only moves when a row's max grows
       // by more than 8 (log2 units), so p <= 2^8 and the accumulators are
       // rescaled on few tiles.  The result is the same softmax (any reference
-      // max gives it) with no risk of overflow in f32 / bf16.
+      // max gives it) with no risk of overflow in f32 / bf16 / fp16.
       const float m_cand = fmaxf(m_run, tmax);
       const bool grow = m_cand > m_run + 8.0f;  // true on the first finite tile
       if (__any(grow)) {
@@ -426,15 +450,15 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
         for (int j = 0; j < 16; j++) p[j] = fast_exp2(__builtin_fmaf(sacc[st][j], c_exp, -mref));
 #pragma unroll
         for (int q = 0; q < 2; q++)
-          pb[2 * st + q] = u32x4_t{pack_bf16(p[8 * q + 0], p[8 * q + 1]), pack_bf16(p[8 * q + 2], p[8 * q + 3]),
-                                   pack_bf16(p[8 * q + 4], p[8 * q + 5]), pack_bf16(p[8 * q + 6], p[8 * q + 7])};
+          pb[2 * st + q] = u32x4_t{pack_16<OP>(p[8 * q + 0], p[8 * q + 1]), pack_16<OP>(p[8 * q + 2], p[8 * q + 3]),
+                                   pack_16<OP>(p[8 * q + 4], p[8 * q + 5]), pack_16<OP>(p[8 * q + 6], p[8 * q + 7])};
       }
-      // row sums of exactly the bf16 weights that enter P V (dot2 with (1, 1))
+      // row sums of exactly the 16-bit weights that enter P V (dot2 with (1, 1))
       float psum = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < KBLK; kb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) psum = dot2_ones(pb[kb][e], psum);
+        for (int e = 0; e < 4; e++) psum = dot2_ones_16<OP>(pb[kb][e], psum);
       l_run += psum;
 
       // ---- O^T += V^T P^T ----
@@ -445,7 +469,7 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
           const uint16_t *vrow = &vl[(kb * D + mt * 32 + col) * V_STRIDE];
           const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
           const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
-          oacc[mt] = mfma32(u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y}, pb[kb], oacc[mt]);
+          oacc[mt] = mfma32<OP>(u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y}, pb[kb], oacc[mt]);
         }
       }
     }
@@ -456,7 +480,7 @@ __global__ __launch_bounds__(kPrefillThreads * HPW, 2 / HPW) void paged_prefill_
 
   // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
   if (bad && tid == 0) atomicOr(a.err, kErrBadBlock);  // a needed block was missing: its keys read as zeros
-  const float l_tot = l_run + xor32_other(l_run);
+  const float l_tot = l_run + xor32_other(l_run, lane);
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   const size_t obase = ((size_t)(c0 + my_row) * Hq + qh) * D;
@@ -603,6 +627,9 @@ hipError_t launch_prefill(const PrefillArgs &a, int variant, hipStream_t s) {
       break;
     case kFp8:
       launch_prefill_fmt<kFp8>(a, variant, grid, s);
+      break;
+    case kF16:
+      launch_prefill_fmt<kF16>(a, variant, grid, s);
       break;
     default:
       return hipErrorInvalidValue;

@@ -283,6 +283,17 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
           for (int j = 0; j < 16; j++) tmin = fminf(tmin, sacc[st][j]);
         tmax = tmin * c;
       }
+      // Raw scores beyond 2^26 (log2 units) once scaled: tmax, a rounded product, can
+      // fall below the fma's exact product c * s by more than the weights' headroom
+      // (|error| <= |tmax| 2^-24), so those tiles scale first, as masked tiles do:
+      // every score rounds as tmax did and the largest weight is exactly 1.
+      if (!need_mask && __any(fabsf(tmax) > 0x1p26f)) {
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) sacc[st][j] *= c;
+        c_exp = 1.0f;
+      }
       tmax = fmaxf(tmax, xor32_other(tmax));
       const float m_cand = fmaxf(m_run, tmax);
       // a row without a finite score yet takes the tile's max (its accumulators are

@@ -8,6 +8,7 @@
 namespace llh {
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -130,6 +131,90 @@ __device__ __forceinline__ float bf16_round(float x) { return bf16_lo(pack_bf16(
 __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
                                          __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+
+// The same three for packed fp16 pairs (v_dot2_f32_f16, f32 accumulation).
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)lo, (_Float16)hi});  // round to nearest even
+}
+__device__ __forceinline__ float dot2_ones_f16(uint32_t pair, float acc) {
+  return dot2_f16(pair, 0x3C003C00u, acc);
+}
+
+// Format-generic forms for the 16-bit pools: FMT is kBf16 or kF16.
+template <int FMT>
+__device__ __forceinline__ float dot2_16(uint32_t a, uint32_t b, float c) {
+  if constexpr (FMT == kF16)
+    return dot2_f16(a, b, c);
+  else
+    return dot2_bf16(a, b, c);
+}
+template <int FMT>
+__device__ __forceinline__ uint32_t pack_16(float lo, float hi) {
+  if constexpr (FMT == kF16)
+    return pack_f16(lo, hi);
+  else
+    return pack_bf16(lo, hi);
+}
+template <int FMT>
+__device__ __forceinline__ float dot2_ones_16(uint32_t pair, float acc) {
+  if constexpr (FMT == kF16)
+    return dot2_ones_f16(pair, acc);
+  else
+    return dot2_ones(pair, acc);
+}
+
+// Largest |x| over the bf16 elements of w[0 .. NW), as integer bits: the bits
+// of |x| order as integers (NaN above infinity).
+template <int NW, int N>
+__device__ __forceinline__ int bf16_absmax_bits(const uint32_t (&w)[N]) {
+  static_assert(NW <= N, "words");
+  typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+  u16x2_t mv = {0, 0};
+#pragma unroll
+  for (int k = 0; k < NW; k++) mv = __builtin_elementwise_max(mv, __builtin_bit_cast(u16x2_t, w[k] & 0x7fff7fffu));
+  return max((int)mv.x, (int)mv.y);
+}
+
+// bf16 -> fp16 for q . k against fp16 K.  A query vector whose largest |x| has
+// the bits mx is scaled by inv = 2^-e, chosen so that its largest scaled element
+// lies in [2^14, 2^15) (no fp16 overflow; e >= -126), and rounded to fp16
+// (nearest even): elements within 2^-28 of the largest convert exactly (bf16
+// holds 8 significant bits), smaller ones keep an absolute error below 2^-38 of
+// it.  step = 2^e (q . k = 2^e * q' . k), NaN when the vector holds an infinity
+// or NaN.
+struct F16Scaling {
+  float inv;
+  float step;
+};
+__device__ __forceinline__ F16Scaling f16_scaling(int mx) {
+  const int ex = mx >> 7;                // biased exponent of the largest |x|
+  const int inv_b = min(268 - ex, 253);  // biased exponent of 2^-e
+  return {__int_as_float(inv_b << 23), ex == 255 ? __builtin_nanf("") : __int_as_float((254 - inv_b) << 23)};
+}
+
+// The scaled fp16 pair of a bf16 pair
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float inv) {
+  return pack_f16(bf16_lo(w) * inv, bf16_hi(w) * inv);
+}
+
+// One query head's bf16 words (the first NW of w; the head's dims spread over
+// the 16 lanes of a row) as fp16 words (f16_scaling over the head's elements).
+// Returns the head's step.
+template <int NW, int N>
+__device__ __forceinline__ float q_bf16_to_f16(uint32_t (&w)[N]) {
+  int mx = bf16_absmax_bits<NW>(w);
+  mx = max(mx, __builtin_amdgcn_update_dpp(0, mx, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  mx = max(mx, __builtin_amdgcn_update_dpp(0, mx, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  mx = max(mx, __builtin_amdgcn_update_dpp(0, mx, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  mx = max(mx, __builtin_amdgcn_update_dpp(0, mx, 0x140, 0xF, 0xF, false));  // row_mirror
+  const F16Scaling sc = f16_scaling(mx);
+#pragma unroll
+  for (int k = 0; k < NW; k++) w[k] = bf16x2_to_f16x2(w[k], sc.inv);
+  return sc.step;
 }
 
 }  // namespace llh

@@ -40,6 +40,7 @@ KV_BF16 = 0
 KV_INT8 = 1
 KV_FP8_E4M3 = 2
 KV_INT8_ROW = 3  # the reference's int8 layout: f32 scale per token row over all kv heads
+KV_F16 = 4  # IEEE fp16 elements (no scales)
 
 ERR_FLAG_BAD_BLOCK = 1
 ERR_FLAG_TOO_MANY_SPLITS = 2
@@ -137,6 +138,7 @@ class Metrics(ctypes.Structure):
         ("stream_slots", ctypes.c_uint64),
         ("workspace_bytes", ctypes.c_uint64),
         ("d256_decode_calls", ctypes.c_uint64),
+        ("generic_decode_calls", ctypes.c_uint64),
     ]
 
 

@@ -25,6 +25,7 @@ KV_BF16 = 0
 KV_INT8 = 1
 KV_FP8_E4M3 = 2
 KV_INT8_ROW = 3
+KV_F16 = 4
 
 _lib = None
 
@@ -319,7 +320,7 @@ class Pool:
     @classmethod
     def from_raw(cls, fmt: int, block_tokens: int, kv_heads: int, head_dim: int, n_blocks: int, raw: dict) -> "Pool":
         """From the raw byte arrays of llm_hip.KvPool.raw()."""
-        if fmt == KV_BF16:
+        if fmt in (KV_BF16, KV_F16):
             k, v = raw["k"].view(np.uint16), raw["v"].view(np.uint16)
             ks = vs = None
         elif fmt == KV_INT8:
@@ -344,7 +345,7 @@ class Pool:
     def gather_raw(self, table: np.ndarray, lo: int, hi: int, tensor: int) -> tuple[int, np.ndarray]:
         t = np.ascontiguousarray(table, dtype=np.int32)
         n = max(0, hi - lo) * self.hkv * self.d
-        out = np.zeros(n, dtype=np.uint16 if self.fmt == KV_BF16 else np.uint8)
+        out = np.zeros(n, dtype=np.uint16 if self.fmt in (KV_BF16, KV_F16) else np.uint8)
         st = lib().orc_pool_gather_raw(ctypes.byref(self.c), _p(t), t.size, lo, hi, tensor, _p(out))
         return st, out
 
@@ -380,10 +381,12 @@ class Pool:
 
 
 def build_bf16_pool(rows_k: np.ndarray, rows_v: np.ndarray, tables: np.ndarray, seq_lens, block_tokens: int,
-                    kv_heads: int, head_dim: int, n_blocks: int) -> Pool:
-    """Host-side pool (bf16) in the device layout from per-sequence token rows.
+                    kv_heads: int, head_dim: int, n_blocks: int, fmt: int = KV_BF16) -> Pool:
+    """Host-side pool (bf16, or f16 with fmt=KV_F16) in the device layout from
+    per-sequence token rows.
 
-    rows_k[b] / rows_v[b]: uint16 arrays [len_b][kv_heads][head_dim]."""
+    rows_k[b] / rows_v[b]: uint16 arrays [len_b][kv_heads][head_dim] of the
+    format's element bits."""
     k = np.zeros((n_blocks, kv_heads, block_tokens, head_dim), dtype=np.uint16)
     v = np.zeros((n_blocks, kv_heads, head_dim, block_tokens), dtype=np.uint16)
     for b, L in enumerate(seq_lens):
@@ -392,7 +395,7 @@ def build_bf16_pool(rows_k: np.ndarray, rows_v: np.ndarray, tables: np.ndarray, 
             t = pos % block_tokens
             k[blk, :, t, :] = rows_k[b][pos]
             v[blk, :, :, t] = rows_v[b][pos]
-    return Pool(KV_BF16, block_tokens, kv_heads, head_dim, n_blocks, k, v)
+    return Pool(fmt, block_tokens, kv_heads, head_dim, n_blocks, k, v)
 
 
 # ---------------- quantisation ----------------

@@ -465,6 +465,8 @@ float orc_pool_elem(const orc_pool *p, int tensor, int64_t block, int32_t head, 
     }
     case ORC_KV_INT8_ROW: /* dequantize_int8_rows (format.rs:739-759): code * row scale */
       return (float)((const int8_t *)base)[idx] * ((const float *)scales)[(int64_t)block * p->block_tokens + t];
+    case ORC_KV_F16: /* the f16 element widened to f32 (exact) */
+      return orc_f16_to_f32(((const uint16_t *)base)[idx]);
     default:
       return NAN;
   }
@@ -511,7 +513,7 @@ int orc_pool_gather_raw(const orc_pool *p, const int32_t *table, int32_t n_table
         int64_t src = tensor ? v_index(p, block, h, t, d) : k_index(p, block, h, t, d);
         int64_t o = (int64_t)(pos - lo) * vl + (int64_t)h * p->head_dim + d;
         const void *base = tensor ? p->v : p->k;
-        if (p->format == ORC_KV_BF16)
+        if (p->format == ORC_KV_BF16 || p->format == ORC_KV_F16)
           ((uint16_t *)out)[o] = ((const uint16_t *)base)[src];
         else
           ((uint8_t *)out)[o] = ((const uint8_t *)base)[src];

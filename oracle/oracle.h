@@ -48,6 +48,7 @@ extern "C" {
 #define ORC_KV_INT8 1
 #define ORC_KV_FP8_E4M3 2
 #define ORC_KV_INT8_ROW 3 /* the reference's own int8 layout: f32 scale per token row over all heads */
+#define ORC_KV_F16 4      /* IEEE binary16 elements (KvCacheConfig::f16, format.rs:69-120) */
 
 /* ---------------- scalar conversions ---------------- */
 uint16_t orc_f32_to_bf16(float x);   /* round to nearest even, NaN kept quiet */
@@ -160,7 +161,7 @@ float orc_pool_elem(const orc_pool *p, int tensor, int64_t block, int32_t head, 
 int orc_pool_gather_f32(const orc_pool *p, const int32_t *table, int32_t n_table, int32_t lo,
                         int32_t hi, float *keys_out, float *values_out);
 /* gather raw storage bits of tensor into [hi-lo][kv_heads][head_dim] elements
- * (2 bytes for bf16, 1 byte for int8/fp8) */
+ * (2 bytes for bf16 / f16, 1 byte for int8/fp8) */
 int orc_pool_gather_raw(const orc_pool *p, const int32_t *table, int32_t n_table, int32_t lo,
                         int32_t hi, int tensor, void *out);
 /* write one token row ([kv_heads*head_dim] f32) into slot (block, t) of a bf16 pool */

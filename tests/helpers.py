@@ -15,6 +15,21 @@ def rows_bf16(seed: int, b: int, lo: int, hi: int, kv_heads: int, head_dim: int)
     return oracle.normal_bf16(seed, n, off).reshape(hi - lo, kv_heads, head_dim)
 
 
+# query magnitudes from bf16 subnormal to 1e30, zero included
+MAGNITUDES = np.array([1.0, 1e-30, 6.0, 1e-3, 1e-39, 0.0, 3e4, 1e30], np.float32)
+
+
+def magnitude_rows(q_bf16: np.ndarray, heads: int, head_dim: int) -> np.ndarray:
+    """q (bf16 bits, rows x heads x head_dim) with (row, head) scaled by MAGNITUDES in turn
+    and dim 3 of every 7th row 100x its row: rows and heads of very different size side
+    by side (scores up to ~1e31 in log2 units)."""
+    qf = oracle.bf16_to_f32(q_bf16.ravel()).reshape(-1, heads, head_dim).copy()
+    rows = qf.shape[0]
+    qf *= MAGNITUDES[(np.arange(rows)[:, None] + np.arange(heads)[None, :]) % MAGNITUDES.size][:, :, None]
+    qf[::7, :, 3] *= np.float32(100.0)
+    return oracle.f32_to_bf16(qf.ravel())
+
+
 def to_dev(a: np.ndarray):
     import torch
 

@@ -11,8 +11,9 @@ one and a token past the end each fail this comparison.
 Covered: both tuned decode kernels on C2 at full size and on window edges (W = 1, 17,
 100, 4096), C4 decode, the full C5 launch (int8 and fp8, all 64 sequences), a window
 ring of exactly W/16 blocks, the fused append (bf16, both kernels) and the quantised
-append-then-attend, the allocation-free entry point, C3 and C4 prefill at full size
-(bf16, int8, fp8 blocks) and the element-wise decode and prefill kernels.  Slots past
+and fp16 append-then-attend, the allocation-free entry point, C3 and C4 prefill at full
+size (bf16, int8, fp8, fp16 blocks), fp16 pools under windows, and the element-wise
+decode and prefill kernels.  Slots past
 a sequence's end and before its window hold codes of their own positions, so
 attending any of them changes a count.
 """
@@ -150,7 +151,7 @@ def test_decode_c5_full_launch_attended_set(ctx, opts, fmt):
     pool.close()
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_F16])
 def test_decode_quantized_windows_attended_set(ctx, decode_kernel, fmt):
     lens = np.array([1, 17, 250, 1025, 3000], np.int32)
     batch = workloads.paged_batch(lens, BT, 0.10, seed=fmt + 70)
@@ -200,7 +201,7 @@ def test_decode_noalloc_attended_set(ctx):
         check_decode(decode_q0(ctx, pool, batch, 16, W, noalloc=True), lens, W, 16, 8, 1.0, f"noalloc W={W}")
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_F16])
 def test_decode_element_wise_kernel_attended_set(ctx, opts, fmt):
     opts(llm_hip.OPT_FORCE_GENERIC, 1)
     lens = np.array([1, 17, 250, 1025], np.int32)
@@ -241,7 +242,7 @@ def decoy_last_slots(ctx, pool, batch, Hkv):
 
 
 @pytest.mark.parametrize("window", [0, 1000])
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_F16])
 def test_decode_append_attended_set(ctx, decode_kernel, fmt, window):
     """llh_paged_decode_append: the step attends [lo, len - 1) from the pool plus the new
     token from the call's rows (never the stale slot), and leaves that token in the slot."""
@@ -286,7 +287,7 @@ def prefill_q0(ctx, pool, batch, chunks, Hq, window):
     return from_dev_bf16(out), starts
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_F16])
 def test_prefill_c3_attended_set(ctx, fmt):
     """configs[2] at full size: 8 x (1536 cached + 512 new), Hq32/Hkv4; every row of every
     sequence attends exactly [0, pos]."""

@@ -32,7 +32,8 @@ def write_case(ctx, fmt, lens, Hkv, seed, head_dim=D, free=0.1):
     return batch, pool, ids, sk, sv
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_INT8_ROW])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_INT8_ROW,
+                                 llm_hip.KV_F16])
 def test_gather_is_bit_exact(ctx, fmt):
     import torch
 
@@ -41,7 +42,7 @@ def test_gather_is_bit_exact(ctx, fmt):
     opool = oracle.Pool.from_raw(fmt, BT, Hkv, D, batch.n_blocks, pool.raw())
     d_lens, d_tab = to_dev(batch.seq_lens), to_dev(batch.tables)
     desc = ctx.decode_desc(d_lens, d_tab, Hkv, int(batch.seq_lens.max()))
-    esz = 2 if fmt == llm_hip.KV_BF16 else 1
+    esz = 2 if fmt in (llm_hip.KV_BF16, llm_hip.KV_F16) else 1
     for b, L in enumerate(batch.seq_lens):
         for lo, hi in ((0, int(L)), (int(L) // 3, int(L))):
             for tensor in (0, 1):
@@ -183,7 +184,7 @@ def test_fp8_quantise_on_write_is_bit_exact(ctx):
             assert np.array_equal(v[blk, h], codes.reshape(BT, D).T) and vs[blk, h] == np.float32(s)
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_F16])
 def test_block_write_vector_and_generic_kernels_agree(ctx, fmt):
     """head_dim 128 / 16-token blocks from 16-byte aligned rows take the vector
     kernel; the same rows 2 bytes off alignment take the generic one.  Pools equal."""
@@ -237,7 +238,7 @@ def test_block_write_flags_bad_block(ctx):
     assert ctx.device_errors() & llm_hip.ERR_FLAG_BAD_BLOCK
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8])
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_F16])
 def test_append_equals_block_write(ctx, fmt):
     import torch
 

@@ -14,7 +14,7 @@ import pytest
 
 import llm_hip
 import oracle
-from helpers import assert_parity, from_dev_bf16, rows_bf16, to_dev
+from helpers import assert_parity, from_dev_bf16, magnitude_rows, rows_bf16, to_dev
 from llm_hip import workloads
 
 pytestmark = pytest.mark.gpu
@@ -151,10 +151,11 @@ def test_prefill_quantized_ragged_full_oracle(ctx, fmt, W):
     assert_parity(out, ref, what=f"ragged fmt={fmt} W={W}")
 
 
-def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm_hip.KV_BF16, misalign=False):
+def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm_hip.KV_BF16, misalign=False,
+                q_magnitudes=False):
     """Any pool shape: the rows go in through llh_kv_write_blocks, prefill runs on q / out
-    that are 2 bytes off 16-byte alignment when misalign is set.  Returns what the oracle
-    check needs and the output."""
+    that are 2 bytes off 16-byte alignment when misalign is set (q scaled by
+    helpers.magnitude_rows with q_magnitudes).  Returns the output and the oracle's."""
     import torch
 
     ctxlen = [p + c for p, c in zip(prefix, chunk)]
@@ -168,6 +169,8 @@ def build_shape(ctx, prefix, chunk, Hq, Hkv, window, seed, head_dim, bt, fmt=llm
     starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
     n = int(starts[-1]) * Hq * head_dim
     q = oracle.normal_bf16(seed + 3, n)
+    if q_magnitudes:
+        q = magnitude_rows(q, Hq, head_dim)
     off = 1 if misalign else 0
     qbuf = torch.zeros(n + 8, dtype=torch.int16, device="cuda")
     qbuf[off:off + n] = to_dev(q)
@@ -225,6 +228,19 @@ def test_prefill_force_generic_matches_mfma_kernel(ctx, opts, W):
     assert_parity(fast, ref, what="mfma")
     assert_parity(gen, ref, what="generic")
     assert_parity(gen, oracle.bf16_to_f32(fast), what="generic vs mfma")
+
+
+def test_prefill_query_magnitudes(ctx):
+    """Query rows from bf16 subnormal to 1e30 (scores to ~1e31 in log2 units) on the MFMA
+    kernel: tiles whose scaled max passes 2^26 scale their scores before the exponent
+    (the fused form's rounding would overflow the weights there); every row at the bar.
+    bf16 blocks (fp16 ones in test_gpu_f16.py): int8 / fp8 tiles are dequantised to bf16
+    (code x scale rounded, relative error 2^-9), so at these magnitudes, where softmax is
+    one-hot, a row can pick a different top key than the oracle's f32 dequantisation."""
+    before = ctx.metrics()["generic_prefill_calls"]
+    out, ref = build_shape(ctx, [300, 0], [200, 129], 16, 8, 0, 95, D, BT, q_magnitudes=True)
+    assert ctx.metrics()["generic_prefill_calls"] == before
+    assert_parity(out, ref, what="prefill query magnitudes")
 
 
 def test_prefill_rejects_head_dim_beyond_generic_bound(ctx):

@@ -13,7 +13,7 @@ import pytest
 import llm_hip
 import oracle
 from attended_set import check_prefill, coded_rows
-from helpers import assert_parity, from_dev_bf16, rows_bf16, to_dev
+from helpers import assert_parity, from_dev_bf16, magnitude_rows, rows_bf16, to_dev
 from llm_hip import workloads
 
 pytestmark = pytest.mark.gpu
@@ -23,9 +23,10 @@ BT = 16
 HQ, HKV = 16, 2
 
 
-def run(ctx, prefix, chunk, window, seed, gate=False, coded=False):
+def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=False):
     """Prefill of `chunk` rows after `prefix` cached ones per sequence; returns (out, ref) with
-    ref None for the coded probe (q = 0, V one-hot position codes)."""
+    ref None for the coded probe (q = 0, V one-hot position codes); q scaled by
+    helpers.magnitude_rows with q_magnitudes."""
     import torch
 
     ctxlen = [p + c for p, c in zip(prefix, chunk)]
@@ -40,6 +41,8 @@ def run(ctx, prefix, chunk, window, seed, gate=False, coded=False):
     starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
     T = int(starts[-1])
     q = np.zeros(T * HQ * D, np.uint16) if coded else oracle.normal_bf16(seed + 3, T * HQ * D)
+    if q_magnitudes:
+        q = magnitude_rows(q, HQ, D)
     g = oracle.f32_to_bf16(oracle.bf16_to_f32(oracle.normal_bf16(seed + 4, T * HQ * D)) * np.float32(2.0)) \
         if gate else None
     out = torch.full((T * HQ * D,), 0x7FC0, dtype=torch.int16, device="cuda")
@@ -67,6 +70,13 @@ def test_prefill256_ragged_full_oracle(ctx, window):
     0 .. 1536 tokens, every row against the oracle."""
     out, ref = run(ctx, [0, 300, 1000, 1536, 7], [130, 64, 257, 17, 0], window, 41 + window)
     assert_parity(out, ref, what=f"prefill d256 W={window}")
+
+
+def test_prefill256_query_magnitudes(ctx):
+    """Query rows from bf16 subnormal to 1e30 (scores to ~1e31 in log2 units): tiles whose
+    scaled max passes 2^26 scale their scores before the exponent."""
+    out, ref = run(ctx, [300, 0], [200, 129], 0, 95, q_magnitudes=True)
+    assert_parity(out, ref, what="prefill d256 query magnitudes")
 
 
 def test_prefill256_qwen36_chunk(ctx):

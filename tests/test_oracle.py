@@ -496,6 +496,46 @@ def test_pool_gather_is_bit_exact():
         assert np.array_equal(kf, oracle.bf16_to_f32(rk[b].ravel()))
 
 
+def test_f16_pool_elements_are_the_widened_halves():
+    """An f16 pool (KvCacheConfig::f16, format.rs:69-120) holds IEEE binary16 bits:
+    the oracle reads element (block, head, token, dim) as numpy's float16 -> float32
+    of those bits (subnormals, infinities, signed zeros included), through the same
+    K token-row / V dim-row layout as the bf16 pool, and decode over it equals the
+    reference attention of the widened rows."""
+    from llm_hip import workloads
+
+    Hkv, D, BT, Hq = 2, 8, 4, 4
+    lens = [5, 16, 23]
+    batch = workloads.paged_batch(lens, BT, 0.2, 61)
+    rng = np.random.default_rng(61)
+    rk = [rng.integers(0, 65536, size=(L, Hkv, D), dtype=np.uint16) for L in lens]
+    rv = [rng.integers(0, 65536, size=(L, Hkv, D), dtype=np.uint16) for L in lens]
+    for r in rk + rv:  # finite values only (the decode below needs finite scores)
+        r[np.isnan(r.view(np.float16)) | np.isinf(r.view(np.float16))] = 0x3C00
+    rk[0][0, 0, :4] = [0x0001, 0x8000, 0x03FF, 0x7BFF]  # smallest subnormal, -0, largest subnormal, 65504
+    pool = oracle.build_bf16_pool(rk, rv, batch.tables, lens, BT, Hkv, D, batch.n_blocks, fmt=oracle.KV_F16)
+    for b, L in enumerate(lens):
+        for tensor, rows in ((0, rk[b]), (1, rv[b])):
+            st, raw = pool.gather_raw(batch.tables[b], 0, L, tensor)
+            assert st == oracle.OK and np.array_equal(raw, rows.ravel())
+        st, kf, vf = pool.gather_f32(batch.tables[b], 0, L)
+        assert np.array_equal(kf, rk[b].view(np.float16).astype(np.float32).ravel())
+        assert np.array_equal(vf, rv[b].view(np.float16).astype(np.float32).ravel())
+    # small-magnitude rows so that softmax stays finite
+    sk = [(r.view(np.float16).astype(np.float32) * 1e-4).astype(np.float16).view(np.uint16) for r in rk]
+    sv = [(r.view(np.float16).astype(np.float32) * 1e-4).astype(np.float16).view(np.uint16) for r in rv]
+    pool = oracle.build_bf16_pool(sk, sv, batch.tables, lens, BT, Hkv, D, batch.n_blocks, fmt=oracle.KV_F16)
+    q = oracle.normal_bf16(62, len(lens) * Hq * D)
+    st, out = pool.decode(Hq, batch.seq_lens, batch.tables, 0, q, 0.5)
+    assert st == oracle.OK
+    qf = oracle.bf16_to_f32(q).reshape(len(lens), Hq * D)
+    for b, L in enumerate(lens):
+        kf = sk[b].view(np.float16).astype(np.float32).reshape(L, -1)
+        vf = sv[b].view(np.float16).astype(np.float32).reshape(L, -1)
+        st, ref = oracle.attention_mix(qf[b], kf, vf, L, Hq, Hkv, D, 0.5)
+        assert st == oracle.OK and np.array_equal(out.reshape(len(lens), -1)[b], ref)
+
+
 def test_pool_gather_rejects_out_of_pool_blocks():
     batch, rk, rv, pool = _paged_case([20], 1, 4, 4, 11)
     t = batch.tables[0].copy()
