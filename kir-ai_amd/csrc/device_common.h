@@ -28,6 +28,17 @@ __device__ __forceinline__ int8_t quant_int8(float x, float s) {
   return (int8_t)c;
 }
 
+// x / s rounded to nearest even for a divisor s > 0 shared by many x, given
+// r = RN(1 / s): Markstein's method, q = RN(x r), e = x - q s (exact by fma),
+// RN(q + e r), with x's sign (which restores -0).  Three instructions instead of a
+// correctly rounded division per element.  Used only where tests/quotient_check.c
+// shows exhaustively that its codes equal those of the correctly rounded quotient
+// (under IEEE and flush-to-zero arithmetic alike).
+__device__ __forceinline__ float div_shared(float x, float s, float r) {
+  const float q = __fmul_rn(x, r);
+  return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), r, q), x);
+}
+
 // OCP e4m3fn encode, round to nearest even, saturate to +-448, NaN -> 0x7f.
 __device__ __forceinline__ uint8_t encode_e4m3(float x) {
   const uint32_t u = __float_as_uint(x);

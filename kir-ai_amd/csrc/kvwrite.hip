@@ -146,10 +146,16 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
       const float m = fmaxf(fmaxf(red[tensor][0], red[tensor][1]), fmaxf(red[tensor][2], red[tensor][3]));
       const float sc = m == 0.0f ? 0.0f : __fdiv_rn(m, 448.0f);
       uint32_t q[2] = {0u, 0u};
+      if (sc >= 0x1p-90f) {  // block-uniform: the shared-divisor quotient (div_shared)
+        const float rr = __fdiv_rn(1.0f, sc);
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint32_t code = sc == 0.0f ? 0u : encode_e4m3(__fdiv_rn(x[tensor][j], sc));
-        q[j >> 2] |= code << (8 * (j & 3));
+        for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)encode_e4m3(div_shared(x[tensor][j], sc, rr)) << (8 * (j & 3));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const uint32_t code = sc == 0.0f ? 0u : encode_e4m3(__fdiv_rn(x[tensor][j], sc));
+          q[j >> 2] |= code << (8 * (j & 3));
+        }
       }
       codes[tensor][0] = q[0];
       codes[tensor][1] = q[1];
@@ -173,8 +179,17 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     const _Float16 s16 = (_Float16)(mx == 0.0f ? 0.0f : __fdiv_rn(mx, 127.0f));
     const float sc = (float)s16;
     uint32_t q[2] = {0u, 0u};
+    if (sc > 0.0f && sc < INFINITY) {  // (per token row) the shared-divisor quotient (div_shared)
+      const float rr = __fdiv_rn(1.0f, sc);
 #pragma unroll
-    for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)(uint8_t)quant_int8(x[j], sc) << (8 * (j & 3));
+      for (int j = 0; j < 8; j++) {
+        const float c = fminf(fmaxf(roundf(div_shared(x[j], sc, rr)), -127.0f), 127.0f);
+        q[j >> 2] |= (uint32_t)(uint8_t)(int8_t)c << (8 * (j & 3));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)(uint8_t)quant_int8(x[j], sc) << (8 * (j & 3));
+    }
     codes[tensor][0] = q[0];
     codes[tensor][1] = q[1];
     if (c == 0)
