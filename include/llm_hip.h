@@ -362,6 +362,11 @@ int llh_debug_gather(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
 /* Decodes `n` raw fp8 e4m3 codes with the kernels' own conversion (f32 out). */
 int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int32_t n, void *stream);
 
+/* Runs the kernels' fp8 e4m3 encoder (the hardware conversion) and the integer
+ * reference rule on every f32 bit pattern but NaNs and stores how many codes differ
+ * (a test hook, no reference counterpart; synchronous, allocates 8 bytes). */
+int llh_debug_fp8_encode_check(llh_ctx *ctx, uint64_t *h_mismatches);
+
 /* ------------------------------------------------------------------ */
 /* trait mirror: LayerKvCache + NativeMatvecBackend attention hooks    */
 /* ------------------------------------------------------------------ */

@@ -993,6 +993,21 @@ int llh_debug_decode_fp8(llh_ctx *ctx, const uint8_t *d_codes, float *d_out, int
   return LLH_OK;
 }
 
+int llh_debug_fp8_encode_check(llh_ctx *ctx, uint64_t *h_mismatches) {
+  if (!ctx || !h_mismatches) return LLH_ERR_NULL;
+  unsigned long long *d = nullptr;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc(&d, sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMemset(d, 0, sizeof(unsigned long long));
+  if (e == hipSuccess) e = launch_fp8_encode_check(d, nullptr);
+  unsigned long long h = 0;
+  if (e == hipSuccess) e = hipMemcpy(&h, d, sizeof(h), hipMemcpyDeviceToHost);
+  if (d) (void)hipFree(d);
+  if (e != hipSuccess) return ctx->hip_fail(e, "fp8 encode check");
+  *h_mismatches = h;
+  return LLH_OK;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

@@ -39,8 +39,10 @@ __device__ __forceinline__ float div_shared(float x, float s, float r) {
   return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), r, q), x);
 }
 
-// OCP e4m3fn encode, round to nearest even, saturate to +-448, NaN -> 0x7f.
-__device__ __forceinline__ uint8_t encode_e4m3(float x) {
+// OCP e4m3fn encode in integer arithmetic: round to nearest even, saturate to
+// +-448, NaN -> 0x7f.  The reference rule for encode_e4m3 below
+// (llh_debug_fp8_encode_check compares the two on every f32).
+__device__ __forceinline__ uint8_t encode_e4m3_soft(float x) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t au = u & 0x7fffffffu;
@@ -66,6 +68,17 @@ __device__ __forceinline__ uint8_t encode_e4m3(float x) {
   if (q > 0x7eu) q = 0x7eu;
   return (uint8_t)(sign | q);
 }
+
+// OCP e4m3fn codes of a and b into bytes 0-1 (HI: bytes 2-3) of old: v_cvt_pk_fp8_f32
+// (round to nearest even) on the inputs clamped to +-448, which gives encode_e4m3_soft's
+// code for every f32 but NaN (checked exhaustively on gfx950 by
+// llh_debug_fp8_encode_check).
+template <bool HI>
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b, uint32_t old) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, -448.0f, 448.0f),
+                                                   __builtin_amdgcn_fmed3f(b, -448.0f, 448.0f), (int)old, HI);
+}
+__device__ __forceinline__ uint8_t encode_e4m3(float x) { return (uint8_t)e4m3x2<false>(x, 0.0f, 0u); }
 
 // fp8 e4m3 code as f32 (exact).
 __device__ __forceinline__ float decode_e4m3(uint32_t code) { return __builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0]; }

@@ -148,8 +148,12 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
       uint32_t q[2] = {0u, 0u};
       if (sc >= 0x1p-90f) {  // block-uniform: the shared-divisor quotient (div_shared)
         const float rr = __fdiv_rn(1.0f, sc);
+        float y[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)encode_e4m3(div_shared(x[tensor][j], sc, rr)) << (8 * (j & 3));
+        for (int j = 0; j < 8; j++) y[j] = div_shared(x[tensor][j], sc, rr);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+          q[k] = e4m3x2<true>(y[4 * k + 2], y[4 * k + 3], e4m3x2<false>(y[4 * k], y[4 * k + 1], 0u));
       } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -679,7 +683,27 @@ __global__ __launch_bounds__(64) void gather_kernel(const GatherArgs a) {
   }
 }
 
+// Every f32 bit pattern but NaNs: the fp8 encoder the kernels use (encode_e4m3,
+// v_cvt_pk_fp8_f32 on clamped inputs) against the integer reference rule
+// (encode_e4m3_soft); one count per thread, added once.
+__global__ __launch_bounds__(256) void fp8_encode_check_kernel(unsigned long long *mismatches) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  unsigned long long bad = 0;
+  for (uint64_t i = tid; i < (1ull << 32); i += stride) {
+    const float x = __uint_as_float((uint32_t)i);
+    if (x != x) continue;
+    bad += encode_e4m3(x) != encode_e4m3_soft(x);
+  }
+  atomicAdd(mismatches, bad);
+}
+
 }  // namespace
+
+hipError_t launch_fp8_encode_check(unsigned long long *mismatches, hipStream_t s) {
+  hipLaunchKernelGGL(fp8_encode_check_kernel, dim3(8192), dim3(256), 0, s, mismatches);
+  return hipGetLastError();
+}
 
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;

@@ -222,6 +222,9 @@ constexpr int64_t kNoSlot = INT64_MIN;
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s);
 hipError_t launch_decode_fp8(const uint8_t *codes, float *out, int32_t n, hipStream_t s);
+// adds to *mismatches the f32 values (NaNs excepted) whose fp8 code from the kernels'
+// encoder differs from the integer reference rule
+hipError_t launch_fp8_encode_check(unsigned long long *mismatches, hipStream_t s);
 hipError_t launch_matvec_bf16(const MatvecArgs &a, hipStream_t s);
 
 }  // namespace llh

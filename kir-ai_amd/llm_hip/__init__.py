@@ -320,6 +320,7 @@ SIGNATURES = {
     "llh_paged_prefill": (ctypes.c_int, [_P, _P, ctypes.POINTER(PrefillDesc), _P, _P, ctypes.c_float, _P]),
     "llh_debug_gather": (ctypes.c_int, [_P, _P, ctypes.POINTER(DecodeDesc), _I32, _I32, _I32, _I32, _P, _P]),
     "llh_debug_decode_fp8": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
+    "llh_debug_fp8_encode_check": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "llh_layer_cache_create": (ctypes.c_int, [_P, _SZ, _SZ, _SZ, _I32, ctypes.POINTER(_P)]),
     "llh_layer_cache_destroy": (ctypes.c_int, [_P]),
     "llh_layer_cache_create_from_rows": (ctypes.c_int, [_P, ctypes.POINTER(LayerCacheRows), ctypes.POINTER(_P)]),
@@ -674,6 +675,13 @@ class Context:
 
     def decode_fp8(self, codes, out, stream=None) -> None:
         self.check(self.lib.llh_debug_decode_fp8(self.handle, _ptr(codes), _ptr(out), codes.numel(), _stream(stream)))
+
+    def fp8_encode_check(self) -> int:
+        """llh_debug_fp8_encode_check: f32 values (NaNs excepted) whose fp8 code from the
+        kernels' encoder differs from the integer reference rule."""
+        n = ctypes.c_uint64(0)
+        self.check(self.lib.llh_debug_fp8_encode_check(self.handle, ctypes.byref(n)))
+        return int(n.value)
 
     def layer_cache(self, max_tokens: int, kv_heads: int, head_dim: int, fmt: int = KV_BF16) -> "LayerKvCache":
         return LayerKvCache.new_with_config(self, max_tokens, kv_heads, head_dim, fmt)

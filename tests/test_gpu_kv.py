@@ -338,6 +338,14 @@ def test_fp8_decode_table(ctx):
     assert np.array_equal(np.isnan(got), nan) and np.array_equal(got[~nan], ref[~nan])
 
 
+def test_fp8_encoder_equals_reference_rule_on_every_f32(ctx):
+    """The kernels encode fp8 with the hardware conversion (v_cvt_pk_fp8_f32 on inputs
+    clamped to +-448); on every f32 bit pattern but NaNs its code equals the integer
+    round-to-nearest-even rule (encode_e4m3_soft), which the quantise-on-write tests hold
+    to the oracle's encoder."""
+    assert ctx.fp8_encode_check() == 0
+
+
 def test_fp8_append_one_call_equals_token_by_token_calls(ctx):
     """A call of 128 tokens whose blocks' tokens are interleaved across the whole call
     (token i goes to block i % 8 at offset i // 8, so each block's tokens sit in both
