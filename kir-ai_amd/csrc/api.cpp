@@ -128,6 +128,24 @@ int stream_grid(const llh_ctx *ctx) {
   return std::min(kStreamMaxWgs, std::max(1, wgs > 0 ? wgs : kStreamWgsPerCu * ctx->cus));
 }
 
+// The head_dim-256 kernels: the persistent stream grid when the step gives every
+// wavefront at least kD256StreamMinUnitsPerWave units (block x kv head), else 0
+// (split-K).  LLH_OPT_DECODE_KERNEL forces either.
+constexpr int kD256StreamMinUnitsPerWave = 2;
+
+int plan_stream_d256(const llh_ctx *ctx, int num_seqs, int kv_heads, int est_blocks, int total_tokens_hint) {
+  const int force = ctx->opt(LLH_OPT_DECODE_KERNEL);
+  if (force == 1) return 0;
+  const int wgs = stream_grid(ctx);
+  const long long max_units = (long long)kv_heads * est_blocks * num_seqs;
+  if (max_units >= (1LL << 31)) return 0;
+  if (force == 2) return wgs;
+  const long long units = total_tokens_hint > 0
+                              ? (long long)kv_heads * ((long long)total_tokens_hint / kFastBlockTokens + num_seqs)
+                              : max_units;
+  return units >= (long long)kD256StreamMinUnitsPerWave * 4 * wgs ? wgs : 0;
+}
+
 // Returns the stream grid (workgroups) for this step, or 0 for split-K.
 int plan_stream(const llh_ctx *ctx, int format, int num_seqs, int kv_heads, int est_blocks, int total_tokens_hint) {
   const int force = ctx->opt(LLH_OPT_DECODE_KERNEL);
@@ -296,10 +314,17 @@ size_t llh_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t
   const size_t srows = (size_t)2 * 4 * kStreamMaxWgs * std::min(num_q_heads, 8);
   const size_t stream = align_up(srows * sizeof(float2)) + align_up(srows * kFastHeadDim * sizeof(float)) +
                         align_up((size_t)num_seqs * num_q_heads * 2 * sizeof(int32_t));
-  // head_dim-256 kernel: at most kD256MaxSplits partial rows per (sequence, head), 256 floats each
+  // head_dim-256 split-K kernel: at most kD256MaxSplits partial rows per (sequence, head), 256 floats each
   const size_t rows256 = (size_t)num_seqs * num_q_heads * std::min<size_t>(max_splits, kD256MaxSplits);
   const size_t d256 = align_up(rows256 * sizeof(float2)) + rows256 * kD256HeadDim * sizeof(float);
-  return std::max({align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic, stream, d256});
+  // head_dim-256 stream kernel (groups of 8 query heads): two slots per wavefront, 8 rows of 256 floats each
+  const size_t srows256 = num_q_heads >= kD256Group ? (size_t)2 * 4 * kStreamMaxWgs * kD256Group : 0;
+  const size_t stream256 = srows256 ? align_up(srows256 * sizeof(float2)) +
+                                          align_up(srows256 * kD256HeadDim * sizeof(float)) +
+                                          align_up((size_t)num_seqs * num_q_heads * 2 * sizeof(int32_t))
+                                    : 0;
+  return std::max({align_up(rows * sizeof(float2)) + rows * kFastHeadDim * sizeof(float), generic, stream, d256,
+                   stream256});
 }
 
 int llh_ctx_metrics(const llh_ctx *ctx, llh_metrics *out) {
@@ -579,7 +604,7 @@ static int check_span(llh_ctx *ctx, const llh_kv_pool *pool, int32_t max_seq_len
 // Plans one decode step: validates the call, chooses the kernel and lays out
 // its workspace (offsets from the workspace base; plan->bytes in all).
 int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
-                     const void *d_out, float score_scale, DecodePlan *plan) {
+                     const void *d_out, float score_scale, DecodePlan *plan, size_t max_bytes) {
   if (!ctx || !pool || !desc || !plan) return LLH_ERR_NULL;
   *plan = DecodePlan{};
   int st = check_desc_common(ctx, pool, desc->num_seqs, desc->num_q_heads, desc->max_blocks_per_seq, desc->window);
@@ -606,11 +631,27 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
                (group == 1 || group == 2 || group == 4 || group == 8) && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   // head_dim 256 (Qwen3.5 / 3.6 full attention: Hq16 / Hkv2): bf16 pools, G = 8
   plan->d256 = pv.format == LLH_KV_BF16 && pv.head_dim == kD256HeadDim && pv.block_tokens == kFastBlockTokens &&
-               rows_aligned && group == 8 && !ctx->opt(LLH_OPT_FORCE_GENERIC);
+               rows_aligned && group == kD256Group && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   if (plan->d256) {
     plan->fast = true;
     SplitPlan sp = plan_splits(ctx, desc->num_seqs, pv.kv_heads, desc->max_seq_len, desc->window,
                                desc->total_tokens_hint, pv.format);
+    // persistent stream: partials (max, sum) and outputs of two slots per wavefront, segment descriptors
+    const int wgs = plan_stream_d256(ctx, desc->num_seqs, pv.kv_heads, sp.est_blocks, desc->total_tokens_hint);
+    if (wgs > 0) {
+      const size_t rows = (size_t)2 * 4 * wgs * kD256Group;
+      const size_t o_off = align_up(rows * sizeof(float2));
+      const size_t desc_off = align_up(o_off + rows * kD256HeadDim * sizeof(float));
+      const size_t bytes = align_up(desc_off + (size_t)desc->num_seqs * pv.kv_heads * 2 * sizeof(int32_t));
+      if (bytes <= max_bytes) {
+        plan->stream_wgs = wgs;
+        plan->ml_off = 0;
+        plan->o_off = o_off;
+        plan->desc_off = desc_off;
+        plan->bytes = bytes;
+        return LLH_OK;
+      }
+    }
     if (ctx->opt(LLH_OPT_DECODE_SPLIT_BLOCKS) <= 0) {
       // Long splits: each wavefront keeps one block in flight, so a workgroup's
       // start (q, first loads) and its merge are paid once per split.  The longest

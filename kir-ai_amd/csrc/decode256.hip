@@ -8,10 +8,16 @@
 // native_attention.rs:731-771; window rule qwen/ops/cache.rs:116-121), times
 // sigmoid(gate) when the call carries a gate (native_attention.rs:765-781).
 //
-// Split-K: one workgroup per (split, kv head, sequence); a split is
-// `split_blocks` consecutive blocks and its four wavefronts take them
-// round-robin.  A single-split sequence writes its output directly, otherwise
-// decode_merge_d256_kernel merges the splits' (max, sum, output) partials.
+// Two launch shapes over the same per-block math:
+// * split-K: one workgroup per (split, kv head, sequence); a split is
+//   `split_blocks` consecutive blocks and its four wavefronts take them
+//   round-robin.  A single-split sequence writes its output directly, otherwise
+//   decode_merge_d256_kernel merges the splits' (max, sum, output) partials.
+// * persistent stream (paged_decode_d256_stream_kernel): the step's units
+//   (sequence, kv head, block) cut into equal consecutive ranges, one per
+//   wavefront of a grid that fills every SIMD (stream_partition.h), as the
+//   head_dim-128 stream kernel does; decode_stream_merge_d256_kernel merges the
+//   segments cut between wavefronts.
 //
 // Lane roles per block (64 lanes, row g = lane / 16, c = lane % 16):
 //   K: lane loads token 4g + i (i = 0..3) at dims 8c..8c+7 and 128+8c..+7
@@ -30,6 +36,7 @@
 // Running max / sum live in the 8 lanes that score a head; outputs in
 // registers (8 heads x 4 dims per lane).  HBM-bound; no MFMA.
 #include "device_common.h"
+#include "stream_partition.h"
 #include "wave_ops.h"
 
 namespace llh {
@@ -38,7 +45,7 @@ namespace {
 
 constexpr int D2 = kD256HeadDim;
 constexpr int BT = kFastBlockTokens;
-constexpr int G2 = 8;
+constexpr int G2 = kD256Group;
 constexpr int kBlockBytes2 = BT * D2 * 2;  // one (block, kv head) of K (and of V), bf16
 constexpr int kMerge256MaxSplits = 64;
 
@@ -210,6 +217,29 @@ __device__ __forceinline__ void block_accumulate(const Vregs &vr, uint32_t w, co
   }
 }
 
+// Query slot s of this lane: head s ^ fold(c), dims 8c..8c+7 and 128+8c..+7 of
+// the kv head whose first query row is qrow0.
+__device__ __forceinline__ void load_q256(const DecodeArgs &a, size_t qrow0, int lane, uint32_t (&qw)[G2][8]) {
+  const int c = lane & 15;
+#pragma unroll
+  for (int s = 0; s < G2; s++) {
+    const uint16_t *qr = a.q + (qrow0 + (size_t)(s ^ fold(c))) * D2 + 8 * c;
+    const uint4 x = *reinterpret_cast<const uint4 *>(qr);
+    const uint4 y = *reinterpret_cast<const uint4 *>(qr + 128);
+    qw[s][0] = x.x, qw[s][1] = x.y, qw[s][2] = x.z, qw[s][3] = x.w;
+    qw[s][4] = y.x, qw[s][5] = y.y, qw[s][6] = y.z, qw[s][7] = y.w;
+  }
+}
+
+__device__ __forceinline__ void reset256(State256 &st) {
+  st.m = -INFINITY;
+  st.l = 0.0f;
+#pragma unroll
+  for (int h = 0; h < G2; h++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) st.o[h][j] = 0.0f;
+}
+
 __device__ __forceinline__ void seq_range256(const DecodeArgs &a, int b, int &len, int &lo, int &first_blk,
                                              int &n_blk, int &n_splits) {
   len = a.seq_lens[b];
@@ -253,27 +283,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
     return stable[(blk_begin + wave + 4 * k) % a.max_blocks];
   };
 
-  // query slot s of this lane: head s ^ fold(c), dims 8c..8c+7 and 128+8c..+7
   uint32_t qw[G2][8];
-  {
-    const int c = lane & 15;
-#pragma unroll
-    for (int s = 0; s < G2; s++) {
-      const uint16_t *qr = a.q + (qrow0 + (size_t)(s ^ fold(c))) * D2 + 8 * c;
-      const uint4 x = *reinterpret_cast<const uint4 *>(qr);
-      const uint4 y = *reinterpret_cast<const uint4 *>(qr + 128);
-      qw[s][0] = x.x, qw[s][1] = x.y, qw[s][2] = x.z, qw[s][3] = x.w;
-      qw[s][4] = y.x, qw[s][5] = y.y, qw[s][6] = y.z, qw[s][7] = y.w;
-    }
-  }
-
+  load_q256(a, qrow0, lane, qw);
   State256 st;
-  st.m = -INFINITY;
-  st.l = 0.0f;
-#pragma unroll
-  for (int h = 0; h < G2; h++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) st.o[h][j] = 0.0f;
+  reset256(st);
 
   if (nbw > 0) {
     // K of the next block loads behind this block's p . v, V of the next block
@@ -397,9 +410,224 @@ __global__ __launch_bounds__(D2) void decode_merge_d256_kernel(const DecodeArgs 
   return merge256<64>(a, row0, last, d, orow);
 }
 
+// ---------------------------------------------------------------------------
+// Persistent stream form.  Wavefront w of the grid takes units [r0, r0 + n) of
+// the step (stream_partition.h) and walks them with the split-K kernel's
+// register pipeline (one block's registers, the next block's K loading behind
+// this block's p . v and its V behind the next q . k).  A segment (sequence, kv
+// head) that ends inside the range is flushed by this wavefront alone (no LDS,
+// no barrier): its bf16 output when the segment also began inside the range,
+// else a (max, sum, output) partial in slot 2w (the wavefront's first segment)
+// or 2w + 1 (its last), and the wavefront that holds the segment's first unit
+// records (first slot, pieces) in seg_desc for decode_stream_merge_d256_kernel.
+// ---------------------------------------------------------------------------
+
+// Ends a segment: head h's (max, sum) from the lanes that score it (their
+// 8-lane sum for the sum), the outputs as every lane holds them (dims 64j + lane).
+__device__ __forceinline__ void flush256(const DecodeArgs &a, State256 &st, int b, int kvh, bool complete, int slot,
+                                         int lane) {
+  float l = st.l + dpp<0xB1>(st.l);
+  l += xor16_other(l, lane);
+  l += xor32_other(l, lane);
+  const size_t qrow0 = (size_t)b * a.q_heads + (size_t)kvh * G2;
+#pragma unroll
+  for (int h = 0; h < G2; h++) {
+    const int src = 2 * pair_of_head(h);
+    const float mh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(st.m), src));
+    const float lh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), src));
+    if (complete) {
+      const float inv = 1.0f / lh;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const size_t o = (qrow0 + h) * D2 + 64 * j + lane;
+        a.out[o] = f32_to_bf16_rne(gated(st.o[h][j] * inv, a.gate, o));
+      }
+    } else {
+      const size_t row = (size_t)slot * G2 + h;
+#pragma unroll
+      for (int j = 0; j < 4; j++) a.ws_o[row * D2 + 64 * j + lane] = st.o[h][j];
+      if (lane == 0) a.ws_ml[row] = make_float2(mh, lh);
+    }
+  }
+  reset256(st);
+}
+
+__global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
+  const int w = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int W = gridDim.x * 4;
+  const int Hkv = a.pool.kv_heads;
+  const int B = a.num_seqs;
+  const int len0 = lane < B ? a.seq_lens[lane] : 0;  // sequences 0..63, one per lane
+  int bad_flags;
+  const StreamRange sr = stream_range(a, W, w, lane, len0, &bad_flags);
+  if (bad_flags) {
+    if (w == 0 && lane == 0) atomicOr(a.err, bad_flags);
+    return;
+  }
+  // empty sequences: zero output (weighted sum of nothing), nothing to merge
+  for (int b = w; b < B; b += W) {
+    if (attended_blocks(a, b < 64 ? __builtin_amdgcn_readlane(len0, b) : a.seq_lens[b]) == 0) {
+      for (int idx = lane; idx < a.q_heads * D2; idx += 64) a.out[(size_t)b * a.q_heads * D2 + idx] = 0;
+      for (int idx = lane; idx < 2 * Hkv; idx += 64) a.seg_desc[(size_t)b * Hkv * 2 + idx] = 0;
+    }
+  }
+  const int n = __builtin_amdgcn_readfirstlane(sr.n);
+  if (n == 0) return;
+  const int U = __builtin_amdgcn_readfirstlane(sr.U);
+  const int Wu = __builtin_amdgcn_readfirstlane(sr.Wu);
+  const stream_const_i32 *stable = (const stream_const_i32 *)a.tables;
+  // cursors: the next block-table entry to fetch (one unit ahead of the loads),
+  // the next unit to load, the unit being computed
+  UnitCursor C = cursor_at(a, len0, sr);
+  UnitCursor L = C, E = C;
+  auto next_entry = [&]() __attribute__((always_inline)) -> int {
+    const int e = stable[(size_t)E.b * a.max_blocks + E.tab];
+    cursor_advance(a, len0, E);
+    return e;
+  };
+  uint32_t qw[G2][8];
+  load_q256(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G2, lane, qw);
+  int e = next_entry();
+  bool valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
+  Kregs kr;
+  Vregs vr;
+  load_k(a, valid ? e : 0, L.kvh, lane, kr);
+  __builtin_amdgcn_sched_barrier(0);  // K before V, as in the loop
+  load_v(a, valid ? e : 0, L.kvh, lane, vr);
+  cursor_advance(a, len0, L);
+  int e_next = n > 1 ? next_entry() : -1;
+
+  State256 st;
+  reset256(st);
+  bool seg_from_start = C.j == 0;
+  bool first_seg = true;
+  auto end_segment = [&](bool complete) __attribute__((always_inline)) {
+    const int slot = w * 2 + (first_seg ? 0 : 1);
+    flush256(a, st, C.b, C.kvh, complete, slot, lane);
+    if (lane == 0 && (complete || seg_from_start)) {
+      // this wavefront holds the segment's first unit: record how to merge it
+      int2 d = make_int2(0, 0);
+      if (!complete) d = make_int2(slot, wave_of_unit(C.base + (C.kvh + 1) * C.nb - 1, U, Wu) - w + 1);
+      reinterpret_cast<int2 *>(a.seg_desc)[(size_t)C.b * Hkv + C.kvh] = d;
+    }
+    first_seg = false;
+  };
+
+  // Units 0 .. n-2 issue the next unit's loads; the last is peeled off (loads
+  // under a condition would make the compiler wait for every load in flight).
+  // A segment's last unit loads the next segment's q (its registers are free
+  // after the scores) before the next unit's V, so the next scores wait for K
+  // and q only; an entry outside the pool is masked and flagged after the loop.
+  bool bad = false;
+  for (int k = 0; k + 1 < n; k++) {
+    bad |= !valid;
+    uint32_t vm[8];
+    const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
+    valid = e_next >= 0 && (int64_t)e_next < a.pool.n_blocks;
+    const int phys = valid ? e_next : 0;
+    load_k(a, phys, L.kvh, lane, kr);
+    const bool seg_end = C.j == C.nb - 1;  // then unit L starts the next segment
+    if (seg_end) load_q256(a, (size_t)L.b * a.q_heads + (size_t)L.kvh * G2, lane, qw);
+    // nothing of p . v (which waits for V) moves above the K loads
+    __builtin_amdgcn_sched_barrier(0);
+    block_accumulate(vr, wp, vm, st);
+    if (seg_end) {
+      end_segment(seg_from_start);
+      seg_from_start = true;
+    }
+    load_v(a, phys, L.kvh, lane, vr);
+    cursor_advance(a, len0, L);
+    e_next = k + 2 < n ? next_entry() : -1;
+    cursor_advance(a, len0, C);
+  }
+  bad |= !valid;
+  {
+    uint32_t vm[8];
+    const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
+    block_accumulate(vr, wp, vm, st);
+  }
+  // the range ends with the segment (complete if it also began here) or inside it
+  end_segment(C.j == C.nb - 1 && seg_from_start);
+  if (bad && lane == 0) atomicOr(a.err, kErrBadBlock);
+}
+
+// One round of the stream merge over pieces i0 .. i0+cnt-1 (1 <= cnt <= N) of a
+// cut segment, one dim per thread: every partial of the round is loaded before
+// any is used (pieces past the last re-read it and get weight 0), lane j of each
+// wavefront loads piece j's (max, sum), and the weights reach all lanes by
+// readlane -- two dependent memory round trips (descriptor, then partials).
+template <int N>
+__device__ __forceinline__ void stream_merge256_round(const DecodeArgs &a, int first_slot, int wf, int gi, int i0,
+                                                      int cnt, int d, float &mm, float &ll, float &oo) {
+  static_assert(N == 16 || N == 32, "one or two DPP rows of pieces");
+  const int lane = d & 63;
+  // piece k of the segment: the first wavefront's slot, then the later wavefronts' first-segment slots
+  auto row_of = [&](int k) { return (size_t)(k == 0 ? first_slot : (wf + k) * 2) * G2 + gi; };
+  const float2 ml = a.ws_ml[row_of(i0 + min(lane, cnt - 1))];
+  float ov[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) ov[i] = a.ws_o[row_of(i0 + min(i, cnt - 1)) * D2 + d];
+  __builtin_amdgcn_sched_barrier(0);
+  const float m = lane < cnt ? ml.x : -INFINITY;
+  float nm = m;
+  nm = fmaxf(nm, dpp<0xB1>(nm));   // quad_perm [1,0,3,2]
+  nm = fmaxf(nm, dpp<0x4E>(nm));   // quad_perm [2,3,0,1]
+  nm = fmaxf(nm, dpp<0x141>(nm));  // row_half_mirror
+  nm = fmaxf(nm, dpp<0x140>(nm));  // row_mirror
+  if constexpr (N == 32) nm = fmaxf(nm, xor16_other(nm, lane));
+  nm = fmaxf(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nm))), mm);
+  const float mref = (nm == -INFINITY) ? 0.0f : nm;
+  const float f = fast_exp2(m - mref);  // 0 on lanes past the last piece
+  float ls = row_sum16(ml.y * f);
+  if constexpr (N == 32) ls += xor16_other(ls, lane);
+  const float f0 = fast_exp2(mm - mref);
+  ll = ll * f0 + __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ls)));
+  oo *= f0;
+#pragma unroll
+  for (int i = 0; i < N; i++) oo += ov[i] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), i));
+  mm = nm;
+}
+
+// Merges the stream kernel's cut segments: one workgroup of 256 threads (one per
+// dim) per (query head, sequence); up to 16 pieces in one round, more in rounds
+// of 32.
+__global__ __launch_bounds__(D2) void decode_stream_merge_d256_kernel(const DecodeArgs a) {
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int d = threadIdx.x;
+  const int kvh = h / G2;
+  const int gi = h - kvh * G2;
+  const int2 sd = reinterpret_cast<const int2 *>(a.seg_desc)[(size_t)b * a.pool.kv_heads + kvh];
+  const int W = a.stream_wgs * 4;
+  const int wf = sd.x >> 1;
+  // written by the stream kernel; a call it aborted (error flags) may leave any
+  // values, so only descriptors naming slots of this grid are followed
+  if (sd.y < 2 || sd.x < 0 || sd.x >= 2 * W || wf + sd.y > W) return;
+  float mm = -INFINITY, ll = 0.0f, oo = 0.0f;
+  if (sd.y <= 16) {
+    stream_merge256_round<16>(a, sd.x, wf, gi, 0, sd.y, d, mm, ll, oo);
+  } else {
+#pragma unroll 1
+    for (int i0 = 0; i0 < sd.y; i0 += 32) stream_merge256_round<32>(a, sd.x, wf, gi, i0, min(32, sd.y - i0), d, mm, ll, oo);
+  }
+  const size_t o = ((size_t)b * a.q_heads + h) * D2 + d;
+  a.out[o] = f32_to_bf16_rne(gated(oo / ll, a.gate, o));
+}
+
 }  // namespace
 
 hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
+  if (a.stream_wgs > 0) {
+    if (hook) hook(hu, 0, s);
+    hipLaunchKernelGGL(paged_decode_d256_stream_kernel, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (hook) hook(hu, 1, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(decode_stream_merge_d256_kernel, dim3(a.q_heads, a.num_seqs), dim3(D2), 0, s, a);
+    return hipGetLastError();
+  }
   if (a.max_splits > kMerge256MaxSplits) return hipErrorInvalidValue;
   const int max_blk = (max_seq_len + BT - 1) / BT + 1;
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);

@@ -202,7 +202,7 @@ namespace llh {
 struct DecodePlan {
   bool empty = false;  // nothing to launch (no sequences)
   bool fast = false;   // tuned kernels (else the reference-order kernel)
-  bool d256 = false;   // tuned: the head_dim-256 (G = 8, bf16) split-K kernel
+  bool d256 = false;   // tuned: the head_dim-256 (G = 8, bf16) kernels (split-K, or stream when stream_wgs > 0)
   int group = 0;
   int split_blocks = 0, max_splits = 0, stream_wgs = 0;
   size_t ml_off = 0, o_off = 0, desc_off = 0;  // tuned: partial (max, sum), partial outputs, segment descriptors
@@ -210,8 +210,10 @@ struct DecodePlan {
   size_t scores_off = 0;  // reference order: score rows
   size_t bytes = 0;
 };
+// max_bytes: the most workspace the caller can give; a layout choice that would
+// need more falls back to one that fits (llh_paged_decode_noalloc's scratch)
 int plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_desc *desc, const void *d_q,
-                const void *d_out, float score_scale, DecodePlan *plan);
+                const void *d_out, float score_scale, DecodePlan *plan, size_t max_bytes = SIZE_MAX);
 // err: the device error word the kernels raise flags in; timed = false leaves out
 // the kernel-timing events (no event is created or recorded); k_new / v_new
 // (tuned kernels): fused append of each sequence's new token

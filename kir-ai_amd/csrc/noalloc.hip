@@ -55,7 +55,7 @@ extern "C" int llh_paged_decode_noalloc(llh_ctx *ctx, const llh_kv_pool *pool, c
   if (!ctx || !pool || !desc) return LLH_ERR_NULL;
   if (!d_out && desc->num_seqs > 0) return ctx->fail(LLH_ERR_NULL, "null device pointer in decode call");
   llh::DecodePlan plan;
-  int st = llh::plan_decode(ctx, pool, desc, d_q, d_out, score_scale, &plan);
+  int st = llh::plan_decode(ctx, pool, desc, d_q, d_out, score_scale, &plan, kScratchBytes);
   if (st != LLH_OK || plan.empty) return st;
   if (plan.bytes > kScratchBytes)
     return ctx->fail(LLH_ERR_CAPACITY, "decode step needs " + std::to_string(plan.bytes) +

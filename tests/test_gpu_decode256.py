@@ -1,10 +1,12 @@
-"""The head_dim-256 decode kernel (decode256.hip): Qwen3.5 / 3.6 full-attention layers,
+"""The head_dim-256 decode kernels (decode256.hip): Qwen3.5 / 3.6 full-attention layers,
 16 query heads over 2 kv heads, head_dim 256 (fixtures/qwen36/config.json), bf16 blocks
-of 16 tokens.  Checked against the oracle (the per-head loop of crates/llm-backend/
-src/core/native_attention.rs:731-771, head_dim taken from the call) at the parity bar,
-its attended set bit-exactly with the position-coded probe (tests/attended_set.py), the
-output gate (native_attention.rs:765-781), split counts from 1 to the merge's 64, and
-the entry points that share the plan (noalloc, decode+append)."""
+of 16 tokens.  Both launch shapes (split-K and the persistent stream kernel, forced in
+turn) are checked against the oracle (the per-head loop of crates/llm-backend/src/core/
+native_attention.rs:731-771, head_dim taken from the call) at the parity bar, their
+attended set bit-exactly with the position-coded probe (tests/attended_set.py), the
+output gate (native_attention.rs:765-781), split counts from 1 to the merge's 64, stream
+segments cut into 1 to hundreds of pieces, and the entry points that share the plan
+(noalloc, decode+append)."""
 import math
 
 import numpy as np
@@ -24,6 +26,14 @@ BT = 16
 HQ, HKV = 16, 2
 
 
+@pytest.fixture(params=["split", "stream"])
+def d256_kernel(request, opts):
+    """Both head_dim-256 kernels (LLH_OPT_DECODE_KERNEL forces the one the planner
+    otherwise picks by the step's size)."""
+    opts(llm_hip.OPT_DECODE_KERNEL, request.param)
+    return request.param
+
+
 def run(ctx, pool, batch, q, window, scale, Hq=HQ, gate=None, fn="decode", kv_new=None, expect_d256=True):
     import torch
 
@@ -32,6 +42,7 @@ def run(ctx, pool, batch, q, window, scale, Hq=HQ, gate=None, fn="decode", kv_ne
     desc = ctx.decode_desc(to_dev(batch.seq_lens), to_dev(batch.tables), Hq, int(batch.seq_lens.max()), window,
                            gate=to_dev(gate) if gate is not None else None)
     before = ctx.metrics()["d256_decode_calls"]
+    streamed0 = ctx.metrics()["stream_decode_calls"]
     if fn == "decode":
         ctx.paged_decode(pool, desc, to_dev(q), out, scale)
     elif fn == "noalloc":
@@ -41,6 +52,12 @@ def run(ctx, pool, batch, q, window, scale, Hq=HQ, gate=None, fn="decode", kv_ne
     torch.cuda.synchronize()
     assert ctx.device_errors() == 0, ctx.last_error()
     assert ctx.metrics()["d256_decode_calls"] == before + (1 if expect_d256 else 0)
+    forced = ctx.get_option(llm_hip.OPT_DECODE_KERNEL)
+    streamed = ctx.metrics()["stream_decode_calls"] - streamed0
+    if expect_d256 and fn != "noalloc" and forced == llm_hip.DECODE_KERNELS["stream"]:
+        assert streamed == 1, "the stream kernel did not run"
+    if forced == llm_hip.DECODE_KERNELS["split"]:
+        assert streamed == 0, "the stream kernel ran under the split-K option"
     return from_dev_bf16(out)
 
 
@@ -50,7 +67,7 @@ def case(ctx, lens, seed, free=0.10, Hq=HQ):
     return batch, pool, q
 
 
-def test_decode256_qwen36_step(ctx):
+def test_decode256_qwen36_step(ctx, d256_kernel):
     """The Qwen3.6-shaped step: 32 sequences, lengths in [256, 4096], edges included."""
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     lens[:6] = [1, 16, 17, 32, 33, 4096]
@@ -62,7 +79,7 @@ def test_decode256_qwen36_step(ctx):
 
 
 @pytest.mark.parametrize("window", [1, 17, 100, 4096])
-def test_decode256_windows(ctx, window):
+def test_decode256_windows(ctx, d256_kernel, window):
     lens = np.array([1, 15, 16, 17, 100, 101, 700, 4100, 5000], np.int32)
     batch, pool, q = case(ctx, lens, 102 + window)
     out = run(ctx, pool, batch, q, window, 0.0625)
@@ -74,6 +91,7 @@ def test_decode256_windows(ctx, window):
 def test_decode256_split_counts(ctx, opts, split_blocks):
     """One split (split_blocks 256 over 4096 tokens) up to 64 (4 blocks a split), and the
     planner's growth of the split past 64 partials for a 20000-token context."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
     opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, split_blocks)
     lens = np.array([4096, 20000, 1, 333], np.int32)
     batch, pool, q = case(ctx, lens, 103)
@@ -82,7 +100,21 @@ def test_decode256_split_counts(ctx, opts, split_blocks):
                   what=f"split_blocks {split_blocks}")
 
 
-def test_decode256_is_deterministic(ctx):
+@pytest.mark.parametrize("wgs", [1, 7, 64, 512])
+def test_decode256_stream_pieces(ctx, opts, wgs):
+    """The stream kernel over grids of 4 to 2048 wavefronts: segments whole inside one
+    wavefront, and segments cut into up to 16, up to 32 and hundreds of pieces (the
+    merge's one-round and 32-piece-round paths), ragged and empty sequences included."""
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
+    opts(llm_hip.OPT_DECODE_STREAM_WGS, wgs)
+    lens = np.array([20000, 1, 0, 333, 4096, 17, 2500], np.int32)
+    batch, pool, q = case(ctx, lens, 116 + wgs)
+    out = run(ctx, pool, batch, q, 0, 0.0625)
+    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"stream over {wgs} workgroups")
+
+
+def test_decode256_is_deterministic(ctx, d256_kernel):
     lens = workloads.uniform_lengths(8, 256, 4096, 104)
     batch, pool, q = case(ctx, lens, 104)
     a = run(ctx, pool, batch, q, 0, 0.0625)
@@ -90,7 +122,7 @@ def test_decode256_is_deterministic(ctx):
     assert np.array_equal(a, b)
 
 
-def test_decode256_empty_sequence_is_zero(ctx):
+def test_decode256_empty_sequence_is_zero(ctx, d256_kernel):
     lens = np.array([0, 20, 0, 300], np.int32)
     batch, pool, q = case(ctx, lens, 105)
     out = run(ctx, pool, batch, q, 0, 0.0625).reshape(4, -1)
@@ -99,7 +131,7 @@ def test_decode256_empty_sequence_is_zero(ctx):
                   what="empty rows")
 
 
-def test_decode256_bad_block_is_masked_and_flagged(ctx):
+def test_decode256_bad_block_is_masked_and_flagged(ctx, d256_kernel):
     import torch
 
     lens = np.array([100, 300], np.int32)
@@ -121,7 +153,7 @@ def gate_rows(seed, n):
 
 
 @pytest.mark.parametrize("window", [0, 333])
-def test_decode256_gate(ctx, window):
+def test_decode256_gate(ctx, d256_kernel, window):
     """The Qwen3.6 attention output gate: out * sigmoid(gate), applied before the bf16 rounding."""
     lens = workloads.uniform_lengths(16, 1, 3000, 107)
     batch, pool, q = case(ctx, lens, 107)
@@ -132,15 +164,22 @@ def test_decode256_gate(ctx, window):
     assert_parity(out, ref, what=f"gated W={window}")
 
 
-def test_decode256_noalloc_matches_decode(ctx):
-    lens = workloads.uniform_lengths(16, 256, 4096, 109)  # partials within the static scratch
+def test_decode256_noalloc_matches_decode(ctx, opts):
+    """llh_paged_decode_noalloc runs split-K at head_dim 256 whatever the option asks: the
+    stream kernel's partials (two slots per wavefront) exceed the static scratch.  Its
+    output equals the split-K call's bit for bit and the stream call's within the bar."""
+    lens = workloads.uniform_lengths(16, 256, 4096, 109)  # split-K partials within the static scratch
     batch, pool, q = case(ctx, lens, 109)
+    opts(llm_hip.OPT_DECODE_KERNEL, "split")
     a = run(ctx, pool, batch, q, 0, 0.0625)
+    opts(llm_hip.OPT_DECODE_KERNEL, "stream")
     b = run(ctx, pool, batch, q, 0, 0.0625, fn="noalloc")
     assert np.array_equal(a, b)
+    c = run(ctx, pool, batch, q, 0, 0.0625)
+    assert_parity(c, oracle.bf16_to_f32(a), what="stream vs split-K")
 
 
-def test_decode256_append_then_attend(ctx):
+def test_decode256_append_then_attend(ctx, d256_kernel):
     """llh_paged_decode_append at head_dim 256: the append kernel, then this kernel; the
     pool holds the new rows and the output matches the oracle on that pool."""
     lens = np.array([1, 17, 256, 999, 4096], np.int32)
@@ -172,7 +211,7 @@ def coded_case(ctx, lens, seed, code_base):
 
 @pytest.mark.parametrize("code_base", [0, 2])
 @pytest.mark.parametrize("window", [0, 1, 17, 100, 4096])
-def test_decode256_attended_set(ctx, code_base, window):
+def test_decode256_attended_set(ctx, d256_kernel, code_base, window):
     """q = 0: every attended token weighs exactly 1 and the output counts the position codes
     of the attended set, compared exactly with the reference's set."""
     lens = workloads.uniform_lengths(32, 256, 4096, 113)
