@@ -429,14 +429,24 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         k = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
         v = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.write_blocks(pool, ids, k, v, stream=s), steps, warmup)
+        host_us = HOST["us"]
+        # the same write replayed from a HIP graph (the GPU's own time per call, which a
+        # slow host's issue time can hide); writing the same rows again leaves the pool as it was
+        before = pool.raw()
+        gms = time_graph([lambda s: ctx.write_blocks(pool, ids, k, v, stream=s)], steps)
+        if any(not np.array_equal(a, b) for a, b in zip(before.values(), pool.raw().values())):
+            raise RuntimeError("block write: graph replay changed the pool")
         esz = 2 if fmt in (llm_hip.KV_BF16, llm_hip.KV_F16) else 1
         T = nblk * BT
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: nblk * H * 4 * 2}.get(fmt, 0)
         nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + scales
         out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
-                    "us_per_step": round(ms * 1e3, 2), "host_us_per_call": HOST["us"], "bytes_per_step": nbytes,
+                    "us_per_step": round(ms * 1e3, 2), "host_us_per_call": host_us, "bytes_per_step": nbytes,
                     "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": "write_blocks_d128_kernel"})
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "graph_us_per_step": round(gms * 1e3, 2),
+                    "graph_hbm_frac": round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "kernel": "write_blocks_d128_kernel"})
         del pool
     for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv),
                           (llm_hip.KV_FP8_E4M3, "fp8", B, Hkv), (llm_hip.KV_F16, "fp16", B, Hkv)):
@@ -712,7 +722,8 @@ def summarize(root: str) -> int:
         "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
         "c2f16": {"paged_decode_stream_kernel": ("B", decode_bytes(c2lens, 16, 8, 4))},
         "c3f16": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
-        "q36": {"paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
+        "q36": {"paged_decode_d256_stream_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256)),
+                "paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
         "q36prefill": {"paged_prefill_d256_kernel": ("F", prefill_flops(8, 1536, 512, 16, 0, 256))},
         "c3": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
         "c3int8": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},

@@ -130,13 +130,18 @@ int stream_grid(const llh_ctx *ctx) {
 
 // The head_dim-256 kernels: the persistent stream grid when the step gives every
 // wavefront at least kD256StreamMinUnitsPerWave units (block x kv head), else 0
-// (split-K).  LLH_OPT_DECODE_KERNEL forces either.
+// (split-K).  One workgroup per compute unit, measured on MI355X for the Qwen3.6
+// step (32 x U[256, 4096], Hq16 / Hkv2): 256 workgroups 32.8 us, 192 33.8, 320
+// (some CUs running two) 42.3, 512 37.4, split-K 38.3.  Fewer, longer ranges
+// leave fewer partials (8 KiB per wavefront) for the merge.
+// LLH_OPT_DECODE_KERNEL forces either, LLH_OPT_DECODE_STREAM_WGS sets the grid.
 constexpr int kD256StreamMinUnitsPerWave = 2;
 
 int plan_stream_d256(const llh_ctx *ctx, int num_seqs, int kv_heads, int est_blocks, int total_tokens_hint) {
   const int force = ctx->opt(LLH_OPT_DECODE_KERNEL);
   if (force == 1) return 0;
-  const int wgs = stream_grid(ctx);
+  const int opt_wgs = ctx->opt(LLH_OPT_DECODE_STREAM_WGS);
+  const int wgs = std::min(kStreamMaxWgs, std::max(1, opt_wgs > 0 ? opt_wgs : ctx->cus));
   const long long max_units = (long long)kv_heads * est_blocks * num_seqs;
   if (max_units >= (1LL << 31)) return 0;
   if (force == 2) return wgs;
