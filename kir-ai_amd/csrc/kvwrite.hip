@@ -184,12 +184,21 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     const float sc = (float)s16;
     uint32_t q[2] = {0u, 0u};
     if (sc > 0.0f && sc < INFINITY) {  // (per token row) the shared-divisor quotient (div_shared)
+      // Rust's round (half away from zero) as trunc(y + copysign(0.5, y)): not that rule
+      // for every float, but for every quotient this kernel forms (tests/quotient_check.c);
+      // the integer c + 1.5 * 2^23 holds c's two's-complement byte in its low mantissa byte
       const float rr = __fdiv_rn(1.0f, sc);
+      uint32_t cb[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float c = fminf(fmaxf(roundf(div_shared(x[j], sc, rr)), -127.0f), 127.0f);
-        q[j >> 2] |= (uint32_t)(uint8_t)(int8_t)c << (8 * (j & 3));
+        const float y = div_shared(x[j], sc, rr);
+        const float c = __builtin_amdgcn_fmed3f(__builtin_truncf(y + __builtin_copysignf(0.5f, y)), -127.0f, 127.0f);
+        cb[j] = __float_as_uint(c + 12582912.0f);
       }
+#pragma unroll
+      for (int k = 0; k < 2; k++)
+        q[k] = __builtin_amdgcn_perm(cb[4 * k + 1], cb[4 * k], 0x0c0c0400u) |
+               __builtin_amdgcn_perm(cb[4 * k + 3], cb[4 * k + 2], 0x04000c0cu);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; j++) q[j >> 2] |= (uint32_t)(uint8_t)quant_int8(x[j], sc) << (8 * (j & 3));

@@ -7,6 +7,7 @@
  * and, per element (Markstein's method),
  *     q = RN(x r),  e = fma(-q, s, x) (exact),  x / s ~ copysign(fma(e, r, q), x)
  * (the sign restores -0 for x = -0 and for negative x whose quotient underflows).
+ * int8 codes round that quotient as trunc(q + copysign(0.5, q)).
  * The codes must equal those of the correctly rounded x / s.  This program takes every
  * absmax m the kernel can see (every positive finite bf16 value), derives s as the
  * kernel does, and compares the codes of every finite bf16 x with |x| <= m, under IEEE
@@ -38,6 +39,13 @@ static uint32_t bits(float f) {
 static int code_int8(float q) {
   float c = roundf(q);
   return (int)fminf(fmaxf(c, -127.0f), 127.0f);
+}
+
+/* the kernel's int8 code of its quotient: trunc(q + copysign(0.5, q)), clamped.  Not
+ * round-half-away for every float (q = 0.5 - 2^-25 sums to 1), so it is checked here
+ * against code_int8 of the exact quotient like the quotient itself */
+static int code_int8_kernel(float q) {
+  return (int)fminf(fmaxf(truncf(q + copysignf(0.5f, q)), -127.0f), 127.0f);
 }
 
 /* OCP e4m3fn code of a quotient, round to nearest even, saturating at +-448 (the
@@ -79,7 +87,7 @@ static long check_absmax(uint32_t mb, float s, int fp8, int *ref) {
       const float q = x * r;
       const float e = fmaf(-q, s, x);
       const float m = copysignf(fmaf(e, r, q), x);  /* s > 0: the quotient has x's sign, zeros too */
-      const int c = fp8 ? code_e4m3(m) : code_int8(m);
+      const int c = fp8 ? code_e4m3(m) : code_int8_kernel(m);
       bad += c != ref[2 * b + sg];
     }
   }
