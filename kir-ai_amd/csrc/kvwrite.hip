@@ -106,7 +106,10 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     return;
   }
   // quantised blocks: a NaN or an infinity in the block's rows is NonFiniteValue
-  // in the reference (format.rs:713-716): flagged, and the block is left as it was
+  // in the reference (format.rs:713-716): flagged, and the block is left as it was.
+  // Each wave posts its verdict in LDS; the workgroup reads the four after a barrier
+  // the kernel has anyway (fp8: the absmax reduction; int8: the V transpose), before
+  // any global store.
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -115,12 +118,18 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     for (int k = 0; k < 2; k++)
       bad = bad || (u[k] & 0x7f80u) == 0x7f80u || (u[k] & 0x7f800000u) == 0x7f800000u;
   }
-  if (__syncthreads_or(bad)) {
-    if (tid == 0) atomicOr(a.err, kErrNonFinite);
-    return;
+  __shared__ __align__(16) uint32_t wave_bad[4];
+  {
+    const uint32_t wb = __any(bad) ? 1u : 0u;
+    if ((tid & 63) == 0) wave_bad[tid >> 6] = wb;
   }
+  const auto block_bad = [&]() {
+    const uint4 f = *reinterpret_cast<const uint4 *>(wave_bad);
+    return (f.x | f.y | f.z | f.w) != 0u;
+  };
   __shared__ uint8_t lq[BT][Dh + 16];
   uint32_t codes[2][2];
+  uint16_t s16b[2] = {0u, 0u};  // int8: the token's fp16 K and V scales
   if (a.pool.format == kFp8) {
     // one f32 scale per (block, head) and tensor: absmax over the block / 448,
     // codes as the generic kernel computes them (RNE e4m3 of x / scale)
@@ -141,6 +150,10 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
       if ((tid & 63) == 0) red[tensor][tid >> 6] = mx[tensor];
     }
     __syncthreads();
+    if (block_bad()) {
+      if (tid == 0) atomicOr(a.err, kErrNonFinite);
+      return;
+    }
 #pragma unroll
     for (int tensor = 0; tensor < 2; tensor++) {
       const float m = fmaxf(fmaxf(red[tensor][0], red[tensor][1]), fmaxf(red[tensor][2], red[tensor][3]));
@@ -205,16 +218,20 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
     }
     codes[tensor][0] = q[0];
     codes[tensor][1] = q[1];
-    if (c == 0)
-      reinterpret_cast<uint16_t *>(tensor ? a.vs_dst : a.ks_dst)[int8_scale_index(bh, t, BT)] =
-          __builtin_bit_cast(uint16_t, s16);
+    s16b[tensor] = __builtin_bit_cast(uint16_t, s16);
   }
   }
   // one-byte codes (int8 / fp8): K rows straight out, V transposed through LDS
-  *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) =
-      make_uint2(codes[0][0], codes[0][1]);
   *reinterpret_cast<uint2 *>(&lq[t][8 * c]) = make_uint2(codes[1][0], codes[1][1]);
   __syncthreads();
+  if (a.pool.format != kFp8 && block_bad()) {  // fp8 checked at its reduction barrier
+    if (tid == 0) atomicOr(a.err, kErrNonFinite);
+    return;
+  }
+  *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) =
+      make_uint2(codes[0][0], codes[0][1]);
+  if (a.pool.format != kFp8 && c < 2)
+    reinterpret_cast<uint16_t *>(c ? a.vs_dst : a.ks_dst)[int8_scale_index(bh, t, BT)] = c ? s16b[1] : s16b[0];
   uint32_t w[2] = {0u, 0u};
 #pragma unroll
   for (int j = 0; j < 8; j++) w[j >> 2] |= (uint32_t)lq[8 * half + j][d] << (8 * (j & 3));
