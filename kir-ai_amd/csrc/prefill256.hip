@@ -5,16 +5,23 @@
 // [lo(pos), pos] (crates/llm-backend/src/core/native_attention.rs:356-464),
 // times sigmoid(gate) when the call carries one (native_attention.rs:765-781).
 //
-// Same dataflow as the head_dim-128 kernel -- S^T = K Q^T and O^T += V^T P^T on
-// v_mfma_f32_32x32x16_bf16, P^T taken straight from the S^T accumulators, V^T
-// read from the dim-major pool layout, K/V tiles of 64 keys double-buffered in
-// LDS, online softmax in log2 units with a lazy rescale -- at twice the row
-// width: a wavefront holds its 32 query rows' Q^T (16 k-steps, 64 registers)
-// and O^T (8 blocks of 32 dims, 128 accumulators), a tile is 64 MFMAs per
-// wavefront, two tile buffers take 146 KB of LDS.  One query head per
-// workgroup of 4 wavefronts, one workgroup per CU (one wavefront per SIMD, up
-// to 512 registers each): the per-wavefront state of head_dim 256 does not fit
-// the 256 registers two wavefronts per SIMD would leave.
+// S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16, P^T taken straight
+// from the S^T accumulators, V^T read from the dim-major pool layout, K/V tiles of
+// 64 keys double-buffered in LDS, online softmax in log2 units with a lazy
+// rescale.  A wavefront owns 16 query rows: their Q^T (8 k-steps of 32 dims, 32
+// registers), O^T (16 blocks of 16 dims, 64 accumulators) and S^T (4 blocks of 16
+// keys, 16 accumulators) fit the 256 registers of two wavefronts per SIMD, so one
+// workgroup of 8 wavefronts (128 rows of one query head) per CU keeps two
+// wavefronts on every SIMD to cover each other's LDS and exponent latency.  (With
+// 32-row tiles on the 32x32x16 form the same state needs ~450 registers and leaves
+// one wavefront per SIMD.)
+//
+// MFMA operand layouts (16x16x32, bf16): A 16 x 32, lane l holds row l%16, k
+// 8(l/16)..+8; B 32 x 16, lane l holds column l%16, k 8(l/16)..+8; D 16 x 16, lane
+// l holds column l%16, rows 4(l/16)..+4.  So S^T block kb gives lane l the scores
+// of keys 16kb + 4g .. +4 (g = l/16) for query row l%16, and the P^T operand of a
+// 32-key step s takes keys {32s + 4g .. +4, 32s + 16 + 4g .. +4} in its k-slots
+// 8g..8g+7; the V^T operand reads the same keys (one 16-byte LDS read).
 #include "device_common.h"
 
 namespace llh {
@@ -23,26 +30,31 @@ namespace {
 
 constexpr int D = kD256HeadDim;
 constexpr int BT = kFastBlockTokens;
-constexpr int BM = 128;          // query rows per workgroup
-constexpr int BN = 64;           // key positions per tile
-constexpr int KBLK = BN / BT;    // pool blocks per tile
-constexpr int K_STRIDE = D + 8;  // bf16 elements per K row in LDS (528 B)
-constexpr int V_STRIDE = BT + 4; // bf16 elements per V^T row in LDS (40 B)
+constexpr int ROWS = 16;            // query rows per wavefront
+constexpr int WAVES = 8;
+constexpr int BM = ROWS * WAVES;    // query rows per workgroup (the host's q_tiles unit)
+constexpr int BN = 64;              // key positions per tile
+constexpr int KBLK = BN / BT;       // pool blocks per tile
+constexpr int K_STRIDE = D + 8;     // bf16 elements per K row in LDS (528 B: 16 rows' b128 reads hit distinct banks)
 constexpr int K_TILE = BN * K_STRIDE;
-constexpr int V_TILE = KBLK * D * V_STRIDE;
-constexpr int kThreads = 256;
+constexpr int V_ROW = 2 * BT;          // bf16 elements per V^T dim row of one 32-key step in LDS
+constexpr int V_STEP = D * V_ROW;      // one 32-key step (two blocks) of V^T
+constexpr int V_TILE = 2 * V_STEP;
+constexpr int kThreads = 64 * WAVES;
+static_assert(BM == 128, "q_tiles is computed for 128-row query tiles");
+constexpr int PF_S = 8;  // K fragment reads kept in flight ahead of the S^T MFMAs
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
 }
 
-__device__ __forceinline__ f32x16_t mfma32(const u32x4_t &a, const u32x4_t &b, const f32x16_t &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                   0, 0, 0);
 }
 
@@ -54,17 +66,35 @@ __device__ __forceinline__ float xor32_other(float v) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// Reduction over the four lanes l%16 + 16g that hold one query row.
+__device__ __forceinline__ float row_max4(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, xor32_other(v));
+}
+__device__ __forceinline__ float row_sum4(float v) {
+  v += __shfl_xor(v, 16);
+  return v + xor32_other(v);
+}
+
 __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
                                          __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
 }
 
-// One thread's share of a tile: for each of the 4 blocks, K of token tid/16
-// at dims 8(tid%16).. and 128 + 8(tid%16).., and V^T of dims tid/2 and
-// 128 + tid/2 at tokens 8(tid&1).. (16 bytes each).
+// V^T in LDS, per 32-key step s (blocks 2s, 2s+1): a 64-byte row per dim holding,
+// for each 4-token chunk g, chunk g of block 2s then chunk g of block 2s+1 -- the
+// 16 bytes one lane's A operand takes (keys 32s + 4g .. +4, 32s + 16 + 4g .. +4).
+// Dim row d keeps chunk pair g at pair g ^ v_swz(d), so the lanes of one 16-byte
+// read (dims 16db + r, one g) and of one 16-byte store (4 dims x 4 pairs) cover
+// the banks once.
+__device__ __forceinline__ int v_swz(int dim) { return ((dim >> 2) ^ (dim & 2)) & 3; }
+
+// One thread's share of a tile: for each of the 4 blocks, 16 bytes of K at
+// token tid/32, dims 8(tid%32).. (the thread's 16-byte slot of the block's 8 KiB),
+// and 8 bytes of V^T (tokens 4(tid&3) .. +4) at dims tid/4 and 128 + tid/4.
 struct Tile256 {
-  u32x4_t k[KBLK][2];
-  u32x4_t v[KBLK][2];
+  u32x4_t k[KBLK];
+  uint2 v[KBLK][2];
 };
 
 // Block-table entries of the tile starting at kt: lane kb holds block kb's
@@ -89,13 +119,10 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
     const bool use = needed && ok;
     use_mask |= use ? (1u << kb) : 0u;
     const size_t base = ((size_t)(use ? phys : 0) * a.pool.kv_heads + kvh) * (BT * D);
-    const uint16_t *kp = reinterpret_cast<const uint16_t *>(a.pool.k) + base + (tid >> 4) * D + (tid & 15) * 8;
-    const uint16_t *vp = reinterpret_cast<const uint16_t *>(a.pool.v) + base + (tid >> 1) * BT + (tid & 1) * 8;
-#pragma unroll
-    for (int hf = 0; hf < 2; hf++) {
-      r.k[kb][hf] = *reinterpret_cast<const u32x4_t *>(kp + hf * 128);
-      r.v[kb][hf] = *reinterpret_cast<const u32x4_t *>(vp + hf * 128 * BT);
-    }
+    r.k[kb] = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const uint16_t *>(a.pool.k) + base + tid * 8);
+    const uint16_t *vp = reinterpret_cast<const uint16_t *>(a.pool.v) + base + tid * 4;
+    r.v[kb][0] = *reinterpret_cast<const uint2 *>(vp);
+    r.v[kb][1] = *reinterpret_cast<const uint2 *>(vp + 128 * BT);
   }
   return use_mask;
 }
@@ -106,24 +133,30 @@ __device__ __forceinline__ uint32_t load_tile(const PrefillArgs &a, int entries,
 __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int tid, const Tile256 &r,
                                            uint32_t use_mask, int kt, int ctx) {
   const bool tail = kt + BN > ctx;
+  const int g = tid & 3;
 #pragma unroll
-  for (int kb = 0; kb < KBLK; kb++) {
+  for (int kb = 0; kb < KBLK; kb++)
+    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 5)) * K_STRIDE + (tid & 31) * 8]) = r.k[kb];
+#pragma unroll
+  for (int s = 0; s < 2; s++) {
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
-      *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 4)) * K_STRIDE + hf * 128 + (tid & 15) * 8]) =
-          r.k[kb][hf];
-      u32x4_t v = r.v[kb][hf];
-      if (!(use_mask & (1u << kb))) v = u32x4_t{0u, 0u, 0u, 0u};
-      if (tail) {
-        const int valid = ctx - (kt + kb * BT + (tid & 1) * 8);  // tokens of this 8-run inside the context
-        v[0] &= (valid > 0 ? 0x0000ffffu : 0u) | (valid > 1 ? 0xffff0000u : 0u);
-        v[1] &= (valid > 2 ? 0x0000ffffu : 0u) | (valid > 3 ? 0xffff0000u : 0u);
-        v[2] &= (valid > 4 ? 0x0000ffffu : 0u) | (valid > 5 ? 0xffff0000u : 0u);
-        v[3] &= (valid > 6 ? 0x0000ffffu : 0u) | (valid > 7 ? 0xffff0000u : 0u);
+      uint2 c[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int kb = 2 * s + e;
+        uint2 v = r.v[kb][hf];
+        if (!(use_mask & (1u << kb))) v = make_uint2(0u, 0u);
+        if (tail) {
+          const int valid = ctx - (kt + kb * BT + 4 * g);  // tokens of this 4-run inside the context
+          v.x &= (valid > 0 ? 0x0000ffffu : 0u) | (valid > 1 ? 0xffff0000u : 0u);
+          v.y &= (valid > 2 ? 0x0000ffffu : 0u) | (valid > 3 ? 0xffff0000u : 0u);
+        }
+        c[e] = v;
       }
-      uint16_t *dst = &v_lds[(kb * D + hf * 128 + (tid >> 1)) * V_STRIDE + (tid & 1) * 8];
-      *reinterpret_cast<uint2 *>(dst) = make_uint2(v[0], v[1]);
-      *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(v[2], v[3]);
+      const int dim = (tid >> 2) + 128 * hf;
+      *reinterpret_cast<u32x4_t *>(&v_lds[s * V_STEP + dim * V_ROW + 8 * (g ^ v_swz(dim))]) =
+          u32x4_t{c[0].x, c[0].y, c[1].x, c[1].y};
     }
   }
 }
@@ -166,24 +199,24 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int h = lane >> 5;
-  const int col = lane & 31;
+  const int g = lane >> 4;   // k-slot group of the MFMA operands
+  const int r = lane & 15;   // query row of the wavefront; also the A-operand row
   const int prefix = ctx - chunk;
   const int rows_wg = min(BM, chunk - i0);
   const int qpos_first = prefix + i0;
   const int qpos_last = prefix + i0 + rows_wg - 1;
-  const int my_row = i0 + wave * 32 + col;
+  const int my_row = i0 + wave * ROWS + r;
   const bool row_ok = my_row < chunk;
   const int my_pos = prefix + my_row;
   const int my_lo = a.window > 0 ? max(0, my_pos - a.window + 1) : 0;
 
-  // ---- Q^T operand: 16 k-steps of 16 dims; lane holds dims 16ks + 8h .. +8 of its row ----
-  u32x4_t qb[16];
+  // ---- Q^T operand: 8 k-steps of 32 dims; lane holds dims 32ks + 8g .. +8 of its row ----
+  u32x4_t qb[8];
   {
     const uint16_t *qrow = a.q + ((size_t)(c0 + (row_ok ? my_row : 0)) * Hq + qh) * D;
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++) {
-      u32x4_t t = *reinterpret_cast<const u32x4_t *>(qrow + ks * 16 + h * 8);
+    for (int ks = 0; ks < 8; ks++) {
+      u32x4_t t = *reinterpret_cast<const u32x4_t *>(qrow + ks * 32 + g * 8);
       if (!row_ok) t = u32x4_t{0u, 0u, 0u, 0u};
       qb[ks] = t;
     }
@@ -192,11 +225,9 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][K_TILE];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][V_TILE];
 
-  f32x16_t oacc[8];
+  f32x4_t oacc[16];
 #pragma unroll
-  for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-    for (int j = 0; j < 16; j++) oacc[mt][j] = 0.0f;
+  for (int db = 0; db < 16; db++) oacc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
@@ -204,12 +235,13 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
   const int khi = qpos_last + 1;  // exclusive
   const int t_begin = (klo / BN) * BN;
   const int32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const int wrow0 = i0 + wave * 32;
+  const int wrow0 = i0 + wave * ROWS;
   const int wpos_first = prefix + wrow0;
-  const int wpos_last = prefix + min(wrow0 + 31, chunk - 1);
+  const int wpos_last = prefix + min(wrow0 + ROWS - 1, chunk - 1);
   const int wlo_first = a.window > 0 ? max(0, wpos_first - a.window + 1) : 0;
   const int wlo_last = a.window > 0 ? max(0, wpos_last - a.window + 1) : 0;
   const bool wave_live = wrow0 < chunk;
+  const int vsw = 8 * (g ^ v_swz(r));  // element offset of this lane's V^T chunk pair (dims 16db + r)
 
   Tile256 next;
   bool bad = false;
@@ -218,17 +250,8 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
   store_tile(k_lds[0], v_lds[0], tid, next, use_next, t_begin, ctx);
   __syncthreads();
 
-  // The O^T accumulators live in AGPRs, where only the MFMAs touch them: the rare
-  // rescale (a row's max grew by more than 16 in log2 units) leaves the tile loop,
-  // multiplies them, and re-enters at the same tile, reissuing its loads and
-  // recomputing its scores.  (A rescale inside the loop made the compiler copy
-  // all 128 accumulators out of and back into AGPRs on every tile.)
   int buf = 0;
-  int kt = t_begin;
-  for (;;) {
-  bool rescale = false;
-  float m_next = m_run;  // this lane's new running max when leaving to rescale
-  for (; kt < khi; kt += BN, buf ^= 1) {
+  for (int kt = t_begin; kt < khi; kt += BN, buf ^= 1) {
     const bool has_next = kt + BN < khi;
     if (has_next)  // in flight during the math
       use_next = load_tile(a, ent_next, kvh, kt + BN, ctx, klo, tid, next, bad);
@@ -237,19 +260,27 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
     if (wave_live && kt <= wpos_last && kt + BN > wlo_first) {
       const uint16_t *kl = k_lds[buf];
       const uint16_t *vl = v_lds[buf];
-      // ---- S^T = K Q^T for two 32-key sub-tiles (their chains interleaved) ----
-      f32x16_t sacc[2];
+      // ---- S^T = K Q^T: four 16-key blocks, four independent chains ----
+      f32x4_t sacc[KBLK];
 #pragma unroll
-      for (int st = 0; st < 2; st++)
+      for (int kb = 0; kb < KBLK; kb++) sacc[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 16; j++) sacc[st][j] = 0.0f;
+      for (int ks = 0; ks < 8; ks++)
 #pragma unroll
-      for (int ks = 0; ks < 16; ks++)
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-          const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(st * 32 + col) * K_STRIDE + ks * 16 + h * 8]);
-          sacc[st] = mfma32(ka, qb[ks], sacc[st]);
+        for (int kb = 0; kb < KBLK; kb++) {
+          const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(kb * BT + r) * K_STRIDE + ks * 32 + g * 8]);
+          sacc[kb] = mfma16(ka, qb[ks], sacc[kb]);
         }
+      // keep PF_S fragment reads in flight ahead of the MFMAs (left to itself the
+      // scheduler keeps one or two, exposing the LDS latency on every MFMA):
+      // PF_S reads, then one MFMA and one read at a time, then the last PF_S MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, PF_S, 0);
+#pragma unroll
+      for (int i = 0; i < 32 - PF_S; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, PF_S, 0);
 
       // ---- scale, mask, online softmax (as the head_dim-128 kernel) ----
       const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
@@ -258,29 +289,29 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
       float tmax = -INFINITY;
       if (need_mask) {
 #pragma unroll
-        for (int st = 0; st < 2; st++) {
+        for (int kb = 0; kb < KBLK; kb++) {
 #pragma unroll
-          for (int j = 0; j < 16; j++) {
-            float s = sacc[st][j] * c;
-            const int kp = kt + st * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+          for (int i = 0; i < 4; i++) {
+            float s = sacc[kb][i] * c;
+            const int kp = kt + kb * BT + 4 * g + i;
             if (kp > my_pos || kp < my_lo || kp >= ctx || !row_ok) s = -INFINITY;
-            sacc[st][j] = s;
+            sacc[kb][i] = s;
             tmax = fmaxf(tmax, s);
           }
         }
         c_exp = 1.0f;
       } else if (c >= 0.0f) {
 #pragma unroll
-        for (int st = 0; st < 2; st++)
+        for (int kb = 0; kb < KBLK; kb++)
 #pragma unroll
-          for (int j = 0; j < 16; j++) tmax = fmaxf(tmax, sacc[st][j]);
+          for (int i = 0; i < 4; i++) tmax = fmaxf(tmax, sacc[kb][i]);
         tmax *= c;
       } else {
         float tmin = INFINITY;
 #pragma unroll
-        for (int st = 0; st < 2; st++)
+        for (int kb = 0; kb < KBLK; kb++)
 #pragma unroll
-          for (int j = 0; j < 16; j++) tmin = fminf(tmin, sacc[st][j]);
+          for (int i = 0; i < 4; i++) tmin = fminf(tmin, sacc[kb][i]);
         tmax = tmin * c;
       }
       // Raw scores beyond 2^26 (log2 units) once scaled: tmax, a rounded product, can
@@ -289,50 +320,50 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
       // every score rounds as tmax did and the largest weight is exactly 1.
       if (!need_mask && __any(fabsf(tmax) > 0x1p26f)) {
 #pragma unroll
-        for (int st = 0; st < 2; st++)
+        for (int kb = 0; kb < KBLK; kb++)
 #pragma unroll
-          for (int j = 0; j < 16; j++) sacc[st][j] *= c;
+          for (int i = 0; i < 4; i++) sacc[kb][i] *= c;
         c_exp = 1.0f;
       }
-      tmax = fmaxf(tmax, xor32_other(tmax));
+      tmax = row_max4(tmax);
       const float m_cand = fmaxf(m_run, tmax);
       // a row without a finite score yet takes the tile's max (its accumulators are
-      // still zero); a row whose max grows by more than 16 needs a rescale first
+      // still zero); a row whose max grows by more than 16 is rescaled first, so
+      // the weights stay below 2^16
       const bool grow = m_run != -INFINITY && m_cand > m_run + 16.0f;
       if (__any(grow)) {
-        m_next = grow ? m_cand : m_run;
-        rescale = true;
-        break;
+        const float m_new = grow ? m_cand : m_run;
+        const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that did not grow
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 16; db++) oacc[db] *= alpha;
       }
       if (m_run == -INFINITY) m_run = m_cand;
       const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
-      u32x4_t pb[4];
-#pragma unroll
-      for (int st = 0; st < 2; st++) {
-        float p[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) p[j] = fast_exp2(__builtin_fmaf(sacc[st][j], c_exp, -mref));
-#pragma unroll
-        for (int q = 0; q < 2; q++)
-          pb[2 * st + q] = u32x4_t{pack_bf16(p[8 * q + 0], p[8 * q + 1]), pack_bf16(p[8 * q + 2], p[8 * q + 3]),
-                                   pack_bf16(p[8 * q + 4], p[8 * q + 5]), pack_bf16(p[8 * q + 6], p[8 * q + 7])};
-      }
+      u32x4_t pb[2];
       float psum = 0.0f;  // row sums of exactly the bf16 weights that enter P V
 #pragma unroll
-      for (int kb = 0; kb < KBLK; kb++)
+      for (int s = 0; s < 2; s++) {
+        float p[8];
 #pragma unroll
-        for (int e = 0; e < 4; e++) psum = dot2_ones(pb[kb][e], psum);
+        for (int i = 0; i < 4; i++) {
+          p[i] = fast_exp2(__builtin_fmaf(sacc[2 * s][i], c_exp, -mref));
+          p[4 + i] = fast_exp2(__builtin_fmaf(sacc[2 * s + 1][i], c_exp, -mref));
+        }
+        pb[s] = u32x4_t{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+#pragma unroll
+        for (int e = 0; e < 4; e++) psum = dot2_ones(pb[s][e], psum);
+      }
       l_run += psum;
 
-      // ---- O^T += V^T P^T over 8 blocks of 32 dims ----
+      // ---- O^T += V^T P^T over 16 blocks of 16 dims, two 32-key steps ----
 #pragma unroll
-      for (int kb = 0; kb < KBLK; kb++) {
+      for (int s = 0; s < 2; s++) {
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++) {
-          const uint16_t *vrow = &vl[(kb * D + mt * 32 + col) * V_STRIDE];
-          const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + 4 * h);
-          const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + 8 + 4 * h);
-          oacc[mt] = mfma32(u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y}, pb[kb], oacc[mt]);
+        for (int db = 0; db < 16; db++) {
+          const u32x4_t va = *reinterpret_cast<const u32x4_t *>(&vl[s * V_STEP + (db * 16 + r) * V_ROW + vsw]);
+          oacc[db] = mfma16(va, pb[s], oacc[db]);
         }
       }
     }
@@ -340,36 +371,21 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
     if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
     __syncthreads();  // next tile visible; this tile no longer read
   }
-  if (!rescale) break;
-  {
-    const float alpha = fast_exp2(m_run - m_next);  // 1 for rows that did not grow
-    m_run = m_next;
-    l_run *= alpha;
-#pragma unroll
-    for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-      for (int j = 0; j < 16; j++) oacc[mt][j] *= alpha;
-    ent_next = fetch_entries(a, table, kt + BN, lane);  // the re-entered tile's next-tile entries
-  }
-  }
 
-  // ---- normalise and store: lane holds dims 32mt + 8(j/4) + 4h + (j%4) of its row ----
+  // ---- normalise and store: lane holds dims 16db + 4g .. +4 of its row ----
   if (bad && tid == 0) atomicOr(a.err, kErrBadBlock);  // a needed block was missing: its keys read as zeros
-  const float l_tot = l_run + xor32_other(l_run);
+  const float l_tot = row_sum4(l_run);
   if (!row_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   const size_t obase = ((size_t)(c0 + my_row) * Hq + qh) * D;
   uint16_t *orow = a.out + obase;
 #pragma unroll
-  for (int mt = 0; mt < 8; mt++) {
+  for (int db = 0; db < 16; db++) {
+    const int d0 = db * 16 + 4 * g;
+    float v[4];
 #pragma unroll
-    for (int jq = 0; jq < 4; jq++) {
-      const int d0 = mt * 32 + jq * 8 + 4 * h;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) v[e] = gated(oacc[mt][4 * jq + e] * inv, a.gate, obase + d0 + e);
-      *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-    }
+    for (int e = 0; e < 4; e++) v[e] = gated(oacc[db][e] * inv, a.gate, obase + d0 + e);
+    *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
   }
 }
 
