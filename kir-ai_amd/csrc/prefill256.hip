@@ -35,8 +35,7 @@ constexpr int WAVES = 8;
 constexpr int BM = ROWS * WAVES;    // query rows per workgroup (the host's q_tiles unit)
 constexpr int BN = 64;              // key positions per tile
 constexpr int KBLK = BN / BT;       // pool blocks per tile
-constexpr int K_STRIDE = D + 8;     // bf16 elements per K row in LDS (528 B: 16 rows' b128 reads hit distinct banks)
-constexpr int K_TILE = BN * K_STRIDE;
+constexpr int K_TILE = BN * D;      // K rows unpadded; 16-byte chunk c of key row t sits at c ^ (t & 15)
 constexpr int V_ROW = 2 * BT;          // bf16 elements per V^T dim row of one 32-key step in LDS
 constexpr int V_STEP = D * V_ROW;      // one 32-key step (two blocks) of V^T
 constexpr int V_TILE = 2 * V_STEP;
@@ -136,7 +135,7 @@ __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int
   const int g = tid & 3;
 #pragma unroll
   for (int kb = 0; kb < KBLK; kb++)
-    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 5)) * K_STRIDE + (tid & 31) * 8]) = r.k[kb];
+    *reinterpret_cast<u32x4_t *>(&k_lds[(kb * BT + (tid >> 5)) * D + (((tid & 31) ^ (tid >> 5)) * 8)]) = r.k[kb];
 #pragma unroll
   for (int s = 0; s < 2; s++) {
 #pragma unroll
@@ -268,7 +267,7 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
       for (int ks = 0; ks < 8; ks++)
 #pragma unroll
         for (int kb = 0; kb < KBLK; kb++) {
-          const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(kb * BT + r) * K_STRIDE + ks * 32 + g * 8]);
+          const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(kb * BT + r) * D + (((ks * 4 + g) ^ r) * 8)]);
           sacc[kb] = mfma16(ka, qb[ks], sacc[kb]);
         }
       // keep PF_S fragment reads in flight ahead of the MFMAs (left to itself the
