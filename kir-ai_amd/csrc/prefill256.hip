@@ -42,6 +42,7 @@ constexpr int V_TILE = 2 * V_STEP;
 constexpr int kThreads = 64 * WAVES;
 static_assert(BM == 128, "q_tiles is computed for 128-row query tiles");
 constexpr int PF_S = 8;  // K fragment reads kept in flight ahead of the S^T MFMAs
+constexpr int PF_V = 6;  // V^T fragment reads kept in flight ahead of the P V MFMAs
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
@@ -365,6 +366,13 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
           oacc[db] = mfma16(va, pb[s], oacc[db]);
         }
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, PF_V, 0);  // the same for the V^T reads
+#pragma unroll
+      for (int i = 0; i < 32 - PF_V; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, PF_V, 0);
     }
 
     if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
