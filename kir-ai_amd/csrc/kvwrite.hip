@@ -433,6 +433,169 @@ __device__ __forceinline__ int64_t append_slot(const AppendArgs &a, int i) {
                  : (int64_t)a.tables[(size_t)i * a.max_blocks + (pos / bt) % a.max_blocks] * bt + pos % bt;
 }
 
+// Row element d of a bf16 or f32 source row as f32.
+template <typename ST>
+__device__ __forceinline__ float src_elem(const ST *p, int d) {
+  if constexpr (sizeof(ST) == 4)
+    return p[d];
+  else
+    return bf16_to_f32(p[d]);
+}
+
+// fp8 blocks: the tokens of one call that go to block blk are appended by the
+// wavefront of the block's first token in call order, all of them, in that
+// order (each may rescale the block).  Row i's wavefront returns at once when
+// an earlier row of the call goes to the same block.
+template <typename ST>
+__device__ __forceinline__ void append_fp8_in_order(const AppendArgs &a, int i, int h, int64_t blk, size_t bh,
+                                                    int lane) {
+  const int BT = a.pool.block_tokens;
+  const int Hkv = a.pool.kv_heads;
+  const int Dh = a.pool.head_dim;
+  auto ld = [](const ST *p, int d) -> float { return src_elem<ST>(p, d); };
+  for (int j0 = 0; j0 < i; j0 += 64) {
+    const int j = j0 + lane;
+    const int64_t sj = j < i ? append_slot(a, j) : (int64_t)-1;
+    const bool same = sj >= 0 && sj / BT == blk;
+    if (__any(same)) return;
+  }
+  float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[fp8_scale_index(bh)],
+                    reinterpret_cast<const float *>(a.vs_dst)[fp8_scale_index(bh)]};
+  // this call's tokens of the block, in call order: the slots are read 64 at a
+  // time (one vector load per lane) and walked through a ballot mask
+  for (int j0 = i; j0 < a.n; j0 += 64) {
+    const int64_t sl = j0 + lane < a.n ? append_slot(a, j0 + lane) : (int64_t)-1;
+    uint64_t pending = __ballot(sl >= 0 && sl / BT == blk);
+    while (pending) {
+      const int k = __builtin_ctzll(pending);
+      pending &= pending - 1;
+      const int j = j0 + k;
+      const int64_t sj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sl >> 32), k) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sl, k));
+      const int offj = (int)(sj % BT);
+      const ST *kj = reinterpret_cast<const ST *>(a.k) + ((size_t)j * Hkv + h) * Dh;
+      const ST *vj = reinterpret_cast<const ST *>(a.v) + ((size_t)j * Hkv + h) * Dh;
+      bool finite = true;
+      for (int d = lane; d < Dh; d += 64) finite = finite && isfinite(ld(kj, d)) && isfinite(ld(vj, d));
+      if (__any(!finite)) {
+        if (lane == 0) atomicOr(a.err, kErrNonFinite);
+        continue;
+      }
+      // this wavefront's earlier stores to the block are complete before it reads the block again
+      if (j > i) __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      scale[0] = append_fp8_row(reinterpret_cast<uint8_t *>(a.k_dst), false, bh, BT, Dh, offj, kj, ld, scale[0], lane);
+      scale[1] = append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
+    }
+  }
+  if (lane == 0) {
+    reinterpret_cast<float *>(a.ks_dst)[fp8_scale_index(bh)] = scale[0];
+    reinterpret_cast<float *>(a.vs_dst)[fp8_scale_index(bh)] = scale[1];
+  }
+}
+
+// fp8 blocks of 16 tokens x 128 dims, calls of at most 64 rows: append_kernel's fp8
+// result (append_fp8_in_order, append_fp8_row's arithmetic bit for bit) in three
+// memory round trips.  The call's slots (one per lane) and the row come first; a row
+// that shares its block with a later row of the call takes the in-order path; else
+// the block's scales and codes come together, and a scale that grows re-encodes the
+// earlier tokens in registers.  Lane l holds K token l/4, bytes 32(l&3) .. +32, and
+// V^T dims 2l, 2l + 1 (16 tokens each).
+template <typename ST>
+__global__ __launch_bounds__(64) void append_fp8_d128_kernel(const AppendArgs a) {
+  constexpr int BT = 16, Dh = 128;
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int Hkv = a.pool.kv_heads;
+  const ST *ks = reinterpret_cast<const ST *>(a.k) + ((size_t)i * Hkv + h) * Dh;
+  const ST *vs = reinterpret_cast<const ST *>(a.v) + ((size_t)i * Hkv + h) * Dh;
+  const int64_t sl = lane < a.n ? append_slot(a, lane) : (int64_t)-1;
+  float kx[2], vx[2], vp[2];  // K and V dims lane, lane + 64; V dims 2 lane, 2 lane + 1
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    kx[r] = src_elem<ST>(ks, lane + 64 * r);
+    vx[r] = src_elem<ST>(vs, lane + 64 * r);
+    vp[r] = src_elem<ST>(vs, 2 * lane + r);
+  }
+  const int64_t slot = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sl >> 32), i) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sl, i));
+  if (slot == kNoSlot) return;  // a sequence with no new token (fused-append fallback)
+  const int64_t blk = slot / BT;
+  const int off = (int)(slot % BT);
+  if (slot < 0 || blk >= a.pool.n_blocks) {
+    if (lane == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const bool same = sl >= 0 && sl / BT == blk;
+  if (__ballot(same && lane < i)) return;  // an earlier row's wavefront appends this one
+  if (__ballot(same && lane > i)) {
+    append_fp8_in_order<ST>(a, i, h, blk, bh, lane);
+    return;
+  }
+  uint8_t *kd = reinterpret_cast<uint8_t *>(a.k_dst) + bh * BT * Dh;
+  uint8_t *vd = reinterpret_cast<uint8_t *>(a.v_dst) + bh * Dh * BT;
+  float *ksc = reinterpret_cast<float *>(a.ks_dst) + fp8_scale_index(bh);
+  float *vsc = reinterpret_cast<float *>(a.vs_dst) + fp8_scale_index(bh);
+  const float sc_k = *ksc, sc_v = *vsc;
+  const uint4 kc0 = reinterpret_cast<const uint4 *>(kd)[2 * lane], kc1 = reinterpret_cast<const uint4 *>(kd)[2 * lane + 1];
+  const uint4 vc[2] = {reinterpret_cast<const uint4 *>(vd)[2 * lane], reinterpret_cast<const uint4 *>(vd)[2 * lane + 1]};
+  if (__any(!(isfinite(kx[0]) && isfinite(kx[1]) && isfinite(vx[0]) && isfinite(vx[1])))) {
+    if (lane == 0) atomicOr(a.err, kErrNonFinite);  // NonFiniteValue: the block is left as it was
+    return;
+  }
+  float s_old[2], s_new[2];
+#pragma unroll
+  for (int tensor = 0; tensor < 2; tensor++) {
+    const float *x = tensor ? vx : kx;
+    const float mx = wave_max(fmaxf(fabsf(x[0]), fabsf(x[1])));
+    const float cand = mx == 0.0f ? 0.0f : __fdiv_rn(mx, 448.0f);
+    s_old[tensor] = off == 0 ? 0.0f : (tensor ? sc_v : sc_k);
+    s_new[tensor] = fmaxf(s_old[tensor], cand);
+  }
+  auto enc = [](float v, float s) -> uint32_t { return s == 0.0f ? 0u : encode_e4m3(__fdiv_rn(v, s)); };
+  auto recode = [](uint32_t code, float so, float s) -> uint32_t {
+    const float x = so == 0.0f ? 0.0f : decode_e4m3(code) * so;
+    return encode_e4m3(__fdiv_rn(x, s));
+  };
+  // K: the scale grew -> tokens before off re-encoded (32 bytes per lane); row off
+  if (s_new[0] != s_old[0] && (lane >> 2) < off) {
+    uint32_t w[8] = {kc0.x, kc0.y, kc0.z, kc0.w, kc1.x, kc1.y, kc1.z, kc1.w};
+#pragma unroll
+    for (int e = 0; e < 32; e++) {
+      const uint32_t code = recode((w[e >> 2] >> (8 * (e & 3))) & 0xffu, s_old[0], s_new[0]);
+      w[e >> 2] = (w[e >> 2] & ~(0xffu << (8 * (e & 3)))) | (code << (8 * (e & 3)));
+    }
+    reinterpret_cast<uint4 *>(kd)[2 * lane] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4 *>(kd)[2 * lane + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; r++) kd[off * Dh + lane + 64 * r] = (uint8_t)enc(kx[r], s_new[0]);
+  // V: the scale grew -> this lane's two dim rows rewritten whole (tokens before
+  // off re-encoded, the new token at off); else the new token's byte of each dim
+  if (s_new[1] != s_old[1] && off > 0) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      uint32_t w[4] = {vc[r].x, vc[r].y, vc[r].z, vc[r].w};
+#pragma unroll
+      for (int u = 0; u < BT; u++) {
+        if (u > off) break;
+        const uint32_t old = (w[u >> 2] >> (8 * (u & 3))) & 0xffu;
+        const uint32_t code = u == off ? enc(vp[r], s_new[1]) : recode(old, s_old[1], s_new[1]);
+        w[u >> 2] = (w[u >> 2] & ~(0xffu << (8 * (u & 3)))) | (code << (8 * (u & 3)));
+      }
+      reinterpret_cast<uint4 *>(vd)[2 * lane + r] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 2; r++) vd[(lane + 64 * r) * BT + off] = (uint8_t)enc(vx[r], s_new[1]);
+  }
+  if (lane == 0) {
+    *ksc = s_new[0];
+    *vsc = s_new[1];
+  }
+}
+
 // One wavefront per token row i: the reference's int8 row layout (one f32
 // scale over all kv heads of the row; write_blocks_row_kernel's rule).
 template <typename ST>
@@ -560,48 +723,7 @@ __global__ __launch_bounds__(64) void append_kernel(const AppendArgs a) {
     return;
   }
   if (a.pool.format == kFp8) {
-    // Tokens of one block in one call: the wavefront of the block's first token
-    // in call order appends them all, in that order (each may rescale the block).
-    for (int j0 = 0; j0 < i; j0 += 64) {
-      const int j = j0 + lane;
-      const int64_t sj = j < i ? append_slot(a, j) : (int64_t)-1;
-      const bool same = sj >= 0 && sj / BT == blk;
-      if (__any(same)) return;
-    }
-    float scale[2] = {reinterpret_cast<const float *>(a.ks_dst)[fp8_scale_index(bh)],
-                      reinterpret_cast<const float *>(a.vs_dst)[fp8_scale_index(bh)]};
-    // this call's tokens of the block, in call order: the slots are read 64 at a
-    // time (one vector load per lane) and walked through a ballot mask
-    for (int j0 = i; j0 < a.n; j0 += 64) {
-      const int64_t sl = j0 + lane < a.n ? append_slot(a, j0 + lane) : (int64_t)-1;
-      uint64_t pending = __ballot(sl >= 0 && sl / BT == blk);
-      while (pending) {
-        const int k = __builtin_ctzll(pending);
-        pending &= pending - 1;
-        const int j = j0 + k;
-        const int64_t sj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(sl >> 32), k) << 32) |
-                                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)sl, k));
-        const int offj = (int)(sj % BT);
-        const ST *kj = reinterpret_cast<const ST *>(a.k) + ((size_t)j * Hkv + h) * Dh;
-        const ST *vj = reinterpret_cast<const ST *>(a.v) + ((size_t)j * Hkv + h) * Dh;
-        bool finite = true;
-        for (int d = lane; d < Dh; d += 64) finite = finite && isfinite(ld(kj, d)) && isfinite(ld(vj, d));
-        if (__any(!finite)) {
-          if (lane == 0) atomicOr(a.err, kErrNonFinite);
-          continue;
-        }
-        // this wavefront's earlier stores to the block are complete before it reads the block again
-        if (j > i) __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-        scale[0] =
-            append_fp8_row(reinterpret_cast<uint8_t *>(a.k_dst), false, bh, BT, Dh, offj, kj, ld, scale[0], lane);
-        scale[1] =
-            append_fp8_row(reinterpret_cast<uint8_t *>(a.v_dst), true, bh, BT, Dh, offj, vj, ld, scale[1], lane);
-      }
-    }
-    if (lane == 0) {
-      reinterpret_cast<float *>(a.ks_dst)[fp8_scale_index(bh)] = scale[0];
-      reinterpret_cast<float *>(a.vs_dst)[fp8_scale_index(bh)] = scale[1];
-    }
+    append_fp8_in_order<ST>(a, i, h, blk, bh, lane);
     return;
   }
   // int8 with per (token, head) fp16 scale; a NaN or an infinity in either row
@@ -758,6 +880,10 @@ hipError_t launch_append(const AppendArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(append_row_kernel<float>, dim3(a.n), dim3(64), 0, s, a);
   else if (a.pool.format == kInt8Row)
     hipLaunchKernelGGL(append_row_kernel<uint16_t>, dim3(a.n), dim3(64), 0, s, a);
+  else if (a.pool.format == kFp8 && a.pool.head_dim == 128 && a.pool.block_tokens == 16 && a.n <= 64 && a.src_f32)
+    hipLaunchKernelGGL(append_fp8_d128_kernel<float>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
+  else if (a.pool.format == kFp8 && a.pool.head_dim == 128 && a.pool.block_tokens == 16 && a.n <= 64)
+    hipLaunchKernelGGL(append_fp8_d128_kernel<uint16_t>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
   else if (a.src_f32)
     hipLaunchKernelGGL(append_kernel<float>, dim3(a.n, a.pool.kv_heads), dim3(64), 0, s, a);
   else

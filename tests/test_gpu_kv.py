@@ -325,6 +325,67 @@ def test_fp8_append_matches_oracle_token_by_token(ctx):
     assert_parity(out.cpu().numpy().view(np.uint16), ref, what="decode over appended fp8 blocks")
 
 
+@pytest.mark.parametrize("src_f32", [False, True])
+def test_fp8_append_one_row_per_block_calls(ctx, src_f32):
+    """Calls whose rows each go to a different block (the single-token fp8 kernel for
+    16-token, head_dim-128 blocks) from bf16 or f32 rows: 16 calls fill 8 blocks token by
+    token over stale codes, with magnitudes that grow the scale at some offsets (earlier
+    tokens re-encoded) and not at others; one row holds a NaN in one kv head's V (flagged;
+    that (block, head) left as it was, every other head and row of the call written).  Codes and scales equal the oracle's
+    restatement of the rule bit for bit."""
+    import torch
+
+    Hkv, nb = 2, 8
+    blocks = [5, 0, 7, 2, 9, 4, 1, 6]
+    pool = ctx.pool(llm_hip.KV_FP8_E4M3, BT, Hkv, D, 10)
+    stale = torch.randn((10, BT, Hkv, D), device="cuda").mul(30.0).to(torch.bfloat16)
+    ctx.write_blocks(pool, torch.arange(10, dtype=torch.int32, device="cuda"), stale, stale)
+    rng = np.random.default_rng(23)
+    mag = np.exp(rng.uniform(-3, 3, (BT, nb))).astype(np.float32)
+    x = (rng.standard_normal((BT, nb, 2, Hkv, D)) * mag[:, :, None, None, None]).astype(np.float32)
+    if not src_f32:
+        x = oracle.bf16_to_f32(oracle.f32_to_bf16(x.ravel())).reshape(x.shape)
+    nan_at = (6, 3, 1)  # (offset, row of the call, kv head): block 2's token 6, head 1, holds a NaN
+    x[nan_at[0], nan_at[1], 1, nan_at[2], 5] = np.nan
+    flags = []
+    for t in range(BT):
+        slots = np.array([b * BT + t for b in blocks], np.int64)
+        k, v = np.ascontiguousarray(x[t, :, 0]), np.ascontiguousarray(x[t, :, 1])
+        if src_f32:
+            ctx.append_f32(pool, to_dev(slots), to_dev(k), to_dev(v))
+        else:
+            ctx.append(pool, to_dev(slots), to_dev(oracle.f32_to_bf16(k.ravel()).reshape(k.shape)),
+                       to_dev(oracle.f32_to_bf16(v.ravel()).reshape(v.shape)))
+        torch.cuda.synchronize()
+        flags.append(ctx.device_errors())
+    assert all((f & llm_hip.ERR_FLAG_NON_FINITE) != 0 for i, f in enumerate(flags) if i == nan_at[0])
+    assert all(f == 0 for i, f in enumerate(flags) if i != nan_at[0])
+    raw = pool.raw()
+    kc = raw["k"].reshape(10, Hkv, BT, D)
+    vc = raw["v"].reshape(10, Hkv, D, BT)
+    ks = raw["k_scales"].view(np.float32).reshape(10, Hkv)
+    vs = raw["v_scales"].view(np.float32).reshape(10, Hkv)
+    grew = 0
+    for r, blk in enumerate(blocks):
+        for h in range(Hkv):
+            for tensor, got, gs in ((0, kc[blk, h], ks[blk, h]), (1, vc[blk, h].T, vs[blk, h])):
+                codes = np.zeros((BT, D), np.uint8)
+                s = 999.0
+                for t in range(BT):
+                    if (t, r, h) == nan_at:
+                        continue  # rejected for both tensors: the block-head keeps what it held
+                    s_before = s
+                    st, s = oracle.append_fp8_token(codes, s, t, x[t, r, tensor, h])
+                    assert st == oracle.OK
+                    grew += t > 0 and s != s_before
+                assert gs == np.float32(s), (blk, h, tensor)
+                keep = np.ones(BT, bool)
+                if (r, h) == nan_at[1:]:
+                    keep[nan_at[0]] = False  # that slot still holds the stale block's code
+                assert np.array_equal(got[keep], codes[keep]), (blk, h, tensor)
+    assert grew > 20  # the re-encoding branch ran many times
+
+
 def test_fp8_decode_table(ctx):
     import torch
 
