@@ -60,6 +60,22 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, co
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Scheduling order for a region of N LDS reads feeding N MFMAs: AHEAD reads,
+// then one MFMA and one read at a time, then the last AHEAD MFMAs -- so AHEAD
+// fragment reads stay in flight (left to itself the scheduler keeps one or two,
+// exposing the LDS latency on every MFMA).
+template <int N, int AHEAD>
+__device__ __forceinline__ void reads_ahead_of_mfma() {
+  constexpr int kMfma = 0x008, kDsRead = 0x100;  // sched_group_barrier instruction classes
+  __builtin_amdgcn_sched_group_barrier(kDsRead, AHEAD, 0);
+#pragma unroll
+  for (int i = 0; i < N - AHEAD; i++) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kMfma, AHEAD, 0);
+}
+
 // Value of lane (l ^ 32) (v_permlane32_swap: no LDS round trip).
 __device__ __forceinline__ float xor32_other(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -271,16 +287,7 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
           const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(kb * BT + r) * D + (((ks * 4 + g) ^ r) * 8)]);
           sacc[kb] = mfma16(ka, qb[ks], sacc[kb]);
         }
-      // keep PF_S fragment reads in flight ahead of the MFMAs (left to itself the
-      // scheduler keeps one or two, exposing the LDS latency on every MFMA):
-      // PF_S reads, then one MFMA and one read at a time, then the last PF_S MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, PF_S, 0);
-#pragma unroll
-      for (int i = 0; i < 32 - PF_S; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, PF_S, 0);
+      reads_ahead_of_mfma<KBLK * 8, PF_S>();
 
       // ---- scale, mask, online softmax (as the head_dim-128 kernel) ----
       const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
@@ -366,13 +373,7 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
           oacc[db] = mfma16(va, pb[s], oacc[db]);
         }
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, PF_V, 0);  // the same for the V^T reads
-#pragma unroll
-      for (int i = 0; i < 32 - PF_V; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, PF_V, 0);
+      reads_ahead_of_mfma<2 * 16, PF_V>();
     }
 
     if (has_next) store_tile(k_lds[buf ^ 1], v_lds[buf ^ 1], tid, next, use_next, kt + BN, ctx);
