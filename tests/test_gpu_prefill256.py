@@ -72,6 +72,15 @@ def test_prefill256_ragged_full_oracle(ctx, window):
     assert_parity(out, ref, what=f"prefill d256 W={window}")
 
 
+@pytest.mark.parametrize("window", [0, 64])
+def test_prefill256_tile_boundaries(ctx, window):
+    """Chunk lengths either side of a wavefront's 16 rows and a workgroup's 128 (1, 15, 16,
+    127, 128, 129, 255: wavefronts with no rows, partly filled workgroups) over prefixes
+    either side of a 64-key tile (63, 64, 65, 0, 1, 127, 16), every row against the oracle."""
+    out, ref = run(ctx, [63, 64, 65, 0, 1, 127, 16], [1, 15, 16, 127, 128, 129, 255], window, 47 + window)
+    assert_parity(out, ref, what=f"prefill d256 tile boundaries W={window}")
+
+
 def test_prefill256_query_magnitudes(ctx):
     """Query rows from bf16 subnormal to 1e30 (scores to ~1e31 in log2 units): tiles whose
     scaled max passes 2^26 scale their scores before the exponent."""
