@@ -420,14 +420,19 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
     g.manual_seed(workloads.SEED_BASE + 7)
     B, Hkv, Hq = 32, 8, 16
     # decode: the C2 batch's 32 new tokens (one row per sequence, scattered slots);
-    # prefill: C3's 8 x 512-token chunks, whole 16-token blocks (llh_kv_write_blocks)
-    for fmt, nm in ((llm_hip.KV_BF16, "bf16"), (llm_hip.KV_INT8, "int8"), (llm_hip.KV_FP8_E4M3, "fp8"),
-                    (llm_hip.KV_F16, "fp16")):
-        nblk, H = 8 * 512 // BT, 4
-        pool = ctx.pool(fmt, BT, H, D, 8192)
+    # prefill: C3's 8 x 512-token chunks, whole 16-token blocks (llh_kv_write_blocks), and
+    # the same chunks at the Qwen3.6 shape (head_dim 256, Hkv 2, bf16)
+    for fmt, nm, hd, H, shape, kern in (
+            (llm_hip.KV_BF16, "bf16", D, 4, "C3", "write_blocks_d128_kernel"),
+            (llm_hip.KV_INT8, "int8", D, 4, "C3", "write_blocks_d128_kernel"),
+            (llm_hip.KV_FP8_E4M3, "fp8", D, 4, "C3", "write_blocks_d128_kernel"),
+            (llm_hip.KV_F16, "fp16", D, 4, "C3", "write_blocks_d128_kernel"),
+            (llm_hip.KV_BF16, "bf16, head_dim 256", 256, 2, "Q36", "write_blocks16_d256_kernel")):
+        nblk = 8 * 512 // BT
+        pool = ctx.pool(fmt, BT, H, hd, 8192)
         ids = torch.randperm(8192, generator=g, device="cuda")[:nblk].to(torch.int32)
-        k = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
-        v = torch.randn((nblk, BT, H, D), generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn((nblk, BT, H, hd), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((nblk, BT, H, hd), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_steps(lambda s: ctx.write_blocks(pool, ids, k, v, stream=s), steps, warmup)
         host_us = HOST["us"]
         # the same write replayed from a HIP graph (the GPU's own time per call, which a
@@ -439,14 +444,14 @@ def measure_neighbours(ctx, steps: int, warmup: int) -> list:
         esz = 2 if fmt in (llm_hip.KV_BF16, llm_hip.KV_F16) else 1
         T = nblk * BT
         scales = {llm_hip.KV_INT8: T * H * 2 * 2, llm_hip.KV_FP8_E4M3: nblk * H * 4 * 2}.get(fmt, 0)
-        nbytes = T * H * D * 2 * 2 + T * H * D * esz * 2 + nblk * 4 + scales
-        out.append({"config": f"KV write C3 prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
+        nbytes = T * H * hd * 2 * 2 + T * H * hd * esz * 2 + nblk * 4 + scales
+        out.append({"config": f"KV write {shape} prefill chunks ({nblk} blocks = {T} tokens, Hkv{H}, {nm})",
                     "us_per_step": round(ms * 1e3, 2), "host_us_per_call": host_us, "bytes_per_step": nbytes,
                     "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "graph_us_per_step": round(gms * 1e3, 2),
                     "graph_hbm_frac": round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                    "kernel": "write_blocks_d128_kernel"})
+                    "kernel": kern})
         del pool
     for fmt, nm, T, H in ((llm_hip.KV_BF16, "bf16", B, Hkv), (llm_hip.KV_INT8, "int8", B, Hkv),
                           (llm_hip.KV_FP8_E4M3, "fp8", B, Hkv), (llm_hip.KV_F16, "fp16", B, Hkv)):

@@ -239,6 +239,44 @@ __global__ __launch_bounds__(256) void write_blocks_d128_kernel(const WriteBlock
 }
 
 // One workgroup per (block i, kv head).  Source rows src[i][t][h][d].
+// bf16 / fp16 pools at head_dim 256 (the Qwen3.5 / 3.6 full-attention layers), 16-token
+// blocks, 16-byte aligned rows: write_blocks_d128_kernel's 16-bit path at twice the row
+// width.  One workgroup of 512 per (block i, kv head); thread tid loads 16 bytes of token
+// tid/32's K and V rows (dims 8(tid%32) ..), stores K straight out and V through LDS, then
+// writes 16 bytes of V^T dim row tid/2 (tokens 8(tid&1) ..).
+__global__ __launch_bounds__(512) void write_blocks16_d256_kernel(const WriteBlocksArgs a) {
+  constexpr int BT = 16, Dh = 256;
+  const int i = blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t = tid >> 5, c = tid & 31;
+  const int Hkv = a.pool.kv_heads;
+  const int blk = a.blocks[i];
+  if (blk < 0 || (int64_t)blk >= a.pool.n_blocks) {
+    if (tid == 0) atomicOr(a.err, kErrBadBlock);
+    return;
+  }
+  const size_t bh = (size_t)blk * Hkv + h;
+  const size_t src = (((size_t)i * BT + t) * Hkv + h) * Dh + 8 * c;
+  uint4 kw = *reinterpret_cast<const uint4 *>(a.k + src);
+  uint4 vw = *reinterpret_cast<const uint4 *>(a.v + src);
+  if (a.pool.format == kF16) {  // each bf16 element widened (exact), then rounded to fp16
+    kw = bf16x8_to_f16x8(kw);
+    vw = bf16x8_to_f16x8(vw);
+  }
+  __shared__ uint16_t lv[BT][Dh + 8];
+  *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.k_dst) + (bh * BT + t) * Dh + 8 * c) = kw;
+  *reinterpret_cast<uint4 *>(&lv[t][8 * c]) = vw;
+  __syncthreads();
+  const int d = tid >> 1, half = tid & 1;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    w[j] = (uint32_t)lv[8 * half + 2 * j][d] | ((uint32_t)lv[8 * half + 2 * j + 1][d] << 16);
+  *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.v_dst) + (bh * Dh + d) * BT + 8 * half) =
+      make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 __global__ __launch_bounds__(256) void write_blocks_kernel(const WriteBlocksArgs a) {
   const int i = blockIdx.x;
   const int h = blockIdx.y;
@@ -861,14 +899,16 @@ hipError_t launch_export_rows(const ExportArgs &a, hipStream_t s) {
 
 hipError_t launch_write_blocks(const WriteBlocksArgs &a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  const bool fast = a.pool.head_dim == 128 && a.pool.block_tokens == 16 &&
-                    a.pool.format != kInt8Row &&
-                    reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
+  const bool aligned = reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(a.k_dst) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v_dst) % 16 == 0;
+  const bool fast = a.pool.head_dim == 128 && a.pool.block_tokens == 16 && a.pool.format != kInt8Row && aligned;
+  const bool fast256 = a.pool.head_dim == 256 && a.pool.block_tokens == 16 && is16(a.pool.format) && aligned;
   if (a.pool.format == kInt8Row)
     hipLaunchKernelGGL(write_blocks_row_kernel, dim3(a.n), dim3(256), 0, s, a);
   else if (fast)
     hipLaunchKernelGGL(write_blocks_d128_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
+  else if (fast256)
+    hipLaunchKernelGGL(write_blocks16_d256_kernel, dim3(a.n, a.pool.kv_heads), dim3(512), 0, s, a);
   else
     hipLaunchKernelGGL(write_blocks_kernel, dim3(a.n, a.pool.kv_heads), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -184,15 +184,17 @@ def test_fp8_quantise_on_write_is_bit_exact(ctx):
             assert np.array_equal(v[blk, h], codes.reshape(BT, D).T) and vs[blk, h] == np.float32(s)
 
 
-@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_INT8, llm_hip.KV_FP8_E4M3, llm_hip.KV_F16])
-def test_block_write_vector_and_generic_kernels_agree(ctx, fmt):
-    """head_dim 128 / 16-token blocks from 16-byte aligned rows take the vector
-    kernel; the same rows 2 bytes off alignment take the generic one.  Pools equal."""
+@pytest.mark.parametrize("fmt,head_dim", [(llm_hip.KV_BF16, D), (llm_hip.KV_INT8, D), (llm_hip.KV_FP8_E4M3, D),
+                                          (llm_hip.KV_F16, D), (llm_hip.KV_BF16, 256), (llm_hip.KV_F16, 256)])
+def test_block_write_vector_and_generic_kernels_agree(ctx, fmt, head_dim):
+    """16-token blocks from 16-byte aligned rows take the vector kernels (head_dim 128, every
+    format; head_dim 256, bf16 and fp16); the same rows 2 bytes off alignment take the
+    generic one.  Pools equal."""
     import torch
 
     Hkv = 4
-    batch, pool_fast, ids, sk, sv = write_case(ctx, fmt, [40, 17, 300], Hkv, 500)
-    pool_gen = ctx.pool(fmt, BT, Hkv, D, batch.n_blocks)
+    batch, pool_fast, ids, sk, sv = write_case(ctx, fmt, [40, 17, 300], Hkv, 500, head_dim=head_dim)
+    pool_gen = ctx.pool(fmt, BT, Hkv, head_dim, batch.n_blocks)
 
     def misaligned(a):
         flat = torch.zeros(a.size + 1, dtype=torch.int16, device="cuda")
