@@ -923,6 +923,13 @@ def run_sections(ctx, args, lens, sel) -> list:
                               sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, graph=True, head_dim=256)
         secondary.append(r)
         log(f"Q36 decode: {r}")
+        # kir-ai's step order on the same shape, in one call: the append kernel, then the stream kernel
+        _, r = measure_decode(ctx, "Q36 append + attend in one call (llh_paged_decode_append)", lens, 16, 2,
+                              llm_hip.KV_BF16, sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, fused=True,
+                              head_dim=256)
+        r["decode_alone_us"] = secondary[-1]["us_per_step"]
+        secondary.append(r)
+        log(f"Q36 append+attend: {r}")
     if sel("c2f16"):
         # C2's shape over an fp16 pool (the element type of the reference's Metal KV mirror)
         _, r = measure_decode(ctx, "C2 decode over fp16 blocks", lens, 16, 8, llm_hip.KV_F16, sec_steps, sec_warm,

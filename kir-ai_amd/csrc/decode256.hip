@@ -452,6 +452,78 @@ __device__ __forceinline__ void flush256(const DecodeArgs &a, State256 &st, int 
   reset256(st);
 }
 
+// ---- fused append (llh_paged_decode_append, bf16 pools) ----
+// kir-ai appends the new token, then attends (native_attention.rs:307-329).  Here the
+// wavefront that computes the block receiving the token (its segment's last unit) puts
+// the token's bf16 bits into the registers it loaded that block into and stores them to
+// the token's slot -- a slot no other wavefront reads during the launch -- so the step
+// attends exactly what the append kernel would have stored.  A block entry outside the
+// pool is flagged (as the append kernel flags it) and nothing is written.
+
+// The new token's K at this lane's dims (8c .., 128 + 8c ..) and V at dims 64j + lane
+// (two per word), for sequence b, kv head kvh.
+__device__ __forceinline__ void load_new_k(const DecodeArgs &a, int b, int kvh, int lane, uint4 (&nk)[2]) {
+  const uint16_t *kn = a.k_new + ((size_t)b * a.pool.kv_heads + kvh) * D2 + 8 * (lane & 15);
+  nk[0] = *reinterpret_cast<const uint4 *>(kn);
+  nk[1] = *reinterpret_cast<const uint4 *>(kn + 128);
+}
+__device__ __forceinline__ void load_new_v(const DecodeArgs &a, int b, int kvh, int lane, uint32_t (&nv)[2]) {
+  const uint16_t *vn = a.v_new + ((size_t)b * a.pool.kv_heads + kvh) * D2 + lane;
+  nv[0] = (uint32_t)vn[0] | ((uint32_t)vn[64] << 16);
+  nv[1] = (uint32_t)vn[128] | ((uint32_t)vn[192] << 16);
+}
+// Token off of the block in kr / vr replaced by the new token (lanes of row off / 4 hold
+// its K as kr.k[2 (off % 4)], kr.k[2 (off % 4) + 1]; element off % 8 of vr.v[2j + off / 8]).
+// (Selects on every register, so the arrays stay in registers: an index that is not a
+// compile-time constant would put them in scratch.)
+__device__ __forceinline__ uint4 sel4(bool c, const uint4 &a, const uint4 &b) {
+  return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+__device__ __forceinline__ void patch_new_k(Kregs &kr, const uint4 (&nk)[2], int off, int lane) {
+  const bool row = (lane >> 4) == (off >> 2);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const bool hit = row && i == (off & 3);
+    kr.k[2 * i] = sel4(hit, nk[0], kr.k[2 * i]);
+    kr.k[2 * i + 1] = sel4(hit, nk[1], kr.k[2 * i + 1]);
+  }
+}
+__device__ __forceinline__ void patch_new_v(Vregs &vr, const uint32_t (&nv)[2], int off) {
+  const int word = (off & 7) >> 1, sh = 16 * (off & 1);
+  const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t x = ((nv[j >> 1] >> (16 * (j & 1))) & 0xffffu) << sh;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const bool h = hh == (off >> 3);
+      uint4 &r = vr.v[2 * j + hh];
+      r.x = (h && word == 0) ? ((r.x & keep) | x) : r.x;
+      r.y = (h && word == 1) ? ((r.y & keep) | x) : r.y;
+      r.z = (h && word == 2) ? ((r.z & keep) | x) : r.z;
+      r.w = (h && word == 3) ? ((r.w & keep) | x) : r.w;
+    }
+  }
+}
+// The new token into its pool slot (block phys, kv head kvh, offset off), from the
+// registers the patch used: K from the 16 lanes of row 0 (each holds dims 8c .. and
+// 128 + 8c ..), V from every lane (dims 64j + lane).  Written by the wavefront that
+// computes the block, at the patch, so no other wavefront waits on it.
+__device__ __forceinline__ void store_new_k(const DecodeArgs &a, int phys, int kvh, int off, const uint4 (&nk)[2],
+                                            int lane) {
+  if (lane >= 16) return;
+  char *kb = const_cast<char *>(block_base(a.pool.k, phys, kvh, a.pool.kv_heads)) + off * (D2 * 2) + 16 * lane;
+  *reinterpret_cast<uint4 *>(kb) = nk[0];
+  *reinterpret_cast<uint4 *>(kb + 256) = nk[1];
+}
+__device__ __forceinline__ void store_new_v(const DecodeArgs &a, int phys, int kvh, int off, const uint32_t (&nv)[2],
+                                            int lane) {
+  uint16_t *vb = reinterpret_cast<uint16_t *>(const_cast<char *>(block_base(a.pool.v, phys, kvh, a.pool.kv_heads)));
+#pragma unroll
+  for (int j = 0; j < 4; j++) vb[(64 * j + lane) * BT + off] = (uint16_t)(nv[j >> 1] >> (16 * (j & 1)));
+}
+
+template <bool FUSED>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
@@ -493,11 +565,18 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
   bool valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
   Kregs kr;
   Vregs vr;
+  uint4 nk[2];      // fused: the new token's rows for the unit in kr / vr when it is its segment's last
+  uint32_t nv[2];
   load_k(a, valid ? e : 0, L.kvh, lane, kr);
+  if constexpr (FUSED)
+    if (L.j == L.nb - 1) load_new_k(a, L.b, L.kvh, lane, nk);
   __builtin_amdgcn_sched_barrier(0);  // K before V, as in the loop
   load_v(a, valid ? e : 0, L.kvh, lane, vr);
+  if constexpr (FUSED)
+    if (L.j == L.nb - 1) load_new_v(a, L.b, L.kvh, lane, nv);
   cursor_advance(a, len0, L);
   int e_next = n > 1 ? next_entry() : -1;
+  int cphys = valid ? e : 0;  // the block of unit C
 
   State256 st;
   reset256(st);
@@ -524,28 +603,54 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
   for (int k = 0; k + 1 < n; k++) {
     bad |= !valid;
     uint32_t vm[8];
+    const bool seg_end = C.j == C.nb - 1;  // then unit L starts the next segment
+    const bool cvalid = valid;
+    if constexpr (FUSED)
+      if (seg_end) {
+        patch_new_k(kr, nk, (C.len - 1) % BT, lane);
+        if (cvalid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
+      }
     const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
     valid = e_next >= 0 && (int64_t)e_next < a.pool.n_blocks;
     const int phys = valid ? e_next : 0;
     load_k(a, phys, L.kvh, lane, kr);
-    const bool seg_end = C.j == C.nb - 1;  // then unit L starts the next segment
+    if constexpr (FUSED)
+      if (L.j == L.nb - 1) load_new_k(a, L.b, L.kvh, lane, nk);
     if (seg_end) load_q256(a, (size_t)L.b * a.q_heads + (size_t)L.kvh * G2, lane, qw);
     // nothing of p . v (which waits for V) moves above the K loads
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FUSED)
+      if (seg_end) {
+        patch_new_v(vr, nv, (C.len - 1) % BT);
+        if (cvalid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
+      }
     block_accumulate(vr, wp, vm, st);
     if (seg_end) {
       end_segment(seg_from_start);
       seg_from_start = true;
     }
     load_v(a, phys, L.kvh, lane, vr);
+    if constexpr (FUSED)
+      if (L.j == L.nb - 1) load_new_v(a, L.b, L.kvh, lane, nv);
     cursor_advance(a, len0, L);
     e_next = k + 2 < n ? next_entry() : -1;
     cursor_advance(a, len0, C);
+    cphys = phys;
   }
   bad |= !valid;
   {
     uint32_t vm[8];
+    if constexpr (FUSED)
+      if (C.j == C.nb - 1) {
+        patch_new_k(kr, nk, (C.len - 1) % BT, lane);
+        if (valid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
+      }
     const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
+    if constexpr (FUSED)
+      if (C.j == C.nb - 1) {
+        patch_new_v(vr, nv, (C.len - 1) % BT);
+        if (valid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
+      }
     block_accumulate(vr, wp, vm, st);
   }
   // the range ends with the segment (complete if it also began here) or inside it
@@ -621,7 +726,10 @@ __global__ __launch_bounds__(D2) void decode_stream_merge_d256_kernel(const Deco
 hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   if (a.stream_wgs > 0) {
     if (hook) hook(hu, 0, s);
-    hipLaunchKernelGGL(paged_decode_d256_stream_kernel, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+    if (a.k_new)
+      hipLaunchKernelGGL(paged_decode_d256_stream_kernel<true>, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL(paged_decode_d256_stream_kernel<false>, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (hook) hook(hu, 1, s);
     if (e != hipSuccess) return e;

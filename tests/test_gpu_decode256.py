@@ -180,8 +180,9 @@ def test_decode256_noalloc_matches_decode(ctx, opts):
 
 
 def test_decode256_append_then_attend(ctx, d256_kernel):
-    """llh_paged_decode_append at head_dim 256: the append kernel, then this kernel; the
-    pool holds the new rows and the output matches the oracle on that pool."""
+    """llh_paged_decode_append at head_dim 256 (split-K: the append kernel, then this kernel;
+    stream: one launch): the pool holds the new rows and the output matches the oracle on
+    that pool."""
     lens = np.array([1, 17, 256, 999, 4096], np.int32)
     batch, pool, q = case(ctx, lens, 110)
     kn = oracle.normal_bf16(111, lens.size * HKV * D).reshape(lens.size, HKV, D)
@@ -195,6 +196,37 @@ def test_decode256_append_then_attend(ctx, d256_kernel):
         assert np.array_equal(k[blk, :, p % BT, :], kn[b])
     ref = oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D)
     assert_parity(out, ref, what="append + attend")
+
+
+@pytest.mark.parametrize("window", [0, 100])
+def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window):
+    """llh_paged_decode_append at head_dim 256 in one launch (the stream kernel writes the new
+    token's rows to their slot and attends them from the registers of the block it loads):
+    the pool and the output are bit-identical to llh_kv_append followed by llh_paged_decode
+    on the same kernel; under the split-K option the call appends through the append kernel."""
+    import torch
+
+    lens = workloads.uniform_lengths(24, 256, 4096, 120)
+    lens[:8] = [1, 2, 15, 16, 17, 256, 999, 4096]
+    batch, pool_two, q = case(ctx, lens, 121)
+    _, pool_one, _ = case(ctx, lens, 121)
+    kn = oracle.normal_bf16(122, lens.size * HKV * D).reshape(lens.size, HKV, D)
+    vn = oracle.normal_bf16(123, lens.size * HKV * D).reshape(lens.size, HKV, D)
+    slots = np.array([int(batch.tables[b, (int(L) - 1) // BT]) * BT + (int(L) - 1) % BT for b, L in enumerate(lens)],
+                     np.int64)
+    ctx.append(pool_two, to_dev(slots), to_dev(kn), to_dev(vn))
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(D)
+    out_two = run(ctx, pool_two, batch, q, window, scale)
+    fused0 = ctx.metrics()["fused_append_calls"]
+    out_one = run(ctx, pool_one, batch, q, window, scale, fn="append", kv_new=(kn, vn))
+    assert ctx.metrics()["fused_append_calls"] - fused0 == (1 if d256_kernel == "stream" else 0)
+    a, b = pool_two.raw(), pool_one.raw()
+    for key in a:
+        assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(out_one, out_two)
+    ref = oracle_decode(pool_one, batch, llm_hip.KV_BF16, HQ, HKV, window, q, scale, head_dim=D)
+    assert_parity(out_one, ref, what=f"fused append + attend W={window}")
 
 
 def coded_case(ctx, lens, seed, code_base):
