@@ -14,7 +14,7 @@ import pytest
 
 import llm_hip
 import oracle
-from attended_set import check_decode, coded_rows
+from attended_set import check_decode, code, coded_rows
 from helpers import assert_parity, from_dev_bf16, to_dev
 from llm_hip import workloads
 from test_gpu_decode import build_case, oracle_decode
@@ -252,6 +252,38 @@ def test_decode256_attended_set(ctx, d256_kernel, code_base, window):
     q = np.zeros(lens.size * HQ * D, np.uint16)
     out = run(ctx, pool, batch, q, window, 0.0625)
     check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 W={window}", head_dim=D, code_base=code_base)
+
+
+@pytest.mark.parametrize("window", [0, 17, 1000])
+def test_decode256_fused_append_attended_set(ctx, d256_kernel, window):
+    """llh_paged_decode_append at head_dim 256 with q = 0 and position-coded V: the step
+    attends the pool's [lo, len - 1) plus the new token from the call's rows -- the stale
+    slot holds a decoy code (its code + 64), so attending it instead is caught -- and the
+    slot holds the new token afterwards (a plain decode counts the same set)."""
+    import torch
+
+    code_base = 2
+    lens = workloads.uniform_lengths(32, 256, 4096, 130)
+    lens[:8] = [1, 15, 16, 17, 33, 4096, 5000, 8191]
+    batch, pool = coded_case(ctx, lens, 131, code_base)
+    B = lens.size
+    pos = lens.astype(np.int64) - 1
+    decoy = np.zeros((B, HKV, D), np.uint16)
+    new_v = np.zeros((B, HKV, D), np.uint16)
+    for b, p in enumerate(pos):
+        for h in range(HKV):
+            decoy[b, h, (code(p, code_base + h) + 64) % 128] = 0x3F80
+            new_v[b, h, code(p, code_base + h)] = 0x3F80
+    slots = np.array([int(batch.tables[b, p // BT]) * BT + p % BT for b, p in enumerate(pos)], np.int64)
+    ctx.append(pool, to_dev(slots), to_dev(oracle.normal_bf16(132, B * HKV * D).reshape(B, HKV, D)), to_dev(decoy))
+    torch.cuda.synchronize()
+    kn = oracle.normal_bf16(133, B * HKV * D).reshape(B, HKV, D)
+    q = np.zeros(B * HQ * D, np.uint16)
+    out = run(ctx, pool, batch, q, window, 0.0625, fn="append", kv_new=(kn, new_v))
+    check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 fused append W={window}", head_dim=D, code_base=code_base)
+    out = run(ctx, pool, batch, q, window, 0.0625)
+    check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 decode after the append W={window}", head_dim=D,
+                 code_base=code_base)
 
 
 def test_decode256_other_shapes_stay_generic(ctx):
