@@ -855,7 +855,7 @@ def traffic_from_profile(kernel: str):
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
 SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "q36", "neighbours", "trait", "c3", "c4prefill",
-            "c3int8", "c3fp8", "q36prefill", "c2f16", "c3f16")
+            "c3int8", "c3fp8", "q36prefill", "c2f16", "c3f16", "q36prefillf16")
 
 
 def run_sections(ctx, args, lens, sel) -> list:
@@ -952,7 +952,8 @@ def run_sections(ctx, args, lens, sel) -> list:
             ("c3f16", "C3 prefill over fp16 blocks", 8, 1536, 512, 32, 4, 0, None, llm_hip.KV_F16, D),
             # Qwen3.6 full-attention layer (Hq16 / Hkv2, head_dim 256) on C3's chunking: the head_dim-256 kernel
             ("q36prefill", "Q36 prefill 8x(1536+512) Hq16/Hkv2 D=256", 8, 1536, 512, 16, 2, 0, None, llm_hip.KV_BF16,
-             256)):
+             256),
+            ("q36prefillf16", "Q36 prefill over fp16 blocks", 8, 1536, 512, 16, 2, 0, None, llm_hip.KV_F16, 256)):
         if not sel(key):
             continue
         step, flops, keep = prefill_case(ctx, B, prefix, chunk, Hq, Hkv, window, workloads.SEED_BASE + 2, res, fmt,

@@ -966,13 +966,14 @@ int llh_paged_prefill(llh_ctx *ctx, const llh_kv_pool *pool, const llh_prefill_d
     return ctx->fail(LLH_ERR_INVALID_SHAPE, "prefill q and output must be bf16-aligned (2 bytes)");
   if (!std::isfinite(score_scale)) return ctx->fail(LLH_ERR_NON_FINITE, "score scale must be finite");
   // the tuned MFMA kernels take 16-token blocks and 16-byte aligned rows at head_dim
-  // 128 (bf16, int8, fp8, fp16 pools) and 256 (bf16); every other call runs the
+  // 128 (bf16, int8, fp8, fp16 pools) and 256 (bf16, fp16); every other call runs the
   // element-wise kernel
   const bool tuned_shape = pv.block_tokens == kFastBlockTokens &&
                            ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_out)) & 15) == 0 &&
                            ctx->opt(LLH_OPT_FORCE_GENERIC) == 0;
   const bool fast = tuned_shape && pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim;
-  const bool fast256 = tuned_shape && pv.format == LLH_KV_BF16 && pv.head_dim == kD256HeadDim;
+  const bool fast256 =
+      tuned_shape && (pv.format == LLH_KV_BF16 || pv.format == LLH_KV_F16) && pv.head_dim == kD256HeadDim;
   PrefillArgs a{};
   a.pool = pv;
   a.q = static_cast<const uint16_t *>(d_q);

@@ -23,6 +23,7 @@
 // 32-key step s takes keys {32s + 4g .. +4, 32s + 16 + 4g .. +4} in its k-slots
 // 8g..8g+7; the V^T operand reads the same keys (one 16-byte LDS read).
 #include "device_common.h"
+#include "wave_ops.h"
 
 namespace llh {
 
@@ -49,16 +50,18 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // round to nearest even
-}
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 
+// 16x16x32 MFMA on packed 16-bit operands: fp16 for fp16 pools (OP = kF16), else bf16
+template <int OP>
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                  0, 0, 0);
+  if constexpr (OP == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
 }
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Scheduling order for a region of N LDS reads feeding N MFMAs: AHEAD reads,
 // then one MFMA and one read at a time, then the last AHEAD MFMAs -- so AHEAD
@@ -90,11 +93,6 @@ __device__ __forceinline__ float row_max4(float v) {
 __device__ __forceinline__ float row_sum4(float v) {
   v += __shfl_xor(v, 16);
   return v + xor32_other(v);
-}
-
-__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair),
-                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
 }
 
 // V^T in LDS, per 32-key step s (blocks 2s, 2s+1): a 64-byte row per dim holding,
@@ -177,6 +175,7 @@ __device__ __forceinline__ void store_tile(uint16_t *k_lds, uint16_t *v_lds, int
   }
 }
 
+template <int FMT>
 __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const PrefillArgs a) {
   // ---- XCD-aware logical work item (as the head_dim-128 kernel) ----
   const int Hq = a.q_heads;
@@ -237,6 +236,25 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
       qb[ks] = t;
     }
   }
+  // fp16 pools: the row's q in fp16, scaled by 2^-e over its 256 dims (held by lanes
+  // r, r + 16, r + 32, r + 48); its scores carry the step 2^e
+  float qstep = 1.0f;
+  if constexpr (FMT == kF16) {
+    uint32_t w[32];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) w[4 * ks + e] = qb[ks][e];
+    int mx = bf16_absmax_bits<32>(w);
+    mx = max(mx, __shfl_xor(mx, 16));
+    mx = max(mx, __float_as_int(xor32_other(__int_as_float(mx))));
+    const F16Scaling sc = f16_scaling(mx);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) qb[ks][e] = bf16x2_to_f16x2(w[4 * ks + e], sc.inv);
+    qstep = sc.step;
+  }
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][K_TILE];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][V_TILE];
@@ -285,13 +303,13 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
 #pragma unroll
         for (int kb = 0; kb < KBLK; kb++) {
           const u32x4_t ka = *reinterpret_cast<const u32x4_t *>(&kl[(kb * BT + r) * D + (((ks * 4 + g) ^ r) * 8)]);
-          sacc[kb] = mfma16(ka, qb[ks], sacc[kb]);
+          sacc[kb] = mfma16<FMT>(ka, qb[ks], sacc[kb]);
         }
       reads_ahead_of_mfma<KBLK * 8, PF_S>();
 
       // ---- scale, mask, online softmax (as the head_dim-128 kernel) ----
       const bool need_mask = (kt + BN - 1 > wpos_first) || (kt < wlo_last) || (kt + BN > ctx);
-      const float c = a.scale_log2e;
+      const float c = a.scale_log2e * qstep;
       float c_exp = c;
       float tmax = -INFINITY;
       if (need_mask) {
@@ -358,9 +376,10 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
           p[i] = fast_exp2(__builtin_fmaf(sacc[2 * s][i], c_exp, -mref));
           p[4 + i] = fast_exp2(__builtin_fmaf(sacc[2 * s + 1][i], c_exp, -mref));
         }
-        pb[s] = u32x4_t{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+        pb[s] = u32x4_t{pack_16<FMT>(p[0], p[1]), pack_16<FMT>(p[2], p[3]), pack_16<FMT>(p[4], p[5]),
+                        pack_16<FMT>(p[6], p[7])};
 #pragma unroll
-        for (int e = 0; e < 4; e++) psum = dot2_ones(pb[s][e], psum);
+        for (int e = 0; e < 4; e++) psum = dot2_ones_16<FMT>(pb[s][e], psum);
       }
       l_run += psum;
 
@@ -370,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
 #pragma unroll
         for (int db = 0; db < 16; db++) {
           const u32x4_t va = *reinterpret_cast<const u32x4_t *>(&vl[s * V_STEP + (db * 16 + r) * V_ROW + vsw]);
-          oacc[db] = mfma16(va, pb[s], oacc[db]);
+          oacc[db] = mfma16<FMT>(va, pb[s], oacc[db]);
         }
       }
       reads_ahead_of_mfma<2 * 16, PF_V>();
@@ -402,7 +421,10 @@ __global__ __launch_bounds__(kThreads, 1) void paged_prefill_d256_kernel(const P
 hipError_t launch_prefill_d256(const PrefillArgs &a, hipStream_t s) {
   const int n_items = a.q_tiles * a.q_heads * a.num_seqs;
   const int grid = (n_items + 7) / 8 * 8;
-  hipLaunchKernelGGL(paged_prefill_d256_kernel, dim3(grid), dim3(kThreads), 0, s, a);
+  if (a.pool.format == kF16)
+    hipLaunchKernelGGL(paged_prefill_d256_kernel<kF16>, dim3(grid), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(paged_prefill_d256_kernel<kBf16>, dim3(grid), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -23,10 +23,11 @@ BT = 16
 HQ, HKV = 16, 2
 
 
-def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=False):
+def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=False, fmt=llm_hip.KV_BF16):
     """Prefill of `chunk` rows after `prefix` cached ones per sequence; returns (out, ref) with
     ref None for the coded probe (q = 0, V one-hot position codes); q scaled by
-    helpers.magnitude_rows with q_magnitudes."""
+    helpers.magnitude_rows with q_magnitudes; fmt: the pool's element type (bf16 or fp16,
+    the rows rounded to it on write)."""
     import torch
 
     ctxlen = [p + c for p, c in zip(prefix, chunk)]
@@ -36,7 +37,7 @@ def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=
         _, sv = workloads.block_sources(batch, lambda b, lo, hi: coded_rows(lo, hi, HKV, D, 2), HKV, D)
     else:
         _, sv = workloads.block_sources(batch, lambda b, lo, hi: rows_bf16(seed + 2, b, lo, hi, HKV, D), HKV, D)
-    pool = ctx.pool(llm_hip.KV_BF16, BT, HKV, D, batch.n_blocks)
+    pool = ctx.pool(fmt, BT, HKV, D, batch.n_blocks)
     ctx.write_blocks(pool, to_dev(ids), to_dev(sk), to_dev(sv))
     starts = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
     T = int(starts[-1])
@@ -56,7 +57,7 @@ def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=
     assert ctx.metrics()["generic_prefill_calls"] == before, "the element-wise kernel ran"
     if coded:
         return from_dev_bf16(out), (starts, batch.seq_lens)
-    opool = oracle.Pool.from_raw(llm_hip.KV_BF16, BT, HKV, D, batch.n_blocks, pool.raw())
+    opool = oracle.Pool.from_raw(fmt, BT, HKV, D, batch.n_blocks, pool.raw())
     st, ref = opool.prefill(HQ, starts, batch.seq_lens, batch.tables, window, q, scale, threads=16)
     assert st == oracle.OK
     if gate:
@@ -64,12 +65,14 @@ def run(ctx, prefix, chunk, window, seed, gate=False, coded=False, q_magnitudes=
     return from_dev_bf16(out), ref
 
 
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_F16])
 @pytest.mark.parametrize("window", [0, 90])
-def test_prefill256_ragged_full_oracle(ctx, window):
+def test_prefill256_ragged_full_oracle(ctx, window, fmt):
     """Ragged chunks (an empty one, one of a single row, one past a tile) over prefixes of
-    0 .. 1536 tokens, every row against the oracle."""
-    out, ref = run(ctx, [0, 300, 1000, 1536, 7], [130, 64, 257, 17, 0], window, 41 + window)
-    assert_parity(out, ref, what=f"prefill d256 W={window}")
+    0 .. 1536 tokens, every row against the oracle; bf16 and fp16 pools (fp16: both products
+    on the fp16 MFMA, each query row scaled into fp16 by its own power of two)."""
+    out, ref = run(ctx, [0, 300, 1000, 1536, 7], [130, 64, 257, 17, 0], window, 41 + window, fmt=fmt)
+    assert_parity(out, ref, what=f"prefill d256 W={window} fmt={fmt}")
 
 
 @pytest.mark.parametrize("window", [0, 64])
@@ -81,11 +84,13 @@ def test_prefill256_tile_boundaries(ctx, window):
     assert_parity(out, ref, what=f"prefill d256 tile boundaries W={window}")
 
 
-def test_prefill256_query_magnitudes(ctx):
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_F16])
+def test_prefill256_query_magnitudes(ctx, fmt):
     """Query rows from bf16 subnormal to 1e30 (scores to ~1e31 in log2 units): tiles whose
-    scaled max passes 2^26 scale their scores before the exponent."""
-    out, ref = run(ctx, [300, 0], [200, 129], 0, 95, q_magnitudes=True)
-    assert_parity(out, ref, what="prefill d256 query magnitudes")
+    scaled max passes 2^26 scale their scores before the exponent; over fp16 blocks each row's
+    power-of-two scaling keeps q in fp16's range."""
+    out, ref = run(ctx, [300, 0], [200, 129], 0, 95, q_magnitudes=True, fmt=fmt)
+    assert_parity(out, ref, what=f"prefill d256 query magnitudes fmt={fmt}")
 
 
 def test_prefill256_qwen36_chunk(ctx):
@@ -100,7 +105,8 @@ def test_prefill256_gate(ctx, window):
     assert_parity(out, ref, what=f"gated prefill d256 W={window}")
 
 
+@pytest.mark.parametrize("fmt", [llm_hip.KV_BF16, llm_hip.KV_F16])
 @pytest.mark.parametrize("window", [0, 1, 17, 100])
-def test_prefill256_attended_set(ctx, window):
-    out, (starts, lens) = run(ctx, [100, 1000, 0], [37, 200, 129], window, 45, coded=True)
+def test_prefill256_attended_set(ctx, window, fmt):
+    out, (starts, lens) = run(ctx, [100, 1000, 0], [37, 200, 129], window, 45, coded=True, fmt=fmt)
     check_prefill(out, starts, lens, window, HQ, HKV, 1.0, f"prefill d256 W={window}", head_dim=D, code_base=2)
