@@ -727,6 +727,9 @@ def summarize(root: str) -> int:
         "c5fp8": {"paged_decode_stream_kernel": ("B", decode_bytes([8192] * 64, 32, 8, 2))},
         "c2f16": {"paged_decode_stream_kernel": ("B", decode_bytes(c2lens, 16, 8, 4))},
         "c3f16": {"paged_prefill_kernel": ("F", prefill_flops(8, 1536, 512, 32, 0))},
+        "q36f16": {"paged_decode_d256_stream_kernel": ("B", decode_bytes(c2lens, 16, 2, 4, 0, 256)),
+                   "paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 4, 0, 256))},
+        "q36prefillf16": {"paged_prefill_d256_kernel": ("F", prefill_flops(8, 1536, 512, 16, 0, 256))},
         "q36": {"paged_decode_d256_stream_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256)),
                 "paged_decode_d256_kernel": ("B", decode_bytes(c2lens, 16, 2, 0, 0, 256))},
         "q36prefill": {"paged_prefill_d256_kernel": ("F", prefill_flops(8, 1536, 512, 16, 0, 256))},
@@ -744,7 +747,8 @@ def summarize(root: str) -> int:
         ("decode_c5_int8_fp8.md", "Quantized-KV decode, C5 (B=64, L=8192, Hq32/Hkv8): int8 (fp16 per (token, head) "
                                   "scales) and fp8 e4m3 (per (block, head) scales)", ("c5int8", "c5fp8")),
         ("f16_kv.md", "fp16 KV pools (the reference's Metal mirror dtype): decode on C2 (B=32, L~U[256,4096], "
-                      "Hq16/Hkv8) and prefill on C3 (8 x (1536 + 512), Hq32/Hkv4)", ("c2f16", "c3f16")),
+                      "Hq16/Hkv8) and prefill on C3 (8 x (1536 + 512), Hq32/Hkv4); the Qwen3.6 head_dim-256 shape "
+                      "(Hq16/Hkv2) on the same lengths", ("c2f16", "c3f16", "q36f16", "q36prefillf16")),
         ("decode_q36_d256.md", "Paged GQA decode at head_dim 256, the Qwen3.6 full-attention shape (Hq16/Hkv2, "
                                "bf16 KV): decode on C2's lengths (B=32, L~U[256,4096]) and prefill on C3's chunking "
                                "(8 x (1536 + 512))", ("q36", "q36prefill")),
@@ -855,7 +859,7 @@ def traffic_from_profile(kernel: str):
 
 # sections of the secondary measurements (--only runs one, for a profiler run)
 SECTIONS = ("c1", "c2", "c2append", "c2fused", "c4", "c5int8", "c5fp8", "q36", "neighbours", "trait", "c3", "c4prefill",
-            "c3int8", "c3fp8", "q36prefill", "c2f16", "c3f16", "q36prefillf16")
+            "c3int8", "c3fp8", "q36prefill", "c2f16", "c3f16", "q36f16", "q36prefillf16")
 
 
 def run_sections(ctx, args, lens, sel) -> list:
@@ -936,6 +940,13 @@ def run_sections(ctx, args, lens, sel) -> list:
                               seed=workloads.SEED_BASE + 1)
         secondary.append(r)
         log(f"C2 f16: {r}")
+        torch.cuda.empty_cache()
+    if sel("q36f16"):
+        # the Qwen3.6 full-attention shape over an fp16 pool: the head_dim-256 kernel, fp16 instance
+        _, r = measure_decode(ctx, "Q36 decode over fp16 blocks", lens, 16, 2, llm_hip.KV_F16, sec_steps, sec_warm,
+                              seed=workloads.SEED_BASE + 5, graph=True, head_dim=256)
+        secondary.append(r)
+        log(f"Q36 f16: {r}")
         torch.cuda.empty_cache()
     if sel("neighbours"):
         secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))

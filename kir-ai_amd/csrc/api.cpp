@@ -634,8 +634,9 @@ int llh::plan_decode(llh_ctx *ctx, const llh_kv_pool *pool, const llh_decode_des
   plan->fast = pv.format != LLH_KV_INT8_ROW && pv.head_dim == kFastHeadDim && pv.block_tokens == kFastBlockTokens &&
                rows_aligned &&
                (group == 1 || group == 2 || group == 4 || group == 8) && !ctx->opt(LLH_OPT_FORCE_GENERIC);
-  // head_dim 256 (Qwen3.5 / 3.6 full attention: Hq16 / Hkv2): bf16 pools, G = 8
-  plan->d256 = pv.format == LLH_KV_BF16 && pv.head_dim == kD256HeadDim && pv.block_tokens == kFastBlockTokens &&
+  // head_dim 256 (Qwen3.5 / 3.6 full attention: Hq16 / Hkv2): bf16 or fp16 pools, G = 8
+  plan->d256 = (pv.format == LLH_KV_BF16 || pv.format == LLH_KV_F16) && pv.head_dim == kD256HeadDim &&
+               pv.block_tokens == kFastBlockTokens &&
                rows_aligned && group == kD256Group && !ctx->opt(LLH_OPT_FORCE_GENERIC);
   if (plan->d256) {
     plan->fast = true;

@@ -1,7 +1,8 @@
 // Paged GQA decode attention for head_dim 256 on gfx950 (MI355X): the
 // full-attention layers of Qwen3.5 / 3.6 (fixtures/qwen36/config.json: 16 query
-// heads, 2 kv heads, head_dim 256, so G = 8 query heads per kv head), bf16 K/V in
-// 16-token blocks.  Same contract as the head_dim-128 kernels in decode.hip: per
+// heads, 2 kv heads, head_dim 256, so G = 8 query heads per kv head), bf16 or fp16
+// K/V in 16-token blocks (fp16: each head's q is scaled into fp16 by a power of two
+// chosen from its largest magnitude, undone on the scores).  Same contract as the head_dim-128 kernels in decode.hip: per
 // sequence b and query head h,
 //   out[b][h] = sum_t softmax_t(scale * q[b][h] . K[t][kv]) V[t][kv]
 // over the attended positions [lo, len) (crates/llm-backend/src/core/
@@ -30,7 +31,8 @@
 //      4g + 2 (c % 2) + {0, 1}, each computed once per wavefront.
 //   V: lane owns dims 64 j + lane (j = 0..3), all 16 tokens (two 16-byte
 //      loads per dim row): no two lanes accumulate the same output element.
-//   The 64 packed bf16 weight pairs (8 heads x 8 token pairs, one per lane)
+//   The 64 packed weight pairs (8 heads x 8 token pairs, one per lane, in the pool's
+//   16-bit format)
 //   reach every lane as scalar registers (v_readlane), the scalar operand of
 //   p . v's dot2 instructions.
 // Running max / sum live in the 8 lanes that score a head; outputs in
@@ -103,9 +105,12 @@ struct State256 {
 // sequence (positions 16 jb ..); valid: its table entry is inside the pool.
 // Returns this lane's packed weight pair (head fold(c), tokens 4g + 2 (c % 2) + {0, 1})
 // and, per token pair, the mask that zeroes V of unattended tokens.
+// FMT: kBf16, or kF16 (fp16 blocks, q scaled per head into fp16 by prep_q256_f16; qstep
+// is this lane's head's step, folded into the score scale).
+template <int FMT>
 __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kregs &kr, bool valid, int jb, int lo,
                                                  int len, int lane, const uint32_t (&qw)[G2][8], State256 &st,
-                                                 uint32_t (&vm)[8]) {
+                                                 uint32_t (&vm)[8], float qstep) {
   const int g = lane >> 4;
   const int b0 = lane & 1;
   // ---- partial q . k: slot s, token 4g + i, over this lane's 16 dims ----
@@ -115,14 +120,14 @@ __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kreg
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint4 lo4 = kr.k[2 * i], hi4 = kr.k[2 * i + 1];
-      float acc = dot2_bf16(lo4.x, qw[s][0], 0.0f);
-      acc = dot2_bf16(lo4.y, qw[s][1], acc);
-      acc = dot2_bf16(lo4.z, qw[s][2], acc);
-      acc = dot2_bf16(lo4.w, qw[s][3], acc);
-      acc = dot2_bf16(hi4.x, qw[s][4], acc);
-      acc = dot2_bf16(hi4.y, qw[s][5], acc);
-      acc = dot2_bf16(hi4.z, qw[s][6], acc);
-      acc = dot2_bf16(hi4.w, qw[s][7], acc);
+      float acc = dot2_16<FMT>(lo4.x, qw[s][0], 0.0f);
+      acc = dot2_16<FMT>(lo4.y, qw[s][1], acc);
+      acc = dot2_16<FMT>(lo4.z, qw[s][2], acc);
+      acc = dot2_16<FMT>(lo4.w, qw[s][3], acc);
+      acc = dot2_16<FMT>(hi4.x, qw[s][4], acc);
+      acc = dot2_16<FMT>(hi4.y, qw[s][5], acc);
+      acc = dot2_16<FMT>(hi4.z, qw[s][6], acc);
+      acc = dot2_16<FMT>(hi4.w, qw[s][7], acc);
       p[s][i] = acc;
     }
   // ---- reduce-scatter over the row (see fold) ----
@@ -142,6 +147,7 @@ __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kreg
     const float keep = b0 ? p[0][2 + k] : p[0][k];
     const float send = b0 ? p[0][k] : p[0][2 + k];
     sc[k] = (keep + dpp<0xB1>(send)) * a.scale_log2e;  // quad_perm [1,0,3,2]
+    if constexpr (FMT == kF16) sc[k] *= qstep;
   }
   // ---- mask: tokens outside [lo, len) or in a block outside the pool ----
   const bool partial = (jb * BT < lo) || (jb * BT + BT > len) || !valid;
@@ -180,13 +186,14 @@ __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kreg
     }
   }
   const float mref = (st.m == -INFINITY) ? 0.0f : st.m;
-  const uint32_t w = pack_bf16(fast_exp2(sc[0] - mref), fast_exp2(sc[1] - mref));
-  st.l = dot2_ones(w, st.l);  // the normaliser sums exactly the bf16 weights that enter p . v
+  const uint32_t w = pack_16<FMT>(fast_exp2(sc[0] - mref), fast_exp2(sc[1] - mref));
+  st.l = dot2_ones_16<FMT>(w, st.l);  // the normaliser sums exactly the bf16 weights that enter p . v
   return w;
 }
 
 // Second half: p . v over this lane's 4 dims for every head, head h's weights as
 // scalars read from the lanes that hold them.
+template <int FMT>
 __device__ __forceinline__ void block_accumulate(const Vregs &vr, uint32_t w, const uint32_t (&vm)[8], State256 &st) {
   uint32_t vv[4][8];
 #pragma unroll
@@ -211,7 +218,7 @@ __device__ __forceinline__ void block_accumulate(const Vregs &vr, uint32_t w, co
     for (int j = 0; j < 4; j++) {
       float acc = st.o[h][j];
 #pragma unroll
-      for (int t = 0; t < 8; t++) acc = dot2_bf16(vv[j][t], sw[t], acc);
+      for (int t = 0; t < 8; t++) acc = dot2_16<FMT>(vv[j][t], sw[t], acc);
       st.o[h][j] = acc;
     }
   }
@@ -229,6 +236,45 @@ __device__ __forceinline__ void load_q256(const DecodeArgs &a, size_t qrow0, int
     qw[s][0] = x.x, qw[s][1] = x.y, qw[s][2] = x.z, qw[s][3] = x.w;
     qw[s][4] = y.x, qw[s][5] = y.y, qw[s][6] = y.z, qw[s][7] = y.w;
   }
+}
+
+// fp16 blocks: q of each head scaled into fp16 by its own power of two over its 256
+// dims (f16_scaling); lane c holds head s ^ fold(c) in slot s, so each head's maximum
+// is gathered by selects and a row reduction.  Returns the step of the head this lane
+// scores (fold(c)), which multiplies its scores.
+__device__ __forceinline__ float prep_q256_f16(uint32_t (&qw)[G2][8], int lane) {
+  const int fc = fold(lane & 15);
+  int mxs[G2];  // per slot
+#pragma unroll
+  for (int s = 0; s < G2; s++) mxs[s] = bf16_absmax_bits<8>(qw[s]);
+  float inv[G2], step[G2];  // per head
+#pragma unroll
+  for (int h = 0; h < G2; h++) {
+    const int x = h ^ fc;  // this lane's slot of head h
+    int m = mxs[0];
+#pragma unroll
+    for (int s = 1; s < G2; s++) m = x == s ? mxs[s] : m;
+    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x140, 0xF, 0xF, false));  // row_mirror
+    const F16Scaling sc = f16_scaling(m);
+    inv[h] = sc.inv;
+    step[h] = sc.step;
+  }
+  float my_step = step[0];
+#pragma unroll
+  for (int h = 1; h < G2; h++) my_step = fc == h ? step[h] : my_step;
+#pragma unroll
+  for (int s = 0; s < G2; s++) {
+    const int hs = s ^ fc;  // the head of slot s
+    float iv = inv[0];
+#pragma unroll
+    for (int h = 1; h < G2; h++) iv = hs == h ? inv[h] : iv;
+#pragma unroll
+    for (int k = 0; k < 8; k++) qw[s][k] = bf16x2_to_f16x2(qw[s][k], iv);
+  }
+  return my_step;
 }
 
 __device__ __forceinline__ void reset256(State256 &st) {
@@ -249,6 +295,7 @@ __device__ __forceinline__ void seq_range256(const DecodeArgs &a, int b, int &le
   n_splits = (n_blk + a.split_blocks - 1) / a.split_blocks;
 }
 
+template <int FMT>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(const DecodeArgs a) {
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -285,6 +332,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
 
   uint32_t qw[G2][8];
   load_q256(a, qrow0, lane, qw);
+  float qstep = 1.0f;
+  if constexpr (FMT == kF16) qstep = prep_q256_f16(qw, lane);
   State256 st;
   reset256(st);
 
@@ -309,20 +358,20 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
     for (; k + 1 < nbw; k++) {
       bad |= !valid;
       uint32_t vm[8];
-      const uint32_t w = block_scores(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm);
+      const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, qstep);
       e = entry(k + 1);
       valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
       phys = valid ? e : 0;
       load_k(a, phys, kvh, lane, kr);
       // nothing of p . v (which waits for V) moves above the K loads
       __builtin_amdgcn_sched_barrier(0);
-      block_accumulate(vr, w, vm, st);
+      block_accumulate<FMT>(vr, w, vm, st);
       load_v(a, phys, kvh, lane, vr);
     }
     bad |= !valid;
     uint32_t vm[8];
-    const uint32_t w = block_scores(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm);
-    block_accumulate(vr, w, vm, st);
+    const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, qstep);
+    block_accumulate<FMT>(vr, w, vm, st);
     if (bad && lane == 0) atomicOr(a.err, kErrBadBlock);
   }
 
@@ -523,7 +572,7 @@ __device__ __forceinline__ void store_new_v(const DecodeArgs &a, int phys, int k
   for (int j = 0; j < 4; j++) vb[(64 * j + lane) * BT + off] = (uint16_t)(nv[j >> 1] >> (16 * (j & 1)));
 }
 
-template <bool FUSED>
+template <int FMT, bool FUSED>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   // wave-uniform (readfirstlane): the partition, cursors and branches stay scalar
@@ -561,6 +610,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
   };
   uint32_t qw[G2][8];
   load_q256(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G2, lane, qw);
+  float qstep = 1.0f;
+  bool q_new = true;  // fp16: qw holds a segment's bf16 q not yet scaled
   int e = next_entry();
   bool valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
   Kregs kr;
@@ -610,13 +661,21 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
         patch_new_k(kr, nk, (C.len - 1) % BT, lane);
         if (cvalid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
       }
-    const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
+    if constexpr (FMT == kF16)
+      if (q_new) {
+        qstep = prep_q256_f16(qw, lane);
+        q_new = false;
+      }
+    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, qstep);
     valid = e_next >= 0 && (int64_t)e_next < a.pool.n_blocks;
     const int phys = valid ? e_next : 0;
     load_k(a, phys, L.kvh, lane, kr);
     if constexpr (FUSED)
       if (L.j == L.nb - 1) load_new_k(a, L.b, L.kvh, lane, nk);
-    if (seg_end) load_q256(a, (size_t)L.b * a.q_heads + (size_t)L.kvh * G2, lane, qw);
+    if (seg_end) {
+      load_q256(a, (size_t)L.b * a.q_heads + (size_t)L.kvh * G2, lane, qw);
+      q_new = true;
+    }
     // nothing of p . v (which waits for V) moves above the K loads
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (FUSED)
@@ -624,7 +683,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
         patch_new_v(vr, nv, (C.len - 1) % BT);
         if (cvalid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
       }
-    block_accumulate(vr, wp, vm, st);
+    block_accumulate<FMT>(vr, wp, vm, st);
     if (seg_end) {
       end_segment(seg_from_start);
       seg_from_start = true;
@@ -645,13 +704,18 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
         patch_new_k(kr, nk, (C.len - 1) % BT, lane);
         if (valid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
       }
-    const uint32_t wp = block_scores(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm);
+    if constexpr (FMT == kF16)
+      if (q_new) {
+        qstep = prep_q256_f16(qw, lane);
+        q_new = false;
+      }
+    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, qstep);
     if constexpr (FUSED)
       if (C.j == C.nb - 1) {
         patch_new_v(vr, nv, (C.len - 1) % BT);
         if (valid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
       }
-    block_accumulate(vr, wp, vm, st);
+    block_accumulate<FMT>(vr, wp, vm, st);
   }
   // the range ends with the segment (complete if it also began here) or inside it
   end_segment(C.j == C.nb - 1 && seg_from_start);
@@ -726,10 +790,15 @@ __global__ __launch_bounds__(D2) void decode_stream_merge_d256_kernel(const Deco
 hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   if (a.stream_wgs > 0) {
     if (hook) hook(hu, 0, s);
-    if (a.k_new)
-      hipLaunchKernelGGL(paged_decode_d256_stream_kernel<true>, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+    if (a.pool.format == kF16)  // (no fused form: the host appends first)
+      hipLaunchKernelGGL((paged_decode_d256_stream_kernel<kF16, false>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
+                         s, a);
+    else if (a.k_new)
+      hipLaunchKernelGGL((paged_decode_d256_stream_kernel<kBf16, true>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
+                         s, a);
     else
-      hipLaunchKernelGGL(paged_decode_d256_stream_kernel<false>, dim3(a.stream_wgs), dim3(kDecodeThreads), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_d256_stream_kernel<kBf16, false>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
+                         s, a);
     hipError_t e = hipGetLastError();
     if (hook) hook(hu, 1, s);
     if (e != hipSuccess) return e;
@@ -741,7 +810,10 @@ hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t 
   const int grid_x = max(1, (max_blk + a.split_blocks - 1) / a.split_blocks);
   if (hook) hook(hu, 0, s);
   dim3 grid(min(grid_x, a.max_splits), a.pool.kv_heads, a.num_seqs);
-  hipLaunchKernelGGL(paged_decode_d256_kernel, grid, dim3(kDecodeThreads), 0, s, a);
+  if (a.pool.format == kF16)
+    hipLaunchKernelGGL(paged_decode_d256_kernel<kF16>, grid, dim3(kDecodeThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(paged_decode_d256_kernel<kBf16>, grid, dim3(kDecodeThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (hook) hook(hu, 1, s);
   if (e != hipSuccess || a.max_splits <= 1) return e;

@@ -202,7 +202,7 @@ namespace llh {
 struct DecodePlan {
   bool empty = false;  // nothing to launch (no sequences)
   bool fast = false;   // tuned kernels (else the reference-order kernel)
-  bool d256 = false;   // tuned: the head_dim-256 (G = 8, bf16) kernels (split-K, or stream when stream_wgs > 0)
+  bool d256 = false;   // tuned: the head_dim-256 (G = 8, bf16 / fp16) kernels (split-K, or stream when stream_wgs > 0)
   int group = 0;
   int split_blocks = 0, max_splits = 0, stream_wgs = 0;
   size_t ml_off = 0, o_off = 0, desc_off = 0;  // tuned: partial (max, sum), partial outputs, segment descriptors

@@ -8,7 +8,7 @@
 namespace llh {
 
 constexpr int kFastHeadDim = 128;   // head_dim of the tuned kernels
-constexpr int kD256HeadDim = 256;   // head_dim of the tuned G = 8 bf16 decode kernels (decode256.hip)
+constexpr int kD256HeadDim = 256;   // head_dim of the tuned G = 8 bf16 / fp16 decode kernels (decode256.hip)
 constexpr int kD256Group = 8;        // their query heads per kv head
 constexpr int kFastBlockTokens = 16;  // block_tokens of the tuned kernels
 constexpr int kDecodeThreads = 256;   // 4 wavefronts

@@ -1,6 +1,6 @@
 """The head_dim-256 decode kernels (decode256.hip): Qwen3.5 / 3.6 full-attention layers,
-16 query heads over 2 kv heads, head_dim 256 (fixtures/qwen36/config.json), bf16 blocks
-of 16 tokens.  Both launch shapes (split-K and the persistent stream kernel, forced in
+16 query heads over 2 kv heads, head_dim 256 (fixtures/qwen36/config.json), bf16 or fp16
+blocks of 16 tokens.  Both launch shapes (split-K and the persistent stream kernel, forced in
 turn) are checked against the oracle (the per-head loop of crates/llm-backend/src/core/
 native_attention.rs:731-771, head_dim taken from the call) at the parity bar, their
 attended set bit-exactly with the position-coded probe (tests/attended_set.py), the
@@ -15,7 +15,7 @@ import pytest
 import llm_hip
 import oracle
 from attended_set import check_decode, code, coded_rows
-from helpers import assert_parity, from_dev_bf16, to_dev
+from helpers import assert_parity, from_dev_bf16, magnitude_rows, to_dev
 from llm_hip import workloads
 from test_gpu_decode import build_case, oracle_decode
 
@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
 D = 256
 BT = 16
 HQ, HKV = 16, 2
+FMTS = {"bf16": llm_hip.KV_BF16, "f16": llm_hip.KV_F16}
 
 
 @pytest.fixture(params=["split", "stream"])
@@ -61,30 +62,44 @@ def run(ctx, pool, batch, q, window, scale, Hq=HQ, gate=None, fn="decode", kv_ne
     return from_dev_bf16(out)
 
 
-def case(ctx, lens, seed, free=0.10, Hq=HQ):
+def case(ctx, lens, seed, free=0.10, Hq=HQ, fmt=llm_hip.KV_BF16):
     batch = workloads.paged_batch(np.asarray(lens, np.int32), BT, free, seed)
-    pool, q = build_case(ctx, batch, Hq, HKV, llm_hip.KV_BF16, seed, head_dim=D)
+    pool, q = build_case(ctx, batch, Hq, HKV, fmt, seed, head_dim=D)
     return batch, pool, q
 
 
-def test_decode256_qwen36_step(ctx, d256_kernel):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_qwen36_step(ctx, d256_kernel, fmt):
     """The Qwen3.6-shaped step: 32 sequences, lengths in [256, 4096], edges included."""
     lens = workloads.uniform_lengths(32, 256, 4096, workloads.SEED_BASE + 1)
     lens[:6] = [1, 16, 17, 32, 33, 4096]
-    batch, pool, q = case(ctx, lens, 101)
+    batch, pool, q = case(ctx, lens, 101, fmt=FMTS[fmt])
     scale = 1.0 / math.sqrt(D)
     out = run(ctx, pool, batch, q, 0, scale)
-    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, scale, head_dim=D),
-                  what="qwen36 step")
+    assert_parity(out, oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, scale, head_dim=D),
+                  what=f"qwen36 step {fmt}")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_query_magnitudes(ctx, d256_kernel, fmt):
+    """Query heads from bf16 subnormal to 1e30 (helpers.magnitude_rows): over fp16 blocks
+    each head's power-of-two scaling keeps q in fp16's range and is undone on the scores."""
+    lens = np.array([1, 17, 300, 1000, 4096, 33, 16, 2000], np.int32)
+    batch, pool, q = case(ctx, lens, 140, fmt=FMTS[fmt])
+    q = magnitude_rows(q, HQ, D)
+    out = run(ctx, pool, batch, q, 0, 0.0625)
+    assert_parity(out, oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"query magnitudes {fmt}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("window", [1, 17, 100, 4096])
-def test_decode256_windows(ctx, d256_kernel, window):
+def test_decode256_windows(ctx, d256_kernel, window, fmt):
     lens = np.array([1, 15, 16, 17, 100, 101, 700, 4100, 5000], np.int32)
-    batch, pool, q = case(ctx, lens, 102 + window)
+    batch, pool, q = case(ctx, lens, 102 + window, fmt=FMTS[fmt])
     out = run(ctx, pool, batch, q, window, 0.0625)
-    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, window, q, 0.0625, head_dim=D),
-                  what=f"W={window}")
+    assert_parity(out, oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, window, q, 0.0625, head_dim=D),
+                  what=f"W={window} {fmt}")
 
 
 @pytest.mark.parametrize("split_blocks", [4, 8, 64, 256])
@@ -100,18 +115,19 @@ def test_decode256_split_counts(ctx, opts, split_blocks):
                   what=f"split_blocks {split_blocks}")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("wgs", [1, 7, 64, 512])
-def test_decode256_stream_pieces(ctx, opts, wgs):
+def test_decode256_stream_pieces(ctx, opts, wgs, fmt):
     """The stream kernel over grids of 4 to 2048 wavefronts: segments whole inside one
     wavefront, and segments cut into up to 16, up to 32 and hundreds of pieces (the
     merge's one-round and 32-piece-round paths), ragged and empty sequences included."""
     opts(llm_hip.OPT_DECODE_KERNEL, "stream")
     opts(llm_hip.OPT_DECODE_STREAM_WGS, wgs)
     lens = np.array([20000, 1, 0, 333, 4096, 17, 2500], np.int32)
-    batch, pool, q = case(ctx, lens, 116 + wgs)
+    batch, pool, q = case(ctx, lens, 116 + wgs, fmt=FMTS[fmt])
     out = run(ctx, pool, batch, q, 0, 0.0625)
-    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
-                  what=f"stream over {wgs} workgroups")
+    assert_parity(out, oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"stream over {wgs} workgroups {fmt}")
 
 
 def test_decode256_is_deterministic(ctx, d256_kernel):
@@ -198,18 +214,20 @@ def test_decode256_append_then_attend(ctx, d256_kernel):
     assert_parity(out, ref, what="append + attend")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("window", [0, 100])
-def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window):
-    """llh_paged_decode_append at head_dim 256 in one launch (the stream kernel writes the new
-    token's rows to their slot and attends them from the registers of the block it loads):
-    the pool and the output are bit-identical to llh_kv_append followed by llh_paged_decode
-    on the same kernel; under the split-K option the call appends through the append kernel."""
+def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window, fmt):
+    """llh_paged_decode_append at head_dim 256 in one launch (bf16 on the stream kernel: it
+    writes the new token's rows to their slot and attends them from the registers of the
+    block it loads): the pool and the output are bit-identical to llh_kv_append followed by
+    llh_paged_decode on the same kernel; under the split-K option, and for fp16 pools, the
+    call appends through the append kernel."""
     import torch
 
     lens = workloads.uniform_lengths(24, 256, 4096, 120)
     lens[:8] = [1, 2, 15, 16, 17, 256, 999, 4096]
-    batch, pool_two, q = case(ctx, lens, 121)
-    _, pool_one, _ = case(ctx, lens, 121)
+    batch, pool_two, q = case(ctx, lens, 121, fmt=FMTS[fmt])
+    _, pool_one, _ = case(ctx, lens, 121, fmt=FMTS[fmt])
     kn = oracle.normal_bf16(122, lens.size * HKV * D).reshape(lens.size, HKV, D)
     vn = oracle.normal_bf16(123, lens.size * HKV * D).reshape(lens.size, HKV, D)
     slots = np.array([int(batch.tables[b, (int(L) - 1) // BT]) * BT + (int(L) - 1) % BT for b, L in enumerate(lens)],
@@ -220,35 +238,37 @@ def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window):
     out_two = run(ctx, pool_two, batch, q, window, scale)
     fused0 = ctx.metrics()["fused_append_calls"]
     out_one = run(ctx, pool_one, batch, q, window, scale, fn="append", kv_new=(kn, vn))
-    assert ctx.metrics()["fused_append_calls"] - fused0 == (1 if d256_kernel == "stream" else 0)
+    assert ctx.metrics()["fused_append_calls"] - fused0 == (1 if d256_kernel == "stream" and fmt == "bf16" else 0)
     a, b = pool_two.raw(), pool_one.raw()
     for key in a:
         assert np.array_equal(a[key], b[key]), key
     assert np.array_equal(out_one, out_two)
-    ref = oracle_decode(pool_one, batch, llm_hip.KV_BF16, HQ, HKV, window, q, scale, head_dim=D)
-    assert_parity(out_one, ref, what=f"fused append + attend W={window}")
+    ref = oracle_decode(pool_one, batch, FMTS[fmt], HQ, HKV, window, q, scale, head_dim=D)
+    assert_parity(out_one, ref, what=f"fused append + attend W={window} {fmt}")
 
 
-def coded_case(ctx, lens, seed, code_base):
+def coded_case(ctx, lens, seed, code_base, fmt=llm_hip.KV_BF16):
     """K random, V one-hot codes of the absolute position (attended_set.coded_rows) in
     dims 0..127, zeros above."""
     batch = workloads.paged_batch(np.asarray(lens, np.int32), BT, 0.10, seed)
     ids, src_k = workloads.block_sources(
         batch, lambda b, lo, hi: oracle.normal_bf16(seed + b, (hi - lo) * HKV * D).reshape(hi - lo, HKV, D), HKV, D)
     _, src_v = workloads.block_sources(batch, lambda b, lo, hi: coded_rows(lo, hi, HKV, D, code_base), HKV, D)
-    pool = ctx.pool(llm_hip.KV_BF16, BT, HKV, D, batch.n_blocks)
+    pool = ctx.pool(fmt, BT, HKV, D, batch.n_blocks)
     ctx.write_blocks(pool, to_dev(ids), to_dev(src_k), to_dev(src_v))
     return batch, pool
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("code_base", [0, 2])
 @pytest.mark.parametrize("window", [0, 1, 17, 100, 4096])
-def test_decode256_attended_set(ctx, d256_kernel, code_base, window):
+def test_decode256_attended_set(ctx, d256_kernel, code_base, window, fmt):
     """q = 0: every attended token weighs exactly 1 and the output counts the position codes
-    of the attended set, compared exactly with the reference's set."""
+    of the attended set, compared exactly with the reference's set (V's one-hot 1.0 values
+    are exact in fp16 too)."""
     lens = workloads.uniform_lengths(32, 256, 4096, 113)
     lens[:8] = [1, 15, 16, 17, 33, 4096, 5000, 8191]
-    batch, pool = coded_case(ctx, lens, 114, code_base)
+    batch, pool = coded_case(ctx, lens, 114, code_base, FMTS[fmt])
     q = np.zeros(lens.size * HQ * D, np.uint16)
     out = run(ctx, pool, batch, q, window, 0.0625)
     check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 W={window}", head_dim=D, code_base=code_base)
