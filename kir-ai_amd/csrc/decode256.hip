@@ -105,12 +105,13 @@ struct State256 {
 // sequence (positions 16 jb ..); valid: its table entry is inside the pool.
 // Returns this lane's packed weight pair (head fold(c), tokens 4g + 2 (c % 2) + {0, 1})
 // and, per token pair, the mask that zeroes V of unattended tokens.
-// FMT: kBf16, or kF16 (fp16 blocks, q scaled per head into fp16 by prep_q256_f16; qstep
-// is this lane's head's step, folded into the score scale).
+// FMT: kBf16, or kF16 (fp16 blocks, q scaled per head into fp16 by prep_q256_f16).
+// sscale: the score scale in log2 units, scale_log2e (times this lane's head's step
+// over fp16 blocks).
 template <int FMT>
 __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kregs &kr, bool valid, int jb, int lo,
                                                  int len, int lane, const uint32_t (&qw)[G2][8], State256 &st,
-                                                 uint32_t (&vm)[8], float qstep) {
+                                                 uint32_t (&vm)[8], float sscale) {
   const int g = lane >> 4;
   const int b0 = lane & 1;
   // ---- partial q . k: slot s, token 4g + i, over this lane's 16 dims ----
@@ -146,8 +147,7 @@ __device__ __forceinline__ uint32_t block_scores(const DecodeArgs &a, const Kreg
   for (int k = 0; k < 2; k++) {
     const float keep = b0 ? p[0][2 + k] : p[0][k];
     const float send = b0 ? p[0][k] : p[0][2 + k];
-    sc[k] = (keep + dpp<0xB1>(send)) * a.scale_log2e;  // quad_perm [1,0,3,2]
-    if constexpr (FMT == kF16) sc[k] *= qstep;
+    sc[k] = (keep + dpp<0xB1>(send)) * sscale;  // quad_perm [1,0,3,2]
   }
   // ---- mask: tokens outside [lo, len) or in a block outside the pool ----
   const bool partial = (jb * BT < lo) || (jb * BT + BT > len) || !valid;
@@ -238,43 +238,36 @@ __device__ __forceinline__ void load_q256(const DecodeArgs &a, size_t qrow0, int
   }
 }
 
+// One step of a max over the row's 16 lanes for every slot: the partner lane c ^ d
+// (DPP CTRL) holds this lane's head of slot s (s ^ fold(c)) in its slot s ^ fold(d).
+template <int CTRL, int FD>
+__device__ __forceinline__ void row_max_step(int (&m)[G2]) {
+  int t[G2];
+#pragma unroll
+  for (int s = 0; s < G2; s++) t[s] = __builtin_amdgcn_update_dpp(0, m[s ^ FD], CTRL, 0xF, 0xF, false);
+#pragma unroll
+  for (int s = 0; s < G2; s++) m[s] = max(m[s], t[s]);
+}
+
 // fp16 blocks: q of each head scaled into fp16 by its own power of two over its 256
-// dims (f16_scaling); lane c holds head s ^ fold(c) in slot s, so each head's maximum
-// is gathered by selects and a row reduction.  Returns the step of the head this lane
-// scores (fold(c)), which multiplies its scores.
-__device__ __forceinline__ float prep_q256_f16(uint32_t (&qw)[G2][8], int lane) {
-  const int fc = fold(lane & 15);
-  int mxs[G2];  // per slot
+// dims (f16_scaling).  The row reduction runs in slot order (row_max_step); slot 0
+// holds head fold(c), the head this lane scores, whose step is returned: it
+// multiplies this lane's scores.
+__device__ __forceinline__ float prep_q256_f16(uint32_t (&qw)[G2][8]) {
+  int m[G2];
 #pragma unroll
-  for (int s = 0; s < G2; s++) mxs[s] = bf16_absmax_bits<8>(qw[s]);
-  float inv[G2], step[G2];  // per head
-#pragma unroll
-  for (int h = 0; h < G2; h++) {
-    const int x = h ^ fc;  // this lane's slot of head h
-    int m = mxs[0];
-#pragma unroll
-    for (int s = 1; s < G2; s++) m = x == s ? mxs[s] : m;
-    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x140, 0xF, 0xF, false));  // row_mirror
-    const F16Scaling sc = f16_scaling(m);
-    inv[h] = sc.inv;
-    step[h] = sc.step;
-  }
-  float my_step = step[0];
-#pragma unroll
-  for (int h = 1; h < G2; h++) my_step = fc == h ? step[h] : my_step;
+  for (int s = 0; s < G2; s++) m[s] = bf16_absmax_bits<8>(qw[s]);
+  row_max_step<0xB1, fold(1)>(m);   // quad_perm [1,0,3,2]: c ^ 1
+  row_max_step<0x4E, fold(2)>(m);   // quad_perm [2,3,0,1]: c ^ 2
+  row_max_step<0x141, fold(7)>(m);  // row_half_mirror: c ^ 7
+  row_max_step<0x140, fold(15)>(m); // row_mirror: c ^ 15
 #pragma unroll
   for (int s = 0; s < G2; s++) {
-    const int hs = s ^ fc;  // the head of slot s
-    float iv = inv[0];
-#pragma unroll
-    for (int h = 1; h < G2; h++) iv = hs == h ? inv[h] : iv;
+    const float iv = f16_scaling(m[s]).inv;
 #pragma unroll
     for (int k = 0; k < 8; k++) qw[s][k] = bf16x2_to_f16x2(qw[s][k], iv);
   }
-  return my_step;
+  return f16_scaling(m[0]).step;
 }
 
 __device__ __forceinline__ void reset256(State256 &st) {
@@ -332,8 +325,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
 
   uint32_t qw[G2][8];
   load_q256(a, qrow0, lane, qw);
-  float qstep = 1.0f;
-  if constexpr (FMT == kF16) qstep = prep_q256_f16(qw, lane);
+  float sscale = a.scale_log2e;
+  if constexpr (FMT == kF16) sscale *= prep_q256_f16(qw);
   State256 st;
   reset256(st);
 
@@ -358,7 +351,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
     for (; k + 1 < nbw; k++) {
       bad |= !valid;
       uint32_t vm[8];
-      const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, qstep);
+      const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, sscale);
       e = entry(k + 1);
       valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
       phys = valid ? e : 0;
@@ -370,7 +363,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_kernel(co
     }
     bad |= !valid;
     uint32_t vm[8];
-    const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, qstep);
+    const uint32_t w = block_scores<FMT>(a, kr, valid, blk_begin + wave + 4 * k, lo, len, lane, qw, st, vm, sscale);
     block_accumulate<FMT>(vr, w, vm, st);
     if (bad && lane == 0) atomicOr(a.err, kErrBadBlock);
   }
@@ -610,7 +603,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
   };
   uint32_t qw[G2][8];
   load_q256(a, (size_t)C.b * a.q_heads + (size_t)C.kvh * G2, lane, qw);
-  float qstep = 1.0f;
+  float sscale = a.scale_log2e;
   bool q_new = true;  // fp16: qw holds a segment's bf16 q not yet scaled
   int e = next_entry();
   bool valid = e >= 0 && (int64_t)e < a.pool.n_blocks;
@@ -663,10 +656,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
       }
     if constexpr (FMT == kF16)
       if (q_new) {
-        qstep = prep_q256_f16(qw, lane);
+        sscale = a.scale_log2e * prep_q256_f16(qw);
         q_new = false;
       }
-    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, qstep);
+    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, sscale);
     valid = e_next >= 0 && (int64_t)e_next < a.pool.n_blocks;
     const int phys = valid ? e_next : 0;
     load_k(a, phys, L.kvh, lane, kr);
@@ -706,10 +699,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
       }
     if constexpr (FMT == kF16)
       if (q_new) {
-        qstep = prep_q256_f16(qw, lane);
+        sscale = a.scale_log2e * prep_q256_f16(qw);
         q_new = false;
       }
-    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, qstep);
+    const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, sscale);
     if constexpr (FUSED)
       if (C.j == C.nb - 1) {
         patch_new_v(vr, nv, (C.len - 1) % BT);
