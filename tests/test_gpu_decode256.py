@@ -102,17 +102,18 @@ def test_decode256_windows(ctx, d256_kernel, window, fmt):
                   what=f"W={window} {fmt}")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("split_blocks", [4, 8, 64, 256])
-def test_decode256_split_counts(ctx, opts, split_blocks):
+def test_decode256_split_counts(ctx, opts, split_blocks, fmt):
     """One split (split_blocks 256 over 4096 tokens) up to 64 (4 blocks a split), and the
     planner's growth of the split past 64 partials for a 20000-token context."""
     opts(llm_hip.OPT_DECODE_KERNEL, "split")
     opts(llm_hip.OPT_DECODE_SPLIT_BLOCKS, split_blocks)
     lens = np.array([4096, 20000, 1, 333], np.int32)
-    batch, pool, q = case(ctx, lens, 103)
+    batch, pool, q = case(ctx, lens, 103, fmt=FMTS[fmt])
     out = run(ctx, pool, batch, q, 0, 0.0625)
-    assert_parity(out, oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
-                  what=f"split_blocks {split_blocks}")
+    assert_parity(out, oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"split_blocks {split_blocks} {fmt}")
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -130,28 +131,31 @@ def test_decode256_stream_pieces(ctx, opts, wgs, fmt):
                   what=f"stream over {wgs} workgroups {fmt}")
 
 
-def test_decode256_is_deterministic(ctx, d256_kernel):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_is_deterministic(ctx, d256_kernel, fmt):
     lens = workloads.uniform_lengths(8, 256, 4096, 104)
-    batch, pool, q = case(ctx, lens, 104)
+    batch, pool, q = case(ctx, lens, 104, fmt=FMTS[fmt])
     a = run(ctx, pool, batch, q, 0, 0.0625)
     b = run(ctx, pool, batch, q, 0, 0.0625)
     assert np.array_equal(a, b)
 
 
-def test_decode256_empty_sequence_is_zero(ctx, d256_kernel):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_empty_sequence_is_zero(ctx, d256_kernel, fmt):
     lens = np.array([0, 20, 0, 300], np.int32)
-    batch, pool, q = case(ctx, lens, 105)
+    batch, pool, q = case(ctx, lens, 105, fmt=FMTS[fmt])
     out = run(ctx, pool, batch, q, 0, 0.0625).reshape(4, -1)
     assert np.all(oracle.bf16_to_f32(out[0]) == 0.0) and np.all(oracle.bf16_to_f32(out[2]) == 0.0)
-    assert_parity(out.ravel(), oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D),
-                  what="empty rows")
+    assert_parity(out.ravel(), oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, 0.0625, head_dim=D),
+                  what=f"empty rows {fmt}")
 
 
-def test_decode256_bad_block_is_masked_and_flagged(ctx, d256_kernel):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_bad_block_is_masked_and_flagged(ctx, d256_kernel, fmt):
     import torch
 
     lens = np.array([100, 300], np.int32)
-    batch, pool, q = case(ctx, lens, 106)
+    batch, pool, q = case(ctx, lens, 106, fmt=FMTS[fmt])
     tables = batch.tables.copy()
     tables[1, 3] = batch.n_blocks + 5  # outside the pool
     out = torch.zeros(2 * HQ * D, dtype=torch.int16, device="cuda")
@@ -160,39 +164,41 @@ def test_decode256_bad_block_is_masked_and_flagged(ctx, d256_kernel):
     torch.cuda.synchronize()
     assert ctx.device_errors(reset=True) & llm_hip.ERR_FLAG_BAD_BLOCK
     # sequence 0 is untouched by the bad entry
-    ref = oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, 0, q, 0.0625, head_dim=D)
-    assert_parity(from_dev_bf16(out)[: HQ * D], ref[: HQ * D], what="sequence beside the bad block")
+    ref = oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, 0, q, 0.0625, head_dim=D)
+    assert_parity(from_dev_bf16(out)[: HQ * D], ref[: HQ * D], what=f"sequence beside the bad block {fmt}")
 
 
 def gate_rows(seed, n):
     return oracle.f32_to_bf16(oracle.bf16_to_f32(oracle.normal_bf16(seed, n)) * np.float32(2.0))
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("window", [0, 333])
-def test_decode256_gate(ctx, d256_kernel, window):
+def test_decode256_gate(ctx, d256_kernel, window, fmt):
     """The Qwen3.6 attention output gate: out * sigmoid(gate), applied before the bf16 rounding."""
     lens = workloads.uniform_lengths(16, 1, 3000, 107)
-    batch, pool, q = case(ctx, lens, 107)
+    batch, pool, q = case(ctx, lens, 107, fmt=FMTS[fmt])
     gate = gate_rows(108, lens.size * HQ * D)
     out = run(ctx, pool, batch, q, window, 0.0625, gate=gate)
-    ref = oracle.apply_gate(oracle_decode(pool, batch, llm_hip.KV_BF16, HQ, HKV, window, q, 0.0625, head_dim=D),
+    ref = oracle.apply_gate(oracle_decode(pool, batch, FMTS[fmt], HQ, HKV, window, q, 0.0625, head_dim=D),
                             oracle.bf16_to_f32(gate))
-    assert_parity(out, ref, what=f"gated W={window}")
+    assert_parity(out, ref, what=f"gated W={window} {fmt}")
 
 
-def test_decode256_noalloc_matches_decode(ctx, opts):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode256_noalloc_matches_decode(ctx, opts, fmt):
     """llh_paged_decode_noalloc runs split-K at head_dim 256 whatever the option asks: the
     stream kernel's partials (two slots per wavefront) exceed the static scratch.  Its
     output equals the split-K call's bit for bit and the stream call's within the bar."""
     lens = workloads.uniform_lengths(16, 256, 4096, 109)  # split-K partials within the static scratch
-    batch, pool, q = case(ctx, lens, 109)
+    batch, pool, q = case(ctx, lens, 109, fmt=FMTS[fmt])
     opts(llm_hip.OPT_DECODE_KERNEL, "split")
     a = run(ctx, pool, batch, q, 0, 0.0625)
     opts(llm_hip.OPT_DECODE_KERNEL, "stream")
     b = run(ctx, pool, batch, q, 0, 0.0625, fn="noalloc")
     assert np.array_equal(a, b)
     c = run(ctx, pool, batch, q, 0, 0.0625)
-    assert_parity(c, oracle.bf16_to_f32(a), what="stream vs split-K")
+    assert_parity(c, oracle.bf16_to_f32(a), what=f"stream vs split-K {fmt}")
 
 
 def test_decode256_append_then_attend(ctx, d256_kernel):
