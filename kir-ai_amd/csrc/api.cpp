@@ -887,13 +887,14 @@ int llh_paged_decode_append(llh_ctx *ctx, llh_kv_pool *pool, const llh_decode_de
                      "block_tokens (one block more than the window)");
   // one launch on the tuned kernels (new-token rows 16-byte aligned): bf16 pools attend
   // the new token from its rows, int8 / fp8 pools quantise it into the block that
-  // receives it; at head_dim 256 the stream kernel (bf16) writes the token's rows and
-  // attends them from the registers of the block it loads.  fp8 pools on the persistent
-  // stream kernel are the exception: the scale-growth re-encode doubles that kernel's
-  // code and costs more than the separate append launch it saves; fp16 pools and the
-  // head_dim-256 split-K kernel have no fused form.  Every other case appends through
-  // the append kernel first, then decodes.
-  const bool fused = plan.fast && pv.format != LLH_KV_F16 && aligned16(d_k_new) && aligned16(d_v_new) &&
+  // receives it; at head_dim 256 the stream kernel (bf16 and fp16 pools) writes the
+  // token's rows and attends them from the registers of the block it loads.  fp8 pools
+  // on the persistent stream kernel are the exception: the scale-growth re-encode
+  // doubles that kernel's code and costs more than the separate append launch it
+  // saves; fp16 pools at head_dim 128 and the head_dim-256 split-K kernel have no fused
+  // form.  Every other case appends through the append kernel first, then decodes.
+  const bool fused = plan.fast && (pv.format != LLH_KV_F16 || plan.d256) && aligned16(d_k_new) &&
+                     aligned16(d_v_new) &&
                      !(pv.format == LLH_KV_FP8_E4M3 && plan.stream_wgs > 0) && (!plan.d256 || plan.stream_wgs > 0);
   WsLease lease;
   st = lease.acquire(ctx, s, plan.bytes);

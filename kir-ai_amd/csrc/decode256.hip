@@ -547,6 +547,25 @@ __device__ __forceinline__ void patch_new_v(Vregs &vr, const uint32_t (&nv)[2], 
     }
   }
 }
+// fp16 pools: the new token's bf16 words as the append kernel stores them (each
+// element widened exactly, then rounded to nearest even), converted at the patch,
+// where the rows are first used.
+__device__ __forceinline__ uint32_t bf16x2_as_f16x2(uint32_t w) { return pack_f16(bf16_lo(w), bf16_hi(w)); }
+template <int FMT>
+__device__ __forceinline__ void new_k_words(uint4 (&nk)[2]) {
+  if constexpr (FMT == kF16)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      nk[i] = make_uint4(bf16x2_as_f16x2(nk[i].x), bf16x2_as_f16x2(nk[i].y), bf16x2_as_f16x2(nk[i].z),
+                         bf16x2_as_f16x2(nk[i].w));
+}
+template <int FMT>
+__device__ __forceinline__ void new_v_words(uint32_t (&nv)[2]) {
+  if constexpr (FMT == kF16)
+#pragma unroll
+    for (int i = 0; i < 2; i++) nv[i] = bf16x2_as_f16x2(nv[i]);
+}
+
 // The new token into its pool slot (block phys, kv head kvh, offset off), from the
 // registers the patch used: K from the 16 lanes of row 0 (each holds dims 8c .. and
 // 128 + 8c ..), V from every lane (dims 64j + lane).  Written by the wavefront that
@@ -651,6 +670,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
     const bool cvalid = valid;
     if constexpr (FUSED)
       if (seg_end) {
+        new_k_words<FMT>(nk);
         patch_new_k(kr, nk, (C.len - 1) % BT, lane);
         if (cvalid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
       }
@@ -673,6 +693,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (FUSED)
       if (seg_end) {
+        new_v_words<FMT>(nv);
         patch_new_v(vr, nv, (C.len - 1) % BT);
         if (cvalid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
       }
@@ -694,6 +715,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
     uint32_t vm[8];
     if constexpr (FUSED)
       if (C.j == C.nb - 1) {
+        new_k_words<FMT>(nk);
         patch_new_k(kr, nk, (C.len - 1) % BT, lane);
         if (valid) store_new_k(a, cphys, C.kvh, (C.len - 1) % BT, nk, lane);
       }
@@ -705,6 +727,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_d256_stream_ke
     const uint32_t wp = block_scores<FMT>(a, kr, valid, C.lo / BT + C.j, C.lo, C.len, lane, qw, st, vm, sscale);
     if constexpr (FUSED)
       if (C.j == C.nb - 1) {
+        new_v_words<FMT>(nv);
         patch_new_v(vr, nv, (C.len - 1) % BT);
         if (valid) store_new_v(a, cphys, C.kvh, (C.len - 1) % BT, nv, lane);
       }
@@ -783,7 +806,10 @@ __global__ __launch_bounds__(D2) void decode_stream_merge_d256_kernel(const Deco
 hipError_t launch_decode_d256(const DecodeArgs &a, int max_seq_len, hipStream_t s, void *hu, LaunchHook hook) {
   if (a.stream_wgs > 0) {
     if (hook) hook(hu, 0, s);
-    if (a.pool.format == kF16)  // (no fused form: the host appends first)
+    if (a.pool.format == kF16 && a.k_new)
+      hipLaunchKernelGGL((paged_decode_d256_stream_kernel<kF16, true>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
+                         s, a);
+    else if (a.pool.format == kF16)
       hipLaunchKernelGGL((paged_decode_d256_stream_kernel<kF16, false>), dim3(a.stream_wgs), dim3(kDecodeThreads), 0,
                          s, a);
     else if (a.k_new)

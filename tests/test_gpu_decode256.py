@@ -223,11 +223,11 @@ def test_decode256_append_then_attend(ctx, d256_kernel):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("window", [0, 100])
 def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window, fmt):
-    """llh_paged_decode_append at head_dim 256 in one launch (bf16 on the stream kernel: it
-    writes the new token's rows to their slot and attends them from the registers of the
-    block it loads): the pool and the output are bit-identical to llh_kv_append followed by
-    llh_paged_decode on the same kernel; under the split-K option, and for fp16 pools, the
-    call appends through the append kernel."""
+    """llh_paged_decode_append at head_dim 256 in one launch (the stream kernel writes the new
+    token's rows to their slot -- rounded to fp16 for fp16 pools -- and attends them from the
+    registers of the block it loads): the pool and the output are bit-identical to
+    llh_kv_append followed by llh_paged_decode on the same kernel; under the split-K option
+    the call appends through the append kernel."""
     import torch
 
     lens = workloads.uniform_lengths(24, 256, 4096, 120)
@@ -244,7 +244,7 @@ def test_decode256_fused_append_equals_two_calls(ctx, d256_kernel, window, fmt):
     out_two = run(ctx, pool_two, batch, q, window, scale)
     fused0 = ctx.metrics()["fused_append_calls"]
     out_one = run(ctx, pool_one, batch, q, window, scale, fn="append", kv_new=(kn, vn))
-    assert ctx.metrics()["fused_append_calls"] - fused0 == (1 if d256_kernel == "stream" and fmt == "bf16" else 0)
+    assert ctx.metrics()["fused_append_calls"] - fused0 == (1 if d256_kernel == "stream" else 0)
     a, b = pool_two.raw(), pool_one.raw()
     for key in a:
         assert np.array_equal(a[key], b[key]), key
@@ -280,8 +280,9 @@ def test_decode256_attended_set(ctx, d256_kernel, code_base, window, fmt):
     check_decode(out, lens, window, HQ, HKV, 1.0, f"d256 W={window}", head_dim=D, code_base=code_base)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("window", [0, 17, 1000])
-def test_decode256_fused_append_attended_set(ctx, d256_kernel, window):
+def test_decode256_fused_append_attended_set(ctx, d256_kernel, window, fmt):
     """llh_paged_decode_append at head_dim 256 with q = 0 and position-coded V: the step
     attends the pool's [lo, len - 1) plus the new token from the call's rows -- the stale
     slot holds a decoy code (its code + 64), so attending it instead is caught -- and the
@@ -291,7 +292,7 @@ def test_decode256_fused_append_attended_set(ctx, d256_kernel, window):
     code_base = 2
     lens = workloads.uniform_lengths(32, 256, 4096, 130)
     lens[:8] = [1, 15, 16, 17, 33, 4096, 5000, 8191]
-    batch, pool = coded_case(ctx, lens, 131, code_base)
+    batch, pool = coded_case(ctx, lens, 131, code_base, FMTS[fmt])
     B = lens.size
     pos = lens.astype(np.int64) - 1
     decoy = np.zeros((B, HKV, D), np.uint16)

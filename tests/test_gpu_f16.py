@@ -13,8 +13,10 @@ crates/llm-kv-cache/src/format.rs:69-120).
 * prefill: the MFMA kernel on fp16 operands against the oracle (full and
   sampled rows, windows, groups) and every row against the decode kernel; rows of
   very different magnitude (each row has its own power of two).
-* the element-wise kernels take the other shapes; decode-append on fp16 pools is
-  the append kernel then the decode (no fused launch); layer caches refuse fp16.
+* the element-wise kernels take the other shapes; decode-append on fp16 pools at
+  head_dim 128 is the append kernel then the decode (no fused launch; at head_dim
+  256 the stream kernel fuses it, tests/test_gpu_decode256.py); layer caches refuse
+  fp16.
 """
 import math
 
