@@ -947,6 +947,13 @@ def run_sections(ctx, args, lens, sel) -> list:
                               seed=workloads.SEED_BASE + 5, graph=True, head_dim=256)
         secondary.append(r)
         log(f"Q36 f16: {r}")
+        # append + attend in one call over the fp16 pool (the stream kernel's fused instance)
+        _, r = measure_decode(ctx, "Q36 fp16 append + attend in one call (llh_paged_decode_append)", lens, 16, 2,
+                              llm_hip.KV_F16, sec_steps, sec_warm, seed=workloads.SEED_BASE + 5, fused=True,
+                              head_dim=256)
+        r["decode_alone_us"] = secondary[-1]["us_per_step"]
+        secondary.append(r)
+        log(f"Q36 f16 append+attend: {r}")
         torch.cuda.empty_cache()
     if sel("neighbours"):
         secondary.extend(measure_neighbours(ctx, sec_steps, sec_warm))
